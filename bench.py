@@ -1,0 +1,247 @@
+"""WKV7 benchmark on one MI355X: prefill and T=1 decode
+(config 2), synthetic seeded inputs resident in HBM.
+
+A step is one call of the packed fp32-state recurrence
+(``_C.tmix_wkv7_recurrent_fp32_from_decay_logits`` with a reused metadata
+ticket, as benchmarks/tmix/wkv7/bench.py:309-365 of the reference does) over
+the whole batch.  W warm-up steps, then K timed steps between a
+synchronize/event pair; the state pool is reset before the timed region.
+tokens/s = total tokens per step / seconds per step.
+
+``roofline`` is measured live: the dominant kernel is launched K more times
+through the C ABI directly (no Python checks between launches) on the same
+torch stream, bracketed by HIP events, and its algorithmic bytes
+(896 B per token-head + 2 x 16 KiB of fp32 state per sequence-head) are
+divided by the average launch duration.
+
+``cpu_baseline`` times the oracle's fp32 C recurrence (OpenMP over
+sequence x head) on the host on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "WKV7 tokens/s at h32d64 bf16 (prefill + T=1 decode); % of HBM/MFMA roofline"
+HBM_PEAK_GBS = 8000.0
+BYTES_PER_TOKEN_HEAD = 896          # 6 bf16 inputs x 64 + bf16 output x 64
+STATE_BYTES = 64 * 64 * 4           # one fp32 64x64 state
+
+
+def algorithmic_bytes(total_tokens: int, heads: int, sequences: int) -> int:
+    return total_tokens * heads * BYTES_PER_TOKEN_HEAD + 2 * sequences * heads * STATE_BYTES
+
+
+class Runner:
+    """One workload with its ticket, output buffer and a state pool."""
+
+    def __init__(self, w, torch, flashrwkv2_amd):
+        self.w = w
+        self.torch = torch
+        self.C = flashrwkv2_amd._C
+        self.state0 = w.state_pool
+        self.state = w.state_pool.clone()
+        self.out = torch.empty_like(w.v)
+        self.ticket = flashrwkv2_amd.prepare_tmix_wkv7_recurrent_metadata(
+            w.cu_seqlens, w.state_indices, total_tokens=w.total_tokens,
+            state_pool_size=w.state_pool.shape[0])
+        from flashrwkv2_amd import _native as N
+
+        self.N = N
+        self.lib = N.load()
+        t = self.ticket
+        self._direct = (t._query_start_loc_snapshot().data_ptr(),
+                        t._state_indices_snapshot().data_ptr(), t._status().data_ptr(),
+                        w.state_indices.numel(), w.num_heads, 64, w.total_tokens,
+                        t._max_seqlen(), N.FR2_DTYPE_BFLOAT16, self.state.data_ptr(),
+                        w.r.data_ptr(), w.decay_logits.data_ptr(), None, w.k.data_ptr(),
+                        w.v.data_ptr(), w.a.data_ptr(), w.b.data_ptr(), self.out.data_ptr(),
+                        1.0)
+
+    def step(self):
+        w = self.w
+        self.C.tmix_wkv7_recurrent_fp32_from_decay_logits(
+            w.cu_seqlens, w.state_indices, self.state, *w.tokens, self.out, 1.0, None,
+            self.ticket)
+
+    def direct(self, stream_handle):
+        rc = self.lib.fr2_wkv7_recurrent_fp32_forward(*self._direct, stream_handle)
+        if rc:
+            self.N.check(rc, "fr2_wkv7_recurrent_fp32_forward")
+
+    def reset(self):
+        self.state.copy_(self.state0)
+
+    def time_steps(self, steps: int, warmup: int) -> float:
+        torch = self.torch
+        for _ in range(warmup):
+            self.step()
+        torch.cuda.synchronize()
+        self.reset()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(steps):
+            self.step()
+        end.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        return max(start.elapsed_time(end), wall * 1e3) / steps
+
+    def time_kernel(self, launches: int) -> float:
+        """Average device duration of one launch (ms), direct C-ABI launches."""
+        torch = self.torch
+        stream = torch.cuda.current_stream()
+        handle = stream.cuda_stream
+        for _ in range(3):
+            self.direct(handle)
+        self.reset()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(launches):
+            self.direct(handle)
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / launches
+
+    def kernel_name(self) -> str:
+        from flashrwkv2_amd import _native as N  # noqa: F401
+
+        ms = self.ticket._max_seqlen()
+        if ms <= 4:
+            return "decode64_kernel"
+        if ms >= 128:
+            return "chunked MFMA kernel (serial fallback when not built)"
+        return "serial_kernel"
+
+
+def cpu_baseline(w, threads: int, sample_tokens: int | None):
+    """fp32 C recurrence on the host over the first `sample_tokens` tokens of
+    every sequence (all heads)."""
+    import numpy as np
+
+    import oracle
+
+    cu = w.cu_seqlens.cpu().numpy()
+    lens = np.diff(cu)
+    take = lens if sample_tokens is None else np.minimum(lens, sample_tokens)
+    idx = np.concatenate([np.arange(cu[i], cu[i] + take[i]) for i in range(len(lens))])
+    toks = [t.float().cpu().numpy()[idx] for t in w.tokens]
+    cu_s = np.concatenate([[0], np.cumsum(take)]).astype(np.int32)
+    pool = w.state_pool.cpu().numpy()
+    oracle.wkv7_cpu_f32(*(t[: cu_s[1]] for t in toks), cu_seqlens=cu_s[:2],
+                        state_pool=pool[:1], threads=threads)  # warm-up
+    t0 = time.perf_counter()
+    oracle.wkv7_cpu_f32(*toks, cu_seqlens=cu_s, state_indices=np.arange(len(lens), dtype=np.int32),
+                        state_pool=pool, threads=threads)
+    dt = time.perf_counter() - t0
+    n_tok = int(take.sum())
+    return n_tok / dt, dt, n_tok
+
+
+def roofline_obj(bytes_per_launch: int, kernel_ms: float):
+    achieved = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode (config 2) leg")
+    ap.add_argument("--cpu-sample-tokens", type=int, default=4096,
+                    help="tokens per sequence in the CPU baseline sample")
+    ap.add_argument("--only", choices=["prefill", "decode"], default=None,
+                    help="run one leg only (profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one MI355X only (one GPU per box); "
+              "multi-GPU runs are not part of it", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import flashrwkv2_amd
+    from flashrwkv2_amd import workloads
+
+    if flashrwkv2_amd._C is None:
+        print("bench.py: no GPU backend (flashrwkv2_amd._C is None)", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+    result: dict = {}
+
+    pre = None
+    if args.only in (None, "prefill"):
+        w1 = workloads.config(1, "cuda")
+        pre = Runner(w1, torch, flashrwkv2_amd)
+        ms = pre.time_steps(args.steps, args.warmup)
+        kms = pre.time_kernel(args.steps)
+        bytes1 = algorithmic_bytes(w1.total_tokens, w1.num_heads, w1.state_indices.numel())
+        result.update({
+            "metric": METRIC,
+            "value": round(w1.total_tokens / (ms * 1e-3), 1),
+            "unit": "tokens/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms, 5),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "f32",
+            "data": "synthetic (seeded, BASELINE config 1 distributions; inputs resident in HBM)",
+            "config": {"workload": w1.name, "B": 8, "T": 4096, "H": 32, "D": 64,
+                       "io": "bf16", "state": "fp32", "kernel": pre.kernel_name(),
+                       "parallelism": "single GPU"},
+            "roofline": roofline_obj(bytes1, kms),
+            "kernel_ms": round(kms, 5),
+            "algorithmic_bytes": bytes1,
+        })
+    if args.only in (None, "decode") and not args.no_decode:
+        w2 = workloads.config(2, "cuda")
+        dec = Runner(w2, torch, flashrwkv2_amd)
+        dms = dec.time_steps(max(args.steps, 50), args.warmup)
+        dkms = dec.time_kernel(max(args.steps, 200))
+        bytes2 = algorithmic_bytes(w2.total_tokens, w2.num_heads, w2.state_indices.numel())
+        result["decode"] = {
+            "workload": w2.name, "tokens_per_s": round(w2.total_tokens / (dms * 1e-3), 1),
+            "ms_per_step": round(dms, 5), "kernel_ms": round(dkms, 5),
+            "kernel_tokens_per_s": round(w2.total_tokens / (dkms * 1e-3), 1),
+            "kernel": dec.kernel_name(), "roofline": roofline_obj(bytes2, dkms),
+            "algorithmic_bytes": bytes2,
+        }
+        if not result.get("metric"):
+            result.update({"metric": METRIC, "value": result["decode"]["tokens_per_s"],
+                           "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+                           "warmup": args.warmup, "ms_per_step": round(dms, 5)})
+    if pre is not None and not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        tps, dt, n_tok = cpu_baseline(pre.w, threads, args.cpu_sample_tokens)
+        result["cpu_baseline"] = {
+            "value": round(tps, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"first {args.cpu_sample_tokens} tokens of each of the 8 config-1 "
+                      f"sequences, all 32 heads ({n_tok} tokens, {dt:.2f} s), fp32 C "
+                      "recurrence (oracle/wkv7_oracle.c, OpenMP over sequence x head)",
+        }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

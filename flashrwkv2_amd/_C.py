@@ -1,0 +1,620 @@
+"""Native-layer operator surface of the WKV7 path, on the gfx950 C ABI.
+
+This module plays the role of the reference's private pybind module
+``flashrwkv2._C`` for the WKV7 path: the same function names, positional
+order, keyword defaults, ticket class and ``RuntimeError`` texts where the
+reference's tests match on them.  Argument checks run here in Python; every
+computation runs in the HIP kernels of ``lib/libflashrwkv2_amd.so`` through
+:mod:`flashrwkv2_amd._native`.  There is no other execution path.
+
+Reference bindings mirrored:
+  csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cpp:45-434
+  csrc/validation.cpp:12-129
+  csrc/sm120/tmix/wkv7/pretrain_recurrent_bf16_forward.cpp:20-55
+  csrc/sm120/tmix/wkv7/infer_chunk_bf16_forward_varlen.cpp:44-204
+  csrc/sm120/tmix/wkv7/rl_infctx_chunk_fp32io16_forward.cpp:73-241
+  csrc/sm120/tmix/wkv7/rl_infctx_chunk_fp32io16_backward.cpp:22-135
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Sequence
+
+import torch
+
+from . import _native as N
+
+INT32_MAX = 2**31 - 1
+_TOKEN_DTYPES = {torch.float16: N.FR2_DTYPE_FLOAT16, torch.bfloat16: N.FR2_DTYPE_BFLOAT16}
+
+def _check(cond: bool, *msg: object) -> None:
+    if not cond:
+        raise RuntimeError("".join(str(m) for m in msg))
+
+
+def check_cuda_contiguous(t: torch.Tensor, name: str) -> None:
+    """validation.cpp:12-15."""
+    _check(isinstance(t, torch.Tensor) and t.is_cuda, name, " must be CUDA")
+    _check(t.is_contiguous(), name, " must be contiguous")
+
+
+def check_same_device(ref: torch.Tensor, t: torch.Tensor, name: str) -> None:
+    """validation.cpp:17-25."""
+    _check(t.device == ref.device, name, " must be on the same device as state")
+
+
+def _tensor_version(t: torch.Tensor) -> int | None:
+    if t.is_inference():
+        return None
+    return t._version
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    return _TOKEN_DTYPES[t.dtype]
+
+
+# ---------------------------------------------------------------------------
+# Metadata tickets
+# ---------------------------------------------------------------------------
+class _RecurrentMetadataTicket:
+    """Validated packed metadata bound to a stream.
+
+    Mirrors RecurrentMetadataTicket
+    (infer_recurrent_fp32io16_forward_varlen.cpp:89-225): it keeps the
+    validated snapshot (static form) or the live buffers (graph form), the
+    device status, and the identity/version/shape/stream facts that every
+    consumer re-checks.
+    """
+
+    def __init__(self, qsl, slots, qsl_snap, slots_snap, status, workspace,
+                 live_tokens, live_seqs, total_tokens, pool_size, max_seqlen,
+                 graph_mode, stream):
+        self._qsl = qsl
+        self._slots = slots
+        self._qsl_snap = qsl_snap
+        self._slots_snap = slots_snap
+        self._status_t = status
+        self._workspace = workspace
+        self._live_tokens = live_tokens
+        self._live_seqs = live_seqs
+        self._qsl_version = _tensor_version(qsl)
+        self._slots_version = _tensor_version(slots)
+        self._qsl_ptr = qsl.data_ptr()
+        self._slots_ptr = slots.data_ptr()
+        self._qsl_geom = (tuple(qsl.shape), tuple(qsl.stride()))
+        self._slots_geom = (tuple(slots.shape), tuple(slots.stride()))
+        self._total_tokens = int(total_tokens)
+        self._pool_size = int(pool_size)
+        self._max_seqlen_v = int(max_seqlen)
+        self._graph = bool(graph_mode)
+        self._device = qsl.device
+        self._stream_handle = stream
+
+    def _check_compatible(self, query_start_loc, state_indices, total_tokens,
+                          state_pool_size, max_seqlen) -> None:
+        _check(query_start_loc is self._qsl,
+               "validated_metadata query_start_loc identity mismatch")
+        _check(state_indices is self._slots,
+               "validated_metadata state_indices identity mismatch")
+        _check(query_start_loc.data_ptr() == self._qsl_ptr
+               and state_indices.data_ptr() == self._slots_ptr,
+               "validated_metadata metadata data_ptr mismatch")
+        _check((tuple(query_start_loc.shape), tuple(query_start_loc.stride())) == self._qsl_geom
+               and (tuple(state_indices.shape), tuple(state_indices.stride())) == self._slots_geom,
+               "validated_metadata metadata shape or stride mismatch")
+        if not self._graph and self._qsl_version is not None:
+            _check(_tensor_version(query_start_loc) == self._qsl_version,
+                   "validated_metadata query_start_loc version mismatch")
+        if not self._graph and self._slots_version is not None:
+            _check(_tensor_version(state_indices) == self._slots_version,
+                   "validated_metadata state_indices version mismatch")
+        _check(query_start_loc.device == self._device and state_indices.device == self._device,
+               "validated_metadata device mismatch")
+        _check(int(total_tokens) == self._total_tokens,
+               "validated_metadata total_tokens mismatch")
+        _check(int(state_pool_size) == self._pool_size,
+               "validated_metadata state_pool_size mismatch")
+        if max_seqlen > 0:
+            _check(int(max_seqlen) == self._max_seqlen_v,
+                   "validated_metadata max_seqlen mismatch")
+        _check(_stream(self._device) == self._stream_handle,
+               "validated_metadata stream mismatch; prepare and consume the ticket "
+               "on the same CUDA stream")
+
+    def _query_start_loc_snapshot(self) -> torch.Tensor:
+        return self._qsl_snap
+
+    def _state_indices_snapshot(self) -> torch.Tensor:
+        return self._slots_snap
+
+    def _status(self) -> torch.Tensor:
+        return self._status_t
+
+    def _max_seqlen(self) -> int:
+        return self._max_seqlen_v
+
+    def _is_graph(self) -> bool:
+        return self._graph
+
+    def _num_active_tokens(self):
+        return self._live_tokens
+
+    def _num_active_sequences(self):
+        return self._live_seqs
+
+
+def _launch_validation(qsl, slots, live_tokens, live_seqs, total_tokens, num_seqs,
+                       pool_size, max_seqlen, snapshot):
+    """Device validation (recurrent_metadata.cu:134-194): status, workspace,
+    and private snapshots for the static form."""
+    dev = qsl.device
+    with torch.cuda.device(dev):
+        status = torch.empty(3, device=dev, dtype=torch.int32)
+        seen = torch.empty(pool_size, device=dev, dtype=torch.int32)
+        qsl_snap = torch.empty_like(qsl) if snapshot else qsl
+        slots_snap = torch.empty_like(slots) if snapshot else slots
+        rc = N.load().fr2_wkv7_prepare_metadata(
+            qsl.data_ptr(), slots.data_ptr(), int(num_seqs), int(total_tokens),
+            int(pool_size), int(max_seqlen),
+            N.ptr(live_tokens), N.ptr(live_seqs), status.data_ptr(), seen.data_ptr(),
+            qsl_snap.data_ptr() if snapshot else None,
+            slots_snap.data_ptr() if snapshot else None, _stream(dev))
+    N.check(rc, "prepare_tmix_wkv7_recurrent_metadata")
+    return qsl_snap, slots_snap, status, seen
+
+
+def _host_metadata_max_seqlen(qsl, slots, total_tokens, pool_size) -> int:
+    """Host check of the metadata values (…fp32io16_forward_varlen.cpp:45-80);
+    returns the longest sequence."""
+    offsets = qsl.to("cpu").tolist()
+    slot_list = slots.to("cpu").tolist()
+    n = len(slot_list)
+    _check(offsets[0] == 0, "query_start_loc must start at 0")
+    _check(offsets[n] == total_tokens,
+           "the final query_start_loc offset must equal total_tokens")
+    seen: set[int] = set()
+    longest = 0
+    for i in range(n):
+        lo, hi = offsets[i], offsets[i + 1]
+        _check(lo >= 0 and hi > lo and hi <= total_tokens,
+               "query_start_loc must be strictly increasing with non-empty sequences")
+        s = slot_list[i]
+        _check(0 <= s < pool_size, "state_indices entries must be within the state pool")
+        _check(s not in seen, "state_indices must be unique within one call")
+        seen.add(s)
+        longest = max(longest, hi - lo)
+    return longest
+
+
+def prepare_tmix_wkv7_recurrent_metadata(query_start_loc, state_indices, total_tokens,
+                                         state_pool_size, max_seqlen=-1):
+    """Static ticket (…fp32io16_forward_varlen.cpp:227-275)."""
+    check_cuda_contiguous(query_start_loc, "query_start_loc")
+    check_cuda_contiguous(state_indices, "state_indices")
+    _check(state_indices.device == query_start_loc.device,
+           "state_indices must be on the same device as state")
+    _check(query_start_loc.dtype == torch.int32 and state_indices.dtype == torch.int32,
+           "recurrent metadata must be int32")
+    _check(query_start_loc.dim() == 1 and state_indices.dim() == 1
+           and state_indices.numel() > 0
+           and query_start_loc.numel() == state_indices.numel() + 1,
+           "query_start_loc must have shape [B+1] and state_indices shape [B]")
+    _check(state_indices.numel() <= 65535,
+           "state_indices must contain at most 65535 sequences")
+    _check(0 < total_tokens <= INT32_MAX, "total_tokens must be positive and fit in int32")
+    _check(0 < state_pool_size <= INT32_MAX,
+           "state_pool_size must be positive and fit in int32")
+    inferred = _host_metadata_max_seqlen(query_start_loc, state_indices, int(total_tokens),
+                                         int(state_pool_size))
+    if max_seqlen <= 0:
+        max_seqlen = inferred
+    else:
+        _check(max_seqlen == inferred,
+               "max_seqlen must equal the largest packed sequence length")
+    stream = _stream(query_start_loc.device)
+    snap_q, snap_s, status, seen = _launch_validation(
+        query_start_loc, state_indices, None, None, total_tokens,
+        state_indices.numel(), state_pool_size, total_tokens, True)
+    return _RecurrentMetadataTicket(query_start_loc, state_indices, snap_q, snap_s, status,
+                                    seen, None, None, total_tokens, state_pool_size,
+                                    max_seqlen, False, stream)
+
+
+def _check_graph_scalar(t, ref, name):
+    _check(isinstance(t, torch.Tensor) and t.is_cuda, name, " must be a CUDA tensor")
+    _check(t.is_contiguous(), name, " must be contiguous")
+    _check(t.device == ref.device, name, " must share the metadata CUDA device")
+    _check(t.dtype == torch.int32, name, " must have dtype int32")
+    _check(t.numel() == 1, name, " must contain one element")
+
+
+def prepare_tmix_wkv7_recurrent_graph_metadata(query_start_loc, state_indices,
+                                               num_active_tokens, num_active_sequences,
+                                               token_capacity, sequence_capacity,
+                                               state_pool_size, max_seqlen_capacity):
+    """Live capacity ticket for warmup / graph capture (…cpp:277-326)."""
+    check_cuda_contiguous(query_start_loc, "query_start_loc")
+    check_cuda_contiguous(state_indices, "state_indices")
+    _check(state_indices.device == query_start_loc.device,
+           "state_indices must be on the same device as state")
+    _check(query_start_loc.dtype == torch.int32 and state_indices.dtype == torch.int32,
+           "recurrent metadata must be int32")
+    _check(0 < sequence_capacity <= 65535 and state_indices.dim() == 1
+           and state_indices.numel() == sequence_capacity
+           and query_start_loc.dim() == 1
+           and query_start_loc.numel() == sequence_capacity + 1,
+           "graph metadata shapes must match sequence_capacity")
+    _check(0 < token_capacity <= INT32_MAX,
+           "token_capacity must be positive and fit in int32")
+    _check(0 < state_pool_size <= INT32_MAX,
+           "state_pool_size must be positive and fit in int32")
+    _check(0 < max_seqlen_capacity <= token_capacity,
+           "max_seqlen_capacity must be positive and not exceed token_capacity")
+    _check_graph_scalar(num_active_tokens, query_start_loc, "num_active_tokens")
+    _check_graph_scalar(num_active_sequences, query_start_loc, "num_active_sequences")
+    stream = _stream(query_start_loc.device)
+    snap_q, snap_s, status, seen = _launch_validation(
+        query_start_loc, state_indices, num_active_tokens, num_active_sequences,
+        token_capacity, sequence_capacity, state_pool_size, max_seqlen_capacity, False)
+    return _RecurrentMetadataTicket(query_start_loc, state_indices, snap_q, snap_s, status,
+                                    seen, num_active_tokens, num_active_sequences,
+                                    token_capacity, state_pool_size, max_seqlen_capacity,
+                                    True, stream)
+
+
+# ---------------------------------------------------------------------------
+# fp32-state packed recurrence
+# ---------------------------------------------------------------------------
+def check_recurrent_layout(qsl, slots, state, r, decay_logits, k, v, a, b, output, scale):
+    """validation.cpp:27-129."""
+    for t, name in ((qsl, "query_start_loc"), (slots, "state_indices"), (state, "state"),
+                    (r, "r"), (decay_logits, "decay_logits"), (k, "k"), (v, "v"),
+                    (a, "a"), (b, "b"), (output, "output")):
+        check_cuda_contiguous(t, name)
+    _check(qsl.dtype == torch.int32, "query_start_loc must be int32")
+    _check(slots.dtype == torch.int32, "state_indices must be int32")
+    _check(math.isfinite(scale), "scale must be finite")
+    n = slots.numel()
+    _check(0 < n <= 65535, "state_indices must contain 1..65535 sequences")
+    _check(slots.dim() == 1, "state_indices must have shape [N]")
+    _check(qsl.dim() == 1 and qsl.size(0) == n + 1, "query_start_loc must have shape [N+1]")
+    _check(state.dim() == 4 and state.size(0) > 0 and state.size(1) > 0
+           and state.size(2) == state.size(3), "state must have square shape [slots,H,D,D]")
+    _check(state.dtype == torch.float32, "state must be float32")
+    d = state.size(2)
+    _check(d in (64, 128, 256), "recurrent head size must be 64, 128, or 256, got ", d)
+    _check(state.size(0) <= INT32_MAX, "state slot count must fit in int32")
+    h = state.size(1)
+    _check(h <= INT32_MAX, "head count must fit in int32")
+    _check(r.dim() == 3 and r.size(0) > 0 and r.size(1) == h and r.size(2) == d,
+           "r must have shape [total_tokens,H,D] matching state")
+    _check(r.size(0) <= INT32_MAX, "token count must fit in int32")
+    _check(all(t.shape == r.shape for t in (decay_logits, k, v, a, b, output)),
+           "r,decay_logits,k,v,a,b,output shape mismatch")
+    _check(r.dtype in _TOKEN_DTYPES, "token tensors must be float16 or bfloat16")
+    _check(all(t.dtype == r.dtype for t in (decay_logits, k, v, a, b, output)),
+           "r,decay_logits,k,v,a,b,output dtype mismatch")
+    for t, name in ((qsl, "query_start_loc"), (slots, "state_indices"), (r, "r"),
+                    (decay_logits, "decay_logits"), (k, "k"), (v, "v"), (a, "a"),
+                    (b, "b"), (output, "output")):
+        check_same_device(state, t, name)
+    return n, h, d
+
+
+def _check_decay_bias(decay_bias, state, r, h, d, dtype_msg):
+    check_cuda_contiguous(decay_bias, "decay_bias")
+    check_same_device(state, decay_bias, "decay_bias")
+    _check(decay_bias.dtype == r.dtype, dtype_msg)
+    _check((decay_bias.dim() == 1 and decay_bias.numel() == h * d)
+           or (decay_bias.dim() == 2 and decay_bias.size(0) == h and decay_bias.size(1) == d),
+           "decay_bias must have shape [H*D] or [H,D]")
+
+
+def _resolve_launch_metadata(qsl, slots, total_tokens, pool_size, max_seqlen, ticket):
+    """Ticket path or an implicit device-only validation (…cpp:360-380)."""
+    if ticket is not None:
+        ticket._check_compatible(qsl, slots, total_tokens, pool_size, max_seqlen)
+        return (ticket._query_start_loc_snapshot(), ticket._state_indices_snapshot(),
+                ticket._status(), ticket._max_seqlen(), ticket)
+    snap_q, snap_s, status, seen = _launch_validation(
+        qsl, slots, None, None, total_tokens, slots.numel(), pool_size, total_tokens, True)
+    keep = (snap_q, snap_s, status, seen)
+    return snap_q, snap_s, status, max_seqlen, keep
+
+
+def _recurrent_launch(kernel, qsl, slots, state, r, decay_logits, k, v, a, b, output,
+                      scale, decay_bias, validated_metadata, max_seqlen):
+    n, h, d = check_recurrent_layout(qsl, slots, state, r, decay_logits, k, v, a, b,
+                                     output, scale)
+    if decay_bias is not None:
+        _check_decay_bias(decay_bias, state, r, h, d,
+                          "decay_bias must match the token tensor dtype")
+    lq, ls, status, max_seqlen, keep = _resolve_launch_metadata(
+        qsl, slots, r.size(0), state.size(0), int(max_seqlen), validated_metadata)
+    lib = N.load()
+    common = (lq.data_ptr(), ls.data_ptr(), status.data_ptr(), n, h, d, r.size(0),
+              int(max_seqlen), _dtype_code(r), state.data_ptr(), r.data_ptr(),
+              decay_logits.data_ptr(), N.ptr(decay_bias), k.data_ptr(), v.data_ptr(),
+              a.data_ptr(), b.data_ptr(), output.data_ptr(), float(scale))
+    with torch.cuda.device(state.device):
+        stream = _stream(state.device)
+        if kernel is None:
+            rc = lib.fr2_wkv7_recurrent_fp32_forward(*common, stream)
+        else:
+            rc = lib.fr2_wkv7_recurrent_fp32_forward_kernel(int(kernel), *common, stream)
+    N.check(rc, "tmix_wkv7_recurrent_fp32_from_decay_logits")
+    # Implicit validation buffers (`keep`) are released after the launch; the
+    # caching allocator only hands them out again to work queued later on this
+    # same stream, which runs after the kernels that read them.
+    del keep
+
+
+def tmix_wkv7_recurrent_fp32_from_decay_logits(query_start_loc, state_indices, state, r,
+                                               decay_logits, k, v, a, b, output, scale,
+                                               decay_bias=None, validated_metadata=None,
+                                               max_seqlen=-1):
+    """In-place fp32-state packed recurrence (…fp32io16_forward_varlen.cpp:330-387)."""
+    _recurrent_launch(None, query_start_loc, state_indices, state, r, decay_logits, k, v,
+                      a, b, output, scale, decay_bias, validated_metadata, max_seqlen)
+
+
+def tmix_wkv7_recurrent_fp32_kernel_forced(kernel, query_start_loc, state_indices, state, r,
+                                           decay_logits, k, v, a, b, output, scale,
+                                           decay_bias=None, validated_metadata=None,
+                                           max_seqlen=-1):
+    """Same contract with the kernel family forced (0 serial, 1 decode,
+    2 chunked MFMA).  No reference counterpart: used to pin each kernel."""
+    _recurrent_launch(int(kernel), query_start_loc, state_indices, state, r, decay_logits,
+                      k, v, a, b, output, scale, decay_bias, validated_metadata, max_seqlen)
+
+
+# ---------------------------------------------------------------------------
+# pretrain [B,T,H,D] forward
+# ---------------------------------------------------------------------------
+def pretrain_tmix_wkv7_recurrent_forward(r, w, k, v, a, b, output, boundary, state_dot_a,
+                                         head_size):
+    """pretrain_recurrent_bf16_forward.cpp:20-27 (bf16 [B,T,H,N])."""
+    _check(head_size in (64, 128, 256), "head_size must be one of 64, 128, or 256")
+    _check(r.size(3) == head_size, "input head dimension must equal head_size")
+    B, T, H, _ = r.shape
+    for t, name in ((r, "r"), (w, "w"), (k, "k"), (v, "v"), (a, "a"), (b, "b"),
+                    (output, "output"), (boundary, "boundary"), (state_dot_a, "state_dot_a")):
+        check_cuda_contiguous(t, name)
+    _check(all(t.dtype == torch.bfloat16 for t in (r, w, k, v, a, b, output)),
+           "pretrain token tensors must be bfloat16")
+    _check(all(t.shape == r.shape for t in (w, k, v, a, b, output)),
+           "pretrain token tensors must share shape [B,T,H,N]")
+    _check(T % 16 == 0, "T must be divisible by the canonical chunk length 16")
+    _check(tuple(boundary.shape) == (B, H, T // 16, head_size, head_size)
+           and boundary.dtype == torch.float32, "boundary must be float32 [B,H,T/16,N,N]")
+    _check(state_dot_a.shape == r.shape and state_dot_a.dtype == torch.float32,
+           "state_dot_a must be float32 [B,T,H,N]")
+    with torch.cuda.device(r.device):
+        rc = N.load().fr2_wkv7_pretrain_forward(
+            B, T, H, head_size, r.data_ptr(), w.data_ptr(), k.data_ptr(), v.data_ptr(),
+            a.data_ptr(), b.data_ptr(), output.data_ptr(), boundary.data_ptr(),
+            state_dot_a.data_ptr(), _stream(r.device))
+    N.check(rc, "pretrain_tmix_wkv7_recurrent_forward")
+
+
+def pretrain_tmix_wkv7_recurrent_backward(*args, **kwargs):
+    """Training backward (pretrain_recurrent_bf16_forward.cu:163-486) is not
+    part of this operator build; the forward's boundary and state_dot_a
+    checkpoints are produced so that it can be added."""
+    raise NotImplementedError(
+        "flashrwkv2_amd implements the WKV7 forward path only; "
+        "pretrain_tmix_wkv7_recurrent_backward is not available"
+    )
+
+
+# ---------------------------------------------------------------------------
+# bf16-state packed chunk inference
+# ---------------------------------------------------------------------------
+def _check_bf16(t, ref, name):
+    check_cuda_contiguous(t, name)
+    check_same_device(ref, t, name)
+    _check(t.dtype == torch.bfloat16, name, " must be bf16")
+
+
+def infer_tmix_wkv7_chunk_bf16_forward_varlen(r, decay_logits, k, v, a, b, state_pool,
+                                              cu_seqlens, state_indices, chunk_size=16,
+                                              max_seqlen=-1, scale=1.0, decay_bias=None,
+                                              validated_metadata=None):
+    """bf16 state pool updated in place (infer_chunk_bf16_forward_varlen.cpp:77-192)."""
+    _check_bf16(r, r, "r")
+    for t, name in ((decay_logits, "decay_logits"), (k, "k"), (v, "v"), (a, "a"),
+                    (b, "b"), (state_pool, "state_pool")):
+        _check_bf16(t, r, name)
+    _check(math.isfinite(scale), "scale must be finite")
+    _check(chunk_size > 0, "chunk_size must be positive")
+    _check(max_seqlen > 0, "max_seqlen must be positive")
+    _check(r.dim() == 3 and r.size(0) > 0 and r.size(1) > 0 and r.size(2) == 64,
+           "chunk token tensors must have shape [total_tokens,H,64]")
+    for t, name in ((decay_logits, "decay_logits"), (k, "k"), (v, "v"), (a, "a"), (b, "b")):
+        _check(t.shape == r.shape, name, " must have the same shape as r")
+    _check(state_pool.dim() == 4 and state_pool.size(0) > 0
+           and state_pool.size(1) == r.size(1) and state_pool.size(2) == 64
+           and state_pool.size(3) == 64, "state_pool must have shape [slots,H,64,64]")
+    check_cuda_contiguous(cu_seqlens, "cu_seqlens")
+    check_cuda_contiguous(state_indices, "state_indices")
+    check_same_device(r, cu_seqlens, "cu_seqlens")
+    check_same_device(r, state_indices, "state_indices")
+    _check(cu_seqlens.dtype == torch.int32 and state_indices.dtype == torch.int32,
+           "chunk metadata must be int32")
+    _check(cu_seqlens.dim() == 1 and state_indices.dim() == 1 and state_indices.numel() > 0
+           and cu_seqlens.numel() == state_indices.numel() + 1,
+           "cu_seqlens must have shape [B+1] and state_indices [B]")
+    h = r.size(1)
+    if decay_bias is not None:
+        _check_bf16(decay_bias, r, "decay_bias")
+        _check((decay_bias.dim() == 1 and decay_bias.numel() == h * 64)
+               or (decay_bias.dim() == 2 and decay_bias.size(0) == h
+                   and decay_bias.size(1) == 64),
+               "decay_bias must have shape [H*64] or [H,64]")
+    output = torch.empty_like(v)
+    lq, ls, status, max_seqlen, keep = _resolve_launch_metadata(
+        cu_seqlens, state_indices, r.size(0), state_pool.size(0), int(max_seqlen),
+        validated_metadata)
+    with torch.cuda.device(r.device):
+        rc = N.load().fr2_wkv7_chunk_bf16_forward(
+            lq.data_ptr(), ls.data_ptr(), status.data_ptr(), state_indices.numel(), h,
+            r.size(0), int(chunk_size), int(max_seqlen), state_pool.data_ptr(),
+            r.data_ptr(), decay_logits.data_ptr(), N.ptr(decay_bias), k.data_ptr(),
+            v.data_ptr(), a.data_ptr(), b.data_ptr(), output.data_ptr(), float(scale),
+            _stream(r.device))
+    N.check(rc, "infer_tmix_wkv7_chunk_bf16_forward_varlen")
+    del keep
+    return output, state_pool
+
+
+# ---------------------------------------------------------------------------
+# RL/Infctx fp32-state chunk forward and replay
+# ---------------------------------------------------------------------------
+def _check_chunk_metadata(sco, starts, ends, num_sequences, total_tokens, state):
+    """rl_infctx_chunk_fp32io16_forward.cpp:73-132 (host copy of the metadata)."""
+    for t, name in ((sco, "sequence_chunk_offsets"), (starts, "chunk_token_starts"),
+                    (ends, "chunk_token_ends")):
+        check_cuda_contiguous(t, name)
+        check_same_device(state, t, name)
+        _check(t.dtype == torch.int32, name, " must be int32")
+    _check(sco.dim() == 1 and sco.numel() == num_sequences + 1,
+           "sequence_chunk_offsets must have shape [B+1]")
+    _check(starts.dim() == 1 and starts.numel() > 0 and starts.shape == ends.shape,
+           "chunk token metadata must have matching shape [C]")
+    _check(starts.numel() * state.size(1) <= INT32_MAX, "chunk/head grid must fit in int32")
+    seq = sco.to("cpu").tolist()
+    st = starts.to("cpu").tolist()
+    en = ends.to("cpu").tolist()
+    chunks = len(st)
+    _check(seq[0] == 0 and seq[num_sequences] == chunks,
+           "sequence_chunk_offsets must cover all chunks")
+    prev_end = 0
+    longest = 0
+    longest_chunk = 0
+    for i in range(num_sequences):
+        c0, c1 = seq[i], seq[i + 1]
+        _check(c0 >= 0 and c1 > c0 and c1 <= chunks,
+               "each sequence must own at least one ordered chunk")
+        _check(st[c0] == prev_end, "chunks must cover packed tokens without gaps")
+        for c in range(c0, c1):
+            _check(st[c] >= 0 and en[c] > st[c] and en[c] <= total_tokens
+                   and (c == c0 or st[c] == en[c - 1]),
+                   "chunk token ranges must be contiguous and non-empty")
+            longest_chunk = max(longest_chunk, en[c] - st[c])
+        prev_end = en[c1 - 1]
+        longest = max(longest, en[c1 - 1] - st[c0])
+    _check(prev_end == total_tokens, "chunks must cover exactly all packed tokens")
+    return longest, longest_chunk
+
+
+def rl_infctx_tmix_wkv7_chunk_fp32io16_forward(sequence_chunk_offsets, chunk_token_starts,
+                                               chunk_token_ends, state, r, decay_logits, k,
+                                               v, a, b, strategy=1, scale=1.0,
+                                               decay_bias=None):
+    """Returns (output, final_state); `state` itself is not modified
+    (rl_infctx_chunk_fp32io16_forward.cpp:158-230)."""
+    _check(strategy in (0, 1), "strategy must be 0 (materialized) or 1 (recompute)")
+    _check(isinstance(state, torch.Tensor) and state.is_cuda and state.is_contiguous()
+           and state.dtype == torch.float32, "RL/Infctx state must be contiguous CUDA float32")
+    _check(state.dim() == 4 and state.size(0) > 0 and state.size(1) > 0
+           and state.size(2) == state.size(3) and state.size(2) in (64, 128, 256),
+           "RL/Infctx state must have shape [B,H,D,D], D in {64,128,256}")
+    working = state.clone()
+    output = torch.empty_like(v)
+    internal_slots = torch.arange(state.size(0), device=state.device, dtype=torch.int32)
+    n, h, d = check_recurrent_layout(sequence_chunk_offsets, internal_slots, working, r,
+                                     decay_logits, k, v, a, b, output, scale)
+    longest, longest_chunk = _check_chunk_metadata(sequence_chunk_offsets, chunk_token_starts,
+                                    chunk_token_ends, state.size(0), r.size(0), working)
+    if decay_bias is not None:
+        _check_decay_bias(decay_bias, working, r, h, d, "decay_bias must match token dtype")
+    # The native contract carries no chunk size; the chunk family that the
+    # metadata describes is the smallest of 16/32/64 holding every chunk.
+    _check(longest_chunk <= 64, "chunk token ranges must not exceed 64 tokens")
+    chunk_size = 16 if longest_chunk <= 16 else (32 if longest_chunk <= 32 else 64)
+    with torch.cuda.device(r.device):
+        rc = N.load().fr2_wkv7_rl_infctx_forward(
+            sequence_chunk_offsets.data_ptr(), chunk_token_starts.data_ptr(),
+            chunk_token_ends.data_ptr(), n, chunk_token_starts.numel(), h, d, r.size(0),
+            int(longest), chunk_size, int(strategy), _dtype_code(r), working.data_ptr(),
+            r.data_ptr(), decay_logits.data_ptr(), N.ptr(decay_bias), k.data_ptr(),
+            v.data_ptr(), a.data_ptr(), b.data_ptr(), output.data_ptr(), float(scale),
+            _stream(r.device))
+    N.check(rc, "rl_infctx_tmix_wkv7_chunk_fp32io16_forward")
+    return output, working
+
+
+def rl_infctx_tmix_wkv7_chunk_fp32io16_backward_replay(chunk_token_starts, chunk_token_ends,
+                                                       boundary, r, decay_logits, k, v, a, b,
+                                                       output, state_dot_a, scale=1.0,
+                                                       decay_bias=None):
+    """Replay of each chunk from its start-of-chunk state
+    (rl_infctx_chunk_fp32io16_backward.cpp:22-125)."""
+    for t, name in ((boundary, "boundary"), (r, "r"), (decay_logits, "decay_logits"),
+                    (k, "k"), (v, "v"), (a, "a"), (b, "b"), (output, "output"),
+                    (state_dot_a, "state_dot_a"), (chunk_token_starts, "chunk_token_starts"),
+                    (chunk_token_ends, "chunk_token_ends")):
+        check_cuda_contiguous(t, name)
+    _check(math.isfinite(scale), "scale must be finite")
+    _check(chunk_token_starts.dtype == torch.int32 and chunk_token_ends.dtype == torch.int32,
+           "chunk token metadata must be int32")
+    _check(chunk_token_starts.dim() == 1 and chunk_token_starts.numel() > 0
+           and chunk_token_starts.shape == chunk_token_ends.shape,
+           "chunk token metadata must have shape [C]")
+    _check(boundary.dim() == 4 and boundary.size(0) == chunk_token_starts.numel()
+           and boundary.size(1) == r.size(1) and boundary.size(2) == r.size(2)
+           and boundary.size(3) == r.size(2) and boundary.dtype == torch.float32,
+           "boundary must have shape [C,H,D,D] and be float32")
+    _check(r.dim() == 3 and r.size(0) > 0 and r.size(2) in (64, 128, 256),
+           "replay token tensors must have shape [N,H,D], D in {64,128,256}")
+    for t, name in ((decay_logits, "decay_logits"), (k, "k"), (v, "v"), (a, "a"), (b, "b"),
+                    (output, "output")):
+        _check(t.shape == r.shape, name, " must match r shape")
+        _check(t.dtype == r.dtype, name, " must match r dtype")
+        check_same_device(r, t, name)
+    _check(r.dtype in _TOKEN_DTYPES, "replay token tensors must be float16 or bfloat16")
+    _check(state_dot_a.shape == r.shape and state_dot_a.dtype == torch.float32,
+           "state_dot_a must match r shape and be float32")
+    for t in (chunk_token_starts, chunk_token_ends, boundary, state_dot_a):
+        check_same_device(r, t, "replay metadata/workspace")
+    h, d = r.size(1), r.size(2)
+    if decay_bias is not None:
+        check_cuda_contiguous(decay_bias, "decay_bias")
+        check_same_device(r, decay_bias, "decay_bias")
+        _check(decay_bias.dtype == r.dtype, "decay_bias must match r dtype")
+        _check((decay_bias.dim() == 1 and decay_bias.numel() == h * d)
+               or (decay_bias.dim() == 2 and decay_bias.size(0) == h
+                   and decay_bias.size(1) == d),
+               "decay_bias must have shape [H*D] or [H,D]")
+    # The replay kernels read chunk ranges on the device; the host only checks
+    # them against the token count so that no launch can run out of bounds.
+    st = chunk_token_starts.to("cpu").tolist()
+    en = chunk_token_ends.to("cpu").tolist()
+    _check(all(0 <= s < e <= r.size(0) for s, e in zip(st, en)),
+           "chunk token ranges must be non-empty and within the packed tokens")
+    with torch.cuda.device(r.device):
+        rc = N.load().fr2_wkv7_rl_infctx_replay(
+            chunk_token_starts.data_ptr(), chunk_token_ends.data_ptr(),
+            chunk_token_starts.numel(), h, d, r.size(0), _dtype_code(r), boundary.data_ptr(),
+            r.data_ptr(), decay_logits.data_ptr(), N.ptr(decay_bias), k.data_ptr(),
+            v.data_ptr(), a.data_ptr(), b.data_ptr(), output.data_ptr(),
+            state_dot_a.data_ptr(), float(scale), _stream(r.device))
+    N.check(rc, "rl_infctx_tmix_wkv7_chunk_fp32io16_backward_replay")
+
+
+def exported_names() -> Sequence[str]:
+    return (
+        "prepare_tmix_wkv7_recurrent_metadata",
+        "prepare_tmix_wkv7_recurrent_graph_metadata",
+        "tmix_wkv7_recurrent_fp32_from_decay_logits",
+        "pretrain_tmix_wkv7_recurrent_forward",
+        "pretrain_tmix_wkv7_recurrent_backward",
+        "infer_tmix_wkv7_chunk_bf16_forward_varlen",
+        "rl_infctx_tmix_wkv7_chunk_fp32io16_forward",
+        "rl_infctx_tmix_wkv7_chunk_fp32io16_backward_replay",
+    )

@@ -1,0 +1,121 @@
+"""ctypes binding of the gfx950 C-ABI library (``include/flashrwkv2_amd.h``).
+
+The library is built in-tree by :mod:`flashrwkv2_amd.build`.  Loading never
+falls back to anything: a missing library raises, so no code path can silently
+run elsewhere than the HIP kernels.  ``torch`` is imported first so that the
+library binds to the HIP runtime torch already loaded (both carry the
+``libamdhip64.so.7`` soname).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int32, c_int64, c_void_p, c_char_p, POINTER
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the library load, see docstring)
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libflashrwkv2_amd.so"
+
+FR2_OK = 0
+FR2_ERR_INVALID_ARGUMENT = 1
+FR2_ERR_UNSUPPORTED = 2
+FR2_ERR_LAUNCH = 3
+
+FR2_DTYPE_FLOAT16 = 0
+FR2_DTYPE_BFLOAT16 = 1
+
+KERNEL_SERIAL = 0
+KERNEL_DECODE = 1
+KERNEL_CHUNKED = 2
+
+_i32p = POINTER(c_int32)
+
+# name -> (restype, argtypes); mirrors include/flashrwkv2_amd.h exactly.
+SIGNATURES: dict[str, tuple] = {
+    "fr2_abi_version": (c_int32, []),
+    "fr2_status_string": (c_char_p, [c_int32]),
+    "fr2_last_error": (c_char_p, []),
+    "fr2_wkv7_prepare_metadata": (
+        c_int32,
+        [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
+    "fr2_wkv7_recurrent_fp32_forward": (
+        c_int32,
+        [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64,
+         c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_void_p],
+    ),
+    "fr2_wkv7_recurrent_fp32_forward_kernel": (
+        c_int32,
+        [c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32,
+         c_int64, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_void_p],
+    ),
+    "fr2_wkv7_pretrain_forward": (
+        c_int32,
+        [c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
+    "fr2_wkv7_chunk_bf16_forward": (
+        c_int32,
+        [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int64, c_int32,
+         c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_float, c_void_p],
+    ),
+    "fr2_wkv7_rl_infctx_forward": (
+        c_int32,
+        [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
+         c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_float, c_void_p],
+    ),
+    "fr2_wkv7_rl_infctx_replay": (
+        c_int32,
+        [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64, c_int32,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_float, c_void_p],
+    ),
+}
+
+_LIB: ctypes.CDLL | None = None
+
+
+def load(path: Path | str | None = None) -> ctypes.CDLL:
+    """Load (once) and return the library with every signature bound."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    lib_path = Path(path) if path is not None else LIB_PATH
+    if not lib_path.exists():
+        raise RuntimeError(
+            f"flashrwkv2_amd native library not built: {lib_path} is missing; "
+            "run `python -m flashrwkv2_amd.build` (hipcc, gfx950)"
+        )
+    lib = ctypes.CDLL(str(lib_path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    """Raise RuntimeError for a non-zero fr2_status_t."""
+    if status == FR2_OK:
+        return
+    lib = load()
+    text = lib.fr2_status_string(status).decode()
+    detail = lib.fr2_last_error().decode() if status == FR2_ERR_LAUNCH else ""
+    raise RuntimeError(f"{what} failed: {text}{(': ' + detail) if detail else ''}")
+
+
+def ptr(t: "torch.Tensor | None") -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: "torch.device") -> int:
+    return torch.cuda.current_stream(device).cuda_stream

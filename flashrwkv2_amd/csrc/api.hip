@@ -1,0 +1,221 @@
+// extern "C" entry points of the WKV7 operator (declared in
+// include/flashrwkv2_amd.h).  Each validates pointers and sizes, fills a
+// segment descriptor and enqueues the chosen kernel family on `stream`.
+#include "recurrent.h"
+
+namespace {
+
+using fr2::SegArgs;
+
+// Kernel-family policy (replaces use_small_auto,
+// csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:378-391).
+// Short requests stream the state once with the decode kernel; long ones go
+// to the chunked MFMA kernel; everything else runs token-serial.
+constexpr int kDecodeMaxSeqlen = 4;
+constexpr int kChunkMinSeqlen = 128;
+
+enum Family { kAuto = -1, kSerial = 0, kDecode = 1, kChunked = 2 };
+
+bool tokens_ok(const void* r, const void* l, const void* k, const void* v,
+               const void* a, const void* b, const void* y) {
+  return r && l && k && v && a && b && y;
+}
+
+int run_family(int family, int D, int dtype, bool bf16_state, const SegArgs& p,
+               int nseg, int max_seqlen, hipStream_t s) {
+  if (family == kAuto) {
+    const bool plain = p.sa_out == nullptr && p.boundary == nullptr && !bf16_state;
+    if (D == 64 && plain && max_seqlen > 0 && max_seqlen <= kDecodeMaxSeqlen) {
+      family = kDecode;
+    } else if (D == 64 && plain && max_seqlen >= kChunkMinSeqlen) {
+      const int rc = fr2::launch_chunked(dtype, p, nseg, max_seqlen, s);
+      if (rc != FR2_ERR_UNSUPPORTED) return rc;
+      family = kSerial;
+    } else {
+      family = kSerial;
+    }
+  }
+  switch (family) {
+    case kSerial: return fr2::launch_serial(D, dtype, bf16_state, p, nseg, s);
+    case kDecode:
+      if (bf16_state) return FR2_ERR_UNSUPPORTED;
+      return fr2::launch_decode(D, dtype, p, nseg, s);
+    case kChunked:
+      if (bf16_state || D != 64) return FR2_ERR_UNSUPPORTED;
+      return fr2::launch_chunked(dtype, p, nseg, max_seqlen, s);
+    default: return FR2_ERR_INVALID_ARGUMENT;
+  }
+}
+
+int recurrent_fp32(int family, const int32_t* qsl, const int32_t* slots,
+                   const int32_t* status, int32_t n, int32_t H, int32_t D,
+                   int64_t total_tokens, int32_t max_seqlen, int32_t dtype,
+                   float* state, const void* r, const void* l, const void* bias,
+                   const void* k, const void* v, const void* a, const void* b,
+                   void* out, float scale, void* stream) {
+  if (!qsl || !slots || !status || !state || !tokens_ok(r, l, k, v, a, b, out))
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (n <= 0 || n > 65535 || H <= 0 || total_tokens <= 0)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (D != 64 && D != 128 && D != 256) return FR2_ERR_UNSUPPORTED;
+  SegArgs p;
+  p.bounds = qsl;
+  p.slots = slots;
+  p.status = status;
+  p.num_heads = H;
+  p.out_elems = total_tokens * H * D;
+  p.state_in = state;
+  p.state_out = state;
+  p.r = r; p.logits = l; p.bias = bias; p.k = k; p.v = v; p.a = a; p.b = b;
+  p.y = out;
+  p.scale = scale;
+  return run_family(family, D, dtype, false, p, n, max_seqlen,
+                    static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+extern "C" int fr2_wkv7_recurrent_fp32_forward(
+    const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, int32_t num_sequences, int32_t num_heads,
+    int32_t head_size, int64_t total_tokens, int32_t max_seqlen, int32_t dtype,
+    float* state, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a,
+    const void* b, void* output, float scale, void* stream) {
+  return recurrent_fp32(kAuto, query_start_loc, state_indices, status,
+                        num_sequences, num_heads, head_size, total_tokens,
+                        max_seqlen, dtype, state, r, decay_logits, decay_bias, k,
+                        v, a, b, output, scale, stream);
+}
+
+extern "C" int fr2_wkv7_recurrent_fp32_forward_kernel(
+    int32_t kernel, const int32_t* query_start_loc,
+    const int32_t* state_indices, const int32_t* status,
+    int32_t num_sequences, int32_t num_heads, int32_t head_size,
+    int64_t total_tokens, int32_t max_seqlen, int32_t dtype, float* state,
+    const void* r, const void* decay_logits, const void* decay_bias,
+    const void* k, const void* v, const void* a, const void* b, void* output,
+    float scale, void* stream) {
+  if (kernel < kSerial || kernel > kChunked) return FR2_ERR_INVALID_ARGUMENT;
+  return recurrent_fp32(kernel, query_start_loc, state_indices, status,
+                        num_sequences, num_heads, head_size, total_tokens,
+                        max_seqlen, dtype, state, r, decay_logits, decay_bias, k,
+                        v, a, b, output, scale, stream);
+}
+
+extern "C" int fr2_wkv7_pretrain_forward(int32_t batch, int32_t tokens,
+                                         int32_t num_heads, int32_t head_size,
+                                         const void* r, const void* w,
+                                         const void* k, const void* v,
+                                         const void* a, const void* b,
+                                         void* output, float* boundary,
+                                         float* state_dot_a, void* stream) {
+  if (!tokens_ok(r, w, k, v, a, b, output) || !boundary || !state_dot_a)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (batch <= 0 || batch > 65535 || tokens <= 0 || tokens % 16 != 0 || num_heads <= 0)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return FR2_ERR_UNSUPPORTED;
+  SegArgs p;
+  p.uniform_len = tokens;
+  p.num_heads = num_heads;
+  p.out_elems = static_cast<int64_t>(batch) * tokens * num_heads * head_size;
+  p.r = r; p.logits = w; p.k = k; p.v = v; p.a = a; p.b = b;
+  p.y = output;
+  p.sa_out = state_dot_a;
+  p.boundary = boundary;
+  p.boundary_len = 16;
+  p.boundary_per_seg = tokens / 16;
+  return fr2::launch_serial(head_size, FR2_DTYPE_BFLOAT16, false, p, batch,
+                            static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fr2_wkv7_chunk_bf16_forward(
+    const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, int32_t num_sequences, int32_t num_heads,
+    int64_t total_tokens, int32_t chunk_size, int32_t max_seqlen,
+    uint16_t* state_bf16, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a,
+    const void* b, void* output, float scale, void* stream) {
+  if (!query_start_loc || !state_indices || !status || !state_bf16 ||
+      !tokens_ok(r, decay_logits, k, v, a, b, output))
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 ||
+      total_tokens <= 0 || chunk_size <= 0)
+    return FR2_ERR_INVALID_ARGUMENT;
+  (void)max_seqlen;
+  SegArgs p;
+  p.bounds = query_start_loc;
+  p.slots = state_indices;
+  p.status = status;
+  p.num_heads = num_heads;
+  p.out_elems = total_tokens * num_heads * 64;
+  p.state_in = state_bf16;
+  p.state_out = state_bf16;
+  p.r = r; p.logits = decay_logits; p.bias = decay_bias; p.k = k; p.v = v;
+  p.a = a; p.b = b;
+  p.y = output;
+  p.scale = scale;
+  return fr2::launch_serial(64, FR2_DTYPE_BFLOAT16, true, p, num_sequences,
+                            static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fr2_wkv7_rl_infctx_forward(
+    const int32_t* sequence_chunk_offsets, const int32_t* chunk_token_starts,
+    const int32_t* chunk_token_ends, int32_t num_sequences, int32_t num_chunks,
+    int32_t num_heads, int32_t head_size, int64_t total_tokens,
+    int32_t max_seqlen, int32_t chunk_size, int32_t strategy, int32_t dtype,
+    float* state, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a,
+    const void* b, void* output, float scale, void* stream) {
+  if (!sequence_chunk_offsets || !chunk_token_starts || !chunk_token_ends ||
+      !state || !tokens_ok(r, decay_logits, k, v, a, b, output))
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (num_sequences <= 0 || num_sequences > 65535 || num_chunks <= 0 ||
+      num_heads <= 0 || total_tokens <= 0)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (chunk_size != 16 && chunk_size != 32 && chunk_size != 64) return FR2_ERR_UNSUPPORTED;
+  if (strategy != 0 && strategy != 1) return FR2_ERR_INVALID_ARGUMENT;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return FR2_ERR_UNSUPPORTED;
+  SegArgs p;
+  p.bounds = chunk_token_starts;
+  p.ends = chunk_token_ends;
+  p.chunk_offsets = sequence_chunk_offsets;
+  p.num_heads = num_heads;
+  p.out_elems = total_tokens * num_heads * head_size;
+  p.state_in = state;
+  p.state_out = state;
+  p.r = r; p.logits = decay_logits; p.bias = decay_bias; p.k = k; p.v = v;
+  p.a = a; p.b = b;
+  p.y = output;
+  p.scale = scale;
+  return run_family(kAuto, head_size, dtype, false, p, num_sequences, max_seqlen,
+                    static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fr2_wkv7_rl_infctx_replay(
+    const int32_t* chunk_token_starts, const int32_t* chunk_token_ends,
+    int32_t num_chunks, int32_t num_heads, int32_t head_size,
+    int64_t total_tokens, int32_t dtype, const float* boundary, const void* r,
+    const void* decay_logits, const void* decay_bias, const void* k,
+    const void* v, const void* a, const void* b, void* output,
+    float* state_dot_a, float scale, void* stream) {
+  if (!chunk_token_starts || !chunk_token_ends || !boundary || !state_dot_a ||
+      !tokens_ok(r, decay_logits, k, v, a, b, output))
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (num_chunks <= 0 || num_chunks > 65535 || num_heads <= 0 || total_tokens <= 0)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return FR2_ERR_UNSUPPORTED;
+  SegArgs p;
+  p.bounds = chunk_token_starts;
+  p.ends = chunk_token_ends;
+  p.num_heads = num_heads;
+  p.out_elems = total_tokens * num_heads * head_size;
+  p.state_in = boundary;
+  p.r = r; p.logits = decay_logits; p.bias = decay_bias; p.k = k; p.v = v;
+  p.a = a; p.b = b;
+  p.y = output;
+  p.sa_out = state_dot_a;
+  p.scale = scale;
+  return fr2::launch_serial(head_size, dtype, false, p, num_chunks,
+                            static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,97 @@
+// Shared device helpers for the gfx950 WKV7 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fr2 {
+
+// retention(x) = exp(-exp(-1/2) * sigmoid(x)), written with base-2
+// exponentials: exp2(-exp(-1/2)*log2(e) / (1 + exp2(-log2(e) * x))).
+// Same closed form as recurrent_retention in the reference
+// (csrc/sm120/tmix/wkv7/recurrent_decay.cuh:18-22); the constants follow from
+// the formula: exp(-1/2)*log2(e) = 0.87503877..., log2(e) = 1.44269504...
+constexpr float kNegExpHalfLog2e = -0.8750387749145276f;
+constexpr float kNegLog2e = -1.4426950408889634f;
+
+__device__ __forceinline__ float retention_from_logit(float x) {
+  const float e = __builtin_amdgcn_exp2f(kNegLog2e * x);
+  return __builtin_amdgcn_exp2f(kNegExpHalfLog2e / (1.0f + e));
+}
+
+// ---- token I/O element types -------------------------------------------
+struct IoBF16 {
+  using raw = uint16_t;
+  static __device__ __forceinline__ float to_f32(raw x) {
+    return __uint_as_float(static_cast<uint32_t>(x) << 16);
+  }
+  // round to nearest even; NaN stays a quiet NaN.
+  static __device__ __forceinline__ raw from_f32(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<raw>(0x7fc0u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<raw>(u >> 16);
+  }
+};
+
+struct IoF16 {
+  using raw = _Float16;
+  static __device__ __forceinline__ float to_f32(raw x) {
+    return static_cast<float>(x);
+  }
+  static __device__ __forceinline__ raw from_f32(float f) {
+    return static_cast<raw>(f);
+  }
+};
+
+// ---- state element types -----------------------------------------------
+struct StF32 {
+  using raw = float;
+  static __device__ __forceinline__ float to_f32(raw x) { return x; }
+  static __device__ __forceinline__ raw from_f32(float f) { return f; }
+};
+struct StBF16 {
+  using raw = uint16_t;
+  static __device__ __forceinline__ float to_f32(raw x) {
+    return IoBF16::to_f32(x);
+  }
+  static __device__ __forceinline__ raw from_f32(float f) {
+    return IoBF16::from_f32(f);
+  }
+};
+
+// Native 4-wide float vector (usable with the nontemporal builtins).
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// 8 consecutive 16-bit token elements (one 16-byte global load).
+struct alignas(16) Raw8 {
+  uint16_t h[8];
+};
+
+template <class Io>
+__device__ __forceinline__ float raw8_get(const Raw8& p, int i) {
+  typename Io::raw x;
+  __builtin_memcpy(&x, &p.h[i], 2);
+  return Io::to_f32(x);
+}
+
+__device__ __forceinline__ float quiet_nan() { return __uint_as_float(0x7fc00000u); }
+
+// Fail-closed fill: every output element becomes NaN (grid-stride over the
+// whole output, shared by every workgroup of the launch).
+template <class Io>
+__device__ void fill_output_nan(typename Io::raw* out, int64_t n,
+                                int64_t block, int64_t blocks) {
+  const typename Io::raw nanv = Io::from_f32(quiet_nan());
+  for (int64_t i = block * blockDim.x + threadIdx.x; i < n;
+       i += blocks * blockDim.x) {
+    out[i] = nanv;
+  }
+}
+
+// Records the result of the launches just enqueued (hipGetLastError) and
+// maps it to an fr2_status_t; the HIP error text stays readable through
+// fr2_last_error() in the calling thread.
+int record_launch();
+
+}  // namespace fr2

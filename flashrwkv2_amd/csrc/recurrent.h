@@ -1,0 +1,51 @@
+// Segment descriptor shared by every WKV7 kernel, and the launchers.
+#pragma once
+
+#include "common.h"
+#include "../../include/flashrwkv2_amd.h"
+
+namespace fr2 {
+
+// A launch runs grid (H, num_segments); segment i covers tokens [t0, t1) of
+// the packed [total_tokens, H, D] tensors and reads/writes state slot
+// `slots[i]` (identity when null).  Segment bounds come from, in order of
+// precedence:
+//   uniform_len > 0  : [i*L, (i+1)*L)                       ([B,T,H,D] layout)
+//   chunk_offsets    : [bounds[co[i]], ends[co[i+1]-1])     (RL/Infctx chunks)
+//   ends             : [bounds[i], ends[i])                 (chunk replay)
+//   otherwise        : [bounds[i], bounds[i+1])             (cu_seqlens)
+struct SegArgs {
+  const int32_t* bounds = nullptr;
+  const int32_t* ends = nullptr;
+  const int32_t* chunk_offsets = nullptr;
+  const int32_t* slots = nullptr;
+  const int32_t* status = nullptr;  // validated ticket status, or null
+  int uniform_len = 0;
+  int num_heads = 0;
+  int64_t out_elems = 0;            // for the fail-closed NaN fill
+  const void* state_in = nullptr;   // null: zero initial state
+  void* state_out = nullptr;        // null: final state not written
+  const void* r = nullptr;
+  const void* logits = nullptr;
+  const void* bias = nullptr;       // [H, D] or null
+  const void* k = nullptr;
+  const void* v = nullptr;
+  const void* a = nullptr;
+  const void* b = nullptr;
+  void* y = nullptr;
+  float* sa_out = nullptr;          // per-token pre-update sa, or null
+  float* boundary = nullptr;        // post-chunk state snapshots, or null
+  int boundary_len = 16;
+  int boundary_per_seg = 0;
+  float scale = 1.0f;
+};
+
+int launch_serial(int D, int dtype, bool bf16_state, const SegArgs& p, int nseg,
+                  hipStream_t s);
+int launch_decode(int D, int dtype, const SegArgs& p, int nseg, hipStream_t s);
+// Chunked MFMA prefill (D = 64, fp32 state).  Returns FR2_ERR_UNSUPPORTED
+// for contracts it does not cover (sa output / boundaries / bf16 state).
+int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen,
+                   hipStream_t s);
+
+}  // namespace fr2

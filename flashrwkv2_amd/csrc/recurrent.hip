@@ -1,0 +1,365 @@
+// WKV7 recurrence kernels for gfx950: token-serial (state resident in VGPRs
+// across the whole sequence) and decode (state streamed from HBM with 16-byte
+// loads, T small).  Both are driven by one segment descriptor so that the
+// packed varlen, [B,T,H,D] pretrain, bf16-state, RL/Infctx and chunk-replay
+// contracts share the same code.
+//
+// Per token and head (fp32):
+//   sa[v] = sum_k a[k] S[k,v]; S[k,v] = w[k] S[k,v] + b[k] sa[v] + k[k] v[v];
+//   y[v]  = scale * sum_k r[k] S[k,v]
+// (reference oracle: tests/tmix/wkv7/test.py:66-83; kernel semantics:
+//  csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:90-192).
+#include "recurrent.h"
+
+namespace fr2 {
+
+__device__ __forceinline__ bool resolve_segment(const SegArgs& p, int seg,
+                                                int& t0, int& t1, int& slot) {
+  if (p.uniform_len > 0) {
+    t0 = seg * p.uniform_len;
+    t1 = t0 + p.uniform_len;
+  } else if (p.chunk_offsets != nullptr) {
+    const int c0 = p.chunk_offsets[seg];
+    const int c1 = p.chunk_offsets[seg + 1];
+    t0 = p.bounds[c0];
+    t1 = p.ends[c1 - 1];
+  } else if (p.ends != nullptr) {
+    t0 = p.bounds[seg];
+    t1 = p.ends[seg];
+  } else {
+    t0 = p.bounds[seg];
+    t1 = p.bounds[seg + 1];
+  }
+  slot = p.slots ? p.slots[seg] : seg;
+  return true;
+}
+
+// Returns false when this workgroup has nothing to do (fail-closed status or
+// an inactive sequence).  On a bad status the whole grid writes NaN.
+template <class Io>
+__device__ __forceinline__ bool check_status(const SegArgs& p, int seg,
+                                             int64_t block, int64_t blocks) {
+  if (p.status == nullptr) return true;
+  if (p.status[0] != 0) {
+    fill_output_nan<Io>(static_cast<typename Io::raw*>(p.y), p.out_elems, block,
+                        blocks);
+    return false;
+  }
+  return seg < p.status[2];
+}
+
+// ---------------------------------------------------------------------------
+// Token-serial kernel.  One workgroup of 4*D threads per (segment, head).
+// Thread (q, v) = (tid / D, tid % D) owns state column v for the key rows
+// [q*R, q*R+R), R = D/4, in registers for the whole segment.  Inputs are
+// staged TT = 1024/D tokens at a time through LDS as fp32 (the retention is
+// computed once while staging).  The sa reduction over the 4 key quarters goes
+// through a double-buffered LDS array (one barrier per token); the y partials
+// of a tile are reduced after the tile and stored coalesced.
+// ---------------------------------------------------------------------------
+template <int D, class Io, class St>
+__global__ __launch_bounds__(4 * D) void serial_kernel(SegArgs p) {
+  using raw = typename Io::raw;
+  constexpr int KS = 4;
+  constexpr int NT = KS * D;
+  constexpr int R = D / KS;
+  constexpr int TT = 1024 / D;
+  constexpr int V8 = D / 8;
+
+  __shared__ __attribute__((aligned(16))) float s_in[6][TT][D];
+  __shared__ float s_red[2][KS][D];
+  __shared__ float s_y[TT][KS][D];
+
+  const int h = blockIdx.x;
+  const int seg = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int v = tid % D;
+  const int q = tid / D;
+  const int H = p.num_heads;
+  if (!check_status<Io>(p, seg, static_cast<int64_t>(seg) * gridDim.x + h,
+                        static_cast<int64_t>(gridDim.x) * gridDim.y))
+    return;
+  int t0, t1, slot;
+  resolve_segment(p, seg, t0, t1, slot);
+
+  const int64_t sbase = (static_cast<int64_t>(slot) * H + h) * D * D;
+  float S[R];
+  if (p.state_in != nullptr) {
+    const typename St::raw* sin = static_cast<const typename St::raw*>(p.state_in);
+#pragma unroll
+    for (int j = 0; j < R; ++j) S[j] = St::to_f32(sin[sbase + (q * R + j) * D + v]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < R; ++j) S[j] = 0.0f;
+  }
+
+  const raw* src[6] = {
+      static_cast<const raw*>(p.r), static_cast<const raw*>(p.logits),
+      static_cast<const raw*>(p.k), static_cast<const raw*>(p.v),
+      static_cast<const raw*>(p.a), static_cast<const raw*>(p.b)};
+  const raw* bias = static_cast<const raw*>(p.bias);
+  raw* y = static_cast<raw*>(p.y);
+
+  for (int tile = t0; tile < t1; tile += TT) {
+    const int n = min(TT, t1 - tile);
+    __syncthreads();  // previous tile fully consumed
+    for (int idx = tid; idx < 6 * TT * V8; idx += NT) {
+      const int which = idx / (TT * V8);
+      const int rem = idx - which * (TT * V8);
+      const int tt = rem / V8;
+      const int c8 = rem - tt * V8;
+      if (tt < n) {
+        const int64_t off = (static_cast<int64_t>(tile + tt) * H + h) * D + c8 * 8;
+        const Raw8 pk = *reinterpret_cast<const Raw8*>(src[which] + off);
+        float f[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f[i] = raw8_get<Io>(pk, i);
+        if (which == 1) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            float x = f[i];
+            if (bias != nullptr) x += Io::to_f32(bias[h * D + c8 * 8 + i]);
+            f[i] = retention_from_logit(x);
+          }
+        }
+        float4* dst = reinterpret_cast<float4*>(&s_in[which][tt][c8 * 8]);
+        dst[0] = make_float4(f[0], f[1], f[2], f[3]);
+        dst[1] = make_float4(f[4], f[5], f[6], f[7]);
+      }
+    }
+    __syncthreads();
+
+    for (int tt = 0; tt < n; ++tt) {
+      const float* Ar = &s_in[4][tt][q * R];
+      float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+#pragma unroll
+      for (int j = 0; j < R; j += 4) {
+        p0 = fmaf(Ar[j + 0], S[j + 0], p0);
+        p1 = fmaf(Ar[j + 1], S[j + 1], p1);
+        p2 = fmaf(Ar[j + 2], S[j + 2], p2);
+        p3 = fmaf(Ar[j + 3], S[j + 3], p3);
+      }
+      s_red[tt & 1][q][v] = (p0 + p1) + (p2 + p3);
+      __syncthreads();
+      float sa = 0.f;
+#pragma unroll
+      for (int qq = 0; qq < KS; ++qq) sa += s_red[tt & 1][qq][v];
+      if (p.sa_out != nullptr && q == 0)
+        p.sa_out[(static_cast<int64_t>(tile + tt) * H + h) * D + v] = sa;
+
+      const float vv = s_in[3][tt][v];
+      const float* Wr = &s_in[1][tt][q * R];
+      const float* Kr = &s_in[2][tt][q * R];
+      const float* Br = &s_in[5][tt][q * R];
+      const float* Rr = &s_in[0][tt][q * R];
+      float y0 = 0.f, y1 = 0.f, y2 = 0.f, y3 = 0.f;
+#pragma unroll
+      for (int j = 0; j < R; j += 4) {
+        S[j + 0] = fmaf(Wr[j + 0], S[j + 0], fmaf(Br[j + 0], sa, Kr[j + 0] * vv));
+        S[j + 1] = fmaf(Wr[j + 1], S[j + 1], fmaf(Br[j + 1], sa, Kr[j + 1] * vv));
+        S[j + 2] = fmaf(Wr[j + 2], S[j + 2], fmaf(Br[j + 2], sa, Kr[j + 2] * vv));
+        S[j + 3] = fmaf(Wr[j + 3], S[j + 3], fmaf(Br[j + 3], sa, Kr[j + 3] * vv));
+        y0 = fmaf(Rr[j + 0], S[j + 0], y0);
+        y1 = fmaf(Rr[j + 1], S[j + 1], y1);
+        y2 = fmaf(Rr[j + 2], S[j + 2], y2);
+        y3 = fmaf(Rr[j + 3], S[j + 3], y3);
+      }
+      s_y[tt][q][v] = (y0 + y1) + (y2 + y3);
+
+      if (p.boundary != nullptr) {
+        const int pos = tile + tt - t0 + 1;
+        if (pos % p.boundary_len == 0) {
+          const int c = pos / p.boundary_len - 1;
+          float* bd = p.boundary +
+                      ((static_cast<int64_t>(seg) * H + h) * p.boundary_per_seg + c) *
+                          D * D;
+#pragma unroll
+          for (int j = 0; j < R; ++j) bd[(q * R + j) * D + v] = S[j];
+        }
+      }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < n * D; idx += NT) {
+      const int tt = idx / D;
+      const int vv = idx - tt * D;
+      float acc = 0.f;
+#pragma unroll
+      for (int qq = 0; qq < KS; ++qq) acc += s_y[tt][qq][vv];
+      y[(static_cast<int64_t>(tile + tt) * H + h) * D + vv] = Io::from_f32(p.scale * acc);
+    }
+  }
+
+  if (p.state_out != nullptr) {
+    typename St::raw* sout = static_cast<typename St::raw*>(p.state_out);
+#pragma unroll
+    for (int j = 0; j < R; ++j) sout[sbase + (q * R + j) * D + v] = St::from_f32(S[j]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode kernel (D = 64, fp32 state).  One wavefront per (segment, head).
+// Lane l owns columns 4*(l%16)..+3 of key rows {l/16 + 4j : j < 16}: the 16 KiB
+// state moves as 16 dwordx4 loads per lane, each wave instruction covering 4
+// full 256-byte rows.  sa and y are reduced over the 4 row groups with two
+// cross-lane xor exchanges.  Token vectors go through a 1.5 KiB LDS buffer in
+// which key k sits at (k%4)*16 + k/4, so every lane reads its 16 keys as four
+// 16-byte LDS reads.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f4 shfl_xor4(f4 x, int m) {
+  return f4{__shfl_xor(x.x, m), __shfl_xor(x.y, m), __shfl_xor(x.z, m),
+            __shfl_xor(x.w, m)};
+}
+
+template <class Io>
+__global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
+  using raw = typename Io::raw;
+  constexpr int D = 64;
+  __shared__ __attribute__((aligned(16))) float s_in[6][D];
+
+  const int h = blockIdx.x;
+  const int seg = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int H = p.num_heads;
+  if (!check_status<Io>(p, seg, static_cast<int64_t>(seg) * gridDim.x + h,
+                        static_cast<int64_t>(gridDim.x) * gridDim.y))
+    return;
+  int t0, t1, slot;
+  resolve_segment(p, seg, t0, t1, slot);
+
+  const int c4 = lane & 15;
+  const int rq = lane >> 4;
+  const int64_t sbase = (static_cast<int64_t>(slot) * H + h) * D * D;
+  f4 S[16];
+  if (p.state_in != nullptr) {
+    const float* sin = static_cast<const float*>(p.state_in) + sbase + rq * D + 4 * c4;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      S[j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(sin + 4 * j * D));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) S[j] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const raw* rp = static_cast<const raw*>(p.r);
+  const raw* lp = static_cast<const raw*>(p.logits);
+  const raw* kp = static_cast<const raw*>(p.k);
+  const raw* vp = static_cast<const raw*>(p.v);
+  const raw* ap = static_cast<const raw*>(p.a);
+  const raw* bp = static_cast<const raw*>(p.b);
+  const raw* bias = static_cast<const raw*>(p.bias);
+  raw* y = static_cast<raw*>(p.y);
+  const int pk = (lane & 3) * 16 + (lane >> 2);
+
+  for (int t = t0; t < t1; ++t) {
+    const int64_t base = (static_cast<int64_t>(t) * H + h) * D;
+    float x = Io::to_f32(lp[base + lane]);
+    if (bias != nullptr) x += Io::to_f32(bias[h * D + lane]);
+    s_in[0][pk] = Io::to_f32(rp[base + lane]);
+    s_in[1][pk] = retention_from_logit(x);
+    s_in[2][pk] = Io::to_f32(kp[base + lane]);
+    s_in[3][lane] = Io::to_f32(vp[base + lane]);
+    s_in[4][pk] = Io::to_f32(ap[base + lane]);
+    s_in[5][pk] = Io::to_f32(bp[base + lane]);
+    __syncthreads();
+
+    const float* Ar = &s_in[4][rq * 16];
+    f4 sa = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float aj = Ar[j];
+      sa.x = fmaf(aj, S[j].x, sa.x);
+      sa.y = fmaf(aj, S[j].y, sa.y);
+      sa.z = fmaf(aj, S[j].z, sa.z);
+      sa.w = fmaf(aj, S[j].w, sa.w);
+    }
+    f4 o = shfl_xor4(sa, 16);
+    sa.x += o.x; sa.y += o.y; sa.z += o.z; sa.w += o.w;
+    o = shfl_xor4(sa, 32);
+    sa.x += o.x; sa.y += o.y; sa.z += o.z; sa.w += o.w;
+
+    const f4 vv = *reinterpret_cast<const f4*>(&s_in[3][4 * c4]);
+    const float* Rr = &s_in[0][rq * 16];
+    const float* Wr = &s_in[1][rq * 16];
+    const float* Kr = &s_in[2][rq * 16];
+    const float* Br = &s_in[5][rq * 16];
+    f4 yy = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float wj = Wr[j], bj = Br[j], kj = Kr[j], rj = Rr[j];
+      S[j].x = fmaf(wj, S[j].x, fmaf(bj, sa.x, kj * vv.x));
+      S[j].y = fmaf(wj, S[j].y, fmaf(bj, sa.y, kj * vv.y));
+      S[j].z = fmaf(wj, S[j].z, fmaf(bj, sa.z, kj * vv.z));
+      S[j].w = fmaf(wj, S[j].w, fmaf(bj, sa.w, kj * vv.w));
+      yy.x = fmaf(rj, S[j].x, yy.x);
+      yy.y = fmaf(rj, S[j].y, yy.y);
+      yy.z = fmaf(rj, S[j].z, yy.z);
+      yy.w = fmaf(rj, S[j].w, yy.w);
+    }
+    o = shfl_xor4(yy, 16);
+    yy.x += o.x; yy.y += o.y; yy.z += o.z; yy.w += o.w;
+    o = shfl_xor4(yy, 32);
+    yy.x += o.x; yy.y += o.y; yy.z += o.z; yy.w += o.w;
+    if (rq == 0) {
+      raw* dst = y + base + 4 * c4;
+      dst[0] = Io::from_f32(p.scale * yy.x);
+      dst[1] = Io::from_f32(p.scale * yy.y);
+      dst[2] = Io::from_f32(p.scale * yy.z);
+      dst[3] = Io::from_f32(p.scale * yy.w);
+    }
+    __syncthreads();
+  }
+
+  if (p.state_out != nullptr) {
+    float* sout = static_cast<float*>(p.state_out) + sbase + rq * D + 4 * c4;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      __builtin_nontemporal_store(S[j], reinterpret_cast<f4*>(sout + 4 * j * D));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launch helpers.
+// ---------------------------------------------------------------------------
+template <class Io, class St>
+static int launch_serial_io(int D, const SegArgs& p, int nseg, hipStream_t s) {
+  const dim3 grid(p.num_heads, nseg);
+  switch (D) {
+    case 64:
+      hipLaunchKernelGGL((serial_kernel<64, Io, St>), grid, dim3(256), 0, s, p);
+      break;
+    case 128:
+      hipLaunchKernelGGL((serial_kernel<128, Io, St>), grid, dim3(512), 0, s, p);
+      break;
+    case 256:
+      hipLaunchKernelGGL((serial_kernel<256, Io, St>), grid, dim3(1024), 0, s, p);
+      break;
+    default:
+      return FR2_ERR_UNSUPPORTED;
+  }
+  return record_launch();
+}
+
+int launch_serial(int D, int dtype, bool bf16_state, const SegArgs& p, int nseg,
+                  hipStream_t s) {
+  if (bf16_state) {
+    if (dtype != FR2_DTYPE_BFLOAT16) return FR2_ERR_UNSUPPORTED;
+    return launch_serial_io<IoBF16, StBF16>(D, p, nseg, s);
+  }
+  if (dtype == FR2_DTYPE_BFLOAT16) return launch_serial_io<IoBF16, StF32>(D, p, nseg, s);
+  if (dtype == FR2_DTYPE_FLOAT16) return launch_serial_io<IoF16, StF32>(D, p, nseg, s);
+  return FR2_ERR_UNSUPPORTED;
+}
+
+int launch_decode(int D, int dtype, const SegArgs& p, int nseg, hipStream_t s) {
+  if (D != 64 || p.sa_out != nullptr || p.boundary != nullptr) return FR2_ERR_UNSUPPORTED;
+  const dim3 grid(p.num_heads, nseg);
+  if (dtype == FR2_DTYPE_BFLOAT16)
+    hipLaunchKernelGGL((decode64_kernel<IoBF16>), grid, dim3(64), 0, s, p);
+  else if (dtype == FR2_DTYPE_FLOAT16)
+    hipLaunchKernelGGL((decode64_kernel<IoF16>), grid, dim3(64), 0, s, p);
+  else
+    return FR2_ERR_UNSUPPORTED;
+  return record_launch();
+}
+
+}  // namespace fr2

@@ -1,0 +1,187 @@
+"""Public WKV7 entry points: packed varlen recurrence with an fp32 state pool
+and its metadata tickets.
+
+Names, keyword arguments, defaults and the Python-side error types/messages
+follow ``flashrwkv2.tmix.wkv7`` (flashrwkv2/tmix/wkv7/__init__.py:8-256) so
+that callers can switch packages without code changes.  The native layer is
+:mod:`flashrwkv2_amd._C`, backed by the gfx950 HIP library.
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+def _extension():
+    """The native operator module (…/wkv7/__init__.py:8-17)."""
+    import flashrwkv2_amd
+
+    extension = getattr(flashrwkv2_amd, "_C", None)
+    if extension is None:
+        raise RuntimeError(
+            "FlashRWKV2 CUDA extension is not built; build flashrwkv2._C before "
+            "using the accelerated recurrent operator"
+        )
+    return extension
+
+
+def _validate_packed_inputs(*tensors: torch.Tensor) -> tuple[torch.Tensor, ...]:
+    for name, tensor in zip(("r", "decay_logits", "k", "v", "a", "b"), tensors):
+        if not isinstance(tensor, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if tensor.ndim != 3:
+            raise ValueError(f"{name} must have packed shape [total_tokens,H,D]")
+        if not tensor.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    return tensors
+
+
+def _validate_state(state: torch.Tensor) -> None:
+    if not isinstance(state, torch.Tensor):
+        raise TypeError("state_pool must be a torch.Tensor")
+    if not state.is_contiguous():
+        raise ValueError("state_pool must be contiguous")
+    if state.dtype != torch.float32:
+        raise TypeError("state_pool must have dtype float32")
+
+
+def _check_metadata_inputs(cu_seqlens: torch.Tensor, state_indices: torch.Tensor) -> None:
+    if not isinstance(cu_seqlens, torch.Tensor):
+        raise TypeError("cu_seqlens must be a torch.Tensor")
+    if cu_seqlens.ndim != 1:
+        raise ValueError("cu_seqlens must be one-dimensional")
+    if not isinstance(state_indices, torch.Tensor):
+        raise TypeError("state_indices must be a torch.Tensor")
+
+
+def _resolve_max_seqlen(cu_seqlens: torch.Tensor, max_seqlen: int | None) -> int:
+    if max_seqlen is not None:
+        value = int(max_seqlen)
+        if value <= 0:
+            raise ValueError("max_seqlen must be positive")
+        return value
+    if cu_seqlens.numel() < 2:
+        raise ValueError("cu_seqlens must contain at least one sequence")
+    return int((cu_seqlens[1:] - cu_seqlens[:-1]).max().item())
+
+
+def _positive_int(name: str, value: object) -> None:
+    if not isinstance(value, int) or isinstance(value, bool) or value <= 0:
+        raise ValueError(f"{name} must be a positive integer")
+
+
+def prepare_tmix_wkv7_recurrent_metadata(
+    cu_seqlens: torch.Tensor,
+    state_indices: torch.Tensor,
+    *,
+    state_pool_size: int,
+    total_tokens: int | None = None,
+    max_seqlen: int | None = None,
+    token_capacity: int | None = None,
+    sequence_capacity: int | None = None,
+    max_seqlen_capacity: int | None = None,
+    num_active_tokens: torch.Tensor | None = None,
+    num_active_sequences: torch.Tensor | None = None,
+) -> object:
+    """Validate packed metadata once and return a ticket.
+
+    Static form (``total_tokens``): the metadata values are checked on the
+    host and on the device, and a private snapshot is validated and used by
+    every consumer.  Capacity form (all five capacity/active arguments): the
+    metadata and the two device scalars stay live, which is what a HIP graph
+    needs; warm up with zero active counts, then prepare again inside capture
+    and reuse that ticket for the graph's operators.
+    """
+    _check_metadata_inputs(cu_seqlens, state_indices)
+    live = (token_capacity, sequence_capacity, max_seqlen_capacity,
+            num_active_tokens, num_active_sequences)
+    if any(item is not None for item in live):
+        if total_tokens is not None or max_seqlen is not None:
+            raise ValueError(
+                "graph metadata uses capacity arguments, not total_tokens/max_seqlen"
+            )
+        if any(item is None for item in live):
+            raise ValueError(
+                "all graph metadata capacity and active-count arguments are required"
+            )
+        for name, value in (("token_capacity", token_capacity),
+                            ("sequence_capacity", sequence_capacity),
+                            ("state_pool_size", state_pool_size),
+                            ("max_seqlen_capacity", max_seqlen_capacity)):
+            _positive_int(name, value)
+        for name, value in (("num_active_tokens", num_active_tokens),
+                            ("num_active_sequences", num_active_sequences)):
+            ok = (isinstance(value, torch.Tensor) and value.dtype == torch.int32
+                  and value.is_cuda and value.is_contiguous() and value.numel() == 1
+                  and value.device == cu_seqlens.device)
+            if not ok:
+                raise ValueError(f"{name} must be a one-element contiguous CUDA int32 tensor")
+        return _extension().prepare_tmix_wkv7_recurrent_graph_metadata(
+            cu_seqlens, state_indices, num_active_tokens, num_active_sequences,
+            token_capacity, sequence_capacity, state_pool_size, max_seqlen_capacity,
+        )
+    if total_tokens is None:
+        raise ValueError("total_tokens is required for static recurrent metadata")
+    return _extension().prepare_tmix_wkv7_recurrent_metadata(
+        cu_seqlens, state_indices, total_tokens, state_pool_size,
+        -1 if max_seqlen is None else int(max_seqlen),
+    )
+
+
+def infer_tmix_wkv7_recurrent_fp32io16_forward_varlen(
+    r: torch.Tensor,
+    decay_logits: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    *,
+    state_pool: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    state_indices: torch.Tensor,
+    scale: float = 1.0,
+    decay_bias: torch.Tensor | None = None,
+    max_seqlen: int | None = None,
+    validated_metadata: object | None = None,
+) -> torch.Tensor:
+    """Packed raw-decay-logit RWKV-7 recurrence, ``state_pool`` updated in place.
+
+    Token tensors are fp16/bf16 ``[total_tokens,H,D]``; ``state_pool`` is fp32
+    ``[slots,H,D,D]``; returns the output ``[total_tokens,H,D]`` in the token
+    dtype.  (…/wkv7/__init__.py:179-256.)
+    """
+    packed = _validate_packed_inputs(r, decay_logits, k, v, a, b)
+    _validate_state(state_pool)
+    _check_metadata_inputs(cu_seqlens, state_indices)
+    ticket = validated_metadata
+    if ticket is None:
+        ticket = prepare_tmix_wkv7_recurrent_metadata(
+            cu_seqlens, state_indices, total_tokens=r.shape[0],
+            state_pool_size=state_pool.shape[0], max_seqlen=max_seqlen,
+        )
+    output = torch.empty_like(packed[3])
+    _extension().tmix_wkv7_recurrent_fp32_from_decay_logits(
+        cu_seqlens, state_indices, state_pool, *packed, output, float(scale),
+        decay_bias, ticket, -1 if max_seqlen is None else int(max_seqlen),
+    )
+    return output
+
+
+__all__ = [
+    "infer_tmix_wkv7_recurrent_fp32io16_forward_varlen",
+    "prepare_tmix_wkv7_recurrent_metadata",
+]
+
+from .pretrain import pretrain_tmix_wkv7_recurrent_bf16  # noqa: E402
+from .chunk import infer_tmix_wkv7_chunk_bf16_forward_varlen  # noqa: E402
+from .rl_infctx import (  # noqa: E402
+    rl_infctx_tmix_wkv7_chunk_fp32io16,
+    rl_infctx_tmix_wkv7_chunk_fp32io16_factor_recompute,
+)
+
+__all__ += [
+    "pretrain_tmix_wkv7_recurrent_bf16",
+    "infer_tmix_wkv7_chunk_bf16_forward_varlen",
+    "rl_infctx_tmix_wkv7_chunk_fp32io16",
+    "rl_infctx_tmix_wkv7_chunk_fp32io16_factor_recompute",
+]

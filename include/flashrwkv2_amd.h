@@ -1,0 +1,195 @@
+/*
+ * flashrwkv2_amd — C ABI of the MI355X (gfx950) WKV7 operator library.
+ *
+ * Every entry point takes device pointers, integer sizes, a token dtype tag
+ * and a HIP stream (passed as `void*`, a `hipStream_t`), enqueues its kernels
+ * on that stream and returns an `fr2_status_t`.  Nothing here allocates device
+ * memory; the caller owns every buffer.  No entry point synchronises the
+ * stream.  The library holds no global mutable state, so concurrent calls on
+ * different streams are safe.
+ *
+ * Layouts (all row-major, contiguous):
+ *   token tensors   r, decay_logits, k, v, a, b, output : [total_tokens, H, D]
+ *   decay_bias      [H, D] (nullable), same dtype as the tokens
+ *   state pool      [slots, H, D, D]  (S[slot, h, key, value])
+ *   metadata        query_start_loc [N+1] int32, state_indices [N] int32
+ *   status          int32[3] = {error bits, active tokens, active sequences}
+ *
+ * Recurrence (per token, per head; fp32 arithmetic):
+ *   w[k]  = exp(-exp(-1/2) * sigmoid(decay_logits[k] + decay_bias[h,k]))
+ *   sa[v] = sum_k a[k] S[k,v]                       (pre-update state)
+ *   S[k,v] = w[k] S[k,v] + b[k] sa[v] + k[k] v[v]
+ *   y[v]  = scale * sum_k r[k] S[k,v]               (post-update state)
+ *
+ * Reference interfaces replaced are cited per entry point as
+ * path:line inside rwkv-rs/FlashRWKV2 v0.1.0a7.
+ */
+#ifndef FLASHRWKV2_AMD_H_
+#define FLASHRWKV2_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  FR2_OK = 0,
+  FR2_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size or count */
+  FR2_ERR_UNSUPPORTED = 2,      /* head size / dtype / chunk size not built */
+  FR2_ERR_LAUNCH = 3,           /* hipGetLastError() after a launch */
+} fr2_status_t;
+
+typedef enum {
+  FR2_DTYPE_FLOAT16 = 0,
+  FR2_DTYPE_BFLOAT16 = 1,
+} fr2_dtype_t;
+
+/* Device-detected metadata error bits written to status[0]
+ * (replaces the MetadataError enum, csrc/validation/recurrent_metadata.cu:15-22). */
+enum {
+  FR2_META_INVALID_ENDPOINT = 1 << 0,
+  FR2_META_INVALID_SEQUENCE_RANGE = 1 << 1,
+  FR2_META_INVALID_STATE_SLOT = 1 << 2,
+  FR2_META_DUPLICATE_STATE_SLOT = 1 << 3,
+  FR2_META_INVALID_ACTIVE_COUNT = 1 << 4,
+  FR2_META_SEQUENCE_TOO_LONG = 1 << 5,
+};
+
+/* Library ABI version (major*10000 + minor*100 + patch). */
+int fr2_abi_version(void);
+
+/* Static text for an fr2_status_t value. */
+const char* fr2_status_string(int status);
+
+/* HIP error text of the last failing launch in this thread ("" if none). */
+const char* fr2_last_error(void);
+
+/*
+ * Device-side validation of packed metadata, one 256-thread workgroup.
+ * Writes status[3]; copies query_start_loc/state_indices into the snapshot
+ * buffers when they are non-null (static tickets) and validates the copies.
+ * num_active_tokens / num_active_sequences (device int32[1], nullable) make it
+ * the live graph form: only the active prefix is checked.
+ * seen_slots is a caller workspace of state_pool_size int32 (initialised by
+ * the kernel itself, no memset node).
+ * Replaces prepare_recurrent_metadata_cuda / prepare_recurrent_graph_metadata_cuda
+ * (csrc/validation/recurrent_metadata.cu:24-132, :196-225).
+ */
+int fr2_wkv7_prepare_metadata(const int32_t* query_start_loc,
+                              const int32_t* state_indices,
+                              int32_t num_sequences, int32_t total_tokens,
+                              int32_t state_pool_size, int32_t max_seqlen,
+                              const int32_t* num_active_tokens,
+                              const int32_t* num_active_sequences,
+                              int32_t* status, int32_t* seen_slots,
+                              int32_t* query_start_loc_snapshot,
+                              int32_t* state_indices_snapshot, void* stream);
+
+/*
+ * Packed varlen recurrence with an fp32 state pool updated in place at
+ * state_indices.  `status` is the validated ticket status (required): a
+ * non-zero status[0] makes every output element NaN and leaves the pool
+ * untouched; sequences at or beyond status[2] are skipped.  max_seqlen <= 0
+ * means "unknown" (general kernel).  head_size in {64, 128, 256}.
+ * The kernel family (decode / token-serial / chunked MFMA) is chosen
+ * internally from (head_size, num_sequences, max_seqlen).
+ * Replaces tmix_wkv7_recurrent_fp32_from_decay_logits_cuda
+ * (csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:457-517).
+ */
+int fr2_wkv7_recurrent_fp32_forward(
+    const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, int32_t num_sequences, int32_t num_heads,
+    int32_t head_size, int64_t total_tokens, int32_t max_seqlen, int32_t dtype,
+    float* state, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a,
+    const void* b, void* output, float scale, void* stream);
+
+/*
+ * Same contract, but the kernel family is forced: 0 = token-serial,
+ * 1 = decode (state streaming), 2 = chunked MFMA (head_size 64 only).
+ * Used by tests and benchmarks to pin each kernel against the oracle.
+ * Has no reference counterpart (the reference's dispatch is internal,
+ * README.md:81-85); it exposes the same kernels as the entry above.
+ */
+int fr2_wkv7_recurrent_fp32_forward_kernel(
+    int32_t kernel, const int32_t* query_start_loc,
+    const int32_t* state_indices, const int32_t* status,
+    int32_t num_sequences, int32_t num_heads, int32_t head_size,
+    int64_t total_tokens, int32_t max_seqlen, int32_t dtype, float* state,
+    const void* r, const void* decay_logits, const void* decay_bias,
+    const void* k, const void* v, const void* a, const void* b, void* output,
+    float scale, void* stream);
+
+/*
+ * [B,T,H,D] bf16 training forward with zero initial state.  Writes y (bf16),
+ * state_dot_a [B,T,H,D] fp32 (the pre-update sa of every token) and
+ * boundary [B,H,T/16,D,D] fp32, the post-chunk state after every 16 tokens.
+ * Requires T % 16 == 0.
+ * Replaces forward / cuda_forward_v3
+ * (csrc/sm120/tmix/wkv7/pretrain_recurrent_bf16_forward.cpp:20-27,
+ *  pretrain_recurrent_bf16_forward.cu:32-101).
+ */
+int fr2_wkv7_pretrain_forward(int32_t batch, int32_t tokens, int32_t num_heads,
+                              int32_t head_size, const void* r, const void* w,
+                              const void* k, const void* v, const void* a,
+                              const void* b, void* output, float* boundary,
+                              float* state_dot_a, void* stream);
+
+/*
+ * Packed varlen recurrence with a bf16 state pool [slots,H,64,64] updated in
+ * place (fp32 carry inside the call, rounded to bf16 on store).
+ * Replaces infer_tmix_wkv7_chunk_bf16_forward_varlen_cuda
+ * (csrc/sm120/tmix/wkv7/infer_chunk_bf16_forward_varlen.cu:276-340,
+ *  binding infer_chunk_bf16_forward_varlen.cpp:77-192).
+ */
+int fr2_wkv7_chunk_bf16_forward(
+    const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, int32_t num_sequences, int32_t num_heads,
+    int64_t total_tokens, int32_t chunk_size, int32_t max_seqlen,
+    uint16_t* state_bf16, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a,
+    const void* b, void* output, float scale, void* stream);
+
+/*
+ * RL/Infctx fp32-state chunked forward over chunk metadata
+ * (sequence_chunk_offsets [N+1], chunk_token_starts/ends [C]).  `state` is the
+ * working pool [N,H,D,D] (slot i = sequence i), updated in place to the final
+ * states.  strategy 0 = materialized, 1 = recompute; chunk_size in {16,32,64}.
+ * Replaces rl_infctx_tmix_wkv7_chunk_fp32io16_forward's kernels
+ * (csrc/sm120/tmix/wkv7/rl_infctx_chunk_fp32io16_forward.cpp:158-230,
+ *  rl_infctx_chunk_fp32io16_forward.cu:42-135, :318-539).
+ */
+int fr2_wkv7_rl_infctx_forward(
+    const int32_t* sequence_chunk_offsets, const int32_t* chunk_token_starts,
+    const int32_t* chunk_token_ends, int32_t num_sequences, int32_t num_chunks,
+    int32_t num_heads, int32_t head_size, int64_t total_tokens,
+    int32_t max_seqlen, int32_t chunk_size, int32_t strategy, int32_t dtype,
+    float* state, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a,
+    const void* b, void* output, float scale, void* stream);
+
+/*
+ * Replays chunks [chunk_token_starts[c], chunk_token_ends[c]) from the
+ * start-of-chunk states boundary[c] ([C,H,D,D] fp32, read only) and writes
+ * output and state_dot_a ([total_tokens,H,D] fp32) for those tokens.
+ * Replaces rl_infctx_tmix_wkv7_chunk_fp32io16_backward_replay_cuda
+ * (csrc/sm120/tmix/wkv7/rl_infctx_chunk_fp32io16_backward.cu:45-126,
+ *  binding rl_infctx_chunk_fp32io16_backward.cpp:100-125).
+ */
+int fr2_wkv7_rl_infctx_replay(const int32_t* chunk_token_starts,
+                              const int32_t* chunk_token_ends,
+                              int32_t num_chunks, int32_t num_heads,
+                              int32_t head_size, int64_t total_tokens,
+                              int32_t dtype, const float* boundary,
+                              const void* r, const void* decay_logits,
+                              const void* decay_bias, const void* k,
+                              const void* v, const void* a, const void* b,
+                              void* output, float* state_dot_a, float scale,
+                              void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHRWKV2_AMD_H_ */

@@ -1,0 +1,133 @@
+"""CPU oracle for the WKV7 path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import this package, and only as the checker (or the
+timed CPU baseline).  The product path (``flashrwkv2_amd``) never imports it.
+
+The arithmetic lives in ``wkv7_oracle.c`` (built by ``make -C oracle`` into
+``oracle/_build/libwkv7_oracle.so``); this module binds it with ctypes and
+adds numpy conveniences.  What each function restates:
+
+* ``retention``    — csrc/sm120/tmix/wkv7/recurrent_decay.cuh:10-22
+* ``wkv7_f64``     — tests/tmix/wkv7/test.py:29-85 (packed varlen, slots,
+  decay_bias, scale) and, with ``boundary_len``/``want_sa``, the post-chunk
+  boundary and state_dot_a of
+  csrc/sm120/tmix/wkv7/pretrain_recurrent_bf16_forward.cu:32-97
+* ``wkv7_cpu_f32`` — the same recurrence in float, OpenMP over
+  (sequence, head): the CPU baseline that bench.py times.
+
+How the oracle is pinned (tests/test_oracle.py): the retention against its
+closed form and limits; the recurrence against an explicit-matrix fp64 form
+(S_t = (diag w_t + b_t a_t^T) S_{t-1} + k_t v_t^T), the prefix-sum linear
+attention closed form (a = b = 0, w = 1), pure decay (k = a = b = 0),
+the idempotent projection (w = 1, b = -a = kk, |kk| = 1), split/packing/slot
+invariance, scale linearity, boundary snapshots vs split runs, and the
+committed golden fixture of BASELINE config 0.  The reference ships no golden
+vectors for this path (its only fixture is tests/fixtures/tolerances-v1.json).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from ctypes import c_double, c_int, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "_build" / "libwkv7_oracle.so"
+
+_lib: ctypes.CDLL | None = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+def _load() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        lib = ctypes.CDLL(str(LIB))
+        lib.wkv7_oracle_retention.restype = c_double
+        lib.wkv7_oracle_retention.argtypes = [c_double]
+        lib.wkv7_oracle_f64.restype = None
+        lib.wkv7_oracle_f64.argtypes = [c_int, c_int, c_int] + [c_void_p] * 10 + [
+            c_double, c_void_p, c_void_p, c_void_p, c_int, c_int]
+        lib.wkv7_cpu_f32.restype = None
+        lib.wkv7_cpu_f32.argtypes = [c_int, c_int, c_int] + [c_void_p] * 10 + [
+            c_double, c_void_p, c_int]
+        lib.wkv7_cpu_max_threads.restype = c_int
+        lib.wkv7_cpu_max_threads.argtypes = []
+        _lib = lib
+    return _lib
+
+
+def _p(x: np.ndarray | None):
+    return None if x is None else x.ctypes.data
+
+
+def _f32(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+
+
+def _i32(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=np.int32))
+
+
+def retention(x: float) -> float:
+    return _load().wkv7_oracle_retention(float(x))
+
+
+def wkv7_f64(r, logits, k, v, a, b, *, cu_seqlens, state_indices=None, state_pool=None,
+             decay_bias=None, scale=1.0, want_sa=False, boundary_len=0):
+    """fp64 evaluation of the packed recurrence.
+
+    Token arrays are ``[total, H, D]`` (any float dtype; widened from the
+    values they hold).  Returns ``(y, pool, sa, boundary)`` as float64; ``pool``
+    is a copy of ``state_pool`` with the touched slots updated (``None`` when
+    no pool was given: zero initial states).  ``boundary`` is
+    ``[n, H, L/boundary_len, D, D]`` for uniform lengths L.
+    """
+    arrs = [_f32(t) for t in (r, logits, k, v, a, b)]
+    total, H, D = arrs[0].shape
+    cu = _i32(cu_seqlens)
+    n = cu.size - 1
+    slots = None if state_indices is None else _i32(state_indices)
+    pool = None if state_pool is None else np.array(state_pool, dtype=np.float64, order="C")
+    bias = None if decay_bias is None else _f32(decay_bias).reshape(H, D)
+    y = np.zeros((total, H, D), dtype=np.float64)
+    sa = np.zeros((total, H, D), dtype=np.float64) if want_sa else None
+    boundary = None
+    per_seq = 0
+    if boundary_len:
+        lens = np.diff(cu)
+        per_seq = int(lens.max()) // boundary_len
+        boundary = np.zeros((n, H, per_seq, D, D), dtype=np.float64)
+    _load().wkv7_oracle_f64(n, H, D, _p(cu), _p(slots), _p(pool), *(_p(t) for t in arrs[:2]),
+                            _p(bias), *(_p(t) for t in arrs[2:]), float(scale), _p(y), _p(sa),
+                            _p(boundary), int(boundary_len or 1), per_seq)
+    return y, pool, sa, boundary
+
+
+def wkv7_cpu_f32(r, logits, k, v, a, b, *, cu_seqlens, state_indices=None, state_pool=None,
+                 decay_bias=None, scale=1.0, threads=0):
+    """fp32 CPU recurrence (the timed baseline).  Returns ``(y, pool)``."""
+    arrs = [_f32(t) for t in (r, logits, k, v, a, b)]
+    total, H, D = arrs[0].shape
+    cu = _i32(cu_seqlens)
+    slots = None if state_indices is None else _i32(state_indices)
+    pool = None if state_pool is None else np.array(state_pool, dtype=np.float32, order="C")
+    bias = None if decay_bias is None else _f32(decay_bias).reshape(H, D)
+    y = np.zeros((total, H, D), dtype=np.float32)
+    _load().wkv7_cpu_f32(cu.size - 1, H, D, _p(cu), _p(slots), _p(pool),
+                         *(_p(t) for t in arrs[:2]), _p(bias), *(_p(t) for t in arrs[2:]),
+                         float(scale), _p(y), int(threads))
+    return y, pool
+
+
+def cpu_threads() -> int:
+    return int(_load().wkv7_cpu_max_threads())
