@@ -249,7 +249,9 @@ def test_rl_infctx_backward_replay_matches_recurrence(d):
     C = require_gpu()
     g = torch.Generator().manual_seed(41 + d)
     total, heads = 40, 2
-    inputs = [_randn((total, heads, d), g, 0.3, torch.float16) for _ in range(6)]
+    # keep |y| well inside the fp16 range at every head size
+    inputs = [_randn((total, heads, d), g, 0.3 * (64 / d) ** 0.5, torch.float16)
+              for _ in range(6)]
     init = _randn((1, heads, d, d), g, 0.05, torch.float32)
     bias = _randn((heads, d), g, 0.3, torch.float16)
     cu = np.array([0, total], np.int32)
@@ -257,6 +259,7 @@ def test_rl_infctx_backward_replay_matches_recurrence(d):
                                           state_indices=np.array([0], np.int32),
                                           state_pool=to_np(init), decay_bias=to_np(bias),
                                           scale=0.75, want_sa=True)
+    assert np.abs(y_ref).max() < 1e4
     # chunks [0,16), [16,32), [32,40) with their start-of-chunk states
     starts, ends = [0, 16, 32], [16, 32, 40]
     bounds = [to_np(init)[0]]
