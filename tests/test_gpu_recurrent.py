@@ -78,8 +78,9 @@ def test_packed_fp32_state_precision_and_state_safety(dtype, head_size, with_bia
     assert torch.equal(case["state_pool"], second)
 
 
-@pytest.mark.parametrize("kernel", [SERIAL, DECODE])
-@pytest.mark.parametrize("lengths", [(1,), (1, 2, 4), (1, 15, 16, 17, 65), (3,) * 12])
+@pytest.mark.parametrize("kernel", [SERIAL, DECODE, CHUNKED])
+@pytest.mark.parametrize("lengths", [(1,), (1, 2, 4), (1, 15, 16, 17, 65), (3,) * 12,
+                                     (200, 31, 48)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_each_kernel_family_matches_oracle(kernel, lengths, dtype):
     C = require_gpu()
@@ -366,3 +367,45 @@ def test_baseline_configs_match_fp64_oracle(cfg, overrides):
     torch.cuda.synchronize()
     assert_output_close(out, y_ref)
     assert_state_close(pool, pool_ref)
+
+
+@pytest.mark.parametrize("cfg,overrides", [
+    (1, dict(batch=2, tokens=1024, heads=2)),
+    (4, dict(tokens=8192, heads=1)),
+])
+def test_chunked_kernel_long_sequences_match_fp64_oracle(cfg, overrides):
+    """Chunked MFMA form over many chunks (fp32 carry drift vs fp64)."""
+    C = require_gpu()
+    from flashrwkv2_amd import workloads
+
+    print(f"case chunked config={cfg} {overrides}", flush=True)
+    w = workloads.config(cfg, "cuda", **overrides)
+    y_ref, pool_ref = _oracle_on_workload(w)
+    case = dict(zip(("r", "decay_logits", "k", "v", "a", "b"), w.tokens),
+                cu_seqlens=w.cu_seqlens, state_indices=w.state_indices, decay_bias=None)
+    pool = w.state_pool.clone()
+    out = _run_kernel(C, CHUNKED, case, pool)
+    assert_output_close(out, y_ref)
+    assert_state_close(pool, pool_ref)
+
+
+def test_chunked_and_serial_agree_at_full_prefill_size():
+    """BASELINE config 1 at full size (B8 T4096 H32): the chunked MFMA kernel
+    and the token-serial kernel (pinned to the oracle above) agree to
+    fp32-level accuracy on outputs and final states."""
+    C = require_gpu()
+    from flashrwkv2_amd import workloads
+
+    w = workloads.config(1, "cuda")
+    case = dict(zip(("r", "decay_logits", "k", "v", "a", "b"), w.tokens),
+                cu_seqlens=w.cu_seqlens, state_indices=w.state_indices, decay_bias=None)
+    p_serial = w.state_pool.clone()
+    p_chunk = w.state_pool.clone()
+    y_serial = _run_kernel(C, SERIAL, case, p_serial)
+    y_chunk = _run_kernel(C, CHUNKED, case, p_chunk)
+    dy = (y_chunk.float() - y_serial.float())
+    rel = (dy.square().mean().sqrt() / y_serial.float().square().mean().sqrt()).item()
+    assert rel <= 2e-3, rel  # two independent bf16 roundings of the same output
+    ds = (p_chunk - p_serial).flatten(0, 1).norm(dim=(1, 2))
+    base = p_serial.flatten(0, 1).norm(dim=(1, 2))
+    assert (ds / base).max().item() <= 1e-4
