@@ -35,6 +35,12 @@ METRIC = "WKV7 tokens/s at h32d64 bf16 (prefill + T=1 decode); % of HBM/MFMA roo
 HBM_PEAK_GBS = 8000.0
 BYTES_PER_TOKEN_HEAD = 896          # 6 bf16 inputs x 64 + bf16 output x 64
 STATE_BYTES = 64 * 64 * 4           # one fp32 64x64 state
+MFMA_PEAK_TFLOPS = 2500.0           # dense bf16
+# v_mfma_f32_16x16x32_bf16 instructions the chunked kernel issues per 16-token
+# chunk of one head: 24 token-token products + 16 for T on the key side, 4 x 30
+# on the state side (bf16 hi/lo split products)
+MFMA_PER_CHUNK = 160
+MFMA_FLOPS = 16 * 16 * 32 * 2
 
 
 def algorithmic_bytes(total_tokens: int, heads: int, sequences: int) -> int:
@@ -118,19 +124,17 @@ class Runner:
         return start.elapsed_time(end) / launches
 
     def kernel_name(self) -> str:
-        from flashrwkv2_amd import _native as N  # noqa: F401
-
         ms = self.ticket._max_seqlen()
         if ms <= 4:
-            return "decode64_kernel"
+            return "decode64_kernel<IoBF16>"
         if ms >= 128:
-            return "chunked MFMA kernel (serial fallback when not built)"
-        return "serial_kernel"
+            return "chunk64_kernel<IoBF16>"
+        return "serial_kernel<64,IoBF16,StF32>"
 
 
-def cpu_baseline(w, threads: int, sample_tokens: int | None):
+def cpu_baseline(w, threads: int, sample_tokens: int | None, min_seconds: float = 3.0):
     """fp32 C recurrence on the host over the first `sample_tokens` tokens of
-    every sequence (all heads)."""
+    every sequence (all heads), repeated until `min_seconds` of CPU time."""
     import numpy as np
 
     import oracle
@@ -144,18 +148,49 @@ def cpu_baseline(w, threads: int, sample_tokens: int | None):
     pool = w.state_pool.cpu().numpy()
     oracle.wkv7_cpu_f32(*(t[: cu_s[1]] for t in toks), cu_seqlens=cu_s[:2],
                         state_pool=pool[:1], threads=threads)  # warm-up
-    t0 = time.perf_counter()
-    oracle.wkv7_cpu_f32(*toks, cu_seqlens=cu_s, state_indices=np.arange(len(lens), dtype=np.int32),
-                        state_pool=pool, threads=threads)
-    dt = time.perf_counter() - t0
     n_tok = int(take.sum())
-    return n_tok / dt, dt, n_tok
+    reps, dt = 0, 0.0
+    while dt < min_seconds:
+        t0 = time.perf_counter()
+        oracle.wkv7_cpu_f32(*toks, cu_seqlens=cu_s,
+                            state_indices=np.arange(len(lens), dtype=np.int32),
+                            state_pool=pool.copy(), threads=threads)
+        dt += time.perf_counter() - t0
+        reps += 1
+    return n_tok * reps / dt, dt, n_tok, reps
 
 
-def roofline_obj(bytes_per_launch: int, kernel_ms: float):
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` on `workload` from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE measurement (profiles/hbm_traffic.json),
+    or None when that kernel/workload pair was not measured."""
+    path = ROOT / "profiles" / "hbm_traffic.json"
+    if not path.exists():
+        return None
+    data = json.loads(path.read_text())
+    k = data["kernels"].get(kernel)
+    if k is None or k["workload"] != workload:
+        return None
+    return int(k["fetch_kib"] * 1024 * data["fetch_scale"] + k["write_kib"] * 1024 * data["write_scale"])
+
+
+def roofline_obj(bytes_per_launch: int, kernel_ms: float, traffic=None):
     achieved = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+
+
+def mfma_obj(w, kernel_ms: float):
+    """Matrix-core use of the chunked kernel: issued bf16 MFMA flops (hi/lo
+    split products included) over the launch time, against the dense bf16 peak."""
+    import numpy as np
+
+    lens = np.diff(w.cu_seqlens.cpu().numpy())
+    chunks = int(((lens + 15) // 16).sum()) * w.num_heads
+    flops = chunks * MFMA_PER_CHUNK * MFMA_FLOPS
+    tf = flops / (kernel_ms * 1e-3) / 1e12
+    return {"issued_tflops": round(tf, 2), "peak_tflops": MFMA_PEAK_TFLOPS,
+            "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "instructions": chunks * MFMA_PER_CHUNK}
 
 
 def main() -> int:
@@ -169,6 +204,9 @@ def main() -> int:
                     help="tokens per sequence in the CPU baseline sample")
     ap.add_argument("--only", choices=["prefill", "decode"], default=None,
                     help="run one leg only (profiling)")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="also run one device-to-device copy of this many MiB (a known-size "
+                         "kernel for scaling the HBM byte counters of a profile)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one MI355X only (one GPU per box); "
@@ -185,6 +223,14 @@ def main() -> int:
         return 1
     torch.cuda.set_device(0)
     result: dict = {}
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        result["copy_probe_bytes"] = {"read": n * 4, "written": n * 4}
+        del src, dst
 
     pre = None
     if args.only in (None, "prefill"):
@@ -204,12 +250,15 @@ def main() -> int:
             "higher_is_better": True,
             "scaling": "weak",
             "vs_baseline": None,
-            "dtype": "f32",
+            "dtype": "bf16",
             "data": "synthetic (seeded, BASELINE config 1 distributions; inputs resident in HBM)",
             "config": {"workload": w1.name, "B": 8, "T": 4096, "H": 32, "D": 64,
-                       "io": "bf16", "state": "fp32", "kernel": pre.kernel_name(),
+                       "io": "bf16", "state": "fp32",
+                       "arithmetic": "bf16 MFMA on hi/lo split operands, fp32 accumulate",
+                       "kernel": pre.kernel_name(),
                        "parallelism": "single GPU"},
-            "roofline": roofline_obj(bytes1, kms),
+            "roofline": roofline_obj(bytes1, kms, measured_traffic(pre.kernel_name(), w1.name)),
+            "mfma": mfma_obj(w1, kms) if pre.kernel_name().startswith("chunk") else None,
             "kernel_ms": round(kms, 5),
             "algorithmic_bytes": bytes1,
         })
@@ -223,7 +272,8 @@ def main() -> int:
             "workload": w2.name, "tokens_per_s": round(w2.total_tokens / (dms * 1e-3), 1),
             "ms_per_step": round(dms, 5), "kernel_ms": round(dkms, 5),
             "kernel_tokens_per_s": round(w2.total_tokens / (dkms * 1e-3), 1),
-            "kernel": dec.kernel_name(), "roofline": roofline_obj(bytes2, dkms),
+            "kernel": dec.kernel_name(),
+            "roofline": roofline_obj(bytes2, dkms, measured_traffic(dec.kernel_name(), w2.name)),
             "algorithmic_bytes": bytes2,
         }
         if not result.get("metric"):
@@ -232,11 +282,11 @@ def main() -> int:
                            "warmup": args.warmup, "ms_per_step": round(dms, 5)})
     if pre is not None and not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
-        tps, dt, n_tok = cpu_baseline(pre.w, threads, args.cpu_sample_tokens)
+        tps, dt, n_tok, reps = cpu_baseline(pre.w, threads, args.cpu_sample_tokens)
         result["cpu_baseline"] = {
             "value": round(tps, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"first {args.cpu_sample_tokens} tokens of each of the 8 config-1 "
-                      f"sequences, all 32 heads ({n_tok} tokens, {dt:.2f} s), fp32 C "
+                      f"sequences, all 32 heads ({n_tok} tokens x {reps} passes, {dt:.2f} s), fp32 C "
                       "recurrence (oracle/wkv7_oracle.c, OpenMP over sequence x head)",
         }
     print(json.dumps(result), flush=True)
