@@ -61,24 +61,35 @@ __device__ __forceinline__ f32x4 mma32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-struct Sp4 { bf16x4 hi, lo; };
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 values rounded (nearest-even) to bf16 and packed: v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16(float x0, float x1) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, bf16x2));
+}
+// hi/lo split of two values: hi = bf16(x), lo = bf16(x - hi), packed pairs
+// (three VALU instructions per value)
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+  hi = pack_bf16(x0, x1);
+  lo = pack_bf16(x0 - __uint_as_float(hi << 16), x1 - __uint_as_float(hi & 0xffff0000u));
+}
+
 struct Sp8 { bf16x8 hi, lo; };
 
-__device__ __forceinline__ Sp4 split4(f32x4 x) {
-  Sp4 s;
-  s.hi = __builtin_convertvector(x, bf16x4);
-  s.lo = __builtin_convertvector(x - __builtin_convertvector(s.hi, f32x4), bf16x4);
-  return s;
-}
-typedef float f32x8 __attribute__((ext_vector_type(8)));
+// split of eight values (a 16-byte hi vector and a 16-byte lo vector)
 __device__ __forceinline__ Sp8 split8(const float* x) {
-  f32x8 v;
+  u32x4 h, l;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = x[e];
-  Sp8 s;
-  s.hi = __builtin_convertvector(v, bf16x8);
-  s.lo = __builtin_convertvector(v - __builtin_convertvector(s.hi, f32x8), bf16x8);
-  return s;
+  for (int j = 0; j < 4; ++j) {
+    uint32_t hj, lj;
+    split2(x[2 * j], x[2 * j + 1], hj, lj);
+    h[j] = hj;
+    l[j] = lj;
+  }
+  return Sp8{__builtin_bit_cast(bf16x8, h), __builtin_bit_cast(bf16x8, l)};
 }
 
 __device__ __forceinline__ f32x4 mma32x3(const Sp8& a, const Sp8& b, f32x4 c) {
@@ -87,34 +98,51 @@ __device__ __forceinline__ f32x4 mma32x3(const Sp8& a, const Sp8& b, f32x4 c) {
   return mma32(a.hi, b.hi, c);
 }
 
-// K = 16 products packed into K = 32 instructions: lane group q supplies K
-// positions 8q..8q+7 = (first operand's 4q..4q+3, second's 4q..4q+3), so
-// [x | y] x [u ; v] = x u + y v.  Every product of the kernel runs on the one
-// K = 32 opcode: with this toolchain an accumulator produced by
-// v_mfma_f32_16x16x32_bf16 and consumed as src C by v_mfma_f32_16x16x16_bf16
-// gave wrong sums on gfx950, while same-opcode chains are exact.
-__device__ __forceinline__ bf16x8 cat4(bf16x4 x, bf16x4 y) {
-  return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-__device__ __forceinline__ f32x4 mma2(bf16x4 x, bf16x4 y, bf16x4 u, bf16x4 v, f32x4 c) {
-  return mma32(cat4(x, y), cat4(u, v), c);
-}
-// c += a b (split operands): a.hi b.lo + a.lo b.hi, then a.hi b.hi
-__device__ __forceinline__ f32x4 mma16x3p(Sp4 a, Sp4 b, f32x4 c) {
-  const bf16x4 z = {};
-  c = mma2(a.hi, a.lo, b.lo, b.hi, c);
-  return mma2(a.hi, z, b.hi, z, c);
-}
-// c += a b with b exact in bf16: [a.hi | a.lo] x [b ; b]
-__device__ __forceinline__ f32x4 mma16x2p(Sp4 a, bf16x4 b, f32x4 c) {
-  return mma2(a.hi, a.lo, b, b, c);
-}
+// K = 16 products on the K = 32 instruction.  Lane group q supplies K
+// positions 8q..8q+7 = (first half's 4q..4q+3, second half's 4q..4q+3), so
+// [x | y] x [u ; v] = x u + y v.  Operand forms:
+//   AOp  (A side, split):   [hi | lo]                      one bf16x8
+//   BOp  (B side, split):   [lo | hi | 0 | 0], read through the windows
+//                           [lo | hi] and [hi | 0]
+//   BX   (B side, exact):   [v | v]
+// so  AOp x BOp = hi.lo + lo.hi, then hi.hi + lo.0  (two instructions) and
+//     AOp x BX  = hi.v + lo.v                        (one instruction).
+// Every product of the kernel runs on the one K = 32 opcode: with this
+// toolchain an accumulator produced by v_mfma_f32_16x16x32_bf16 and consumed
+// as src C by v_mfma_f32_16x16x16_bf16 gave wrong sums on gfx950.
+typedef bf16x8 AOp;
+typedef bf16x16 BOp;
+typedef bf16x8 BX;
 
-// X Y for 16x16 matrices held in accumulator layout (lane l: column l%16,
-// rows 4(l/16)+e): the accumulator layout of X^T is the A-operand layout of X
-// and the accumulator layout of Y is the B-operand layout of Y.
-__device__ __forceinline__ f32x4 mm(const Sp4& xt, const Sp4& y, f32x4 c) {
-  return mma16x3p(xt, y, c);
+__device__ __forceinline__ f32x4 mm_ab(AOp a, BOp b, f32x4 c) {
+  c = mma32(a, __builtin_shufflevector(b, b, 0, 1, 2, 3, 4, 5, 6, 7), c);
+  return mma32(a, __builtin_shufflevector(b, b, 4, 5, 6, 7, 8, 9, 10, 11), c);
+}
+__device__ __forceinline__ f32x4 mm_ax(AOp a, BX b, f32x4 c) { return mma32(a, b, c); }
+
+// 16x16 matrices held in accumulator layout (lane l: column l%16, rows
+// 4(l/16)+e): the accumulator layout of X^T is the A-operand layout of X and
+// the accumulator layout of Y is the B-operand layout of Y.
+struct Split4 { uint32_t h0, h1, l0, l1; };
+__device__ __forceinline__ Split4 split4(f32x4 x) {
+  Split4 s;
+  split2(x[0], x[1], s.h0, s.l0);
+  split2(x[2], x[3], s.h1, s.l1);
+  return s;
+}
+__device__ __forceinline__ AOp as_a(const Split4& s) {
+  return __builtin_bit_cast(AOp, u32x4{s.h0, s.h1, s.l0, s.l1});
+}
+__device__ __forceinline__ BOp as_b(const Split4& s) {
+  typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+  return __builtin_bit_cast(BOp, u32x8{s.l0, s.l1, s.h0, s.h1, 0u, 0u, 0u, 0u});
+}
+__device__ __forceinline__ BX as_bx(bf16x4 v) { return __builtin_shufflevector(v, v, 0, 1, 2, 3, 0, 1, 2, 3); }
+__device__ __forceinline__ BOp as_b(bf16x4 hi, bf16x4 lo) {
+  const bf16x4 z = {};
+  return __builtin_shufflevector(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7),
+                                 __builtin_shufflevector(z, z, 0, 1, 2, 3, 4, 5, 6, 7), 0, 1, 2,
+                                 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
 }
 
 // Inclusive prefix sum over the 16 lanes of a DPP row (the token axis).
@@ -129,6 +157,11 @@ __device__ __forceinline__ float row_scan(float x) {
   x += row_shr<4>(x);
   x += row_shr<8>(x);
   return x;
+}
+// x of the previous token in the DPP row; `first` for token 0
+__device__ __forceinline__ float row_prev(float x, float first) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(first), __float_as_int(x),
+                                                    0x111, 0xf, 0xf, false));
 }
 
 // Eight 16-bit token values packed in a 16-byte vector, widened to fp32.
@@ -148,8 +181,17 @@ __device__ __forceinline__ void unpack8(u32x4 v, float* out) {
   }
 }
 
-__device__ __forceinline__ float fast_exp(float x) {
-  return __builtin_amdgcn_exp2f(x * kLog2e);
+// LDS transpose read (ds_read_b64_tr_b16): within each 16-lane group G, lane
+// g receives item e = element g%4 of the 8-byte piece addressed by lane
+// 4e + g/4 of its group.  With lane g of group q addressing
+// &X[4q + g/4][c0 + 4(g%4)] of a row-major [token][column] array, lane g
+// receives X[4q+e][c0+g]: the K = 16 A-operand layout of X^T (row c0+g,
+// K = token), or equally the B-operand layout of X (K = token, column c0+g).
+__device__ __forceinline__ bf16x4 tr_rows(const __bf16* p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  lds_s16x4* lp = (lds_s16x4*)(p);
+  return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(lp));
 }
 
 // Operators of one chunk consumed by the state path.  For bf16 tokens V is
@@ -158,21 +200,22 @@ __device__ __forceinline__ float fast_exp(float x) {
 template <bool kVExact>
 struct alignas(16) ChunkOps {
   static constexpr int RP = kVExact ? D + 8 : D;    // key row length
-  static constexpr int LP = kVExact ? L + 4 : L;    // token row of transposed arrays
+  static constexpr int TP = D + 16;                 // token row of B^, K^, V
   float gl[D];                        // gamma_L (read as 16-byte vectors)
   __bf16 at_h[L][RP], at_l[L][RP];    // A~ rows, keys at key_pos()
   __bf16 r_h[L][RP], r_l[L][RP];      // R~ rows, keys at key_pos()
-  __bf16 bT_h[D][LP], bT_l[D][LP];    // B^ transposed
-  __bf16 kT_h[D][LP], kT_l[D][LP];    // K^ transposed
-  __bf16 vT_h[D][LP];                 // V transposed
-  __bf16 vT_l[kVExact ? 1 : D][LP];   // V lo part (fp16 tokens only)
-  __bf16 t_h[L][L], t_l[L][L];        // T
-  __bf16 mak_h[L][L], mak_l[L][L];    // Mak, Mrb, Mrk (masked)
-  __bf16 mrb_h[L][L], mrb_l[L][L];
-  __bf16 mrk_h[L][L], mrk_l[L][L];
+  __bf16 b_h[L][TP], b_l[L][TP];      // B^ rows (natural key order)
+  __bf16 k_h[L][TP], k_l[L][TP];      // K^ rows
+  __bf16 v_h[L][TP];                  // V rows
+  __bf16 v_l[kVExact ? 1 : L][TP];    // V lo part (fp16 tokens only)
+  // 16x16 token-token operators in A-operand form: row i, positions
+  // 8q..8q+7 = (hi of columns 4q..4q+3, lo of columns 4q..4q+3)
+  __bf16 t[L][2 * L];                 // T
+  __bf16 mak[L][2 * L], mrb[L][2 * L], mrk[L][2 * L];   // masked Mak, Mrb, Mrk
 };
 // every 16-byte vector access above needs its array 16-byte aligned
-static_assert(offsetof(ChunkOps<true>, at_h) % 16 == 0 && offsetof(ChunkOps<true>, r_h) % 16 == 0,
+static_assert(offsetof(ChunkOps<true>, at_h) % 16 == 0 && offsetof(ChunkOps<true>, t) % 16 == 0 &&
+                  offsetof(ChunkOps<false>, t) % 16 == 0,
               "row arrays must be 16-byte aligned");
 static_assert(sizeof(ChunkOps<true>) % 16 == 0 && sizeof(ChunkOps<false>) % 16 == 0,
               "operator blocks must keep 16-byte alignment");
@@ -180,8 +223,12 @@ static_assert(sizeof(ChunkOps<true>) % 16 == 0 && sizeof(ChunkOps<false>) % 16 =
 template <bool kVExact>
 struct alignas(16) Smem {
   ChunkOps<kVExact> ops[2][G];        // [group parity][chunk]
-  float mpart[G][2][4][L][L];         // [chunk][key half][block][t][s]
+  float mpart[2][G][2][4][L][L];      // [group parity][chunk][key half][block][t][s]
   uint16_t yb[2][GT][D];              // outputs of a group, by parity
+  // progress counters, each written by one wave only: groups whose operators
+  // key wave w has stored, groups whose part-1 partials it has stored, groups
+  // whose outputs it has written back, and groups state wave w has finished
+  int ready[4], part1[4], drained[4], consumed[4];
 };
 
 // Column position of key k in the A~ / R~ rows: for each half m = k/32 the 32
@@ -204,13 +251,11 @@ __device__ __forceinline__ Sp8 rows_vs_state(const __bf16 (*xh)[RP], const __bf1
   return s;
 }
 
-template <int N>
-__device__ __forceinline__ Sp4 load_a16(const __bf16 (*h)[N], const __bf16 (*l)[N], int row,
-                                        int q) {
-  Sp4 s;
-  s.hi = *reinterpret_cast<const bf16x4*>(&h[row][4 * q]);
-  s.lo = *reinterpret_cast<const bf16x4*>(&l[row][4 * q]);
-  return s;
+__device__ __forceinline__ AOp load_aop(const __bf16 (*x)[2 * L], int i, int q) {
+  return *reinterpret_cast<const AOp*>(&x[i][8 * q]);
+}
+__device__ __forceinline__ void store_aop(__bf16 (*x)[2 * L], int i, int q, const AOp& v) {
+  *reinterpret_cast<AOp*>(&x[i][8 * q]) = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -225,7 +270,7 @@ struct KeyRegs {
 template <class Io, bool kVExact>
 __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& op,
                                           const u32x4 (&raw)[6], const float (&bias8)[8],
-                                          bool valid, int cc, int hh, int i, int q,
+                                          bool valid, int mp, int cc, int hh, int i, int q,
                                           KeyRegs& kr) {
   const int kbase = 32 * hh + 8 * q;
   float xr[8], xl[8], xk[8], xv[8], xa[8], xb[8];
@@ -243,9 +288,9 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
     // base-2 log of the retention: log2(w) = -exp(-1/2) log2(e) sigmoid(x)
     const float lw2 = valid ? (kNegExpHalf * kLog2e) * sig : 0.0f;
     const float g2 = row_scan(lw2);
-    const float gm = __builtin_amdgcn_exp2f(g2);
-    const float gp = __builtin_amdgcn_exp2f(g2 - lw2);
-    const float ig = __builtin_amdgcn_exp2f(-g2);
+    const float gm = __builtin_amdgcn_exp2f(g2);      // gamma_t
+    const float gp = row_prev(gm, 1.0f);              // gamma_{t-1}
+    const float ig = __builtin_amdgcn_exp2f(-g2);     // 1 / gamma_t
     at[e] = xa[e] * gp;
     rt[e] = xr[e] * gm;
     bh[e] = xb[e] * ig;
@@ -257,10 +302,10 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
   kr.Bs = split8(bh);
   kr.Ks = split8(kh);
   if constexpr (kVExact) {
-    f32x8 v8;
+    u32x4 h;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v8[e] = xv[e];
-    kr.Vs.hi = __builtin_convertvector(v8, bf16x8);
+    for (int j = 0; j < 4; ++j) h[j] = pack_bf16(xv[2 * j], xv[2 * j + 1]);
+    kr.Vs.hi = __builtin_bit_cast(bf16x8, h);
   } else {
     kr.Vs = split8(xv);
   }
@@ -271,10 +316,10 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
   const f32x4 prk = mma32x3(kr.Rs, kr.Ks, zero);
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    sm.mpart[cc][hh][0][4 * q + e][i] = pab[e];
-    sm.mpart[cc][hh][1][4 * q + e][i] = pak[e];
-    sm.mpart[cc][hh][2][4 * q + e][i] = prb[e];
-    sm.mpart[cc][hh][3][4 * q + e][i] = prk[e];
+    sm.mpart[mp][cc][hh][0][4 * q + e][i] = pab[e];
+    sm.mpart[mp][cc][hh][1][4 * q + e][i] = pak[e];
+    sm.mpart[mp][cc][hh][2][4 * q + e][i] = prb[e];
+    sm.mpart[mp][cc][hh][3][4 * q + e][i] = prk[e];
   }
 }
 
@@ -283,8 +328,8 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
 // Mak, Mrb, Mrk
 // ---------------------------------------------------------------------------
 template <bool kVExact>
-__device__ __forceinline__ void key_part2(Smem<kVExact>& sm, ChunkOps<kVExact>& op, int cc,
-                                          int hh, int i, int q, const KeyRegs& kr) {
+__device__ __forceinline__ void key_part2(Smem<kVExact>& sm, ChunkOps<kVExact>& op, int mp,
+                                          int cc, int hh, int i, int q, const KeyRegs& kr) {
   const int kbase = 32 * hh + 8 * q;
   {
     // keys kbase..kbase+7 land in two 4-key runs of the permuted rows
@@ -298,61 +343,56 @@ __device__ __forceinline__ void key_part2(Smem<kVExact>& sm, ChunkOps<kVExact>& 
     *reinterpret_cast<bf16x4*>(&op.at_l[i][p0]) = kr.As.lo.lo;
     *reinterpret_cast<bf16x4*>(&op.at_l[i][p1]) = kr.As.lo.hi;
   }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int k = kbase + e;
-    op.bT_h[k][i] = kr.Bs.hi[e];
-    op.bT_l[k][i] = kr.Bs.lo[e];
-    op.kT_h[k][i] = kr.Ks.hi[e];
-    op.kT_l[k][i] = kr.Ks.lo[e];
-    op.vT_h[k][i] = kr.Vs.hi[e];
-    if constexpr (!kVExact) op.vT_l[k][i] = kr.Vs.lo[e];
-  }
-  const float (*mp0)[4][L][L] = sm.mpart[cc];
+  *reinterpret_cast<bf16x8*>(&op.b_h[i][kbase]) = kr.Bs.hi;
+  *reinterpret_cast<bf16x8*>(&op.b_l[i][kbase]) = kr.Bs.lo;
+  *reinterpret_cast<bf16x8*>(&op.k_h[i][kbase]) = kr.Ks.hi;
+  *reinterpret_cast<bf16x8*>(&op.k_l[i][kbase]) = kr.Ks.lo;
+  *reinterpret_cast<bf16x8*>(&op.v_h[i][kbase]) = kr.Vs.hi;
+  if constexpr (!kVExact) *reinterpret_cast<bf16x8*>(&op.v_l[i][kbase]) = kr.Vs.lo;
+  const float (*mp0)[4][L][L] = sm.mpart[mp][cc];
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   if (hh == 0) {
     f32x4 M, Mt, I4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int r = 4 * q + e;
-      M[e] = (r > i) ? mp0[0][0][r][i] + mp0[1][0][r][i] : 0.f;
-      Mt[e] = (i > r) ? mp0[0][0][i][r] + mp0[1][0][i][r] : 0.f;
+      const float m = mp0[0][0][r][i] + mp0[1][0][r][i];
+      const float mt = mp0[0][0][i][r] + mp0[1][0][i][r];
+      M[e] = (r > i) ? m : 0.f;
+      Mt[e] = (i > r) ? mt : 0.f;
       I4[e] = (r == i) ? 1.0f : 0.0f;
     }
     // T = (I - Mab)^-1 = (I+M)(I+M^2)(I+M^4)(I+M^8) (M strictly lower,
     // 16x16), keeping both orientations of each factor in accumulator
-    // registers; every factor is split into hi/lo once.
-    const Sp4 sM = split4(M), sMt = split4(Mt);
-    const f32x4 M2 = mm(sMt, sM, zero);
-    const f32x4 M2t = mm(sM, sMt, zero);
-    const Sp4 sM2 = split4(M2), sM2t = split4(M2t);
+    // registers; X Y = mm_ab(A form of X^T's accumulator, B form of Y's).
+    const Split4 sM = split4(M), sMt = split4(Mt);
+    const f32x4 M2 = mm_ab(as_a(sMt), as_b(sM), zero);
+    const f32x4 M2t = mm_ab(as_a(sM), as_b(sMt), zero);
+    const Split4 sM2 = split4(M2), sM2t = split4(M2t);
     const f32x4 T1t = I4 + Mt;
-    const f32x4 T2t = mm(sM2, split4(T1t), T1t);
-    const f32x4 M4 = mm(sM2t, sM2, zero);
-    const f32x4 M4t = mm(sM2, sM2t, zero);
-    const Sp4 sM4 = split4(M4);
-    const f32x4 T4t = mm(sM4, split4(T2t), T2t);
-    const f32x4 M8 = mm(split4(M4t), sM4, zero);
-    const f32x4 Tt = mm(split4(M8), split4(T4t), T4t);   // accumulator of T^T
-    const Sp4 Ta = split4(Tt);                            // = A operand of T
-    *reinterpret_cast<bf16x4*>(&op.t_h[i][4 * q]) = Ta.hi;
-    *reinterpret_cast<bf16x4*>(&op.t_l[i][4 * q]) = Ta.lo;
+    const f32x4 T2t = mm_ab(as_a(sM2), as_b(split4(T1t)), T1t);
+    const f32x4 M4 = mm_ab(as_a(sM2t), as_b(sM2), zero);
+    const f32x4 M4t = mm_ab(as_a(sM2), as_b(sM2t), zero);
+    const Split4 sM4 = split4(M4);
+    const f32x4 T4t = mm_ab(as_a(sM4), as_b(split4(T2t)), T2t);
+    const f32x4 M8 = mm_ab(as_a(split4(M4t)), as_b(sM4), zero);
+    const f32x4 Tt = mm_ab(as_a(split4(M8)), as_b(split4(T4t)), T4t);   // accumulator of T^T
+    store_aop(op.t, i, q, as_a(split4(Tt)));                            // = A operand of T
   } else {
     f32x4 mak, mrb, mrk;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int s = 4 * q + e;       // A-operand layout: row i, K = s
-      mak[e] = (i > s) ? mp0[0][1][i][s] + mp0[1][1][i][s] : 0.f;
-      mrb[e] = (i >= s) ? mp0[0][2][i][s] + mp0[1][2][i][s] : 0.f;
-      mrk[e] = (i >= s) ? mp0[0][3][i][s] + mp0[1][3][i][s] : 0.f;
+      const float v1 = mp0[0][1][i][s] + mp0[1][1][i][s];
+      const float v2 = mp0[0][2][i][s] + mp0[1][2][i][s];
+      const float v3 = mp0[0][3][i][s] + mp0[1][3][i][s];
+      mak[e] = (i > s) ? v1 : 0.f;
+      mrb[e] = (i >= s) ? v2 : 0.f;
+      mrk[e] = (i >= s) ? v3 : 0.f;
     }
-    const Sp4 Mak = split4(mak), Mrb = split4(mrb), Mrk = split4(mrk);
-    *reinterpret_cast<bf16x4*>(&op.mak_h[i][4 * q]) = Mak.hi;
-    *reinterpret_cast<bf16x4*>(&op.mak_l[i][4 * q]) = Mak.lo;
-    *reinterpret_cast<bf16x4*>(&op.mrb_h[i][4 * q]) = Mrb.hi;
-    *reinterpret_cast<bf16x4*>(&op.mrb_l[i][4 * q]) = Mrb.lo;
-    *reinterpret_cast<bf16x4*>(&op.mrk_h[i][4 * q]) = Mrk.hi;
-    *reinterpret_cast<bf16x4*>(&op.mrk_l[i][4 * q]) = Mrk.lo;
+    store_aop(op.mak, i, q, as_a(split4(mak)));
+    store_aop(op.mrb, i, q, as_a(split4(mrb)));
+    store_aop(op.mrk, i, q, as_a(split4(mrk)));
   }
 }
 
@@ -365,60 +405,121 @@ __device__ __forceinline__ void state_chunk(const ChunkOps<kVExact>& op, f32x4 (
                                             float scale) {
   using raw = typename Io::raw;
   // all operand reads of the chunk first, so that their LDS latency overlaps
-  const Sp4 Ta = load_a16(op.t_h, op.t_l, i, q);
-  const Sp4 Mak = load_a16(op.mak_h, op.mak_l, i, q);
-  const Sp4 Mrb = load_a16(op.mrb_h, op.mrb_l, i, q);
-  const Sp4 Mrk = load_a16(op.mrk_h, op.mrk_l, i, q);
-  Sp4 Vb;
-  Vb.hi = *reinterpret_cast<const bf16x4*>(&op.vT_h[vcol][4 * q]);   // V[4q+e][vcol]
-  if constexpr (!kVExact) Vb.lo = *reinterpret_cast<const bf16x4*>(&op.vT_l[vcol][4 * q]);
+  const AOp Ta = load_aop(op.t, i, q);
+  const AOp Mak = load_aop(op.mak, i, q);
+  const AOp Mrb = load_aop(op.mrb, i, q);
+  const AOp Mrk = load_aop(op.mrk, i, q);
+  // transposed operands straight from the token rows (see tr_rows)
+  const int trow = 4 * q + (i >> 2), tcol = 4 * (i & 3);
+  const int vc0 = 16 * (vcol >> 4) + tcol;
+  const bf16x4 vh = tr_rows(&op.v_h[trow][vc0]);                       // V[4q+e][vcol]
   const Sp8 Aa0 = rows_vs_state(op.at_h, op.at_l, 0, i, q);
   const Sp8 Aa1 = rows_vs_state(op.at_h, op.at_l, 1, i, q);
   const Sp8 Ra0 = rows_vs_state(op.r_h, op.r_l, 0, i, q);
   const Sp8 Ra1 = rows_vs_state(op.r_h, op.r_l, 1, i, q);
-  Sp4 Bt[4], Kt[4];
+  AOp Bt[4], Kt[4];
   f32x4 gl[4];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
-    Bt[kb] = load_a16(op.bT_h, op.bT_l, kb * 16 + i, q);
-    Kt[kb] = load_a16(op.kT_h, op.kT_l, kb * 16 + i, q);
+    // B^^T, K^^T as A operands: row 16kb+i, K = token
+    Bt[kb] = __builtin_shufflevector(tr_rows(&op.b_h[trow][kb * 16 + tcol]),
+                                     tr_rows(&op.b_l[trow][kb * 16 + tcol]), 0, 1, 2, 3, 4, 5,
+                                     6, 7);
+    Kt[kb] = __builtin_shufflevector(tr_rows(&op.k_h[trow][kb * 16 + tcol]),
+                                     tr_rows(&op.k_l[trow][kb * 16 + tcol]), 0, 1, 2, 3, 4, 5,
+                                     6, 7);
     gl[kb] = *reinterpret_cast<const f32x4*>(&op.gl[kb * 16 + 4 * q]);
   }
+  // S split as B operand against the permuted A~ / R~ rows: K positions
+  // 8q..8q+7 = rows 32m + 4q + (0..3) then 32m + 16 + 4q + (0..3)
   Sp8 Sb[2];
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
-    const Sp4 lo = split4(S[2 * m]);
-    const Sp4 hi = split4(S[2 * m + 1]);
-    Sb[m].hi = cat4(lo.hi, hi.hi);
-    Sb[m].lo = cat4(lo.lo, hi.lo);
+    const Split4 a = split4(S[2 * m]), b = split4(S[2 * m + 1]);
+    Sb[m].hi = __builtin_bit_cast(bf16x8, u32x4{a.h0, a.h1, b.h0, b.h1});
+    Sb[m].lo = __builtin_bit_cast(bf16x8, u32x4{a.l0, a.l1, b.l0, b.l1});
   }
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   // X = A~ S0 + Mak V,  U = T X,  Y = R~ S0 + Mrb U + Mrk V
-  f32x4 X = kVExact ? mma16x2p(Mak, Vb.hi, zero) : mma16x3p(Mak, Vb, zero);
-  X = mma32x3(Aa0, Sb[0], X);
-  X = mma32x3(Aa1, Sb[1], X);
-  f32x4 Y = kVExact ? mma16x2p(Mrk, Vb.hi, zero) : mma16x3p(Mrk, Vb, zero);
-  Y = mma32x3(Ra0, Sb[0], Y);
-  Y = mma32x3(Ra1, Sb[1], Y);
-  const f32x4 U = mma16x3p(Ta, split4(X), zero);
-  const Sp4 Us = split4(U);
-  Y = mma16x3p(Mrb, Us, Y);
+  f32x4 X, Y;
+  if constexpr (kVExact) {
+    const BX Vx = as_bx(vh);
+    X = mm_ax(Mak, Vx, zero);
+    Y = mm_ax(Mrk, Vx, zero);
+    X = mma32x3(Aa0, Sb[0], X);
+    X = mma32x3(Aa1, Sb[1], X);
+    Y = mma32x3(Ra0, Sb[0], Y);
+    Y = mma32x3(Ra1, Sb[1], Y);
+    const BOp Us = as_b(split4(mm_ab(Ta, as_b(split4(X)), zero)));
+    Y = mm_ab(Mrb, Us, Y);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const raw yv = Io::from_f32(scale * Y[e]);
-    yrows[4 * q + e][vcol] = __builtin_bit_cast(uint16_t, yv);
-  }
-  // S += B^^T U + K^^T V: five (bf16 V) or six (fp16 V) K = 16 terms in
-  // three K = 32 products
-  const bf16x4 z = {};
+    for (int e = 0; e < 4; ++e) {
+      const raw yv = Io::from_f32(scale * Y[e]);
+      yrows[4 * q + e][vcol] = __builtin_bit_cast(uint16_t, yv);
+    }
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    f32x4 acc = S[kb];
-    acc = mma2(Bt[kb].hi, Bt[kb].lo, Us.lo, Us.hi, acc);
-    acc = mma2(Bt[kb].hi, Kt[kb].hi, Us.hi, Vb.hi, acc);
-    acc = kVExact ? mma2(Kt[kb].lo, z, Vb.hi, z, acc) : mma2(Kt[kb].lo, Kt[kb].hi, Vb.hi, Vb.lo, acc);
-    S[kb] = acc * gl[kb];
+    for (int kb = 0; kb < 4; ++kb) {
+      f32x4 acc = mm_ab(Bt[kb], Us, S[kb]);
+      acc = mm_ax(Kt[kb], Vx, acc);
+      S[kb] = acc * gl[kb];
+    }
+  } else {
+    const BOp Vs = as_b(vh, tr_rows(&op.v_l[trow][vc0]));
+    X = mm_ab(Mak, Vs, zero);
+    Y = mm_ab(Mrk, Vs, zero);
+    X = mma32x3(Aa0, Sb[0], X);
+    X = mma32x3(Aa1, Sb[1], X);
+    Y = mma32x3(Ra0, Sb[0], Y);
+    Y = mma32x3(Ra1, Sb[1], Y);
+    const BOp Us = as_b(split4(mm_ab(Ta, as_b(split4(X)), zero)));
+    Y = mm_ab(Mrb, Us, Y);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const raw yv = Io::from_f32(scale * Y[e]);
+      yrows[4 * q + e][vcol] = __builtin_bit_cast(uint16_t, yv);
+    }
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      f32x4 acc = mm_ab(Bt[kb], Us, S[kb]);
+      acc = mm_ab(Kt[kb], Vs, acc);
+      S[kb] = acc * gl[kb];
+    }
   }
+}
+
+// Progress counters in LDS.  Producers and consumers exchange LDS data only,
+// so ordering needs only the LDS counter: a wave publishes a counter after
+// waiting for its own LDS operations to complete (lgkmcnt(0)); a waiting wave
+// polls the counter, and its later LDS reads issue after the poll returned.
+// Compiler fences keep the memory operations on their side of each step.
+// (Acquire/release atomics would also wait for outstanding global loads,
+// stalling the row prefetch.)  Every wait is bounded, so a counting mistake
+// can only produce wrong values, never a wave that does not finish.
+constexpr int kSpinLimit = 1 << 20;
+
+__device__ __forceinline__ void signal(int* c, int v) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): own LDS stores have landed
+  __hip_atomic_store(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ int peek(int* c) {
+  return __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void wait_ge(int* c, int v) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  for (int it = 0; it < kSpinLimit && peek(c) < v; ++it) __builtin_amdgcn_s_sleep(1);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// wait until all four counters c[0..3] reach v
+__device__ __forceinline__ void wait_min_ge(int* c, int v) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  for (int it = 0; it < kSpinLimit; ++it) {
+    const int m = min(min(peek(c), peek(c + 1)), min(peek(c + 2), peek(c + 3)));
+    if (m >= v) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 template <class Io>
@@ -465,6 +566,9 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
   const int ngroups = (t1 - t0 + GT - 1) / GT;
   raw* yout = static_cast<raw*>(p.y);
 
+  if (tid < 16) (&sm.ready[0])[tid] = 0;
+  __syncthreads();   // the only workgroup barrier: counters are zero
+
   if (wv < 4) {
     // ---------------- state waves: columns [16wv, 16wv+16)
     const int vcol = 16 * wv + i;
@@ -479,16 +583,14 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) S[kb][e] = sin[sbase + (kb * 16 + 4 * q + e) * D + vcol];
     }
-    __syncthreads();  // prologue: operators of group 0 (part 1)
-    __syncthreads();  // prologue: operators of group 0 (part 2)
     auto group = [&](auto par_c, int gi) {
       constexpr int par = decltype(par_c)::value;
-      const int g0 = t0 + gi * GT;
+      wait_min_ge(sm.ready, gi + 1);          // operators of group gi stored
+      wait_min_ge(sm.drained, gi - 1);        // outputs of group gi-2 written back
       state_chunk<Io, kVExact>(sm.ops[par][0], S, &sm.yb[par][0], vcol, i, q, p.scale);
-      __syncthreads();
-      if (g0 + L < t1)
+      if (t0 + gi * GT + L < t1)
         state_chunk<Io, kVExact>(sm.ops[par][1], S, &sm.yb[par][L], vcol, i, q, p.scale);
-      __syncthreads();
+      signal(&sm.consumed[wv], gi + 1);
     };
     for (int gi = 0; gi < ngroups; gi += 2) {
       group(std::integral_constant<int, 0>{}, gi);
@@ -502,10 +604,11 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
         for (int e = 0; e < 4; ++e) sout[sbase + (kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
     }
   } else {
-    // ---------------- key waves: chunk cc of the group, key half hh
+    // ---------------- key waves: chunk cc of each group, key half hh
     const int kw = wv & 3;
     const int cc = kw >> 1;
     const int hh = kw & 1;
+    const int partner = kw ^ 1;
     const int kbase = 32 * hh + 8 * q;
     float bias8[8];
 #pragma unroll
@@ -537,45 +640,40 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
     const int kt = tid - 256;
     const int o_tok = kt >> 3, o_c8 = kt & 7;
     raw* const ybase = yout + static_cast<int64_t>(t0 + o_tok) * row_stride + head_off + o_c8 * 8;
-    auto write_out = [&](int gi, int par) {
+    auto write_out = [&](int gi) {
+      if (gi < 0) return;
+      wait_min_ge(sm.consumed, gi + 1);
       if (t0 + gi * GT + o_tok < t1)
         *reinterpret_cast<u32x4*>(ybase + static_cast<int64_t>(gi) * gstride) =
-            *reinterpret_cast<const u32x4*>(&sm.yb[par][o_tok][o_c8 * 8]);
+            *reinterpret_cast<const u32x4*>(&sm.yb[gi & 1][o_tok][o_c8 * 8]);
+      signal(&sm.drained[kw], gi + 1);
     };
     u32x4 rawA[6], rawB[6];
     KeyRegs kr;
     load_rows(rawA, 0);
-    if (ngroups > 1) load_rows(rawB, 1);
-    // prologue: group 0 from rawA
-    {
-      const bool active = cc * L < t1 - t0;
-      if (active)
-        key_part1<Io, kVExact>(sm, sm.ops[0][cc], rawA, bias8, tok0 < t1, cc, hh, i, q, kr);
-      __syncthreads();
-      if (active) key_part2(sm, sm.ops[0][cc], cc, hh, i, q, kr);
-      __syncthreads();
-    }
-    // iteration gi prepares group gn = gi + 1 (parity of gn) from the rows
-    // prefetched one group ahead, and writes out the outputs of group gi - 1
-    auto iter = [&](auto par_c, u32x4 (&cur)[6], u32x4 (&nxt)[6], int gi) {
+    // group gn: prefetch the rows of gn + 1, write back the outputs of gn - 2
+    // (which also frees the operator buffers of parity gn), then build the
+    // operators of gn
+    auto iter = [&](auto par_c, u32x4 (&cur)[6], u32x4 (&nxt)[6], int gn) {
       constexpr int par = decltype(par_c)::value;   // parity of gn
-      const int gn = gi + 1;
-      const bool active = gn < ngroups && t0 + gn * GT + cc * L < t1;
-      if (gn + 1 < ngroups) load_rows(cur, gn + 1);   // cur was consumed last time
-      if (gi > 0) write_out(gi - 1, par);             // parity of gi - 1 == parity of gn
+      if (gn + 1 < ngroups) load_rows(nxt, gn + 1);
+      write_out(gn - 2);
+      wait_min_ge(sm.consumed, gn - 1);             // group gn-2 no longer read
+      const bool active = t0 + gn * GT + cc * L < t1;
       if (active)
-        key_part1<Io, kVExact>(sm, sm.ops[par][cc], nxt, bias8, tok0 + gn * GT < t1, cc, hh,
-                               i, q, kr);
-      __syncthreads();
-      if (active) key_part2(sm, sm.ops[par][cc], cc, hh, i, q, kr);
-      __syncthreads();
+        key_part1<Io, kVExact>(sm, sm.ops[par][cc], cur, bias8, tok0 + gn * GT < t1, par, cc,
+                               hh, i, q, kr);
+      signal(&sm.part1[kw], gn + 1);
+      wait_ge(&sm.part1[partner], gn + 1);
+      if (active) key_part2(sm, sm.ops[par][cc], par, cc, hh, i, q, kr);
+      signal(&sm.ready[kw], gn + 1);
     };
-    // rawA holds group 0 (consumed), rawB group 1; alternate the two buffers
-    for (int gi = 0; gi < ngroups; gi += 2) {
-      iter(std::integral_constant<int, 1>{}, rawA, rawB, gi);
-      if (gi + 1 < ngroups) iter(std::integral_constant<int, 0>{}, rawB, rawA, gi + 1);
+    for (int gn = 0; gn < ngroups; gn += 2) {
+      iter(std::integral_constant<int, 0>{}, rawA, rawB, gn);
+      if (gn + 1 < ngroups) iter(std::integral_constant<int, 1>{}, rawB, rawA, gn + 1);
     }
-    if (ngroups > 0) write_out(ngroups - 1, (ngroups - 1) & 1);
+    write_out(ngroups - 2);
+    write_out(ngroups - 1);
   }
 }
 
