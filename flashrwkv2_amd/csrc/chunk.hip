@@ -226,8 +226,8 @@ struct alignas(16) Smem {
   float mpart[2][G][2][4][L][L];      // [group parity][chunk][key half][block][t][s]
   uint16_t yb[2][GT][D];              // outputs of a group, by parity
   // progress counters, each written by one wave only: groups whose operators
-  // key wave w has stored, groups whose part-1 partials it has stored, groups
-  // whose outputs it has written back, and groups state wave w has finished
+  // key wave w has stored, groups whose part-1 partials it has stored, and
+  // groups state wave w has finished / whose output rows it has written back
   int ready[4], part1[4], drained[4], consumed[4];
 };
 
@@ -273,13 +273,16 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
                                           bool valid, int mp, int cc, int hh, int i, int q,
                                           KeyRegs& kr) {
   const int kbase = 32 * hh + 8 * q;
+  // tokens past the sequence end (their rows repeat the last token) carry
+  // zero operands and a unit retention
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
   float xr[8], xl[8], xk[8], xv[8], xa[8], xb[8];
-  unpack8<Io>(raw[0], xr);
+  unpack8<Io>(valid ? raw[0] : zero4, xr);
   unpack8<Io>(raw[1], xl);
-  unpack8<Io>(raw[2], xk);
-  unpack8<Io>(raw[3], xv);
-  unpack8<Io>(raw[4], xa);
-  unpack8<Io>(raw[5], xb);
+  unpack8<Io>(valid ? raw[2] : zero4, xk);
+  unpack8<Io>(valid ? raw[3] : zero4, xv);
+  unpack8<Io>(valid ? raw[4] : zero4, xa);
+  unpack8<Io>(valid ? raw[5] : zero4, xb);
   float at[8], rt[8], bh[8], kh[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -583,6 +586,19 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) S[kb][e] = sin[sbase + (kb * 16 + 4 * q + e) * D + vcol];
     }
+    // outputs of a finished group: 16-byte pieces of the staged rows, token
+    // tid/8, elements 8*(tid%8).. (the four state waves cover the 32 rows)
+    const int o_tok = tid >> 3, o_c8 = tid & 7;
+    raw* const ybase = yout + static_cast<int64_t>(t0 + o_tok) * row_stride + head_off + o_c8 * 8;
+    const int64_t gstride = static_cast<int64_t>(GT) * row_stride;
+    auto write_out = [&](int gi) {
+      if (gi < 0) return;
+      wait_min_ge(sm.consumed, gi + 1);       // every state wave staged its columns
+      if (t0 + gi * GT + o_tok < t1)
+        *reinterpret_cast<u32x4*>(ybase + static_cast<int64_t>(gi) * gstride) =
+            *reinterpret_cast<const u32x4*>(&sm.yb[gi & 1][o_tok][o_c8 * 8]);
+      signal(&sm.drained[wv], gi + 1);
+    };
     auto group = [&](auto par_c, int gi) {
       constexpr int par = decltype(par_c)::value;
       wait_min_ge(sm.ready, gi + 1);          // operators of group gi stored
@@ -591,11 +607,13 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
       if (t0 + gi * GT + L < t1)
         state_chunk<Io, kVExact>(sm.ops[par][1], S, &sm.yb[par][L], vcol, i, q, p.scale);
       signal(&sm.consumed[wv], gi + 1);
+      write_out(gi - 1);
     };
     for (int gi = 0; gi < ngroups; gi += 2) {
       group(std::integral_constant<int, 0>{}, gi);
       if (gi + 1 < ngroups) group(std::integral_constant<int, 1>{}, gi + 1);
     }
+    write_out(ngroups - 1);
     if (p.state_out != nullptr) {
       float* sout = static_cast<float*>(p.state_out);
 #pragma unroll
@@ -628,36 +646,27 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
       src[5] = static_cast<const raw*>(p.b) + off;
     }
     const int64_t gstride = static_cast<int64_t>(GT) * row_stride;
-    const u32x4 zero4 = {0u, 0u, 0u, 0u};
+    // Rows past the sequence end are loaded from the last valid row (always
+    // in bounds); key_part1 zeroes them when it consumes them.  A conditional
+    // load would compile to a branch whose zeroing path waits for every
+    // outstanding memory operation, the previous group's output stores
+    // included, and a select right here would wait for the loads themselves.
     auto load_rows = [&](u32x4 (&dst)[6], int gi) {
-      const bool ok = tok0 + gi * GT < t1;
-      const int64_t off = static_cast<int64_t>(gi) * gstride;
+      const int tok = tok0 + gi * GT;
+      const int64_t off = static_cast<int64_t>(min(tok, t1 - 1) - tok0) * row_stride;
 #pragma unroll
       for (int j = 0; j < 6; ++j)
-        dst[j] = ok ? *reinterpret_cast<const u32x4*>(src[j] + off) : zero4;
-    };
-    // output rows of a finished group: 16-byte pieces, token kt/8, elements 8*(kt%8)..
-    const int kt = tid - 256;
-    const int o_tok = kt >> 3, o_c8 = kt & 7;
-    raw* const ybase = yout + static_cast<int64_t>(t0 + o_tok) * row_stride + head_off + o_c8 * 8;
-    auto write_out = [&](int gi) {
-      if (gi < 0) return;
-      wait_min_ge(sm.consumed, gi + 1);
-      if (t0 + gi * GT + o_tok < t1)
-        *reinterpret_cast<u32x4*>(ybase + static_cast<int64_t>(gi) * gstride) =
-            *reinterpret_cast<const u32x4*>(&sm.yb[gi & 1][o_tok][o_c8 * 8]);
-      signal(&sm.drained[kw], gi + 1);
+        dst[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src[j] + off));
     };
     u32x4 rawA[6], rawB[6];
     KeyRegs kr;
     load_rows(rawA, 0);
-    // group gn: prefetch the rows of gn + 1, write back the outputs of gn - 2
-    // (which also frees the operator buffers of parity gn), then build the
-    // operators of gn
+    // group gn: prefetch the rows of gn + 1, wait until the state waves are
+    // done with group gn - 2 (whose operator buffers gn reuses), then build
+    // the operators of gn
     auto iter = [&](auto par_c, u32x4 (&cur)[6], u32x4 (&nxt)[6], int gn) {
       constexpr int par = decltype(par_c)::value;   // parity of gn
       if (gn + 1 < ngroups) load_rows(nxt, gn + 1);
-      write_out(gn - 2);
       wait_min_ge(sm.consumed, gn - 1);             // group gn-2 no longer read
       const bool active = t0 + gn * GT + cc * L < t1;
       if (active)
@@ -672,8 +681,6 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
       iter(std::integral_constant<int, 0>{}, rawA, rawB, gn);
       if (gn + 1 < ngroups) iter(std::integral_constant<int, 1>{}, rawB, rawA, gn + 1);
     }
-    write_out(ngroups - 2);
-    write_out(ngroups - 1);
   }
 }
 
