@@ -54,6 +54,8 @@ constexpr int L = 16;          // tokens per chunk
 constexpr int G = 2;           // chunks per group
 constexpr int GT = L * G;      // tokens per group
 constexpr int NT = 512;        // 8 wavefronts: 4 state + 4 key
+constexpr int MPP = L + 4;     // padded row of the partial token-token blocks
+constexpr int YP = D + 8;      // padded row of the staged outputs
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegExpHalf = -0.6065306597126334f;   // -exp(-1/2)
 
@@ -223,8 +225,11 @@ static_assert(sizeof(ChunkOps<true>) % 16 == 0 && sizeof(ChunkOps<false>) % 16 =
 template <bool kVExact>
 struct alignas(16) Smem {
   ChunkOps<kVExact> ops[2][G];        // [group parity][chunk]
-  float mpart[2][G][2][4][L][L];      // [group parity][chunk][key half][block][t][s]
-  uint16_t yb[2][GT][D];              // outputs of a group, by parity
+  // partial token-token blocks, transposed (mpart[..][s][t] = P[t][s]) with
+  // rows padded to MPP floats so that both the 16-byte row accesses and the
+  // strided column reads spread over the banks
+  float mpart[2][G][2][4][L][MPP];    // [group parity][chunk][key half][block][s][t]
+  uint16_t yb[2][GT][YP];             // outputs of a group, by parity (padded rows)
   // progress counters, each written by one wave only: groups whose operators
   // key wave w has stored, groups whose part-1 partials it has stored, and
   // groups state wave w has finished / whose output rows it has written back
@@ -317,13 +322,11 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
   const f32x4 pak = mma32x3(kr.As, kr.Ks, zero);
   const f32x4 prb = mma32x3(kr.Rs, kr.Bs, zero);
   const f32x4 prk = mma32x3(kr.Rs, kr.Ks, zero);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    sm.mpart[mp][cc][hh][0][4 * q + e][i] = pab[e];
-    sm.mpart[mp][cc][hh][1][4 * q + e][i] = pak[e];
-    sm.mpart[mp][cc][hh][2][4 * q + e][i] = prb[e];
-    sm.mpart[mp][cc][hh][3][4 * q + e][i] = prk[e];
-  }
+  // lane (i, q) holds P[4q+e][i]: one 16-byte store per block
+  *reinterpret_cast<f32x4*>(&sm.mpart[mp][cc][hh][0][i][4 * q]) = pab;
+  *reinterpret_cast<f32x4*>(&sm.mpart[mp][cc][hh][1][i][4 * q]) = pak;
+  *reinterpret_cast<f32x4*>(&sm.mpart[mp][cc][hh][2][i][4 * q]) = prb;
+  *reinterpret_cast<f32x4*>(&sm.mpart[mp][cc][hh][3][i][4 * q]) = prk;
 }
 
 // ---------------------------------------------------------------------------
@@ -352,16 +355,20 @@ __device__ __forceinline__ void key_part2(Smem<kVExact>& sm, ChunkOps<kVExact>& 
   *reinterpret_cast<bf16x8*>(&op.k_l[i][kbase]) = kr.Ks.lo;
   *reinterpret_cast<bf16x8*>(&op.v_h[i][kbase]) = kr.Vs.hi;
   if constexpr (!kVExact) *reinterpret_cast<bf16x8*>(&op.v_l[i][kbase]) = kr.Vs.lo;
-  const float (*mp0)[4][L][L] = sm.mpart[mp][cc];
+  // P[t][s] of block b, summed over the two key halves, is
+  // mp0[0][b][s][t] + mp0[1][b][s][t]
+  const float (*mp0)[4][L][MPP] = sm.mpart[mp][cc];
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   if (hh == 0) {
+    // M[e] = Mab[4q+e][i] (accumulator layout), Mt[e] = Mab[i][4q+e]
+    const f32x4 m4 = *reinterpret_cast<const f32x4*>(&mp0[0][0][i][4 * q]) +
+                     *reinterpret_cast<const f32x4*>(&mp0[1][0][i][4 * q]);
     f32x4 M, Mt, I4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int r = 4 * q + e;
-      const float m = mp0[0][0][r][i] + mp0[1][0][r][i];
-      const float mt = mp0[0][0][i][r] + mp0[1][0][i][r];
-      M[e] = (r > i) ? m : 0.f;
+      const float mt = mp0[0][0][r][i] + mp0[1][0][r][i];
+      M[e] = (r > i) ? m4[e] : 0.f;
       Mt[e] = (i > r) ? mt : 0.f;
       I4[e] = (r == i) ? 1.0f : 0.0f;
     }
@@ -386,9 +393,9 @@ __device__ __forceinline__ void key_part2(Smem<kVExact>& sm, ChunkOps<kVExact>& 
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int s = 4 * q + e;       // A-operand layout: row i, K = s
-      const float v1 = mp0[0][1][i][s] + mp0[1][1][i][s];
-      const float v2 = mp0[0][2][i][s] + mp0[1][2][i][s];
-      const float v3 = mp0[0][3][i][s] + mp0[1][3][i][s];
+      const float v1 = mp0[0][1][s][i] + mp0[1][1][s][i];
+      const float v2 = mp0[0][2][s][i] + mp0[1][2][s][i];
+      const float v3 = mp0[0][3][s][i] + mp0[1][3][s][i];
       mak[e] = (i > s) ? v1 : 0.f;
       mrb[e] = (i >= s) ? v2 : 0.f;
       mrk[e] = (i >= s) ? v3 : 0.f;
@@ -404,7 +411,7 @@ __device__ __forceinline__ void key_part2(Smem<kVExact>& sm, ChunkOps<kVExact>& 
 // ---------------------------------------------------------------------------
 template <class Io, bool kVExact>
 __device__ __forceinline__ void state_chunk(const ChunkOps<kVExact>& op, f32x4 (&S)[4],
-                                            uint16_t (*yrows)[D], int vcol, int i, int q,
+                                            uint16_t (*yrows)[YP], int vcol, int i, int q,
                                             float scale) {
   using raw = typename Io::raw;
   // all operand reads of the chunk first, so that their LDS latency overlaps
@@ -623,6 +630,9 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
     }
   } else {
     // ---------------- key waves: chunk cc of each group, key half hh
+    // The key waves are the pipeline's critical path and share each SIMD
+    // with a state wave that has slack: let them win instruction issue.
+    __builtin_amdgcn_s_setprio(2);
     const int kw = wv & 3;
     const int cc = kw >> 1;
     const int hh = kw & 1;
