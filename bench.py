@@ -204,6 +204,8 @@ def main() -> int:
                     help="tokens per sequence in the CPU baseline sample")
     ap.add_argument("--only", choices=["prefill", "decode"], default=None,
                     help="run one leg only (profiling)")
+    ap.add_argument("--config", type=int, default=1, choices=[1, 3, 4],
+                    help="prefill workload (BASELINE config; the metric is quoted on 1)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (a known-size "
                          "kernel for scaling the HBM byte counters of a profile)")
@@ -234,7 +236,7 @@ def main() -> int:
 
     pre = None
     if args.only in (None, "prefill"):
-        w1 = workloads.config(1, "cuda")
+        w1 = workloads.config(args.config, "cuda")
         pre = Runner(w1, torch, flashrwkv2_amd)
         ms = pre.time_steps(args.steps, args.warmup)
         kms = pre.time_kernel(args.steps)
@@ -252,7 +254,7 @@ def main() -> int:
             "vs_baseline": None,
             "dtype": "bf16",
             "data": "synthetic (seeded, BASELINE config 1 distributions; inputs resident in HBM)",
-            "config": {"workload": w1.name, "B": 8, "T": 4096, "H": 32, "D": 64,
+            "config": {"workload": w1.name, **w1.info, "D": 64,
                        "io": "bf16", "state": "fp32",
                        "arithmetic": "bf16 MFMA on hi/lo split operands, fp32 accumulate",
                        "kernel": pre.kernel_name(),
@@ -280,7 +282,7 @@ def main() -> int:
             result.update({"metric": METRIC, "value": result["decode"]["tokens_per_s"],
                            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
                            "warmup": args.warmup, "ms_per_step": round(dms, 5)})
-    if pre is not None and not args.no_cpu:
+    if pre is not None and not args.no_cpu and args.config == 1:
         threads = min(16, os.cpu_count() or 1)
         tps, dt, n_tok, reps = cpu_baseline(pre.w, threads, args.cpu_sample_tokens)
         result["cpu_baseline"] = {

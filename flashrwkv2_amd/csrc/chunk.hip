@@ -272,29 +272,34 @@ struct KeyRegs {
   Sp8 As, Rs, Bs, Ks, Vs;
 };
 
-template <class Io, bool kVExact>
+// kFull: every token of the chunk is inside the sequence (no masking).
+// nbias8 holds -log2(e) * decay_bias for the lane's keys.
+template <class Io, bool kVExact, bool kFull>
 __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& op,
-                                          const u32x4 (&raw)[6], const float (&bias8)[8],
+                                          const u32x4 (&raw)[6], const float (&nbias8)[8],
                                           bool valid, int mp, int cc, int hh, int i, int q,
                                           KeyRegs& kr) {
   const int kbase = 32 * hh + 8 * q;
   // tokens past the sequence end (their rows repeat the last token) carry
   // zero operands and a unit retention
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
-  float xr[8], xl[8], xk[8], xv[8], xa[8], xb[8];
-  unpack8<Io>(valid ? raw[0] : zero4, xr);
+  auto tok = [&](int j) { return (kFull || valid) ? raw[j] : zero4; };
+  float xr[8], xl[8], xk[8], xa[8], xb[8];
+  unpack8<Io>(tok(0), xr);
   unpack8<Io>(raw[1], xl);
-  unpack8<Io>(valid ? raw[2] : zero4, xk);
-  unpack8<Io>(valid ? raw[3] : zero4, xv);
-  unpack8<Io>(valid ? raw[4] : zero4, xa);
-  unpack8<Io>(valid ? raw[5] : zero4, xb);
+  unpack8<Io>(tok(2), xk);
+  unpack8<Io>(tok(4), xa);
+  unpack8<Io>(tok(5), xb);
+  // base-2 log of the retention, log2(w) = c sigmoid(x) with
+  // c = -exp(-1/2) log2(e), evaluated as 1 / ((1 + 2^(-log2(e) x)) / c)
+  constexpr float kC = kNegExpHalf * kLog2e;
+  constexpr float kInvC = 1.0f / kC;
   float at[8], rt[8], bh[8], kh[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float x = xl[e] + bias8[e];
-    const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2e * x));
-    // base-2 log of the retention: log2(w) = -exp(-1/2) log2(e) sigmoid(x)
-    const float lw2 = valid ? (kNegExpHalf * kLog2e) * sig : 0.0f;
+    const float ex = __builtin_amdgcn_exp2f(__builtin_fmaf(xl[e], -kLog2e, nbias8[e]));
+    float lw2 = __builtin_amdgcn_rcpf(__builtin_fmaf(ex, kInvC, kInvC));
+    if constexpr (!kFull) lw2 = valid ? lw2 : 0.0f;
     const float g2 = row_scan(lw2);
     const float gm = __builtin_amdgcn_exp2f(g2);      // gamma_t
     const float gp = row_prev(gm, 1.0f);              // gamma_{t-1}
@@ -310,11 +315,10 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
   kr.Bs = split8(bh);
   kr.Ks = split8(kh);
   if constexpr (kVExact) {
-    u32x4 h;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) h[j] = pack_bf16(xv[2 * j], xv[2 * j + 1]);
-    kr.Vs.hi = __builtin_bit_cast(bf16x8, h);
+    kr.Vs.hi = __builtin_bit_cast(bf16x8, tok(3));     // bf16 values are exact
   } else {
+    float xv[8];
+    unpack8<Io>(tok(3), xv);
     kr.Vs = split8(xv);
   }
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -638,10 +642,11 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
     const int hh = kw & 1;
     const int partner = kw ^ 1;
     const int kbase = 32 * hh + 8 * q;
-    float bias8[8];
+    float nbias8[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      bias8[e] = p.bias ? Io::to_f32(static_cast<const raw*>(p.bias)[head_off + kbase + e]) : 0.f;
+      nbias8[e] = p.bias ? -kLog2e * Io::to_f32(static_cast<const raw*>(p.bias)[head_off + kbase + e])
+                         : 0.f;
     // token rows of this lane (token i of chunk cc, keys kbase..+7), as
     // running pointers; the group stride is GT rows
     const int tok0 = t0 + cc * L + i;
@@ -679,9 +684,12 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
       if (gn + 1 < ngroups) load_rows(nxt, gn + 1);
       wait_min_ge(sm.consumed, gn - 1);             // group gn-2 no longer read
       const bool active = t0 + gn * GT + cc * L < t1;
-      if (active)
-        key_part1<Io, kVExact>(sm, sm.ops[par][cc], cur, bias8, tok0 + gn * GT < t1, par, cc,
-                               hh, i, q, kr);
+      if (t0 + gn * GT + cc * L + L <= t1)
+        key_part1<Io, kVExact, true>(sm, sm.ops[par][cc], cur, nbias8, true, par, cc, hh, i, q,
+                                     kr);
+      else if (active)
+        key_part1<Io, kVExact, false>(sm, sm.ops[par][cc], cur, nbias8, tok0 + gn * GT < t1,
+                                      par, cc, hh, i, q, kr);
       signal(&sm.part1[kw], gn + 1);
       wait_ge(&sm.part1[partner], gn + 1);
       if (active) key_part2(sm, sm.ops[par][cc], par, cc, hh, i, q, kr);
