@@ -411,39 +411,69 @@ __device__ __forceinline__ void key_part2(Smem<kVExact>& sm, ChunkOps<kVExact>& 
 }
 
 // ---------------------------------------------------------------------------
-// state side: one chunk for the columns [16w, 16w+16) held in S
+// state side: one chunk for the columns [16w, 16w+16) held in S.  The
+// operand reads of a chunk are separate from its arithmetic so that the
+// reads of the next chunk can be issued before this chunk's dependent chain.
 // ---------------------------------------------------------------------------
-template <class Io, bool kVExact>
-__device__ __forceinline__ void state_chunk(const ChunkOps<kVExact>& op, f32x4 (&S)[4],
-                                            uint16_t (*yrows)[YP], int vcol, int i, int q,
-                                            float scale) {
-  using raw = typename Io::raw;
-  // all operand reads of the chunk first, so that their LDS latency overlaps
-  const AOp Ta = load_aop(op.t, i, q);
-  const AOp Mak = load_aop(op.mak, i, q);
-  const AOp Mrb = load_aop(op.mrb, i, q);
-  const AOp Mrk = load_aop(op.mrk, i, q);
+template <bool kVExact>
+struct StateOps {
+  AOp Ta, Mak, Mrb, Mrk;
+  bf16x4 vh, vl;
+  Sp8 Aa0, Aa1, Ra0, Ra1;
+  AOp Bt[4], Kt[4];
+  f32x4 gl[4];
+};
+
+// operands the chain needs first: Mak, Mrk, V and the A~ / R~ rows
+template <bool kVExact>
+__device__ __forceinline__ void state_load_early(StateOps<kVExact>& o, const ChunkOps<kVExact>& op,
+                                                 int vcol, int i, int q) {
+  o.Mak = load_aop(op.mak, i, q);
+  o.Mrk = load_aop(op.mrk, i, q);
   // transposed operands straight from the token rows (see tr_rows)
   const int trow = 4 * q + (i >> 2), tcol = 4 * (i & 3);
   const int vc0 = 16 * (vcol >> 4) + tcol;
-  const bf16x4 vh = tr_rows(&op.v_h[trow][vc0]);                       // V[4q+e][vcol]
-  const Sp8 Aa0 = rows_vs_state(op.at_h, op.at_l, 0, i, q);
-  const Sp8 Aa1 = rows_vs_state(op.at_h, op.at_l, 1, i, q);
-  const Sp8 Ra0 = rows_vs_state(op.r_h, op.r_l, 0, i, q);
-  const Sp8 Ra1 = rows_vs_state(op.r_h, op.r_l, 1, i, q);
-  AOp Bt[4], Kt[4];
-  f32x4 gl[4];
+  o.vh = tr_rows(&op.v_h[trow][vc0]);                                   // V[4q+e][vcol]
+  if constexpr (!kVExact) o.vl = tr_rows(&op.v_l[trow][vc0]);
+  o.Aa0 = rows_vs_state(op.at_h, op.at_l, 0, i, q);
+  o.Aa1 = rows_vs_state(op.at_h, op.at_l, 1, i, q);
+  o.Ra0 = rows_vs_state(op.r_h, op.r_l, 0, i, q);
+  o.Ra1 = rows_vs_state(op.r_h, op.r_l, 1, i, q);
+}
+// the rest: T, Mrb, B^^T, K^^T and gamma_L
+template <bool kVExact>
+__device__ __forceinline__ void state_load_late(StateOps<kVExact>& o, const ChunkOps<kVExact>& op,
+                                                int vcol, int i, int q) {
+  (void)vcol;
+  o.Ta = load_aop(op.t, i, q);
+  o.Mrb = load_aop(op.mrb, i, q);
+  const int trow = 4 * q + (i >> 2), tcol = 4 * (i & 3);
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
     // B^^T, K^^T as A operands: row 16kb+i, K = token
-    Bt[kb] = __builtin_shufflevector(tr_rows(&op.b_h[trow][kb * 16 + tcol]),
-                                     tr_rows(&op.b_l[trow][kb * 16 + tcol]), 0, 1, 2, 3, 4, 5,
-                                     6, 7);
-    Kt[kb] = __builtin_shufflevector(tr_rows(&op.k_h[trow][kb * 16 + tcol]),
-                                     tr_rows(&op.k_l[trow][kb * 16 + tcol]), 0, 1, 2, 3, 4, 5,
-                                     6, 7);
-    gl[kb] = *reinterpret_cast<const f32x4*>(&op.gl[kb * 16 + 4 * q]);
+    o.Bt[kb] = __builtin_shufflevector(tr_rows(&op.b_h[trow][kb * 16 + tcol]),
+                                       tr_rows(&op.b_l[trow][kb * 16 + tcol]), 0, 1, 2, 3, 4,
+                                       5, 6, 7);
+    o.Kt[kb] = __builtin_shufflevector(tr_rows(&op.k_h[trow][kb * 16 + tcol]),
+                                       tr_rows(&op.k_l[trow][kb * 16 + tcol]), 0, 1, 2, 3, 4,
+                                       5, 6, 7);
+    o.gl[kb] = *reinterpret_cast<const f32x4*>(&op.gl[kb * 16 + 4 * q]);
   }
+}
+template <bool kVExact>
+__device__ __forceinline__ StateOps<kVExact> state_load(const ChunkOps<kVExact>& op, int vcol,
+                                                        int i, int q) {
+  StateOps<kVExact> o;
+  state_load_early(o, op, vcol, i, q);
+  state_load_late(o, op, vcol, i, q);
+  return o;
+}
+
+template <class Io, bool kVExact>
+__device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 (&S)[4],
+                                              uint16_t (*yrows)[YP], int vcol, int i, int q,
+                                              float scale) {
+  using raw = typename Io::raw;
   // S split as B operand against the permuted A~ / R~ rows: K positions
   // 8q..8q+7 = rows 32m + 4q + (0..3) then 32m + 16 + 4q + (0..3)
   Sp8 Sb[2];
@@ -457,15 +487,15 @@ __device__ __forceinline__ void state_chunk(const ChunkOps<kVExact>& op, f32x4 (
   // X = A~ S0 + Mak V,  U = T X,  Y = R~ S0 + Mrb U + Mrk V
   f32x4 X, Y;
   if constexpr (kVExact) {
-    const BX Vx = as_bx(vh);
-    X = mm_ax(Mak, Vx, zero);
-    Y = mm_ax(Mrk, Vx, zero);
-    X = mma32x3(Aa0, Sb[0], X);
-    X = mma32x3(Aa1, Sb[1], X);
-    Y = mma32x3(Ra0, Sb[0], Y);
-    Y = mma32x3(Ra1, Sb[1], Y);
-    const BOp Us = as_b(split4(mm_ab(Ta, as_b(split4(X)), zero)));
-    Y = mm_ab(Mrb, Us, Y);
+    const BX Vx = as_bx(o.vh);
+    X = mm_ax(o.Mak, Vx, zero);
+    Y = mm_ax(o.Mrk, Vx, zero);
+    X = mma32x3(o.Aa0, Sb[0], X);
+    X = mma32x3(o.Aa1, Sb[1], X);
+    Y = mma32x3(o.Ra0, Sb[0], Y);
+    Y = mma32x3(o.Ra1, Sb[1], Y);
+    const BOp Us = as_b(split4(mm_ab(o.Ta, as_b(split4(X)), zero)));
+    Y = mm_ab(o.Mrb, Us, Y);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const raw yv = Io::from_f32(scale * Y[e]);
@@ -473,20 +503,20 @@ __device__ __forceinline__ void state_chunk(const ChunkOps<kVExact>& op, f32x4 (
     }
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      f32x4 acc = mm_ab(Bt[kb], Us, S[kb]);
-      acc = mm_ax(Kt[kb], Vx, acc);
-      S[kb] = acc * gl[kb];
+      f32x4 acc = mm_ab(o.Bt[kb], Us, S[kb]);
+      acc = mm_ax(o.Kt[kb], Vx, acc);
+      S[kb] = acc * o.gl[kb];
     }
   } else {
-    const BOp Vs = as_b(vh, tr_rows(&op.v_l[trow][vc0]));
-    X = mm_ab(Mak, Vs, zero);
-    Y = mm_ab(Mrk, Vs, zero);
-    X = mma32x3(Aa0, Sb[0], X);
-    X = mma32x3(Aa1, Sb[1], X);
-    Y = mma32x3(Ra0, Sb[0], Y);
-    Y = mma32x3(Ra1, Sb[1], Y);
-    const BOp Us = as_b(split4(mm_ab(Ta, as_b(split4(X)), zero)));
-    Y = mm_ab(Mrb, Us, Y);
+    const BOp Vs = as_b(o.vh, o.vl);
+    X = mm_ab(o.Mak, Vs, zero);
+    Y = mm_ab(o.Mrk, Vs, zero);
+    X = mma32x3(o.Aa0, Sb[0], X);
+    X = mma32x3(o.Aa1, Sb[1], X);
+    Y = mma32x3(o.Ra0, Sb[0], Y);
+    Y = mma32x3(o.Ra1, Sb[1], Y);
+    const BOp Us = as_b(split4(mm_ab(o.Ta, as_b(split4(X)), zero)));
+    Y = mm_ab(o.Mrb, Us, Y);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const raw yv = Io::from_f32(scale * Y[e]);
@@ -494,9 +524,9 @@ __device__ __forceinline__ void state_chunk(const ChunkOps<kVExact>& op, f32x4 (
     }
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      f32x4 acc = mm_ab(Bt[kb], Us, S[kb]);
-      acc = mm_ab(Kt[kb], Vs, acc);
-      S[kb] = acc * gl[kb];
+      f32x4 acc = mm_ab(o.Bt[kb], Us, S[kb]);
+      acc = mm_ab(o.Kt[kb], Vs, acc);
+      S[kb] = acc * o.gl[kb];
     }
   }
 }
@@ -614,9 +644,22 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
       constexpr int par = decltype(par_c)::value;
       wait_min_ge(sm.ready, gi + 1);          // operators of group gi stored
       wait_min_ge(sm.drained, gi - 1);        // outputs of group gi-2 written back
-      state_chunk<Io, kVExact>(sm.ops[par][0], S, &sm.yb[par][0], vcol, i, q, p.scale);
-      if (t0 + gi * GT + L < t1)
-        state_chunk<Io, kVExact>(sm.ops[par][1], S, &sm.yb[par][L], vcol, i, q, p.scale);
+      if (t0 + gi * GT + GT <= t1) {
+        // both chunks: the second chunk's first-needed operand reads (the
+        // S-side rows and V-side blocks) go out before the first chunk's chain
+        const StateOps<kVExact> o0 = state_load(sm.ops[par][0], vcol, i, q);
+        StateOps<kVExact> o1;
+        state_load_early(o1, sm.ops[par][1], vcol, i, q);
+        state_compute<Io, kVExact>(o0, S, &sm.yb[par][0], vcol, i, q, p.scale);
+        state_load_late(o1, sm.ops[par][1], vcol, i, q);
+        state_compute<Io, kVExact>(o1, S, &sm.yb[par][L], vcol, i, q, p.scale);
+      } else {
+        state_compute<Io, kVExact>(state_load(sm.ops[par][0], vcol, i, q), S, &sm.yb[par][0],
+                                   vcol, i, q, p.scale);
+        if (t0 + gi * GT + L < t1)
+          state_compute<Io, kVExact>(state_load(sm.ops[par][1], vcol, i, q), S, &sm.yb[par][L],
+                                     vcol, i, q, p.scale);
+      }
       signal(&sm.consumed[wv], gi + 1);
       write_out(gi - 1);
     };
