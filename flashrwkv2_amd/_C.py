@@ -374,6 +374,74 @@ def tmix_wkv7_recurrent_fp32_kernel_forced(kernel, query_start_loc, state_indice
 
 
 # ---------------------------------------------------------------------------
+# FP16-state ("Albatross") packed recurrence
+# ---------------------------------------------------------------------------
+def _check_fp16_recurrent_layout(qsl, slots, elapsed, state, r, decay_logits, k, v, a, b,
+                                 output, scale):
+    """check_fp16_recurrent_layout, infer_recurrent_fp16_forward_varlen.cpp:49-120."""
+    for t, name in ((qsl, "query_start_loc"), (slots, "state_indices"),
+                    (elapsed, "elapsed_state_pool"), (state, "state"), (r, "r"),
+                    (decay_logits, "decay_logits"), (k, "k"), (v, "v"), (a, "a"), (b, "b"),
+                    (output, "output")):
+        check_cuda_contiguous(t, name)
+    for t, name in ((qsl, "query_start_loc"), (slots, "state_indices"),
+                    (elapsed, "elapsed_state_pool"), (r, "r"), (decay_logits, "decay_logits"),
+                    (k, "k"), (v, "v"), (a, "a"), (b, "b"), (output, "output")):
+        check_same_device(state, t, name)
+    _check(qsl.dtype == torch.int32 and slots.dtype == torch.int32
+           and elapsed.dtype == torch.int32, "recurrent metadata must be int32")
+    n = slots.numel()
+    _check(slots.dim() == 1 and n > 0 and qsl.dim() == 1 and qsl.numel() == n + 1,
+           "query_start_loc must have shape [B+1] and state_indices shape [B]")
+    _check(n <= 65535, "state_indices must contain 1..65535 sequences")
+    _check(elapsed.dim() == 1 and elapsed.size(0) == state.size(0),
+           "elapsed_state_pool must have shape [state_pool_slots]")
+    _check(state.dim() == 4 and state.dtype == torch.float16 and state.size(0) > 0
+           and state.size(1) > 0 and state.size(2) == state.size(3),
+           "state must be contiguous float16 [slots,H,D,D]")
+    h, d = state.size(1), state.size(2)
+    _check(d in (64, 128, 256), "recurrent head size must be 64, 128, or 256, got ", d)
+    _check(r.dim() == 3 and r.size(0) > 0 and r.size(1) == h and r.size(2) == d,
+           "r must have packed shape [total_tokens,H,D] matching state")
+    _check(r.size(0) <= INT32_MAX, "token count must fit in int32")
+    _check(all(t.shape == r.shape for t in (decay_logits, k, v, a, b, output)),
+           "r,decay_logits,k,v,a,b,output shape mismatch")
+    _check(all(t.dtype == torch.float16 for t in (r, decay_logits, k, v, a, b, output)),
+           "FP16-state recurrent token tensors must be float16")
+    _check(math.isfinite(scale), "scale must be finite")
+    return n, h, d
+
+
+def tmix_wkv7_recurrent_fp16_from_decay_logits(query_start_loc, state_indices, elapsed_state,
+                                               state, r, decay_logits, k, v, a, b, output,
+                                               scale, decay_bias=None, validated_metadata=None,
+                                               max_seqlen=-1):
+    """In-place FP16-state packed recurrence, then the elapsed-count advance
+    (infer_recurrent_fp16_forward_varlen.cpp:121-187)."""
+    n, h, d = _check_fp16_recurrent_layout(query_start_loc, state_indices, elapsed_state,
+                                           state, r, decay_logits, k, v, a, b, output, scale)
+    if decay_bias is not None:
+        check_cuda_contiguous(decay_bias, "decay_bias")
+        check_same_device(state, decay_bias, "decay_bias")
+        _check(decay_bias.dtype == torch.float16
+               and ((decay_bias.dim() == 1 and decay_bias.numel() == h * d)
+                    or (decay_bias.dim() == 2 and decay_bias.size(0) == h
+                        and decay_bias.size(1) == d)),
+               "decay_bias must be float16 with shape [H*D] or [H,D]")
+    lq, ls, status, max_seqlen, keep = _resolve_launch_metadata(
+        query_start_loc, state_indices, r.size(0), state.size(0), int(max_seqlen),
+        validated_metadata)
+    with torch.cuda.device(state.device):
+        rc = N.load().fr2_wkv7_recurrent_fp16_forward(
+            lq.data_ptr(), ls.data_ptr(), status.data_ptr(), elapsed_state.data_ptr(), n, h, d,
+            r.size(0), int(max_seqlen), state.data_ptr(), r.data_ptr(), decay_logits.data_ptr(),
+            N.ptr(decay_bias), k.data_ptr(), v.data_ptr(), a.data_ptr(), b.data_ptr(),
+            output.data_ptr(), float(scale), _stream(state.device))
+    N.check(rc, "tmix_wkv7_recurrent_fp16_from_decay_logits")
+    del keep
+
+
+# ---------------------------------------------------------------------------
 # pretrain [B,T,H,D] forward
 # ---------------------------------------------------------------------------
 def pretrain_tmix_wkv7_recurrent_forward(r, w, k, v, a, b, output, boundary, state_dot_a,
@@ -612,6 +680,7 @@ def exported_names() -> Sequence[str]:
         "prepare_tmix_wkv7_recurrent_metadata",
         "prepare_tmix_wkv7_recurrent_graph_metadata",
         "tmix_wkv7_recurrent_fp32_from_decay_logits",
+        "tmix_wkv7_recurrent_fp16_from_decay_logits",
         "pretrain_tmix_wkv7_recurrent_forward",
         "pretrain_tmix_wkv7_recurrent_backward",
         "infer_tmix_wkv7_chunk_bf16_forward_varlen",

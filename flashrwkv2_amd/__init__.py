@@ -29,6 +29,7 @@ _C = _load_native_backend()
 
 from .tmix.wkv7 import (  # noqa: E402
     infer_tmix_wkv7_chunk_bf16_forward_varlen,
+    infer_tmix_wkv7_recurrent_fp16_forward_varlen,
     infer_tmix_wkv7_recurrent_fp32io16_forward_varlen,
     prepare_tmix_wkv7_recurrent_metadata,
     pretrain_tmix_wkv7_recurrent_bf16,
@@ -38,6 +39,7 @@ from .tmix.wkv7 import (  # noqa: E402
 
 __all__ = [
     "infer_tmix_wkv7_chunk_bf16_forward_varlen",
+    "infer_tmix_wkv7_recurrent_fp16_forward_varlen",
     "infer_tmix_wkv7_recurrent_fp32io16_forward_varlen",
     "prepare_tmix_wkv7_recurrent_metadata",
     "pretrain_tmix_wkv7_recurrent_bf16",

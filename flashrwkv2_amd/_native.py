@@ -53,6 +53,12 @@ SIGNATURES: dict[str, tuple] = {
          c_int64, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_void_p],
     ),
+    "fr2_wkv7_recurrent_fp16_forward": (
+        c_int32,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64,
+         c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_float, c_void_p],
+    ),
     "fr2_wkv7_pretrain_forward": (
         c_int32,
         [c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,

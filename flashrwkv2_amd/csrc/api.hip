@@ -103,6 +103,35 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kernel(
                         v, a, b, output, scale, stream);
 }
 
+extern "C" int fr2_wkv7_recurrent_fp16_forward(
+    const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, int32_t* elapsed_state, int32_t num_sequences,
+    int32_t num_heads, int32_t head_size, int64_t total_tokens, int32_t max_seqlen,
+    void* state_f16, const void* r, const void* decay_logits, const void* decay_bias,
+    const void* k, const void* v, const void* a, const void* b, void* output, float scale,
+    void* stream) {
+  (void)max_seqlen;
+  if (!query_start_loc || !state_indices || !status || !elapsed_state || !state_f16 ||
+      !tokens_ok(r, decay_logits, k, v, a, b, output))
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 || total_tokens <= 0)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return FR2_ERR_UNSUPPORTED;
+  SegArgs p;
+  p.bounds = query_start_loc;
+  p.slots = state_indices;
+  p.status = status;
+  p.num_heads = num_heads;
+  p.out_elems = total_tokens * num_heads * head_size;
+  p.state_in = state_f16;
+  p.state_out = state_f16;
+  p.r = r; p.logits = decay_logits; p.bias = decay_bias; p.k = k; p.v = v; p.a = a; p.b = b;
+  p.y = output;
+  p.scale = scale;
+  return fr2::launch_fp16_state(head_size, p, num_sequences, elapsed_state,
+                                static_cast<hipStream_t>(stream));
+}
+
 extern "C" int fr2_wkv7_pretrain_forward(int32_t batch, int32_t tokens,
                                          int32_t num_heads, int32_t head_size,
                                          const void* r, const void* w,

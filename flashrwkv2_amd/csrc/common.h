@@ -60,6 +60,27 @@ struct StBF16 {
   }
 };
 
+struct StF16 {
+  using raw = _Float16;
+  static __device__ __forceinline__ float to_f32(raw x) { return static_cast<float>(x); }
+  static __device__ __forceinline__ raw from_f32(float f) { return static_cast<raw>(f); }
+};
+
+// FP16-state ("Albatross") contract, csrc/sm120/tmix/wkv7/recurrent_decay.cuh:36-46:
+// the state update is state + state * delta with
+//   delta = fp16(retention - 1 + dither(phase)),
+//   dither(phase) = int32(0x9E3779B9 * phase mod 2^32) * 2^-41
+// (a golden-ratio multiplicative hash scaled into (-2^-10, 2^-10)), and
+// phase = elapsed[slot] + head * D + key + token offset in the sequence.
+__device__ __forceinline__ float albatross_dither(int phase) {
+  const uint32_t bits = 0x9E3779B9u * static_cast<uint32_t>(phase);
+  return 4.547473508864641e-13f * static_cast<float>(static_cast<int32_t>(bits));
+}
+__device__ __forceinline__ float albatross_delta(float x, int phase) {
+  const float d = retention_from_logit(x) - 1.0f + albatross_dither(phase);
+  return static_cast<float>(static_cast<_Float16>(d));
+}
+
 // Native 4-wide float vector (usable with the nontemporal builtins).
 typedef float f4 __attribute__((ext_vector_type(4)));
 

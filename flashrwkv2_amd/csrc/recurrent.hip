@@ -57,8 +57,14 @@ __device__ __forceinline__ bool check_status(const SegArgs& p, int seg,
 // through a double-buffered LDS array (one barrier per token); the y partials
 // of a tile are reduced after the tile and stored coalesced.
 // ---------------------------------------------------------------------------
+// St = StF16 selects the FP16-state (Albatross) update: the staged retention
+// becomes delta = fp16(w - 1 + dither(phase)), the update is
+// S + S*delta + b*sa + k*v evaluated in fp32 and rounded to fp16 after every
+// token (the state registers always hold fp16 values), and y is read from
+// the rounded state (csrc/sm120/tmix/wkv7/infer_recurrent_fp16_forward_varlen.cu:243-336).
 template <int D, class Io, class St>
 __global__ __launch_bounds__(4 * D) void serial_kernel(SegArgs p) {
+  constexpr bool kAlbatross = __is_same(St, StF16);
   using raw = typename Io::raw;
   constexpr int KS = 4;
   constexpr int NT = KS * D;
@@ -83,6 +89,7 @@ __global__ __launch_bounds__(4 * D) void serial_kernel(SegArgs p) {
   resolve_segment(p, seg, t0, t1, slot);
 
   const int64_t sbase = (static_cast<int64_t>(slot) * H + h) * D * D;
+  const int elapsed_base = (kAlbatross && p.elapsed != nullptr) ? p.elapsed[slot] : 0;
   float S[R];
   if (p.state_in != nullptr) {
     const typename St::raw* sin = static_cast<const typename St::raw*>(p.state_in);
@@ -119,7 +126,10 @@ __global__ __launch_bounds__(4 * D) void serial_kernel(SegArgs p) {
           for (int i = 0; i < 8; ++i) {
             float x = f[i];
             if (bias != nullptr) x += Io::to_f32(bias[h * D + c8 * 8 + i]);
-            f[i] = retention_from_logit(x);
+            if constexpr (kAlbatross)
+              f[i] = albatross_delta(x, elapsed_base + h * D + c8 * 8 + i + (tile + tt - t0));
+            else
+              f[i] = retention_from_logit(x);
           }
         }
         float4* dst = reinterpret_cast<float4*>(&s_in[which][tt][c8 * 8]);
@@ -153,12 +163,24 @@ __global__ __launch_bounds__(4 * D) void serial_kernel(SegArgs p) {
       const float* Br = &s_in[5][tt][q * R];
       const float* Rr = &s_in[0][tt][q * R];
       float y0 = 0.f, y1 = 0.f, y2 = 0.f, y3 = 0.f;
+      if constexpr (kAlbatross) {
+        // Wr holds delta: fp16(S + S*delta + b*sa + k*v)
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+          float u = fmaf(S[j], Wr[j], S[j]);
+          u = fmaf(Br[j], sa, u);
+          u = fmaf(Kr[j], vv, u);
+          S[j] = St::to_f32(St::from_f32(u));
+        }
+      }
 #pragma unroll
       for (int j = 0; j < R; j += 4) {
-        S[j + 0] = fmaf(Wr[j + 0], S[j + 0], fmaf(Br[j + 0], sa, Kr[j + 0] * vv));
-        S[j + 1] = fmaf(Wr[j + 1], S[j + 1], fmaf(Br[j + 1], sa, Kr[j + 1] * vv));
-        S[j + 2] = fmaf(Wr[j + 2], S[j + 2], fmaf(Br[j + 2], sa, Kr[j + 2] * vv));
-        S[j + 3] = fmaf(Wr[j + 3], S[j + 3], fmaf(Br[j + 3], sa, Kr[j + 3] * vv));
+        if constexpr (!kAlbatross) {
+          S[j + 0] = fmaf(Wr[j + 0], S[j + 0], fmaf(Br[j + 0], sa, Kr[j + 0] * vv));
+          S[j + 1] = fmaf(Wr[j + 1], S[j + 1], fmaf(Br[j + 1], sa, Kr[j + 1] * vv));
+          S[j + 2] = fmaf(Wr[j + 2], S[j + 2], fmaf(Br[j + 2], sa, Kr[j + 2] * vv));
+          S[j + 3] = fmaf(Wr[j + 3], S[j + 3], fmaf(Br[j + 3], sa, Kr[j + 3] * vv));
+        }
         y0 = fmaf(Rr[j + 0], S[j + 0], y0);
         y1 = fmaf(Rr[j + 1], S[j + 1], y1);
         y2 = fmaf(Rr[j + 2], S[j + 2], y2);
@@ -336,6 +358,32 @@ static int launch_serial_io(int D, const SegArgs& p, int nseg, hipStream_t s) {
     default:
       return FR2_ERR_UNSUPPORTED;
   }
+  return record_launch();
+}
+
+// Adds each active sequence's token count to its slot's elapsed count
+// (csrc/sm120/tmix/wkv7/infer_recurrent_fp16_forward_varlen.cu:60-75); an
+// invalid ticket leaves every count untouched.  Runs after the recurrence on
+// the same stream, so no recurrence workgroup reads a count this writes.
+__global__ __launch_bounds__(256) void advance_elapsed_kernel(SegArgs p, int nseg,
+                                                              int32_t* elapsed) {
+  const int seg = static_cast<int>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (seg >= nseg) return;
+  if (p.status != nullptr && (p.status[0] != 0 || seg >= p.status[2])) return;
+  int t0, t1, slot;
+  resolve_segment(p, seg, t0, t1, slot);
+  elapsed[slot] += t1 - t0;
+}
+
+int launch_fp16_state(int D, const SegArgs& p, int nseg, int32_t* elapsed, hipStream_t s) {
+  if (elapsed == nullptr || p.sa_out != nullptr || p.boundary != nullptr)
+    return FR2_ERR_INVALID_ARGUMENT;
+  SegArgs q = p;
+  q.elapsed = elapsed;
+  const int rc = launch_serial_io<IoF16, StF16>(D, q, nseg, s);
+  if (rc != FR2_OK) return rc;
+  hipLaunchKernelGGL(advance_elapsed_kernel, dim3((nseg + 255) / 256), dim3(256), 0, s, q, nseg,
+                     elapsed);
   return record_launch();
 }
 

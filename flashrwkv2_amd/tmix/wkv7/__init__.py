@@ -167,8 +167,84 @@ def infer_tmix_wkv7_recurrent_fp32io16_forward_varlen(
     return output
 
 
+def _validate_fp16_state(state: torch.Tensor) -> None:
+    """…/wkv7/__init__.py:41-47."""
+    if not isinstance(state, torch.Tensor):
+        raise TypeError("state_pool must be a torch.Tensor")
+    if not state.is_contiguous():
+        raise ValueError("state_pool must be contiguous")
+    if state.dtype != torch.float16:
+        raise TypeError("FP16-state state_pool must have dtype float16")
+
+
+def _validate_fp16_elapsed_state(elapsed_state_pool: torch.Tensor,
+                                 state_pool: torch.Tensor) -> None:
+    """…/wkv7/__init__.py:50-62."""
+    if not isinstance(elapsed_state_pool, torch.Tensor):
+        raise TypeError("elapsed_state_pool must be a torch.Tensor")
+    if elapsed_state_pool.dtype != torch.int32:
+        raise TypeError("elapsed_state_pool must have dtype torch.int32")
+    if not elapsed_state_pool.is_cuda or not elapsed_state_pool.is_contiguous():
+        raise ValueError("elapsed_state_pool must be contiguous CUDA int32")
+    if elapsed_state_pool.device != state_pool.device:
+        raise ValueError("elapsed_state_pool must share state_pool's device")
+    if elapsed_state_pool.ndim != 1 or elapsed_state_pool.shape[0] != state_pool.shape[0]:
+        raise ValueError("elapsed_state_pool must have shape [state_pool_slots]")
+
+
+def infer_tmix_wkv7_recurrent_fp16_forward_varlen(
+    r: torch.Tensor,
+    decay_logits: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    *,
+    state_pool: torch.Tensor,
+    elapsed_state_pool: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    state_indices: torch.Tensor,
+    scale: float = 1.0,
+    decay_bias: torch.Tensor | None = None,
+    max_seqlen: int | None = None,
+    validated_metadata: object | None = None,
+) -> torch.Tensor:
+    """Packed recurrence with an FP16 state pool (the Albatross delta/phase
+    contract); ``state_pool`` is updated in place and ``elapsed_state_pool``
+    advanced by each active sequence's length.  (…/wkv7/__init__.py:259-318.)
+    """
+    packed = _validate_packed_inputs(r, decay_logits, k, v, a, b)
+    _validate_fp16_state(state_pool)
+    _validate_fp16_elapsed_state(elapsed_state_pool, state_pool)
+    _check_metadata_inputs(cu_seqlens, state_indices)
+    if max_seqlen is None:
+        # max_seqlen inference belongs to metadata preparation: no device sync
+        # on every launch
+        launch_max_seqlen = -1
+    else:
+        if (not isinstance(max_seqlen, int) or isinstance(max_seqlen, bool)
+                or max_seqlen <= 0):
+            raise ValueError("max_seqlen must be a positive integer")
+        launch_max_seqlen = int(max_seqlen)
+    ticket = (
+        validated_metadata
+        if validated_metadata is not None
+        else prepare_tmix_wkv7_recurrent_metadata(
+            cu_seqlens, state_indices, total_tokens=r.shape[0],
+            state_pool_size=state_pool.shape[0], max_seqlen=launch_max_seqlen,
+        )
+    )
+    output = torch.empty_like(packed[3])
+    _extension().tmix_wkv7_recurrent_fp16_from_decay_logits(
+        cu_seqlens, state_indices, elapsed_state_pool, state_pool, *packed, output,
+        float(scale), decay_bias, ticket, launch_max_seqlen,
+    )
+    return output
+
+
 __all__ = [
     "infer_tmix_wkv7_recurrent_fp32io16_forward_varlen",
+    "infer_tmix_wkv7_recurrent_fp16_forward_varlen",
     "prepare_tmix_wkv7_recurrent_metadata",
 ]
 

@@ -122,6 +122,32 @@ int fr2_wkv7_recurrent_fp32_forward_kernel(
     float scale, void* stream);
 
 /*
+ * Packed varlen recurrence with an FP16 state pool [slots,H,D,D] updated in
+ * place (the "Albatross" FP16-state contract, fp16 token tensors only):
+ *   delta  = fp16(w - 1 + dither(phase)),
+ *   dither = int32(0x9E3779B9 * phase mod 2^32) * 2^-41,
+ *   phase  = elapsed_state[slot] + h*D + key + token offset in the sequence,
+ *   S      = fp16(S + S*delta + b*sa + k*v^T) after every token (fp32 math),
+ *   y      = fp16(scale * S^T r) from the rounded state.
+ * Afterwards elapsed_state[slot] += sequence length for every active
+ * sequence (enqueued on the same stream).  A non-zero status[0] makes every
+ * output element NaN and leaves the pool and the elapsed counts untouched.
+ * head_size in {64, 128, 256}.
+ * Replaces tmix_wkv7_recurrent_fp16_from_decay_logits_cuda and
+ * recurrent_fp16_advance_i32_varlen_cuda
+ * (csrc/sm120/tmix/wkv7/infer_recurrent_fp16_forward_varlen.cpp:121-187,
+ *  infer_recurrent_fp16_forward_varlen.cu:60-75, :243-336).
+ */
+int fr2_wkv7_recurrent_fp16_forward(
+    const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, int32_t* elapsed_state, int32_t num_sequences,
+    int32_t num_heads, int32_t head_size, int64_t total_tokens,
+    int32_t max_seqlen, void* state_f16, const void* r,
+    const void* decay_logits, const void* decay_bias, const void* k,
+    const void* v, const void* a, const void* b, void* output, float scale,
+    void* stream);
+
+/*
  * [B,T,H,D] bf16 training forward with zero initial state.  Writes y (bf16),
  * state_dot_a [B,T,H,D] fp32 (the pre-update sa of every token) and
  * boundary [B,H,T/16,D,D] fp32, the post-chunk state after every 16 tokens.

@@ -15,6 +15,12 @@ adds numpy conveniences.  What each function restates:
   csrc/sm120/tmix/wkv7/pretrain_recurrent_bf16_forward.cu:32-97
 * ``wkv7_cpu_f32`` — the same recurrence in float, OpenMP over
   (sequence, head): the CPU baseline that bench.py times.
+* ``albatross_dither`` / ``wkv7_fp16_state`` (numpy) — the FP16-state
+  contract: csrc/sm120/tmix/wkv7/recurrent_decay.cuh:36-46 and
+  tests/tmix/wkv7/test.py:88-149 (delta = fp16(w - 1 + dither(phase)), the
+  update S + S*delta + b*sa + k*v rounded to fp16 each token, y from the
+  rounded state, elapsed phase base per slot); pinned in
+  tests/test_oracle_fp16.py.
 
 How the oracle is pinned (tests/test_oracle.py): the retention against its
 closed form and limits; the recurrence against an explicit-matrix fp64 form
@@ -131,3 +137,53 @@ def wkv7_cpu_f32(r, logits, k, v, a, b, *, cu_seqlens, state_indices=None, state
 
 def cpu_threads() -> int:
     return int(_load().wkv7_cpu_max_threads())
+
+
+# ---------------------------------------------------------------------------
+# FP16-state ("Albatross") contract, numpy
+# ---------------------------------------------------------------------------
+def albatross_dither(phase):
+    """dither(phase) = int32(0x9E3779B9 * phase mod 2^32) * 2^-41 as float32
+    (recurrent_decay.cuh:36-40)."""
+    ph = np.asarray(phase, dtype=np.int64)
+    bits = (ph * 0x9E3779B9) & 0xFFFFFFFF
+    signed = np.where(bits >= 0x80000000, bits - 0x100000000, bits)
+    return (signed.astype(np.float32) * np.float32(2.0 ** -41)).astype(np.float32)
+
+
+def wkv7_fp16_state(r, logits, k, v, a, b, *, cu_seqlens, state_indices, state_pool,
+                    elapsed_state_pool, decay_bias=None, scale=1.0):
+    """FP16-state packed recurrence (tests/tmix/wkv7/test.py:88-149).
+
+    Token arrays ``[total, H, D]`` (fp16 values); ``state_pool`` fp16
+    ``[slots, H, D, D]``; ``elapsed_state_pool`` int ``[slots]``.  Arithmetic
+    in float32 with the contract's fp16 rounding points.  Returns
+    ``(y fp16, new_pool fp16, new_elapsed)``; the elapsed counts advance by
+    each sequence's length, as the native entry does after its kernel.
+    """
+    tok = [np.asarray(t, dtype=np.float32) for t in (r, logits, k, v, a, b)]
+    r_, x_, k_, v_, a_, b_ = tok
+    total, H, D = r_.shape
+    cu = _i32(cu_seqlens)
+    slots = _i32(state_indices)
+    pool = np.array(state_pool, dtype=np.float16)
+    elapsed = np.array(elapsed_state_pool, dtype=np.int64)
+    bias = None if decay_bias is None else np.asarray(decay_bias, dtype=np.float32).reshape(H, D)
+    y = np.zeros((total, H, D), dtype=np.float16)
+    hk = np.arange(H * D, dtype=np.int64).reshape(H, D)
+    for n in range(cu.size - 1):
+        slot = int(slots[n])
+        S = pool[slot].astype(np.float32)                      # [H, K, V]
+        base = int(elapsed[slot])
+        for t in range(int(cu[n]), int(cu[n + 1])):
+            x = x_[t] if bias is None else x_[t] + bias
+            w = np.exp(np.float32(-0.6065306597126334) / (1.0 + np.exp(-x))).astype(np.float32)
+            dither = albatross_dither(hk + base + (t - int(cu[n])))
+            delta = (w - np.float32(1.0) + dither).astype(np.float16).astype(np.float32)
+            sa = np.einsum("hk,hkv->hv", a_[t], S).astype(np.float32)
+            S = (S + S * delta[:, :, None] + b_[t][:, :, None] * sa[:, None, :]
+                 + k_[t][:, :, None] * v_[t][:, None, :]).astype(np.float16).astype(np.float32)
+            y[t] = (np.float32(scale) * np.einsum("hk,hkv->hv", r_[t], S)).astype(np.float16)
+        pool[slot] = S.astype(np.float16)
+        elapsed[slot] += int(cu[n + 1]) - int(cu[n])
+    return y, pool, elapsed.astype(np.int32)

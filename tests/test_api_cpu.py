@@ -19,6 +19,7 @@ from flashrwkv2_amd.tmix.wkv7 import (
 
 EXPECTED = {
     "infer_tmix_wkv7_chunk_bf16_forward_varlen",
+    "infer_tmix_wkv7_recurrent_fp16_forward_varlen",
     "infer_tmix_wkv7_recurrent_fp32io16_forward_varlen",
     "prepare_tmix_wkv7_recurrent_metadata",
     "pretrain_tmix_wkv7_recurrent_bf16",
@@ -100,3 +101,17 @@ def test_workload_distributions_follow_the_config_contract():
     w3 = workloads.config(3, "cpu", sequences=5, heads=2, max_len=50)
     lens = (w3.cu_seqlens[1:] - w3.cu_seqlens[:-1])
     assert (lens >= 1).all() and (lens <= 50).all()
+
+
+def test_fp16_public_signature_is_raw_only_and_has_no_elapsed_alias():
+    """Mirrors tests/tmix/wkv7/test.py:883-895 of the reference."""
+    import inspect
+
+    from flashrwkv2_amd.tmix.wkv7 import infer_tmix_wkv7_recurrent_fp16_forward_varlen as f
+
+    params = inspect.signature(f).parameters
+    for name in ("decay_logits", "state_pool", "elapsed_state_pool", "max_seqlen"):
+        assert name in params
+    for name in ("log_decay", "elapsed_t"):
+        assert name not in params
+    assert params["scale"].default == 1.0 and params["decay_bias"].default is None

@@ -1,0 +1,177 @@
+"""GPU tests of the FP16-state ("Albatross") packed recurrence,
+infer_tmix_wkv7_recurrent_fp16_forward_varlen, against the numpy oracle
+(oracle.wkv7_fp16_state) on the kernel's exact inputs.  Cases follow
+tests/tmix/wkv7/test.py:883-1100 of the reference (family correctness over
+head sizes and lengths, dispatch boundaries at H = 64, the metadata-ticket
+contract, the fp16-only checks); the gate is the reference's relative RMSE
+<= 4e-3 on outputs and active states (test.py:958-961), plus exact elapsed
+counts, untouched slots, fail-closed NaN output and split-call equality.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from wkv7_testlib import relative_rmse, require_gpu, to_np
+
+pytestmark = pytest.mark.gpu
+
+from flashrwkv2_amd.tmix.wkv7 import (  # noqa: E402
+    infer_tmix_wkv7_recurrent_fp16_forward_varlen as wkv7_fp16,
+    prepare_tmix_wkv7_recurrent_metadata,
+)
+
+import oracle  # noqa: E402
+
+NAMES = ("r", "decay_logits", "k", "v", "a", "b")
+GATE = 4.0e-3
+
+
+def make_case(*, head_size=64, lengths=(1, 2, 4), num_heads=2, with_decay_bias=True,
+              state_pool_slots=None, seed=77):
+    g = torch.Generator().manual_seed(seed + head_size + len(lengths))
+    total = sum(lengths)
+    n = len(lengths)
+    slots_n = state_pool_slots if state_pool_slots is not None else max(9, n)
+    shape = (total, num_heads, head_size)
+    scales = (0.12, 3.5, 0.06, 0.06, 0.06, 0.06)
+    case = {nm: (torch.randn(shape, generator=g) * s).half().cuda() for nm, s in zip(NAMES, scales)}
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    case["cu_seqlens"] = torch.tensor(offsets, dtype=torch.int32, device="cuda")
+    slots = (torch.tensor([5, 0, 7, 2, 4][:n], dtype=torch.int32) if n <= 5
+             else torch.arange(n, dtype=torch.int32))
+    case["state_indices"] = slots.cuda()
+    case["state_pool"] = (torch.randn((slots_n, num_heads, head_size, head_size), generator=g)
+                          * 0.03).half().cuda()
+    case["elapsed_state_pool"] = (torch.arange(slots_n, dtype=torch.int32) * 11).cuda()
+    case["decay_bias"] = ((torch.randn((num_heads, head_size), generator=g) * 0.2).half().cuda()
+                          if with_decay_bias else None)
+    return case
+
+
+def tokens(case):
+    return tuple(case[n] for n in NAMES)
+
+
+def expect(case, scale=1.0):
+    return oracle.wkv7_fp16_state(
+        *(to_np(t) for t in tokens(case)), cu_seqlens=case["cu_seqlens"].cpu().numpy(),
+        state_indices=case["state_indices"].cpu().numpy(),
+        state_pool=case["state_pool"].cpu().numpy(),
+        elapsed_state_pool=case["elapsed_state_pool"].cpu().numpy(),
+        decay_bias=None if case["decay_bias"] is None else to_np(case["decay_bias"]),
+        scale=scale)
+
+
+def run(case, *, scale=1.0, **kw):
+    state = case["state_pool"].clone()
+    elapsed = case["elapsed_state_pool"].clone()
+    out = wkv7_fp16(*tokens(case), state_pool=state, elapsed_state_pool=elapsed,
+                    cu_seqlens=case["cu_seqlens"], state_indices=case["state_indices"],
+                    scale=scale, decay_bias=case["decay_bias"], **kw)
+    torch.cuda.synchronize()
+    return out, state, elapsed
+
+
+def check_against_oracle(case, out, state, elapsed, scale=1.0):
+    y_ref, pool_ref, el_ref = expect(case, scale)
+    assert out.dtype == torch.float16 and state.dtype == torch.float16
+    assert torch.isfinite(out).all() and torch.isfinite(state).all()
+    assert relative_rmse(to_np(out), y_ref.astype(np.float64)) <= GATE
+    act = case["state_indices"].long().cpu().numpy()
+    got = to_np(state)
+    assert relative_rmse(got[act], pool_ref[act].astype(np.float64)) <= GATE
+    untouched = np.setdiff1d(np.arange(got.shape[0]), act)
+    assert np.array_equal(got[untouched], to_np(case["state_pool"])[untouched])
+    assert np.array_equal(elapsed.cpu().numpy(), el_ref)
+
+
+@pytest.mark.parametrize("head_size", (64, 128, 256))
+@pytest.mark.parametrize("lengths", ((1,), (1, 2, 4), (8, 8), (3, 40)))
+def test_fp16_state_family_correctness(head_size, lengths):
+    require_gpu()
+    print(f"case fp16-state D={head_size} lengths={lengths}", flush=True)
+    case = make_case(head_size=head_size, lengths=lengths)
+    out, state, elapsed = run(case, scale=0.75)
+    check_against_oracle(case, out, state, elapsed, scale=0.75)
+
+
+@pytest.mark.parametrize("lengths", ((1,), (1,) * 17, (1,) * 128, (2,) * 32, (8,), (4,) * 16))
+def test_fp16_state_grid_boundaries_at_64_heads(lengths):
+    require_gpu()
+    print(f"case fp16-state H=64 lengths={lengths[:3]}x{len(lengths)}", flush=True)
+    case = make_case(lengths=lengths, num_heads=64, state_pool_slots=max(9, len(lengths)))
+    out, state, elapsed = run(case)
+    check_against_oracle(case, out, state, elapsed)
+
+
+def test_fp16_state_ticket_contract_and_elapsed_advance():
+    require_gpu()
+    case = make_case(lengths=(2, 3))
+    ticket = prepare_tmix_wkv7_recurrent_metadata(
+        case["cu_seqlens"], case["state_indices"], total_tokens=case["r"].shape[0],
+        state_pool_size=case["state_pool"].shape[0])
+    out_a, st_a, el_a = run(case)
+    out_b, st_b, el_b = run(case, validated_metadata=ticket)
+    assert torch.equal(out_a, out_b) and torch.equal(st_a, st_b) and torch.equal(el_a, el_b)
+    case["cu_seqlens"][1] += 1
+    with pytest.raises(RuntimeError, match="version"):
+        run(case, validated_metadata=ticket)
+    case["cu_seqlens"][1] -= 1
+
+
+def test_fp16_state_split_calls_equal_one_call():
+    """Two calls with the elapsed count advanced in between reproduce one call
+    bitwise (the phase continues through elapsed_state_pool)."""
+    require_gpu()
+    case = make_case(lengths=(11,))
+    out, state, elapsed = run(case)
+    cut = 5
+    first = {k: (v[:cut] if k in NAMES else v) for k, v in case.items()}
+    first["cu_seqlens"] = torch.tensor([0, cut], dtype=torch.int32, device="cuda")
+    out1, st1, el1 = run(first)
+    second = {k: (v[cut:] if k in NAMES else v) for k, v in case.items()}
+    second["cu_seqlens"] = torch.tensor([0, 11 - cut], dtype=torch.int32, device="cuda")
+    second["state_pool"], second["elapsed_state_pool"] = st1, el1
+    out2, st2, el2 = run(second)
+    assert torch.equal(torch.cat([out1, out2]), out)
+    assert torch.equal(st2, state) and torch.equal(el2, elapsed)
+
+
+def test_fp16_state_invalid_metadata_fails_closed():
+    """Duplicate slots reach the device validation through the _C entry with
+    implicit metadata (the public wrapper's ticket rejects them on the host):
+    the output is NaN and neither the pool nor the elapsed counts change."""
+    C = require_gpu()
+    case = make_case(lengths=(2, 3))
+    slots = torch.tensor([1, 1], dtype=torch.int32, device="cuda")
+    state = case["state_pool"].clone()
+    elapsed = case["elapsed_state_pool"].clone()
+    out = torch.empty_like(case["v"])
+    C.tmix_wkv7_recurrent_fp16_from_decay_logits(
+        case["cu_seqlens"], slots, elapsed, state, *tokens(case), out, 1.0,
+        case["decay_bias"], None, -1)
+    torch.cuda.synchronize()
+    assert torch.isnan(out).all()
+    assert torch.equal(state, case["state_pool"])
+    assert torch.equal(elapsed, case["elapsed_state_pool"])
+
+
+def test_fp16_state_rejects_non_fp16_state_and_tokens():
+    require_gpu()
+    case = make_case(lengths=(2,))
+    with pytest.raises(TypeError, match="FP16-state state_pool"):
+        wkv7_fp16(*tokens(case), state_pool=case["state_pool"].float(),
+                  elapsed_state_pool=case["elapsed_state_pool"],
+                  cu_seqlens=case["cu_seqlens"], state_indices=case["state_indices"])
+    toks = tokens(case)
+    with pytest.raises((TypeError, RuntimeError), match="float16"):
+        wkv7_fp16(toks[0].bfloat16(), *toks[1:], state_pool=case["state_pool"],
+                  elapsed_state_pool=case["elapsed_state_pool"],
+                  cu_seqlens=case["cu_seqlens"], state_indices=case["state_indices"])
+    with pytest.raises(TypeError, match="int32"):
+        wkv7_fp16(*toks, state_pool=case["state_pool"],
+                  elapsed_state_pool=case["elapsed_state_pool"].long(),
+                  cu_seqlens=case["cu_seqlens"], state_indices=case["state_indices"])

@@ -1,0 +1,112 @@
+"""Pins the numpy FP16-state ("Albatross") oracle, oracle.wkv7_fp16_state.
+
+* dither: the constants are the golden-ratio multiplicative hash
+  0x9E3779B9 = floor(2^32 / phi) and 2^-41, the hash value is read as a
+  signed 32-bit integer (so the dither is centred, within (-2^-10, 2^-10)),
+  and phase 0 has no dither;
+* update structure: against the independent fp64 recurrence of the fp32
+  contract (oracle.wkv7_f64) the FP16 state differs only by the fp16 rounding
+  and the dither, so a wrong pre/post-update state, bias or scale placement
+  fails the bound;
+* the elapsed phase: running a sequence in two calls (the count advanced in
+  between) reproduces the single call exactly, and a shifted elapsed count
+  changes the result;
+* untouched slots and counts stay bitwise unchanged.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+import oracle
+
+
+def _case(lengths=(3, 7, 5), H=2, D=64, seed=5, slots=(4, 0, 2), pool_slots=6):
+    g = np.random.default_rng(seed)
+    total = sum(lengths)
+    shape = (total, H, D)
+    scales = (0.12, 3.5, 0.06, 0.06, 0.06, 0.06)
+    tok = [(g.standard_normal(shape) * s).astype(np.float16) for s in scales]
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    pool = (g.standard_normal((pool_slots, H, D, D)) * 0.03).astype(np.float16)
+    elapsed = (np.arange(pool_slots) * 11).astype(np.int32)
+    bias = (g.standard_normal((H, D)) * 0.2).astype(np.float16)
+    return tok, cu, np.asarray(slots, np.int32), pool, elapsed, bias
+
+
+def test_dither_constants_and_distribution():
+    phi = (1 + math.sqrt(5)) / 2
+    assert 0x9E3779B9 == int(2 ** 32 / phi)
+    assert np.float32(4.547473508864641e-13) == np.float32(2.0 ** -41)
+    assert oracle.albatross_dither(0) == 0.0
+    # phase 1: the hash 0x9E3779B9 read as int32 is 0x9E3779B9 - 2^32 < 0
+    assert oracle.albatross_dither(1) == np.float32((0x9E3779B9 - 2 ** 32) * 2.0 ** -41)
+    d = oracle.albatross_dither(np.arange(200_000))
+    assert np.abs(d).max() < 2.0 ** -10
+    assert abs(float(d.mean())) < 2e-6           # signed: centred on zero
+    assert (d > 0).mean() > 0.45 and (d < 0).mean() > 0.45
+
+
+def test_fp16_state_tracks_the_fp64_recurrence():
+    tok, cu, slots, pool, elapsed, bias = _case()
+    y16, pool16, _ = oracle.wkv7_fp16_state(*tok, cu_seqlens=cu, state_indices=slots,
+                                            state_pool=pool, elapsed_state_pool=elapsed,
+                                            decay_bias=bias, scale=0.75)
+    y64, pool64, _, _ = oracle.wkv7_f64(*tok, cu_seqlens=cu, state_indices=slots,
+                                        state_pool=pool.astype(np.float64), decay_bias=bias,
+                                        scale=0.75)
+    rel = np.linalg.norm(y16.astype(np.float64) - y64) / np.linalg.norm(y64)
+    assert rel < 1e-2, rel
+    act = slots.astype(np.int64)
+    srel = np.linalg.norm(pool16[act].astype(np.float64) - pool64[act]) / np.linalg.norm(pool64[act])
+    assert srel < 1e-2, srel
+    # with y taken from the pre-update state (a wrong contract) the error is far larger
+    wrong = np.zeros_like(y64)
+    for n in range(cu.size - 1):
+        S = pool[slots[n]].astype(np.float64)
+        for t in range(cu[n], cu[n + 1]):
+            wrong[t] = 0.75 * np.einsum("hk,hkv->hv", tok[0][t].astype(np.float64), S)
+            y_t, S_pool, _, _ = oracle.wkv7_f64(*(x[t:t + 1] for x in tok),
+                                                cu_seqlens=np.array([0, 1], np.int32),
+                                                state_indices=np.array([0], np.int32),
+                                                state_pool=S[None], decay_bias=bias)
+            S = S_pool[0]
+    assert np.linalg.norm(wrong - y64) / np.linalg.norm(y64) > 10 * rel
+
+
+def test_split_calls_with_advanced_elapsed_reproduce_one_call():
+    tok, cu, slots, pool, elapsed, bias = _case(lengths=(9,), slots=(3,))
+    y, p1, e1 = oracle.wkv7_fp16_state(*tok, cu_seqlens=cu, state_indices=slots,
+                                       state_pool=pool, elapsed_state_pool=elapsed,
+                                       decay_bias=bias)
+    assert e1[3] == elapsed[3] + 9
+    assert np.array_equal(np.delete(e1, 3), np.delete(elapsed, 3))
+    cut = 4
+    ya, pa, ea = oracle.wkv7_fp16_state(*(t[:cut] for t in tok),
+                                        cu_seqlens=np.array([0, cut], np.int32),
+                                        state_indices=slots, state_pool=pool,
+                                        elapsed_state_pool=elapsed, decay_bias=bias)
+    yb, pb, eb = oracle.wkv7_fp16_state(*(t[cut:] for t in tok),
+                                        cu_seqlens=np.array([0, 9 - cut], np.int32),
+                                        state_indices=slots, state_pool=pa,
+                                        elapsed_state_pool=ea, decay_bias=bias)
+    assert np.array_equal(np.concatenate([ya, yb]), y)
+    assert np.array_equal(pb, p1)
+    assert np.array_equal(eb, e1)
+    # the phase matters: a different elapsed count changes the state
+    _, p_shift, _ = oracle.wkv7_fp16_state(*tok, cu_seqlens=cu, state_indices=slots,
+                                           state_pool=pool, elapsed_state_pool=elapsed + 1,
+                                           decay_bias=bias)
+    assert not np.array_equal(p_shift, p1)
+
+
+def test_untouched_slots_and_counts():
+    tok, cu, slots, pool, elapsed, bias = _case()
+    _, p, e = oracle.wkv7_fp16_state(*tok, cu_seqlens=cu, state_indices=slots,
+                                     state_pool=pool, elapsed_state_pool=elapsed)
+    untouched = np.setdiff1d(np.arange(pool.shape[0]), slots)
+    assert np.array_equal(p[untouched], pool[untouched])
+    assert np.array_equal(e[untouched], elapsed[untouched])
+    assert np.array_equal(e[slots], elapsed[slots] + np.diff(cu))
