@@ -126,7 +126,7 @@ class Runner:
     def kernel_name(self) -> str:
         ms = self.ticket._max_seqlen()
         if ms <= 4:
-            return "decode64_kernel<IoBF16>"
+            return "decode64_kernel<IoBF16,StF32>"
         if ms >= 128:
             return "chunk64_kernel<IoBF16>"
         return "serial_kernel<64,IoBF16,StF32>"
@@ -178,6 +178,56 @@ def roofline_obj(bytes_per_launch: int, kernel_ms: float, traffic=None):
     achieved = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+
+
+def time_fp16_state_decode(torch, flashrwkv2_amd, w, steps: int, warmup: int):
+    """Per-step and per-launch times (ms) of the FP16-state recurrence on a
+    decode workload: public entry with a reused ticket, then direct C-ABI
+    launches between HIP events on the launch stream."""
+    from flashrwkv2_amd import _native as N
+
+    state = w.state_pool.half().contiguous()
+    state0 = state.clone()
+    elapsed = torch.zeros(state.shape[0], dtype=torch.int32, device=state.device)
+    out = torch.empty_like(w.v)
+    ticket = flashrwkv2_amd.prepare_tmix_wkv7_recurrent_metadata(
+        w.cu_seqlens, w.state_indices, total_tokens=w.total_tokens,
+        state_pool_size=state.shape[0])
+    C = flashrwkv2_amd._C
+
+    def step():
+        C.tmix_wkv7_recurrent_fp16_from_decay_logits(
+            w.cu_seqlens, w.state_indices, elapsed, state, *w.tokens, out, 1.0, None, ticket)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    state.copy_(state0)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = max(start.elapsed_time(end), (time.perf_counter() - t0) * 1e3) / steps
+    lib = N.load()
+    stream = torch.cuda.current_stream()
+    args = (ticket._query_start_loc_snapshot().data_ptr(), ticket._state_indices_snapshot().data_ptr(),
+            ticket._status().data_ptr(), elapsed.data_ptr(), w.state_indices.numel(), w.num_heads,
+            64, w.total_tokens, ticket._max_seqlen(), state.data_ptr(),
+            *(t.data_ptr() for t in w.tokens[:2]), None, *(t.data_ptr() for t in w.tokens[2:]),
+            out.data_ptr(), 1.0, stream.cuda_stream)
+    state.copy_(state0)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps * 4):
+        rc = lib.fr2_wkv7_recurrent_fp16_forward(*args)
+        if rc:
+            N.check(rc, "fr2_wkv7_recurrent_fp16_forward")
+    end.record(stream)
+    torch.cuda.synchronize()
+    return ms, start.elapsed_time(end) / (steps * 4)
 
 
 def mfma_obj(w, kernel_ms: float):
@@ -277,6 +327,18 @@ def main() -> int:
             "kernel": dec.kernel_name(),
             "roofline": roofline_obj(bytes2, dkms, measured_traffic(dec.kernel_name(), w2.name)),
             "algorithmic_bytes": bytes2,
+        }
+        # the same decode shape with fp16 tokens and the FP16 state pool
+        # (8 KiB per (sequence, head)): infer_tmix_wkv7_recurrent_fp16_forward_varlen
+        w3 = workloads.config(2, "cuda", dtype=torch.float16)
+        f16_ms, f16_kms = time_fp16_state_decode(torch, flashrwkv2_amd, w3, max(args.steps, 50),
+                                                 args.warmup)
+        bytes3 = w3.total_tokens * w3.num_heads * BYTES_PER_TOKEN_HEAD + 2 * w3.state_indices.numel() * w3.num_heads * 64 * 64 * 2
+        result["decode_fp16_state"] = {
+            "workload": w3.name + "_fp16_state", "tokens_per_s": round(w3.total_tokens / (f16_ms * 1e-3), 1),
+            "ms_per_step": round(f16_ms, 5), "kernel_ms": round(f16_kms, 5),
+            "kernel": "decode64_kernel<IoF16,StF16>",
+            "roofline": roofline_obj(bytes3, f16_kms), "algorithmic_bytes": bytes3,
         }
         if not result.get("metric"):
             result.update({"metric": METRIC, "value": result["decode"]["tokens_per_s"],

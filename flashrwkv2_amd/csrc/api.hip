@@ -110,7 +110,6 @@ extern "C" int fr2_wkv7_recurrent_fp16_forward(
     void* state_f16, const void* r, const void* decay_logits, const void* decay_bias,
     const void* k, const void* v, const void* a, const void* b, void* output, float scale,
     void* stream) {
-  (void)max_seqlen;
   if (!query_start_loc || !state_indices || !status || !elapsed_state || !state_f16 ||
       !tokens_ok(r, decay_logits, k, v, a, b, output))
     return FR2_ERR_INVALID_ARGUMENT;
@@ -128,7 +127,7 @@ extern "C" int fr2_wkv7_recurrent_fp16_forward(
   p.r = r; p.logits = decay_logits; p.bias = decay_bias; p.k = k; p.v = v; p.a = a; p.b = b;
   p.y = output;
   p.scale = scale;
-  return fr2::launch_fp16_state(head_size, p, num_sequences, elapsed_state,
+  return fr2::launch_fp16_state(head_size, p, num_sequences, max_seqlen, elapsed_state,
                                 static_cast<hipStream_t>(stream));
 }
 

@@ -232,8 +232,13 @@ __device__ __forceinline__ f4 shfl_xor4(f4 x, int m) {
             __shfl_xor(x.w, m)};
 }
 
-template <class Io>
+// St = StF16: FP16 state pool with the Albatross delta update (see
+// serial_kernel); the staged retention becomes delta and each updated value
+// is rounded to fp16 before it feeds y and the store.
+template <class Io, class St>
 __global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
+  constexpr bool kAlbatross = __is_same(St, StF16);
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
   using raw = typename Io::raw;
   constexpr int D = 64;
   __shared__ __attribute__((aligned(16))) float s_in[6][D];
@@ -252,11 +257,18 @@ __global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
   const int rq = lane >> 4;
   const int64_t sbase = (static_cast<int64_t>(slot) * H + h) * D * D;
   f4 S[16];
+  const int elapsed_base = (kAlbatross && p.elapsed != nullptr) ? p.elapsed[slot] : 0;
   if (p.state_in != nullptr) {
-    const float* sin = static_cast<const float*>(p.state_in) + sbase + rq * D + 4 * c4;
+    const typename St::raw* sin =
+        static_cast<const typename St::raw*>(p.state_in) + sbase + rq * D + 4 * c4;
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
-      S[j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(sin + 4 * j * D));
+    for (int j = 0; j < 16; ++j) {
+      if constexpr (kAlbatross)
+        S[j] = __builtin_convertvector(
+            __builtin_nontemporal_load(reinterpret_cast<const h4*>(sin + 4 * j * D)), f4);
+      else
+        S[j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(sin + 4 * j * D));
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < 16; ++j) S[j] = f4{0.f, 0.f, 0.f, 0.f};
@@ -277,7 +289,10 @@ __global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
     float x = Io::to_f32(lp[base + lane]);
     if (bias != nullptr) x += Io::to_f32(bias[h * D + lane]);
     s_in[0][pk] = Io::to_f32(rp[base + lane]);
-    s_in[1][pk] = retention_from_logit(x);
+    if constexpr (kAlbatross)
+      s_in[1][pk] = albatross_delta(x, elapsed_base + h * D + lane + (t - t0));
+    else
+      s_in[1][pk] = retention_from_logit(x);
     s_in[2][pk] = Io::to_f32(kp[base + lane]);
     s_in[3][lane] = Io::to_f32(vp[base + lane]);
     s_in[4][pk] = Io::to_f32(ap[base + lane]);
@@ -308,10 +323,20 @@ __global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const float wj = Wr[j], bj = Br[j], kj = Kr[j], rj = Rr[j];
-      S[j].x = fmaf(wj, S[j].x, fmaf(bj, sa.x, kj * vv.x));
-      S[j].y = fmaf(wj, S[j].y, fmaf(bj, sa.y, kj * vv.y));
-      S[j].z = fmaf(wj, S[j].z, fmaf(bj, sa.z, kj * vv.z));
-      S[j].w = fmaf(wj, S[j].w, fmaf(bj, sa.w, kj * vv.w));
+      if constexpr (kAlbatross) {
+        // wj holds delta: fp16(S + S*delta + b*sa + k*v)
+        f4 u;
+        u.x = fmaf(kj, vv.x, fmaf(bj, sa.x, fmaf(S[j].x, wj, S[j].x)));
+        u.y = fmaf(kj, vv.y, fmaf(bj, sa.y, fmaf(S[j].y, wj, S[j].y)));
+        u.z = fmaf(kj, vv.z, fmaf(bj, sa.z, fmaf(S[j].z, wj, S[j].z)));
+        u.w = fmaf(kj, vv.w, fmaf(bj, sa.w, fmaf(S[j].w, wj, S[j].w)));
+        S[j] = __builtin_convertvector(__builtin_convertvector(u, h4), f4);
+      } else {
+        S[j].x = fmaf(wj, S[j].x, fmaf(bj, sa.x, kj * vv.x));
+        S[j].y = fmaf(wj, S[j].y, fmaf(bj, sa.y, kj * vv.y));
+        S[j].z = fmaf(wj, S[j].z, fmaf(bj, sa.z, kj * vv.z));
+        S[j].w = fmaf(wj, S[j].w, fmaf(bj, sa.w, kj * vv.w));
+      }
       yy.x = fmaf(rj, S[j].x, yy.x);
       yy.y = fmaf(rj, S[j].y, yy.y);
       yy.z = fmaf(rj, S[j].z, yy.z);
@@ -332,10 +357,15 @@ __global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
   }
 
   if (p.state_out != nullptr) {
-    float* sout = static_cast<float*>(p.state_out) + sbase + rq * D + 4 * c4;
+    typename St::raw* sout =
+        static_cast<typename St::raw*>(p.state_out) + sbase + rq * D + 4 * c4;
 #pragma unroll
     for (int j = 0; j < 16; ++j)
-      __builtin_nontemporal_store(S[j], reinterpret_cast<f4*>(sout + 4 * j * D));
+      if constexpr (kAlbatross)
+        __builtin_nontemporal_store(__builtin_convertvector(S[j], h4),
+                                    reinterpret_cast<h4*>(sout + 4 * j * D));
+      else
+        __builtin_nontemporal_store(S[j], reinterpret_cast<f4*>(sout + 4 * j * D));
   }
 }
 
@@ -375,13 +405,24 @@ __global__ __launch_bounds__(256) void advance_elapsed_kernel(SegArgs p, int nse
   elapsed[slot] += t1 - t0;
 }
 
-int launch_fp16_state(int D, const SegArgs& p, int nseg, int32_t* elapsed, hipStream_t s) {
+// requests with at most this many tokens per sequence stream the state once
+constexpr int kFp16DecodeMaxSeqlen = 4;
+
+int launch_fp16_state(int D, const SegArgs& p, int nseg, int max_seqlen, int32_t* elapsed,
+                      hipStream_t s) {
   if (elapsed == nullptr || p.sa_out != nullptr || p.boundary != nullptr)
     return FR2_ERR_INVALID_ARGUMENT;
   SegArgs q = p;
   q.elapsed = elapsed;
-  const int rc = launch_serial_io<IoF16, StF16>(D, q, nseg, s);
-  if (rc != FR2_OK) return rc;
+  if (D == 64 && max_seqlen > 0 && max_seqlen <= kFp16DecodeMaxSeqlen) {
+    hipLaunchKernelGGL((decode64_kernel<IoF16, StF16>), dim3(p.num_heads, nseg), dim3(64), 0,
+                       s, q);
+    const int rc = record_launch();
+    if (rc != FR2_OK) return rc;
+  } else {
+    const int rc = launch_serial_io<IoF16, StF16>(D, q, nseg, s);
+    if (rc != FR2_OK) return rc;
+  }
   hipLaunchKernelGGL(advance_elapsed_kernel, dim3((nseg + 255) / 256), dim3(256), 0, s, q, nseg,
                      elapsed);
   return record_launch();
@@ -402,9 +443,9 @@ int launch_decode(int D, int dtype, const SegArgs& p, int nseg, hipStream_t s) {
   if (D != 64 || p.sa_out != nullptr || p.boundary != nullptr) return FR2_ERR_UNSUPPORTED;
   const dim3 grid(p.num_heads, nseg);
   if (dtype == FR2_DTYPE_BFLOAT16)
-    hipLaunchKernelGGL((decode64_kernel<IoBF16>), grid, dim3(64), 0, s, p);
+    hipLaunchKernelGGL((decode64_kernel<IoBF16, StF32>), grid, dim3(64), 0, s, p);
   else if (dtype == FR2_DTYPE_FLOAT16)
-    hipLaunchKernelGGL((decode64_kernel<IoF16>), grid, dim3(64), 0, s, p);
+    hipLaunchKernelGGL((decode64_kernel<IoF16, StF32>), grid, dim3(64), 0, s, p);
   else
     return FR2_ERR_UNSUPPORTED;
   return record_launch();

@@ -175,3 +175,39 @@ def test_fp16_state_rejects_non_fp16_state_and_tokens():
         wkv7_fp16(*toks, state_pool=case["state_pool"],
                   elapsed_state_pool=case["elapsed_state_pool"].long(),
                   cu_seqlens=case["cu_seqlens"], state_indices=case["state_indices"])
+
+
+def test_fp16_state_decode_and_serial_paths_agree():
+    """max_seqlen <= 4 at D = 64 selects the state-streaming decode kernel;
+    an unknown max_seqlen selects the token-serial kernel.  They reduce the
+    a^T S and r^T S dot products in different orders (so an fp16 rounding can
+    differ by one unit), and each meets the oracle gate."""
+    require_gpu()
+    from flashrwkv2_amd import _native as N
+
+    case = make_case(lengths=(1, 2, 4, 3), num_heads=8)
+    lib = N.load()
+    results = []
+    for max_seqlen in (4, -1):
+        state = case["state_pool"].clone()
+        elapsed = case["elapsed_state_pool"].clone()
+        out = torch.empty_like(case["v"])
+        ticket = prepare_tmix_wkv7_recurrent_metadata(
+            case["cu_seqlens"], case["state_indices"], total_tokens=out.shape[0],
+            state_pool_size=state.shape[0])
+        rc = lib.fr2_wkv7_recurrent_fp16_forward(
+            ticket._query_start_loc_snapshot().data_ptr(),
+            ticket._state_indices_snapshot().data_ptr(), ticket._status().data_ptr(),
+            elapsed.data_ptr(), case["state_indices"].numel(), 8, 64, out.shape[0], max_seqlen,
+            state.data_ptr(), *(t.data_ptr() for t in tokens(case)[:2]),
+            case["decay_bias"].data_ptr(), *(t.data_ptr() for t in tokens(case)[2:]),
+            out.data_ptr(), 1.0, torch.cuda.current_stream().cuda_stream)
+        N.check(rc, "fr2_wkv7_recurrent_fp16_forward")
+        torch.cuda.synchronize()
+        results.append((out, state, elapsed))
+    (o1, s1, e1), (o2, s2, e2) = results
+    assert torch.equal(e1, e2)
+    assert relative_rmse(to_np(o1), to_np(o2)) <= 1e-3
+    assert relative_rmse(to_np(s1), to_np(s2)) <= 1e-3
+    check_against_oracle(case, o1, s1, e1)
+    check_against_oracle(case, o2, s2, e2)
