@@ -470,14 +470,44 @@ def pretrain_tmix_wkv7_recurrent_forward(r, w, k, v, a, b, output, boundary, sta
     N.check(rc, "pretrain_tmix_wkv7_recurrent_forward")
 
 
-def pretrain_tmix_wkv7_recurrent_backward(*args, **kwargs):
-    """Training backward (pretrain_recurrent_bf16_forward.cu:163-486) is not
-    part of this operator build; the forward's boundary and state_dot_a
-    checkpoints are produced so that it can be added."""
-    raise NotImplementedError(
-        "flashrwkv2_amd implements the WKV7 forward path only; "
-        "pretrain_tmix_wkv7_recurrent_backward is not available"
-    )
+def pretrain_tmix_wkv7_recurrent_backward(r, w, k, v, a, b, grad_output, boundary,
+                                          state_dot_a, grad_r, grad_w, grad_k, grad_v,
+                                          grad_a, grad_b, head_size):
+    """pretrain_recurrent_bf16_forward.cpp:29-46 (backward over bf16 [B,T,H,N]).
+
+    Fills the six bf16 gradient tensors in place.  The fp32 [B,T,H,N]
+    workspace that carries d(sa) between the two kernels is allocated here
+    (the reference allocates the same buffer for its N=256 path).
+    """
+    _check(head_size in (64, 128, 256), "head_size must be one of 64, 128, or 256")
+    _check(r.size(3) == head_size, "input head dimension must equal head_size")
+    B, T, H, _ = r.shape
+    tensors = ((r, "r"), (w, "w"), (k, "k"), (v, "v"), (a, "a"), (b, "b"),
+               (grad_output, "grad_output"), (boundary, "boundary"),
+               (state_dot_a, "state_dot_a"), (grad_r, "grad_r"), (grad_w, "grad_w"),
+               (grad_k, "grad_k"), (grad_v, "grad_v"), (grad_a, "grad_a"), (grad_b, "grad_b"))
+    for t, name in tensors:
+        check_cuda_contiguous(t, name)
+        check_same_device(r, t, name)
+    bf16 = (r, w, k, v, a, b, grad_output, grad_r, grad_w, grad_k, grad_v, grad_a, grad_b)
+    _check(all(t.dtype == torch.bfloat16 for t in bf16),
+           "pretrain token tensors and gradients must be bfloat16")
+    _check(all(t.shape == r.shape for t in bf16),
+           "pretrain token tensors must share shape [B,T,H,N]")
+    _check(T % 16 == 0, "T must be divisible by the canonical chunk length 16")
+    _check(tuple(boundary.shape) == (B, H, T // 16, head_size, head_size)
+           and boundary.dtype == torch.float32, "boundary must be float32 [B,H,T/16,N,N]")
+    _check(state_dot_a.shape == r.shape and state_dot_a.dtype == torch.float32,
+           "state_dot_a must be float32 [B,T,H,N]")
+    workspace = torch.empty(r.shape, device=r.device, dtype=torch.float32)
+    with torch.cuda.device(r.device):
+        rc = N.load().fr2_wkv7_pretrain_backward(
+            B, T, H, head_size, r.data_ptr(), w.data_ptr(), k.data_ptr(), v.data_ptr(),
+            a.data_ptr(), b.data_ptr(), grad_output.data_ptr(), boundary.data_ptr(),
+            state_dot_a.data_ptr(), workspace.data_ptr(), grad_r.data_ptr(),
+            grad_w.data_ptr(), grad_k.data_ptr(), grad_v.data_ptr(), grad_a.data_ptr(),
+            grad_b.data_ptr(), _stream(r.device))
+    N.check(rc, "pretrain_tmix_wkv7_recurrent_backward")
 
 
 # ---------------------------------------------------------------------------

@@ -64,6 +64,10 @@ SIGNATURES: dict[str, tuple] = {
         [c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
     ),
+    "fr2_wkv7_pretrain_backward": (
+        c_int32,
+        [c_int32, c_int32, c_int32, c_int32] + [c_void_p] * 17,
+    ),
     "fr2_wkv7_chunk_bf16_forward": (
         c_int32,
         [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int64, c_int32,

@@ -157,6 +157,27 @@ extern "C" int fr2_wkv7_pretrain_forward(int32_t batch, int32_t tokens,
                             static_cast<hipStream_t>(stream));
 }
 
+extern "C" int fr2_wkv7_pretrain_backward(
+    int32_t batch, int32_t tokens, int32_t num_heads, int32_t head_size, const void* r,
+    const void* w, const void* k, const void* v, const void* a, const void* b,
+    const void* grad_output, const float* boundary, const float* state_dot_a,
+    float* workspace, void* grad_r, void* grad_w, void* grad_k, void* grad_v,
+    void* grad_a, void* grad_b, void* stream) {
+  if (!r || !w || !k || !v || !a || !b || !grad_output || !boundary || !state_dot_a ||
+      !workspace || !grad_r || !grad_w || !grad_k || !grad_v || !grad_a || !grad_b)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (batch <= 0 || tokens <= 0 || tokens % 16 != 0 || num_heads <= 0 ||
+      static_cast<int64_t>(batch) * num_heads > (int64_t{1} << 30) / 4)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return FR2_ERR_UNSUPPORTED;
+  fr2::PretrainBwdArgs p;
+  p.batch = batch; p.tokens = tokens; p.heads = num_heads;
+  p.r = r; p.w = w; p.k = k; p.v = v; p.a = a; p.b = b; p.dy = grad_output;
+  p.boundary = boundary; p.state_dot_a = state_dot_a; p.workspace = workspace;
+  p.dr = grad_r; p.dw = grad_w; p.dk = grad_k; p.dv = grad_v; p.da = grad_a; p.db = grad_b;
+  return fr2::launch_pretrain_backward(head_size, p, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int fr2_wkv7_chunk_bf16_forward(
     const int32_t* query_start_loc, const int32_t* state_indices,
     const int32_t* status, int32_t num_sequences, int32_t num_heads,

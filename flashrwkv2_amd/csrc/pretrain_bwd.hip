@@ -1,0 +1,421 @@
+// Training backward of the [B,T,H,D] zero-state WKV7 recurrence (the
+// pretrain path).  Replaces backward_kernel_preload / backward_kernel_split64
+// / backward_value_columns + backward_key_rows
+// (csrc/sm120/tmix/wkv7/pretrain_recurrent_bf16_forward.cu:163-486) with a
+// two-kernel design of its own.
+//
+// With P_t = dL/dS_t (S_t the post-update state, [key][value]) the backward
+// is
+//   P_t   = r_t dy_t^T + (diag(w_{t+1}) + a_{t+1} b_{t+1}^T) P_{t+1}
+//   dsa_t = P_t^T b_t,   dv_t = P_t^T k_t                  (value columns)
+//   dr_t  = S_t dy_t,    dk_t = P_t v_t,   db_t = P_t sa_t,
+//   da_t  = S_{t-1} dsa_t,   dw_t = rowsum(P_t o S_{t-1}) * dw/dlogit (key rows)
+// and S_{t-1} = (S_t - k_t v_t^T - b_t sa_t^T) / w_t rebuilds the pre-update
+// state from the forward's post-chunk snapshot (boundary) and its saved sa.
+//
+// The only quantity that couples key rows is dsa, a column reduction of P
+// that feeds back into P's next step.  So:
+//   1. value_kernel: one workgroup per (batch, head) runs the column
+//      recurrence of P (4 lanes per value column, D/4 keys each, DPP quad
+//      reductions) backwards over T and writes dv and dsa;
+//   2. key_kernel: rows are then independent; each workgroup owns 64 key rows
+//      of one (batch, head) (4 lanes per row, D/4 values each) and walks T
+//      backwards carrying its rows of S and P, writing dr, dw, dk, db, da.
+// Token operands are staged through LDS as fp32, one tile of TT tokens at a
+// time, double-buffered with the next tile's global loads in flight.  The
+// key kernel keeps S and P row-scaled (S = g Sh, P = hs Ph, g and hs per-row
+// scalars) so the 1/w and w factors cost two multiplies per row instead of
+// one per element; both scales restart at every 16-token boundary snapshot.
+#include "recurrent.h"
+
+namespace fr2 {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kChunk = 16;                       // boundary snapshot period
+constexpr float kWScale = -0.6065306597126334f;  // -exp(-1/2)
+
+// sum over the 4 lanes of a DPP quad (result in every lane of the quad)
+__device__ __forceinline__ float quad_sum(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, false));
+  return x;
+}
+
+__device__ __forceinline__ void widen8(u32x4 u, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(u[i] << 16);
+    f[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+  }
+}
+
+template <int D>
+struct Cfg {
+  static constexpr int E = D / 4;                 // elements per lane
+  static constexpr int TT = D <= 128 ? 16 : 8;    // tokens per LDS tile
+  static constexpr int DP = D + 16;               // padded LDS row
+  // lane quarter q reads elements [q*E, q*E+E) at q*(E+4): the four quarters
+  // start on distinct bank groups, so a b128 read with four distinct
+  // addresses per wave does not conflict.
+  static __device__ __forceinline__ int pos(int j) { return j + 4 * (j / E); }
+};
+
+__device__ __forceinline__ void store8(float* dst, const float* f) {
+  *reinterpret_cast<float4*>(dst) = make_float4(f[0], f[1], f[2], f[3]);
+  *reinterpret_cast<float4*>(dst + 4) = make_float4(f[4], f[5], f[6], f[7]);
+}
+
+// ---------------------------------------------------------------------------
+// 1. value columns: P^T recurrence, dv and dsa
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(4 * D) void value_kernel(
+    int T, int H, const uint16_t* __restrict__ r, const uint16_t* __restrict__ wl,
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ a,
+    const uint16_t* __restrict__ b, const uint16_t* __restrict__ dy,
+    uint16_t* __restrict__ dv, float* __restrict__ dsa) {
+  using C = Cfg<D>;
+  constexpr int NT = 4 * D, E = C::E, TT = C::TT, DP = C::DP;
+  constexpr int kVec = 6;                    // r, w, k, a, b, dy
+  constexpr int UPV = TT * D / 8;            // 16-byte units per vector per tile
+  constexpr int NU = kVec * UPV;
+  constexpr int UPT = (NU + NT - 1) / NT;
+  __shared__ __align__(16) float buf[2][kVec][TT][DP];
+
+  const int bidx = blockIdx.x / H, h = blockIdx.x % H;
+  const int tid = threadIdx.x, c = tid >> 2, q = tid & 3;
+  const int64_t stride = static_cast<int64_t>(H) * D;
+  const int64_t base = (static_cast<int64_t>(bidx) * T * H + h) * D;
+
+  u32x4 pre[UPT];
+  auto load_tile = [&](int t0) {
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int idx = tid + u * NT;
+      if (NU % NT == 0 || idx < NU) {
+        const int m = idx / UPV, rem = idx % UPV;
+        const int tt = rem / (D / 8), g = rem % (D / 8);
+        const uint16_t* src = m == 0 ? r : m == 1 ? wl : m == 2 ? k : m == 3 ? a : m == 4 ? b : dy;
+        pre[u] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(src + base + (t0 + tt) * stride + 8 * g));
+      }
+    }
+  };
+  auto store_tile = [&](int slot) {
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int idx = tid + u * NT;
+      if (NU % NT == 0 || idx < NU) {
+        const int m = idx / UPV, rem = idx % UPV;
+        const int tt = rem / (D / 8), g = rem % (D / 8);
+        float f[8];
+        widen8(pre[u], f);
+        if (m == 1) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) f[i] = retention_from_logit(f[i]);
+        }
+        store8(&buf[slot][m][tt][C::pos(8 * g)], f);
+      }
+    }
+  };
+
+  float P[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) P[e] = 0.0f;
+
+  const int ntile = T / TT;
+  load_tile((ntile - 1) * TT);
+  store_tile(0);
+  __syncthreads();
+  const int qo = q * (E + 4), co = C::pos(c);
+  for (int it = ntile - 1; it >= 0; --it) {
+    const int slot = (ntile - 1 - it) & 1;
+    if (it > 0) load_tile((it - 1) * TT);
+    for (int tt = TT - 1; tt >= 0; --tt) {
+      const float* R = &buf[slot][0][tt][qo];
+      const float* W = &buf[slot][1][tt][qo];
+      const float* K = &buf[slot][2][tt][qo];
+      const float* A = &buf[slot][3][tt][qo];
+      const float* Bv = &buf[slot][4][tt][qo];
+      const float dyc = buf[slot][5][tt][co];
+      float dv0 = 0.0f, dv1 = 0.0f, ds0 = 0.0f, ds1 = 0.0f;
+#pragma unroll
+      for (int e4 = 0; e4 < E; e4 += 4) {
+        const float4 rv = *reinterpret_cast<const float4*>(R + e4);
+        const float4 kv = *reinterpret_cast<const float4*>(K + e4);
+        const float4 bv = *reinterpret_cast<const float4*>(Bv + e4);
+        P[e4 + 0] = fmaf(rv.x, dyc, P[e4 + 0]);
+        P[e4 + 1] = fmaf(rv.y, dyc, P[e4 + 1]);
+        P[e4 + 2] = fmaf(rv.z, dyc, P[e4 + 2]);
+        P[e4 + 3] = fmaf(rv.w, dyc, P[e4 + 3]);
+        dv0 = fmaf(P[e4 + 0], kv.x, dv0);
+        dv1 = fmaf(P[e4 + 1], kv.y, dv1);
+        dv0 = fmaf(P[e4 + 2], kv.z, dv0);
+        dv1 = fmaf(P[e4 + 3], kv.w, dv1);
+        ds0 = fmaf(P[e4 + 0], bv.x, ds0);
+        ds1 = fmaf(P[e4 + 1], bv.y, ds1);
+        ds0 = fmaf(P[e4 + 2], bv.z, ds0);
+        ds1 = fmaf(P[e4 + 3], bv.w, ds1);
+      }
+      const float dvs = quad_sum(dv0 + dv1);
+      const float dss = quad_sum(ds0 + ds1);
+      const int64_t o = base + static_cast<int64_t>(it * TT + tt) * stride + c;
+      if (q == 0) dv[o] = IoBF16::from_f32(dvs);
+      if (q == 1) dsa[o] = dss;
+#pragma unroll
+      for (int e4 = 0; e4 < E; e4 += 4) {
+        const float4 wv = *reinterpret_cast<const float4*>(W + e4);
+        const float4 av = *reinterpret_cast<const float4*>(A + e4);
+        P[e4 + 0] = fmaf(av.x, dss, P[e4 + 0] * wv.x);
+        P[e4 + 1] = fmaf(av.y, dss, P[e4 + 1] * wv.y);
+        P[e4 + 2] = fmaf(av.z, dss, P[e4 + 2] * wv.z);
+        P[e4 + 3] = fmaf(av.w, dss, P[e4 + 3] * wv.w);
+      }
+    }
+    if (it > 0) store_tile(slot ^ 1);
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. key rows: S and P rows, dr dw dk db da
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void key_kernel(
+    int T, int H, const uint16_t* __restrict__ r, const uint16_t* __restrict__ wl,
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
+    const uint16_t* __restrict__ dy, const float* __restrict__ boundary,
+    const float* __restrict__ sa, const float* __restrict__ dsa,
+    uint16_t* __restrict__ dr, uint16_t* __restrict__ dw, uint16_t* __restrict__ dk,
+    uint16_t* __restrict__ db, uint16_t* __restrict__ da) {
+  using C = Cfg<D>;
+  constexpr int NT = 256, E = C::E, TT = C::TT, DP = C::DP, RG = D / 64;
+  constexpr int UB = TT * D / 8;    // units per bf16 vector (dy, v)
+  constexpr int UF = TT * D / 4;    // units per f32 vector (sa, dsa)
+  constexpr int UR = TT * 8;        // units per row-scalar vector (64 rows)
+  constexpr int NB = 2 * UB / NT;            // bf16 vector units per thread
+  constexpr int NF = 2 * UF / NT;            // f32 vector units per thread
+  constexpr int NR = (5 * UR + NT - 1) / NT; // row-scalar units per thread
+  static_assert(2 * UB % NT == 0 && 2 * UF % NT == 0, "tile units must split evenly");
+  // vec: dy, v, sa, dsa at padded value positions; rows: r, w, k, a, b and
+  // the logit derivative factor of w, for this group's 64 rows
+  __shared__ __align__(16) float vec[2][4][TT][DP];
+  __shared__ __align__(16) float rows[2][6][TT][64];
+
+  const int rg = blockIdx.x % RG;
+  const int bh = blockIdx.x / RG;
+  const int bidx = bh / H, h = bh % H;
+  const int tid = threadIdx.x, row = tid >> 2, q = tid & 3;
+  const int i = rg * 64 + row;
+  const int64_t stride = static_cast<int64_t>(H) * D;
+  const int64_t base = (static_cast<int64_t>(bidx) * T * H + h) * D;
+  const int nchunk = T / kChunk;
+  const float* bnd_base = boundary + (static_cast<int64_t>(bh) * nchunk) * D * D +
+                          static_cast<int64_t>(i) * D + q * E;
+
+  u32x4 preB[NB], preF[NF], preR[NR];
+  auto load_tile = [&](int t0) {
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int idx = tid + u * NT;
+      const int m = idx / UB, rem = idx % UB;
+      const int tt = rem / (D / 8), g = rem % (D / 8);
+      preB[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+          (m == 0 ? dy : v) + base + (t0 + tt) * stride + 8 * g));
+    }
+#pragma unroll
+    for (int u = 0; u < NF; ++u) {
+      const int idx = tid + u * NT;
+      const int m = idx / UF, rem = idx % UF;
+      const int tt = rem / (D / 4), g = rem % (D / 4);
+      preF[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+          (m == 0 ? sa : dsa) + base + (t0 + tt) * stride + 4 * g));
+    }
+#pragma unroll
+    for (int u = 0; u < NR; ++u) {
+      const int idx = tid + u * NT;
+      if (5 * UR % NT == 0 || idx < 5 * UR) {
+        const int m = idx / UR, rem = idx % UR;
+        const int tt = rem / 8, g = rem % 8;
+        const uint16_t* s = m == 0 ? r : m == 1 ? wl : m == 2 ? k : m == 3 ? a : b;
+        preR[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+            s + base + (t0 + tt) * stride + rg * 64 + 8 * g));
+      }
+    }
+  };
+  auto store_tile = [&](int slot) {
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int idx = tid + u * NT;
+      const int m = idx / UB, rem = idx % UB;
+      const int tt = rem / (D / 8), g = rem % (D / 8);
+      float f[8];
+      widen8(preB[u], f);
+      store8(&vec[slot][m][tt][C::pos(8 * g)], f);
+    }
+#pragma unroll
+    for (int u = 0; u < NF; ++u) {
+      const int idx = tid + u * NT;
+      const int m = idx / UF, rem = idx % UF;
+      const int tt = rem / (D / 4), g = rem % (D / 4);
+      *reinterpret_cast<u32x4*>(&vec[slot][2 + m][tt][C::pos(4 * g)]) = preF[u];
+    }
+#pragma unroll
+    for (int u = 0; u < NR; ++u) {
+      const int idx = tid + u * NT;
+      if (5 * UR % NT == 0 || idx < 5 * UR) {
+        const int m = idx / UR, rem = idx % UR;
+        const int tt = rem / 8, g = rem % 8;
+        float f[8];
+        widen8(preR[u], f);
+        if (m == 1) {
+          float fs[8];
+#pragma unroll
+          for (int x = 0; x < 8; ++x) {
+            const float s = 1.0f / (1.0f + __builtin_amdgcn_exp2f(kNegLog2e * f[x]));
+            const float w = __builtin_amdgcn_exp2f(kNegExpHalfLog2e * s);
+            f[x] = w;
+            fs[x] = kWScale * w * s * (1.0f - s);
+          }
+          store8(&rows[slot][5][tt][8 * g], fs);
+        }
+        store8(&rows[slot][m][tt][8 * g], f);
+      }
+    }
+  };
+
+  float Sh[E], Ph[E], nb[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) Ph[e] = 0.0f;
+  float hs = 1.0f, ihs = 1.0f, g = 1.0f, ig = 1.0f;
+
+  auto load_bnd = [&](int ci) {
+    const f4* src = reinterpret_cast<const f4*>(bnd_base + static_cast<int64_t>(ci) * D * D);
+#pragma unroll
+    for (int e4 = 0; e4 < E; e4 += 4) {
+      const f4 x = __builtin_nontemporal_load(src + e4 / 4);
+      nb[e4] = x[0]; nb[e4 + 1] = x[1]; nb[e4 + 2] = x[2]; nb[e4 + 3] = x[3];
+    }
+  };
+
+  const int ntile = T / TT;
+  load_bnd(nchunk - 1);
+  load_tile((ntile - 1) * TT);
+  store_tile(0);
+  __syncthreads();
+  const int qo = q * (E + 4);
+  for (int it = ntile - 1; it >= 0; --it) {
+    const int slot = (ntile - 1 - it) & 1;
+    const int tend = it * TT + TT;
+    if (tend % kChunk == 0) {
+      // the tile ends a chunk: restart S from its snapshot and fold the P scale
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        Sh[e] = nb[e];
+        Ph[e] *= hs;
+      }
+      g = ig = hs = ihs = 1.0f;
+      const int ci = tend / kChunk - 1;
+      if (ci > 0) load_bnd(ci - 1);
+    }
+    if (it > 0) load_tile((it - 1) * TT);
+    for (int tt = TT - 1; tt >= 0; --tt) {
+      const float ri = rows[slot][0][tt][row], wi = rows[slot][1][tt][row];
+      const float ki = rows[slot][2][tt][row], ai = rows[slot][3][tt][row];
+      const float bi = rows[slot][4][tt][row], wsi = rows[slot][5][tt][row];
+      const float* DY = &vec[slot][0][tt][qo];
+      const float* V = &vec[slot][1][tt][qo];
+      const float* SA = &vec[slot][2][tt][qo];
+      const float* DS = &vec[slot][3][tt][qo];
+      const float rw = __builtin_amdgcn_rcpf(wi);
+      const float kg = -ki * ig, bg = -bi * ig;
+      const float g_prev = g * rw, ihs_prev = ihs * rw;
+      const float rh = ri * ihs, ah = ai * ihs_prev;
+      float pr = 0.0f, pw = 0.0f, pk = 0.0f, pb = 0.0f, pa = 0.0f;
+#pragma unroll
+      for (int e4 = 0; e4 < E; e4 += 4) {
+        const float4 d4 = *reinterpret_cast<const float4*>(DY + e4);
+        const float4 v4 = *reinterpret_cast<const float4*>(V + e4);
+        const float4 s4 = *reinterpret_cast<const float4*>(SA + e4);
+        const float4 x4 = *reinterpret_cast<const float4*>(DS + e4);
+        const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
+        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+        const float ss[4] = {s4.x, s4.y, s4.z, s4.w};
+        const float xx[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+        for (int z = 0; z < 4; ++z) {
+          const int e = e4 + z;
+          float s = Sh[e];
+          pr = fmaf(s, dd[z], pr);
+          s = fmaf(kg, vv[z], s);
+          s = fmaf(bg, ss[z], s);
+          Sh[e] = s;
+          const float p = fmaf(rh, dd[z], Ph[e]);
+          pw = fmaf(p, s, pw);
+          pk = fmaf(p, vv[z], pk);
+          pb = fmaf(p, ss[z], pb);
+          pa = fmaf(s, xx[z], pa);
+          Ph[e] = fmaf(ah, xx[z], p);
+        }
+      }
+      pr = quad_sum(pr) * g;
+      pw = quad_sum(pw) * (g_prev * hs) * wsi;
+      pk = quad_sum(pk) * hs;
+      pb = quad_sum(pb) * hs;
+      pa = quad_sum(pa) * g_prev;
+      const int64_t o = base + static_cast<int64_t>(it * TT + tt) * stride + i;
+      if (q == 0) {
+        dr[o] = IoBF16::from_f32(pr);
+        da[o] = IoBF16::from_f32(pa);
+      } else if (q == 1) {
+        dw[o] = IoBF16::from_f32(pw);
+      } else if (q == 2) {
+        dk[o] = IoBF16::from_f32(pk);
+      } else {
+        db[o] = IoBF16::from_f32(pb);
+      }
+      g = g_prev;
+      ig *= wi;
+      hs *= wi;
+      ihs = ihs_prev;
+    }
+    if (it > 0) store_tile(slot ^ 1);
+    __syncthreads();
+  }
+}
+
+template <int D>
+int launch_d(const PretrainBwdArgs& p, hipStream_t s) {
+  const auto* r = static_cast<const uint16_t*>(p.r);
+  const auto* w = static_cast<const uint16_t*>(p.w);
+  const auto* k = static_cast<const uint16_t*>(p.k);
+  const auto* v = static_cast<const uint16_t*>(p.v);
+  const auto* a = static_cast<const uint16_t*>(p.a);
+  const auto* b = static_cast<const uint16_t*>(p.b);
+  const auto* dy = static_cast<const uint16_t*>(p.dy);
+  const int bh = p.batch * p.heads;
+  hipLaunchKernelGGL(value_kernel<D>, dim3(bh), dim3(4 * D), 0, s, p.tokens, p.heads, r, w, k,
+                     a, b, dy, static_cast<uint16_t*>(p.dv), p.workspace);
+  hipLaunchKernelGGL(key_kernel<D>, dim3(bh * (D / 64)), dim3(256), 0, s, p.tokens, p.heads, r,
+                     w, k, v, a, b, dy, p.boundary, p.state_dot_a, p.workspace,
+                     static_cast<uint16_t*>(p.dr), static_cast<uint16_t*>(p.dw),
+                     static_cast<uint16_t*>(p.dk), static_cast<uint16_t*>(p.db),
+                     static_cast<uint16_t*>(p.da));
+  return record_launch();
+}
+
+}  // namespace
+
+int launch_pretrain_backward(int D, const PretrainBwdArgs& p, hipStream_t s) {
+  switch (D) {
+    case 64: return launch_d<64>(p, s);
+    case 128: return launch_d<128>(p, s);
+    case 256: return launch_d<256>(p, s);
+    default: return FR2_ERR_UNSUPPORTED;
+  }
+}
+
+}  // namespace fr2

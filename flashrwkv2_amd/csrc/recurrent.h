@@ -55,4 +55,20 @@ int launch_fp16_state(int D, const SegArgs& p, int nseg, int max_seqlen, int32_t
 int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen,
                    hipStream_t s);
 
+// Training backward of the [B,T,H,D] zero-state path: bf16 token tensors and
+// gradients, the forward's fp32 boundary [B,H,T/16,D,D] and state_dot_a
+// [B,T,H,D], and an fp32 [B,T,H,D] workspace that carries dsa from the value
+// pass to the key pass.
+struct PretrainBwdArgs {
+  int batch = 0, tokens = 0, heads = 0;
+  const void *r = nullptr, *w = nullptr, *k = nullptr, *v = nullptr, *a = nullptr,
+             *b = nullptr, *dy = nullptr;
+  const float* boundary = nullptr;
+  const float* state_dot_a = nullptr;
+  float* workspace = nullptr;
+  void *dr = nullptr, *dw = nullptr, *dk = nullptr, *dv = nullptr, *da = nullptr,
+       *db = nullptr;
+};
+int launch_pretrain_backward(int D, const PretrainBwdArgs& p, hipStream_t s);
+
 }  // namespace fr2

@@ -3,8 +3,8 @@
 Mirrors ``flashrwkv2.tmix.wkv7.pretrain`` (flashrwkv2/tmix/wkv7/pretrain.py:14-130):
 same validation messages, the same ``boundary`` (post-chunk state every 16
 tokens, fp32 ``[B,H,T/16,N,N]``) and ``state_dot_a`` (fp32 ``[B,T,H,N]``)
-checkpoints.  The backward pass is not part of this build and raises
-``NotImplementedError`` from the native layer.
+checkpoints, and the backward (pretrain.py:88-114 of the reference) that
+consumes them through ``pretrain_tmix_wkv7_recurrent_backward``.
 """
 
 from __future__ import annotations
@@ -69,7 +69,17 @@ class _PretrainRecurrent(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output):  # type: ignore[override]
-        return _extension().pretrain_tmix_wkv7_recurrent_backward(ctx, grad_output)
+        r, w, k, v, a, b, boundary, state_dot_a = ctx.saved_tensors
+        batch, tokens, channels = ctx.input_shape
+        head_size = ctx.head_size
+        heads = channels // head_size
+        grad_output_4d = grad_output.contiguous().view(batch, tokens, heads, head_size)
+        if grad_output_4d.dtype != torch.bfloat16:
+            grad_output_4d = grad_output_4d.to(torch.bfloat16)
+        gradients = tuple(torch.empty_like(t) for t in (r, w, k, v, a, b))
+        _extension().pretrain_tmix_wkv7_recurrent_backward(
+            r, w, k, v, a, b, grad_output_4d, boundary, state_dot_a, *gradients, head_size)
+        return tuple(g.view(batch, tokens, channels) for g in gradients) + (None,)
 
 
 def pretrain_tmix_wkv7_recurrent_bf16(

@@ -163,6 +163,27 @@ int fr2_wkv7_pretrain_forward(int32_t batch, int32_t tokens, int32_t num_heads,
                               float* state_dot_a, void* stream);
 
 /*
+ * Training backward of fr2_wkv7_pretrain_forward: gradients (bf16,
+ * [B,T,H,D]) of sum(y * grad_output) with respect to r, the decay logits w,
+ * k, v, a and b.  boundary and state_dot_a are the forward's outputs.
+ * workspace holds batch*tokens*num_heads*head_size floats (the per-token
+ * gradient of sa, passed from the value pass to the key pass); it needs no
+ * initialisation.  Two kernels on `stream`.  Requires T % 16 == 0.
+ * Replaces backward / cuda_backward_v3 / cuda_backward_split /
+ * cuda_backward_tiled256
+ * (csrc/sm120/tmix/wkv7/pretrain_recurrent_bf16_forward.cpp:29-46,
+ *  pretrain_recurrent_bf16_forward.cu:163-486).
+ */
+int fr2_wkv7_pretrain_backward(int32_t batch, int32_t tokens, int32_t num_heads,
+                               int32_t head_size, const void* r, const void* w,
+                               const void* k, const void* v, const void* a,
+                               const void* b, const void* grad_output,
+                               const float* boundary, const float* state_dot_a,
+                               float* workspace, void* grad_r, void* grad_w,
+                               void* grad_k, void* grad_v, void* grad_a, void* grad_b,
+                               void* stream);
+
+/*
  * Packed varlen recurrence with a bf16 state pool [slots,H,64,64] updated in
  * place (fp32 carry inside the call, rounded to bf16 on store).
  * Replaces infer_tmix_wkv7_chunk_bf16_forward_varlen_cuda

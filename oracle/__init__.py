@@ -13,6 +13,11 @@ adds numpy conveniences.  What each function restates:
   decay_bias, scale) and, with ``boundary_len``/``want_sa``, the post-chunk
   boundary and state_dot_a of
   csrc/sm120/tmix/wkv7/pretrain_recurrent_bf16_forward.cu:32-97
+* ``pretrain_backward_f64`` — reverse-mode gradients of the ``[B,T,H,D]``
+  zero-state path, the backward of
+  csrc/sm120/tmix/wkv7/pretrain_recurrent_bf16_forward.cu:163-286; pinned in
+  tests/test_oracle_backward.py by central differences of ``wkv7_f64`` and
+  by torch autograd of an fp64 per-token loop.
 * ``wkv7_cpu_f32`` — the same recurrence in float, OpenMP over
   (sequence, head): the CPU baseline that bench.py times.
 * ``albatross_dither`` / ``wkv7_fp16_state`` (numpy) — the FP16-state
@@ -66,6 +71,8 @@ def _load() -> ctypes.CDLL:
         lib.wkv7_cpu_f32.restype = None
         lib.wkv7_cpu_f32.argtypes = [c_int, c_int, c_int] + [c_void_p] * 10 + [
             c_double, c_void_p, c_int]
+        lib.wkv7_oracle_pretrain_bwd_f64.restype = None
+        lib.wkv7_oracle_pretrain_bwd_f64.argtypes = [c_int] * 4 + [c_void_p] * 13
         lib.wkv7_cpu_max_threads.restype = c_int
         lib.wkv7_cpu_max_threads.argtypes = []
         _lib = lib
@@ -133,6 +140,19 @@ def wkv7_cpu_f32(r, logits, k, v, a, b, *, cu_seqlens, state_indices=None, state
                          *(_p(t) for t in arrs[:2]), _p(bias), *(_p(t) for t in arrs[2:]),
                          float(scale), _p(y), int(threads))
     return y, pool
+
+
+def pretrain_backward_f64(r, logits, k, v, a, b, dy):
+    """fp64 gradients of ``sum(y * dy)`` for the ``[B,T,H,D]`` zero-state path.
+
+    Returns ``(dr, dlogit, dk, dv, da, db)`` as float64 ``[B,T,H,D]``.
+    """
+    arrs = [_f32(t) for t in (r, logits, k, v, a, b, dy)]
+    B, T, H, D = arrs[0].shape
+    outs = [np.zeros((B, T, H, D), dtype=np.float64) for _ in range(6)]
+    _load().wkv7_oracle_pretrain_bwd_f64(B, T, H, D, *(_p(t) for t in arrs),
+                                         *(_p(o) for o in outs))
+    return tuple(outs)
 
 
 def cpu_threads() -> int:

@@ -128,3 +128,100 @@ int wkv7_cpu_max_threads(void) {
   return 1;
 #endif
 }
+
+/*
+ * Reverse-mode gradient of the [B,T,H,D] training-layout recurrence with zero
+ * initial state (the pretrain path): given dy, returns the gradients of
+ * L = sum(y * dy) with respect to r, the decay logits w, k, v, a and b.
+ *
+ * Restates the backward that csrc/sm120/tmix/wkv7/pretrain_recurrent_bf16_forward.cu:163-286
+ * computes (autograd of tests/tmix/wkv7/pretrain/test.py:44-65 in the
+ * reference's own test), derived here from the forward
+ *   S_t = diag(w_t) S_{t-1} + b_t sa_t^T + k_t v_t^T,  sa_t = S_{t-1}^T a_t,
+ *   y_t = S_t^T r_t,  w_t = exp(-exp(-1/2) sigmoid(logit_t)):
+ * with P_t = dL/dS_t (all paths),
+ *   P_t  = r_t dy_t^T + (diag(w_{t+1}) + a_{t+1} b_{t+1}^T) P_{t+1}
+ *   dr_t = S_t dy_t           dk_t = P_t v_t        dv_t = P_t^T k_t
+ *   dsa  = P_t^T b_t          db_t = P_t sa_t       da_t = S_{t-1} dsa
+ *   dw_t = rowsum(P_t o S_{t-1}),  dlogit = dw * w * (-exp(-1/2)) s (1 - s).
+ * Every state S_t of a (batch, head) is kept (T+1 matrices), so the pass
+ * recomputes nothing and divides by nothing.  Double precision throughout.
+ */
+void wkv7_oracle_pretrain_bwd_f64(int B, int T, int H, int D, const float* r,
+                                  const float* logits, const float* k, const float* v,
+                                  const float* a, const float* b, const float* dy,
+                                  double* dr, double* dlogit, double* dk, double* dv,
+                                  double* da, double* db) {
+  const int64_t DD = (int64_t)D * D;
+  double* S = (double*)malloc(sizeof(double) * DD * (T + 1));
+  double* P = (double*)malloc(sizeof(double) * DD);
+  double* w = (double*)malloc(sizeof(double) * T * D);
+  double* sa = (double*)malloc(sizeof(double) * T * D);
+  double* dsa = (double*)malloc(sizeof(double) * D);
+  for (int bb = 0; bb < B; ++bb)
+    for (int h = 0; h < H; ++h) {
+#define OFF(t) ((((int64_t)bb * T + (t)) * H + h) * D)
+      memset(S, 0, sizeof(double) * DD);
+      for (int t = 0; t < T; ++t) {
+        const int64_t o = OFF(t);
+        const double* Sp = S + DD * t;
+        double* Sn = S + DD * (t + 1);
+        for (int i = 0; i < D; ++i) w[t * D + i] = wkv7_oracle_retention(logits[o + i]);
+        for (int j = 0; j < D; ++j) {
+          double acc = 0;
+          for (int i = 0; i < D; ++i) acc += Sp[(int64_t)i * D + j] * a[o + i];
+          sa[t * D + j] = acc;
+        }
+        for (int i = 0; i < D; ++i)
+          for (int j = 0; j < D; ++j)
+            Sn[(int64_t)i * D + j] = w[t * D + i] * Sp[(int64_t)i * D + j] +
+                                     b[o + i] * sa[t * D + j] + (double)k[o + i] * v[o + j];
+      }
+      memset(P, 0, sizeof(double) * DD);
+      for (int t = T - 1; t >= 0; --t) {
+        const int64_t o = OFF(t);
+        const double* Sp = S + DD * t;
+        const double* Sn = S + DD * (t + 1);
+        for (int i = 0; i < D; ++i)
+          for (int j = 0; j < D; ++j) P[(int64_t)i * D + j] += (double)r[o + i] * dy[o + j];
+        for (int i = 0; i < D; ++i) {
+          double gr = 0, gk = 0, gb = 0, gw = 0;
+          for (int j = 0; j < D; ++j) {
+            const double p = P[(int64_t)i * D + j];
+            gr += Sn[(int64_t)i * D + j] * dy[o + j];
+            gk += p * v[o + j];
+            gb += p * sa[t * D + j];
+            gw += p * Sp[(int64_t)i * D + j];
+          }
+          const double sg = 1.0 / (1.0 + exp(-(double)logits[o + i]));
+          dr[o + i] = gr;
+          dk[o + i] = gk;
+          db[o + i] = gb;
+          dlogit[o + i] = gw * w[t * D + i] * (-exp(-0.5)) * sg * (1.0 - sg);
+        }
+        for (int j = 0; j < D; ++j) {
+          double gv = 0, gs = 0;
+          for (int i = 0; i < D; ++i) {
+            gv += P[(int64_t)i * D + j] * k[o + i];
+            gs += P[(int64_t)i * D + j] * b[o + i];
+          }
+          dv[o + j] = gv;
+          dsa[j] = gs;
+        }
+        for (int i = 0; i < D; ++i) {
+          double g = 0;
+          for (int j = 0; j < D; ++j) g += Sp[(int64_t)i * D + j] * dsa[j];
+          da[o + i] = g;
+        }
+        for (int i = 0; i < D; ++i)
+          for (int j = 0; j < D; ++j)
+            P[(int64_t)i * D + j] = w[t * D + i] * P[(int64_t)i * D + j] + a[o + i] * dsa[j];
+      }
+#undef OFF
+    }
+  free(S);
+  free(P);
+  free(w);
+  free(sa);
+  free(dsa);
+}

@@ -61,7 +61,7 @@ def test_pretrain_forward_matches_oracle(batch, tokens, heads, head_size):
     assert_state_close(boundary, bd_ref)
 
 
-def test_pretrain_rejects_invalid_inputs_and_has_no_backward():
+def test_pretrain_rejects_invalid_inputs():
     require_gpu()
     g = torch.Generator().manual_seed(1)
     valid = [_randn((1, 16, 64), g, 0.05, torch.bfloat16) for _ in range(6)]
@@ -77,10 +77,6 @@ def test_pretrain_rejects_invalid_inputs_and_has_no_backward():
         pretrain_tmix_wkv7_recurrent_bf16(valid[0].transpose(1, 2), *valid[1:])
     with pytest.raises(ValueError, match="contiguous CUDA"):
         pretrain_tmix_wkv7_recurrent_bf16(*(t.cpu() for t in valid))
-    grads = [t.detach().clone().requires_grad_() for t in valid]
-    y = pretrain_tmix_wkv7_recurrent_bf16(*grads)
-    with pytest.raises(NotImplementedError):
-        y.float().sum().backward()
 
 
 # ----------------------------------------------------------- bf16-state chunk

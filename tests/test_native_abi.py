@@ -62,6 +62,12 @@ def test_null_pointers_and_bad_sizes_are_rejected_before_any_launch(lib):
         1, 15, 1, 64, *([fake] * 10), nul) == N.FR2_ERR_INVALID_ARGUMENT
     assert lib.fr2_wkv7_pretrain_forward(
         1, 16, 1, 32, *([fake] * 10), nul) == N.FR2_ERR_UNSUPPORTED
+    assert lib.fr2_wkv7_pretrain_backward(
+        1, 16, 1, 64, *([fake] * 9), nul, *([fake] * 6), nul) == N.FR2_ERR_INVALID_ARGUMENT
+    assert lib.fr2_wkv7_pretrain_backward(
+        1, 24, 1, 64, *([fake] * 16), nul) == N.FR2_ERR_INVALID_ARGUMENT
+    assert lib.fr2_wkv7_pretrain_backward(
+        1, 16, 1, 96, *([fake] * 16), nul) == N.FR2_ERR_UNSUPPORTED
     assert lib.fr2_wkv7_recurrent_fp32_forward(
         fake, fake, fake, 1, 1, 32, 1, 1, N.FR2_DTYPE_BFLOAT16, *([fake] * 9), 1.0,
         nul) == N.FR2_ERR_UNSUPPORTED
