@@ -128,7 +128,7 @@ class Runner:
         if ms <= 4:
             return "decode64_kernel<IoBF16,StF32>"
         if ms >= 128:
-            return "chunk64_kernel<IoBF16>"
+            return "chunk64_kernel<IoBF16,false>"
         return "serial_kernel<64,IoBF16,StF32>"
 
 
@@ -230,6 +230,72 @@ def time_fp16_state_decode(torch, flashrwkv2_amd, w, steps: int, warmup: int):
     return ms, start.elapsed_time(end) / (steps * 4)
 
 
+# FMAs per (token, head) element of the D x D state in the training backward:
+# 5 in the value-column pass (P += r dy^T, dv, dsa, P = w P + a dsa^T) and 9 in
+# the key-row pass (dr, two for the S rebuild, two P updates, dw dk db da)
+BWD_FMA_PER_ELEM = 14
+FP32_VECTOR_PEAK_TFLOPS = 157.3
+
+
+def time_pretrain_training(torch, w, steps: int):
+    """The [B,T,H,D] training path on a config-1-shaped batch: per-launch
+    times (ms) of the forward (y, state_dot_a, boundary) and of the backward
+    (two kernels), each launched `steps` times through the C ABI between HIP
+    events on the launch stream."""
+    from flashrwkv2_amd import _native as N
+
+    B, T, H = w.info["B"], w.info["T"], w.info["H"]
+    D = 64
+    toks = [t.view(B, T, H, D) for t in w.tokens]
+    g = torch.Generator(device=toks[0].device)
+    g.manual_seed(2001)
+    dy = torch.randn((B, T, H, D), generator=g, device=toks[0].device).to(torch.bfloat16)
+    y = torch.empty_like(toks[3])
+    boundary = torch.empty((B, H, T // 16, D, D), device=y.device, dtype=torch.float32)
+    sa = torch.empty((B, T, H, D), device=y.device, dtype=torch.float32)
+    work = torch.empty_like(sa)
+    grads = [torch.empty_like(t) for t in toks]
+    lib = N.load()
+    stream = torch.cuda.current_stream()
+    ptrs = [t.data_ptr() for t in toks]
+    fwd_args = (B, T, H, D, *ptrs, y.data_ptr(), boundary.data_ptr(), sa.data_ptr(),
+                stream.cuda_stream)
+    bwd_args = (B, T, H, D, *ptrs, dy.data_ptr(), boundary.data_ptr(), sa.data_ptr(),
+                work.data_ptr(), *(t.data_ptr() for t in grads), stream.cuda_stream)
+
+    def timed(fn, args, name):
+        N.check(fn(*args), name)  # warm-up
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            rc = fn(*args)
+            if rc:
+                N.check(rc, name)
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
+
+    fwd_ms = timed(lib.fr2_wkv7_pretrain_forward, fwd_args, "fr2_wkv7_pretrain_forward")
+    bwd_ms = timed(lib.fr2_wkv7_pretrain_backward, bwd_args, "fr2_wkv7_pretrain_backward")
+    ok = all(bool(torch.isfinite(t).all()) for t in grads)
+    flops = 2 * BWD_FMA_PER_ELEM * D * D * B * T * H
+    tf = flops / (bwd_ms * 1e-3) / 1e12
+    return {
+        "workload": f"cfg1_shape_training_B{B}_T{T}_H{H}",
+        "forward_ms": round(fwd_ms, 4), "backward_ms": round(bwd_ms, 4),
+        "train_tokens_per_s": round(B * T / ((fwd_ms + bwd_ms) * 1e-3), 1),
+        "backward_tokens_per_s": round(B * T / (bwd_ms * 1e-3), 1),
+        "backward_roofline": {"bound": "valu_fp32", "achieved": round(tf, 2),
+                              "peak": FP32_VECTOR_PEAK_TFLOPS, "unit": "TFLOP/s",
+                              "frac": round(tf / FP32_VECTOR_PEAK_TFLOPS, 4)},
+        "gradients_finite": ok,
+        "kernels": ["chunk64_kernel<IoBF16,true> (forward: y, sa, boundary)", "value_kernel<64>",
+                    "key_kernel<64>"],
+    }
+
+
 def mfma_obj(w, kernel_ms: float):
     """Matrix-core use of the chunked kernel: issued bf16 MFMA flops (hi/lo
     split products included) over the launch time, against the dense bf16 peak."""
@@ -252,7 +318,9 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true", help="skip the decode (config 2) leg")
     ap.add_argument("--cpu-sample-tokens", type=int, default=4096,
                     help="tokens per sequence in the CPU baseline sample")
-    ap.add_argument("--only", choices=["prefill", "decode"], default=None,
+    ap.add_argument("--no-train", action="store_true",
+                    help="skip the training (forward + backward) leg")
+    ap.add_argument("--only", choices=["prefill", "decode", "train"], default=None,
                     help="run one leg only (profiling)")
     ap.add_argument("--config", type=int, default=1, choices=[1, 3, 4],
                     help="prefill workload (BASELINE config; the metric is quoted on 1)")
@@ -344,6 +412,9 @@ def main() -> int:
             result.update({"metric": METRIC, "value": result["decode"]["tokens_per_s"],
                            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
                            "warmup": args.warmup, "ms_per_step": round(dms, 5)})
+    if args.only in (None, "train") and not args.no_train:
+        wt = pre.w if (pre is not None and args.config == 1) else workloads.config(1, "cuda")
+        result["pretrain_training"] = time_pretrain_training(torch, wt, max(3, args.steps // 4))
     if pre is not None and not args.no_cpu and args.config == 1:
         threads = min(16, os.cpu_count() or 1)
         tps, dt, n_tok, reps = cpu_baseline(pre.w, threads, args.cpu_sample_tokens)

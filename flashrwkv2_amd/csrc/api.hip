@@ -153,6 +153,13 @@ extern "C" int fr2_wkv7_pretrain_forward(int32_t batch, int32_t tokens,
   p.boundary = boundary;
   p.boundary_len = 16;
   p.boundary_per_seg = tokens / 16;
+  // D = 64 runs the chunked MFMA kernel, which emits sa and the post-chunk
+  // states of its 16-token chunks directly; other head sizes run token-serial
+  if (head_size == 64) {
+    const int rc = fr2::launch_chunked(FR2_DTYPE_BFLOAT16, p, batch, tokens,
+                                       static_cast<hipStream_t>(stream));
+    if (rc != FR2_ERR_UNSUPPORTED) return rc;
+  }
   return fr2::launch_serial(head_size, FR2_DTYPE_BFLOAT16, false, p, batch,
                             static_cast<hipStream_t>(stream));
 }

@@ -469,10 +469,13 @@ __device__ __forceinline__ StateOps<kVExact> state_load(const ChunkOps<kVExact>&
   return o;
 }
 
-template <class Io, bool kVExact>
+// With kTrain the chunk also writes its per-token sa rows (U, fp32) to
+// sa_col[token * row_stride] and its post-chunk state column to bnd_col[key * D].
+template <class Io, bool kVExact, bool kTrain = false>
 __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 (&S)[4],
                                               uint16_t (*yrows)[YP], int vcol, int i, int q,
-                                              float scale) {
+                                              float scale, float* sa_col = nullptr,
+                                              int64_t row_stride = 0, float* bnd_col = nullptr) {
   using raw = typename Io::raw;
   // S split as B operand against the permuted A~ / R~ rows: K positions
   // 8q..8q+7 = rows 32m + 4q + (0..3) then 32m + 16 + 4q + (0..3)
@@ -494,8 +497,13 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
     X = mma32x3(o.Aa1, Sb[1], X);
     Y = mma32x3(o.Ra0, Sb[0], Y);
     Y = mma32x3(o.Ra1, Sb[1], Y);
-    const BOp Us = as_b(split4(mm_ab(o.Ta, as_b(split4(X)), zero)));
+    const f32x4 Uf = mm_ab(o.Ta, as_b(split4(X)), zero);
+    const BOp Us = as_b(split4(Uf));
     Y = mm_ab(o.Mrb, Us, Y);
+    if constexpr (kTrain) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sa_col[(4 * q + e) * row_stride] = Uf[e];
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const raw yv = Io::from_f32(scale * Y[e]);
@@ -506,6 +514,10 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
       f32x4 acc = mm_ab(o.Bt[kb], Us, S[kb]);
       acc = mm_ax(o.Kt[kb], Vx, acc);
       S[kb] = acc * o.gl[kb];
+      if constexpr (kTrain) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bnd_col[(16 * kb + 4 * q + e) * D] = S[kb][e];
+      }
     }
   } else {
     const BOp Vs = as_b(o.vh, o.vl);
@@ -515,8 +527,13 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
     X = mma32x3(o.Aa1, Sb[1], X);
     Y = mma32x3(o.Ra0, Sb[0], Y);
     Y = mma32x3(o.Ra1, Sb[1], Y);
-    const BOp Us = as_b(split4(mm_ab(o.Ta, as_b(split4(X)), zero)));
+    const f32x4 Uf = mm_ab(o.Ta, as_b(split4(X)), zero);
+    const BOp Us = as_b(split4(Uf));
     Y = mm_ab(o.Mrb, Us, Y);
+    if constexpr (kTrain) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sa_col[(4 * q + e) * row_stride] = Uf[e];
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const raw yv = Io::from_f32(scale * Y[e]);
@@ -527,6 +544,10 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
       f32x4 acc = mm_ab(o.Bt[kb], Us, S[kb]);
       acc = mm_ab(o.Kt[kb], Vs, acc);
       S[kb] = acc * o.gl[kb];
+      if constexpr (kTrain) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bnd_col[(16 * kb + 4 * q + e) * D] = S[kb][e];
+      }
     }
   }
 }
@@ -566,7 +587,10 @@ __device__ __forceinline__ void wait_min_ge(int* c, int v) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-template <class Io>
+// kTrain: the training-forward contract (pretrain path) also writes every
+// token's sa (p.sa_out) and the post-chunk state of every 16-token chunk
+// (p.boundary, [segment, H, boundary_per_seg, D, D]).
+template <class Io, bool kTrain>
 __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
   using raw = typename Io::raw;
   constexpr bool kVExact = !__is_same(Io, IoF16);
@@ -640,6 +664,19 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
             *reinterpret_cast<const u32x4*>(&sm.yb[gi & 1][o_tok][o_c8 * 8]);
       signal(&sm.drained[wv], gi + 1);
     };
+    // training outputs: sa column of this lane and the boundary column
+    float* const sa_base =
+        kTrain ? p.sa_out + static_cast<int64_t>(t0) * row_stride + head_off + vcol : nullptr;
+    float* const bnd_base =
+        kTrain ? p.boundary + (static_cast<int64_t>(seg) * H + h) * p.boundary_per_seg * D * D + vcol
+               : nullptr;
+    auto chunk = [&](const StateOps<kVExact>& o, int gi, int c) {
+      const int ci = gi * G + c;   // chunk index within the segment
+      state_compute<Io, kVExact, kTrain>(
+          o, S, &sm.yb[gi & 1][c * L], vcol, i, q, p.scale,
+          kTrain ? sa_base + static_cast<int64_t>(ci) * L * row_stride : nullptr, row_stride,
+          kTrain ? bnd_base + static_cast<int64_t>(ci) * D * D : nullptr);
+    };
     auto group = [&](auto par_c, int gi) {
       constexpr int par = decltype(par_c)::value;
       wait_min_ge(sm.ready, gi + 1);          // operators of group gi stored
@@ -650,15 +687,12 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
         const StateOps<kVExact> o0 = state_load(sm.ops[par][0], vcol, i, q);
         StateOps<kVExact> o1;
         state_load_early(o1, sm.ops[par][1], vcol, i, q);
-        state_compute<Io, kVExact>(o0, S, &sm.yb[par][0], vcol, i, q, p.scale);
+        chunk(o0, gi, 0);
         state_load_late(o1, sm.ops[par][1], vcol, i, q);
-        state_compute<Io, kVExact>(o1, S, &sm.yb[par][L], vcol, i, q, p.scale);
+        chunk(o1, gi, 1);
       } else {
-        state_compute<Io, kVExact>(state_load(sm.ops[par][0], vcol, i, q), S, &sm.yb[par][0],
-                                   vcol, i, q, p.scale);
-        if (t0 + gi * GT + L < t1)
-          state_compute<Io, kVExact>(state_load(sm.ops[par][1], vcol, i, q), S, &sm.yb[par][L],
-                                     vcol, i, q, p.scale);
+        chunk(state_load(sm.ops[par][0], vcol, i, q), gi, 0);
+        if (t0 + gi * GT + L < t1) chunk(state_load(sm.ops[par][1], vcol, i, q), gi, 1);
       }
       signal(&sm.consumed[wv], gi + 1);
       write_out(gi - 1);
@@ -749,14 +783,23 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
 
 int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen, hipStream_t s) {
   (void)max_seqlen;
-  if (p.sa_out != nullptr || p.boundary != nullptr) return FR2_ERR_UNSUPPORTED;
+  const bool train = p.sa_out != nullptr || p.boundary != nullptr;
   const dim3 grid(p.num_heads, nseg);
-  if (dtype == FR2_DTYPE_BFLOAT16)
-    hipLaunchKernelGGL((chunk64_kernel<IoBF16>), grid, dim3(NT), 0, s, p);
-  else if (dtype == FR2_DTYPE_FLOAT16)
-    hipLaunchKernelGGL((chunk64_kernel<IoF16>), grid, dim3(NT), 0, s, p);
-  else
+  if (train) {
+    // the training contract: uniform segments whose length is a multiple of
+    // the 16-token chunk, both outputs present, bf16 tokens
+    if (p.sa_out == nullptr || p.boundary == nullptr || p.boundary_len != L ||
+        p.uniform_len <= 0 || p.uniform_len % L != 0 || p.state_in != nullptr ||
+        dtype != FR2_DTYPE_BFLOAT16)
+      return FR2_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL((chunk64_kernel<IoBF16, true>), grid, dim3(NT), 0, s, p);
+  } else if (dtype == FR2_DTYPE_BFLOAT16) {
+    hipLaunchKernelGGL((chunk64_kernel<IoBF16, false>), grid, dim3(NT), 0, s, p);
+  } else if (dtype == FR2_DTYPE_FLOAT16) {
+    hipLaunchKernelGGL((chunk64_kernel<IoF16, false>), grid, dim3(NT), 0, s, p);
+  } else {
     return FR2_ERR_UNSUPPORTED;
+  }
   return record_launch();
 }
 

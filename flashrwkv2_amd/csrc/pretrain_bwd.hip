@@ -22,7 +22,12 @@
 //      of one (batch, head) (4 lanes per row, D/4 values each) and walks T
 //      backwards carrying its rows of S and P, writing dr, dw, dk, db, da.
 // Token operands are staged through LDS as fp32, one tile of TT tokens at a
-// time, double-buffered with the next tile's global loads in flight.  The
+// time, double-buffered with the next tile's global loads in flight.  Lane
+// 4c+q of each 16-lane DPP row (q = quarter of the reduced index, c = one of
+// the row's four columns/rows) reads only its own D/16 operand values per
+// token and receives the other three lanes' values of its quarter through
+// DPP row rotations, folded into the FMAs as DPP operands: LDS delivers each
+// operand value once per 16-lane row instead of once per lane.  The
 // key kernel keeps S and P row-scaled (S = g Sh, P = hs Ph, g and hs per-row
 // scalars) so the 1/w and w factors cost two multiplies per row instead of
 // one per element; both scales restart at every 16-token boundary snapshot.
@@ -54,17 +59,60 @@ __device__ __forceinline__ void widen8(u32x4 u, float* f) {
 template <int D>
 struct Cfg {
   static constexpr int E = D / 4;                 // elements per lane
+  static constexpr int Q = E / 4;                 // own operand values per lane per token
   static constexpr int TT = D <= 128 ? 16 : 8;    // tokens per LDS tile
-  static constexpr int DP = D + 16;               // padded LDS row
-  // lane quarter q reads elements [q*E, q*E+E) at q*(E+4): the four quarters
-  // start on distinct bank groups, so a b128 read with four distinct
-  // addresses per wave does not conflict.
-  static __device__ __forceinline__ int pos(int j) { return j + 4 * (j / E); }
+};
+
+// Lane 4c+q of a 16-lane DPP row receives the value of lane 4((c-m)&3)+q.
+// Element e = m*Q + s of a lane therefore refers to index
+//   q*E + Q*((c - m) & 3) + s
+// of the D-long reduced axis.
+// The rotated operand is always src0 of a VOP2 instruction with a DPP
+// row_ror modifier, so the rotation costs no instruction: the compiler folds
+// it into v_mul_f32 (mul_rot); for v_fmac_f32, which it does not fold on this
+// target, fmac_rot writes the DPP form directly.  The rotated sources are
+// LDS-loaded operand values that no VALU instruction writes, so the
+// VALU-write -> DPP-read wait states never apply to them.
+template <int M>
+__device__ __forceinline__ float mul_rot(float x, float y) {
+  if constexpr (M == 0) {
+    return x * y;
+  } else {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + 4 * M,
+                                                      0xf, 0xf, true)) * y;
+  }
+}
+// acc += rot_M(x) * y
+template <int M>
+__device__ __forceinline__ void fmac_rot(float& acc, float x, float y) {
+  if constexpr (M == 0) {
+    acc = fmaf(x, y, acc);
+  } else if constexpr (M == 1) {
+    asm("v_fmac_f32_dpp %0, %1, %2 row_ror:4 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(x), "v"(y));
+  } else if constexpr (M == 2) {
+    asm("v_fmac_f32_dpp %0, %1, %2 row_ror:8 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(x), "v"(y));
+  } else {
+    asm("v_fmac_f32_dpp %0, %1, %2 row_ror:12 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(x), "v"(y));
+  }
+}
+
+template <int M>
+struct IC {
+  static constexpr int value = M;
 };
 
 __device__ __forceinline__ void store8(float* dst, const float* f) {
   *reinterpret_cast<float4*>(dst) = make_float4(f[0], f[1], f[2], f[3]);
   *reinterpret_cast<float4*>(dst + 4) = make_float4(f[4], f[5], f[6], f[7]);
+}
+
+template <int Q>
+__device__ __forceinline__ void lds_read(const float* src, float* dst) {
+#pragma unroll
+  for (int x = 0; x < Q; x += 4) {
+    const float4 v = *reinterpret_cast<const float4*>(src + x);
+    dst[x] = v.x; dst[x + 1] = v.y; dst[x + 2] = v.z; dst[x + 3] = v.w;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -77,15 +125,18 @@ __global__ __launch_bounds__(4 * D) void value_kernel(
     const uint16_t* __restrict__ b, const uint16_t* __restrict__ dy,
     uint16_t* __restrict__ dv, float* __restrict__ dsa) {
   using C = Cfg<D>;
-  constexpr int NT = 4 * D, E = C::E, TT = C::TT, DP = C::DP;
+  constexpr int NT = 4 * D, E = C::E, Q = C::Q, TT = C::TT;
   constexpr int kVec = 6;                    // r, w, k, a, b, dy
   constexpr int UPV = TT * D / 8;            // 16-byte units per vector per tile
   constexpr int NU = kVec * UPV;
   constexpr int UPT = (NU + NT - 1) / NT;
-  __shared__ __align__(16) float buf[2][kVec][TT][DP];
+  __shared__ __align__(16) float buf[2][kVec][TT][D];
 
   const int bidx = blockIdx.x / H, h = blockIdx.x % H;
-  const int tid = threadIdx.x, c = tid >> 2, q = tid & 3;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int q = lane & 3, c4 = (lane >> 2) & 3;
+  const int col = 16 * (tid >> 6) + 4 * (lane >> 4) + c4;   // value column
+  const int own = q * E + Q * c4;                           // this lane's operand slice
   const int64_t stride = static_cast<int64_t>(H) * D;
   const int64_t base = (static_cast<int64_t>(bidx) * T * H + h) * D;
 
@@ -116,7 +167,7 @@ __global__ __launch_bounds__(4 * D) void value_kernel(
 #pragma unroll
           for (int i = 0; i < 8; ++i) f[i] = retention_from_logit(f[i]);
         }
-        store8(&buf[slot][m][tt][C::pos(8 * g)], f);
+        store8(&buf[slot][m][tt][8 * g], f);
       }
     }
   };
@@ -129,50 +180,44 @@ __global__ __launch_bounds__(4 * D) void value_kernel(
   load_tile((ntile - 1) * TT);
   store_tile(0);
   __syncthreads();
-  const int qo = q * (E + 4), co = C::pos(c);
   for (int it = ntile - 1; it >= 0; --it) {
     const int slot = (ntile - 1 - it) & 1;
     if (it > 0) load_tile((it - 1) * TT);
     for (int tt = TT - 1; tt >= 0; --tt) {
-      const float* R = &buf[slot][0][tt][qo];
-      const float* W = &buf[slot][1][tt][qo];
-      const float* K = &buf[slot][2][tt][qo];
-      const float* A = &buf[slot][3][tt][qo];
-      const float* Bv = &buf[slot][4][tt][qo];
-      const float dyc = buf[slot][5][tt][co];
+      float R[Q], W[Q], K[Q], A[Q], Bv[Q];
+      lds_read<Q>(&buf[slot][0][tt][own], R);
+      lds_read<Q>(&buf[slot][2][tt][own], K);
+      lds_read<Q>(&buf[slot][4][tt][own], Bv);
+      const float dyc = buf[slot][5][tt][col];
       float dv0 = 0.0f, dv1 = 0.0f, ds0 = 0.0f, ds1 = 0.0f;
+      auto part1 = [&](auto mc) {
+        constexpr int m = decltype(mc)::value;
 #pragma unroll
-      for (int e4 = 0; e4 < E; e4 += 4) {
-        const float4 rv = *reinterpret_cast<const float4*>(R + e4);
-        const float4 kv = *reinterpret_cast<const float4*>(K + e4);
-        const float4 bv = *reinterpret_cast<const float4*>(Bv + e4);
-        P[e4 + 0] = fmaf(rv.x, dyc, P[e4 + 0]);
-        P[e4 + 1] = fmaf(rv.y, dyc, P[e4 + 1]);
-        P[e4 + 2] = fmaf(rv.z, dyc, P[e4 + 2]);
-        P[e4 + 3] = fmaf(rv.w, dyc, P[e4 + 3]);
-        dv0 = fmaf(P[e4 + 0], kv.x, dv0);
-        dv1 = fmaf(P[e4 + 1], kv.y, dv1);
-        dv0 = fmaf(P[e4 + 2], kv.z, dv0);
-        dv1 = fmaf(P[e4 + 3], kv.w, dv1);
-        ds0 = fmaf(P[e4 + 0], bv.x, ds0);
-        ds1 = fmaf(P[e4 + 1], bv.y, ds1);
-        ds0 = fmaf(P[e4 + 2], bv.z, ds0);
-        ds1 = fmaf(P[e4 + 3], bv.w, ds1);
-      }
+        for (int x = 0; x < Q; ++x) {
+          float& p = P[m * Q + x];
+          fmac_rot<m>(p, R[x], dyc);
+          fmac_rot<m>((x & 1) ? dv1 : dv0, K[x], p);
+          fmac_rot<m>((x & 1) ? ds1 : ds0, Bv[x], p);
+        }
+      };
+      part1(IC<0>{}); part1(IC<1>{}); part1(IC<2>{}); part1(IC<3>{});
+      lds_read<Q>(&buf[slot][1][tt][own], W);
+      lds_read<Q>(&buf[slot][3][tt][own], A);
       const float dvs = quad_sum(dv0 + dv1);
       const float dss = quad_sum(ds0 + ds1);
-      const int64_t o = base + static_cast<int64_t>(it * TT + tt) * stride + c;
+      const int64_t o = base + static_cast<int64_t>(it * TT + tt) * stride + col;
       if (q == 0) dv[o] = IoBF16::from_f32(dvs);
       if (q == 1) dsa[o] = dss;
+      auto part2 = [&](auto mc) {
+        constexpr int m = decltype(mc)::value;
 #pragma unroll
-      for (int e4 = 0; e4 < E; e4 += 4) {
-        const float4 wv = *reinterpret_cast<const float4*>(W + e4);
-        const float4 av = *reinterpret_cast<const float4*>(A + e4);
-        P[e4 + 0] = fmaf(av.x, dss, P[e4 + 0] * wv.x);
-        P[e4 + 1] = fmaf(av.y, dss, P[e4 + 1] * wv.y);
-        P[e4 + 2] = fmaf(av.z, dss, P[e4 + 2] * wv.z);
-        P[e4 + 3] = fmaf(av.w, dss, P[e4 + 3] * wv.w);
-      }
+        for (int x = 0; x < Q; ++x) {
+          float& p = P[m * Q + x];
+          p = mul_rot<m>(W[x], p);
+          fmac_rot<m>(p, A[x], dss);
+        }
+      };
+      part2(IC<0>{}); part2(IC<1>{}); part2(IC<2>{}); part2(IC<3>{});
     }
     if (it > 0) store_tile(slot ^ 1);
     __syncthreads();
@@ -192,7 +237,7 @@ __global__ __launch_bounds__(256) void key_kernel(
     uint16_t* __restrict__ dr, uint16_t* __restrict__ dw, uint16_t* __restrict__ dk,
     uint16_t* __restrict__ db, uint16_t* __restrict__ da) {
   using C = Cfg<D>;
-  constexpr int NT = 256, E = C::E, TT = C::TT, DP = C::DP, RG = D / 64;
+  constexpr int NT = 256, E = C::E, Q = C::Q, TT = C::TT, RG = D / 64;
   constexpr int UB = TT * D / 8;    // units per bf16 vector (dy, v)
   constexpr int UF = TT * D / 4;    // units per f32 vector (sa, dsa)
   constexpr int UR = TT * 8;        // units per row-scalar vector (64 rows)
@@ -200,21 +245,24 @@ __global__ __launch_bounds__(256) void key_kernel(
   constexpr int NF = 2 * UF / NT;            // f32 vector units per thread
   constexpr int NR = (5 * UR + NT - 1) / NT; // row-scalar units per thread
   static_assert(2 * UB % NT == 0 && 2 * UF % NT == 0, "tile units must split evenly");
-  // vec: dy, v, sa, dsa at padded value positions; rows: r, w, k, a, b and
-  // the logit derivative factor of w, for this group's 64 rows
-  __shared__ __align__(16) float vec[2][4][TT][DP];
+  // vec: dy, v, sa, dsa; rows: r, w, k, a, b and the logit derivative
+  // factor of w, for this group's 64 rows
+  __shared__ __align__(16) float vec[2][4][TT][D];
   __shared__ __align__(16) float rows[2][6][TT][64];
 
   const int rg = blockIdx.x % RG;
   const int bh = blockIdx.x / RG;
   const int bidx = bh / H, h = bh % H;
-  const int tid = threadIdx.x, row = tid >> 2, q = tid & 3;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int q = lane & 3, c4 = (lane >> 2) & 3;
+  const int row = 16 * (tid >> 6) + 4 * (lane >> 4) + c4;   // key row within the group
   const int i = rg * 64 + row;
+  const int own = q * E + Q * c4;                           // this lane's operand slice
   const int64_t stride = static_cast<int64_t>(H) * D;
   const int64_t base = (static_cast<int64_t>(bidx) * T * H + h) * D;
   const int nchunk = T / kChunk;
   const float* bnd_base = boundary + (static_cast<int64_t>(bh) * nchunk) * D * D +
-                          static_cast<int64_t>(i) * D + q * E;
+                          static_cast<int64_t>(i) * D + q * E;  // + Q*((c4-m)&3) per m
 
   u32x4 preB[NB], preF[NF], preR[NR];
   auto load_tile = [&](int t0) {
@@ -254,14 +302,14 @@ __global__ __launch_bounds__(256) void key_kernel(
       const int tt = rem / (D / 8), g = rem % (D / 8);
       float f[8];
       widen8(preB[u], f);
-      store8(&vec[slot][m][tt][C::pos(8 * g)], f);
+      store8(&vec[slot][m][tt][8 * g], f);
     }
 #pragma unroll
     for (int u = 0; u < NF; ++u) {
       const int idx = tid + u * NT;
       const int m = idx / UF, rem = idx % UF;
       const int tt = rem / (D / 4), g = rem % (D / 4);
-      *reinterpret_cast<u32x4*>(&vec[slot][2 + m][tt][C::pos(4 * g)]) = preF[u];
+      *reinterpret_cast<u32x4*>(&vec[slot][2 + m][tt][4 * g]) = preF[u];
     }
 #pragma unroll
     for (int u = 0; u < NR; ++u) {
@@ -287,80 +335,126 @@ __global__ __launch_bounds__(256) void key_kernel(
     }
   };
 
-  float Sh[E], Ph[E], nb[E];
+  // With whole-chunk tiles the key pass rebuilds each chunk's states
+  // forwards from the chunk's start state and walks backwards through 1/w
+  // for at most 8 tokens (from the rebuilt S_15 and S_7).  The 1/w walk
+  // amplifies any mismatch between the saved sa and the snapshots by up to
+  // exp(exp(-1/2))^n; rebuilding keeps n <= 8 and makes the walk start from
+  // states consistent with sa, whatever forward kernel produced them.
+  // (N = 256 tiles hold half a chunk: that path walks back from the chunk's
+  // own snapshot, which the token-serial forward writes consistently.)
+  constexpr bool kRecompute = TT == kChunk;
+  float Sh[E], Ph[E], nb[E], Mid[kRecompute ? E : 1];
 #pragma unroll
   for (int e = 0; e < E; ++e) Ph[e] = 0.0f;
   float hs = 1.0f, ihs = 1.0f, g = 1.0f, ig = 1.0f;
 
   auto load_bnd = [&](int ci) {
-    const f4* src = reinterpret_cast<const f4*>(bnd_base + static_cast<int64_t>(ci) * D * D);
+    const float* src = bnd_base + static_cast<int64_t>(ci) * D * D;
 #pragma unroll
-    for (int e4 = 0; e4 < E; e4 += 4) {
-      const f4 x = __builtin_nontemporal_load(src + e4 / 4);
-      nb[e4] = x[0]; nb[e4 + 1] = x[1]; nb[e4 + 2] = x[2]; nb[e4 + 3] = x[3];
+    for (int m = 0; m < 4; ++m) {
+      const f4* part = reinterpret_cast<const f4*>(src + Q * ((c4 - m) & 3));
+#pragma unroll
+      for (int x = 0; x < Q; x += 4) {
+        const f4 y = __builtin_nontemporal_load(part + x / 4);
+        nb[m * Q + x] = y[0]; nb[m * Q + x + 1] = y[1];
+        nb[m * Q + x + 2] = y[2]; nb[m * Q + x + 3] = y[3];
+      }
     }
   };
 
   const int ntile = T / TT;
-  load_bnd(nchunk - 1);
+  if constexpr (kRecompute) {
+    if (nchunk >= 2) load_bnd(nchunk - 2);
+  } else {
+    load_bnd(nchunk - 1);
+  }
   load_tile((ntile - 1) * TT);
   store_tile(0);
   __syncthreads();
-  const int qo = q * (E + 4);
   for (int it = ntile - 1; it >= 0; --it) {
     const int slot = (ntile - 1 - it) & 1;
     const int tend = it * TT + TT;
     if (tend % kChunk == 0) {
-      // the tile ends a chunk: restart S from its snapshot and fold the P scale
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        Sh[e] = nb[e];
-        Ph[e] *= hs;
-      }
-      g = ig = hs = ihs = 1.0f;
       const int ci = tend / kChunk - 1;
-      if (ci > 0) load_bnd(ci - 1);
+      if constexpr (kRecompute) {
+        // rebuild the chunk's states forwards from its start state (the
+        // previous chunk's snapshot, zero for the first chunk), in the scaled
+        // form S_t = G_t Sh_t with G_t the running product of w_i; keep S_7
+        float G = 1.0f, iG = 1.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) Sh[e] = ci > 0 ? nb[e] : 0.0f;
+        if (ci >= 2) load_bnd(ci - 2);
+        for (int tt = 0; tt < TT; ++tt) {
+          const float wi = rows[slot][1][tt][row], ki = rows[slot][2][tt][row];
+          const float bi = rows[slot][4][tt][row];
+          float V[Q], SA[Q];
+          lds_read<Q>(&vec[slot][1][tt][own], V);
+          lds_read<Q>(&vec[slot][2][tt][own], SA);
+          G *= wi;
+          iG *= __builtin_amdgcn_rcpf(wi);
+          const float kf = ki * iG, bf = bi * iG;
+          auto fwd = [&](auto mc) {
+            constexpr int m = decltype(mc)::value;
+#pragma unroll
+            for (int x = 0; x < Q; ++x) {
+              fmac_rot<m>(Sh[m * Q + x], V[x], kf);
+              fmac_rot<m>(Sh[m * Q + x], SA[x], bf);
+            }
+          };
+          fwd(IC<0>{}); fwd(IC<1>{}); fwd(IC<2>{}); fwd(IC<3>{});
+          if (tt == kChunk / 2 - 1) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) Mid[e] = Sh[e] * G;
+          }
+        }
+        g = G;
+        ig = iG;
+      } else {
+        // restart S from the chunk's snapshot
+#pragma unroll
+        for (int e = 0; e < E; ++e) Sh[e] = nb[e];
+        g = ig = 1.0f;
+        if (ci > 0) load_bnd(ci - 1);
+      }
+      // fold the P scale
+#pragma unroll
+      for (int e = 0; e < E; ++e) Ph[e] *= hs;
+      hs = ihs = 1.0f;
     }
     if (it > 0) load_tile((it - 1) * TT);
     for (int tt = TT - 1; tt >= 0; --tt) {
       const float ri = rows[slot][0][tt][row], wi = rows[slot][1][tt][row];
       const float ki = rows[slot][2][tt][row], ai = rows[slot][3][tt][row];
       const float bi = rows[slot][4][tt][row], wsi = rows[slot][5][tt][row];
-      const float* DY = &vec[slot][0][tt][qo];
-      const float* V = &vec[slot][1][tt][qo];
-      const float* SA = &vec[slot][2][tt][qo];
-      const float* DS = &vec[slot][3][tt][qo];
+      float DY[Q], V[Q], SA[Q], DS[Q];
+      lds_read<Q>(&vec[slot][0][tt][own], DY);
+      lds_read<Q>(&vec[slot][1][tt][own], V);
+      lds_read<Q>(&vec[slot][2][tt][own], SA);
+      lds_read<Q>(&vec[slot][3][tt][own], DS);
       const float rw = __builtin_amdgcn_rcpf(wi);
       const float kg = -ki * ig, bg = -bi * ig;
       const float g_prev = g * rw, ihs_prev = ihs * rw;
       const float rh = ri * ihs, ah = ai * ihs_prev;
       float pr = 0.0f, pw = 0.0f, pk = 0.0f, pb = 0.0f, pa = 0.0f;
+      auto step = [&](auto mc) {
+        constexpr int m = decltype(mc)::value;
 #pragma unroll
-      for (int e4 = 0; e4 < E; e4 += 4) {
-        const float4 d4 = *reinterpret_cast<const float4*>(DY + e4);
-        const float4 v4 = *reinterpret_cast<const float4*>(V + e4);
-        const float4 s4 = *reinterpret_cast<const float4*>(SA + e4);
-        const float4 x4 = *reinterpret_cast<const float4*>(DS + e4);
-        const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
-        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-        const float ss[4] = {s4.x, s4.y, s4.z, s4.w};
-        const float xx[4] = {x4.x, x4.y, x4.z, x4.w};
-#pragma unroll
-        for (int z = 0; z < 4; ++z) {
-          const int e = e4 + z;
-          float s = Sh[e];
-          pr = fmaf(s, dd[z], pr);
-          s = fmaf(kg, vv[z], s);
-          s = fmaf(bg, ss[z], s);
-          Sh[e] = s;
-          const float p = fmaf(rh, dd[z], Ph[e]);
-          pw = fmaf(p, s, pw);
-          pk = fmaf(p, vv[z], pk);
-          pb = fmaf(p, ss[z], pb);
-          pa = fmaf(s, xx[z], pa);
-          Ph[e] = fmaf(ah, xx[z], p);
+        for (int x = 0; x < Q; ++x) {
+          float& sh = Sh[m * Q + x];
+          float& ph = Ph[m * Q + x];
+          fmac_rot<m>(pr, DY[x], sh);
+          fmac_rot<m>(sh, V[x], kg);
+          fmac_rot<m>(sh, SA[x], bg);
+          fmac_rot<m>(ph, DY[x], rh);
+          pw = fmaf(ph, sh, pw);
+          fmac_rot<m>(pk, V[x], ph);
+          fmac_rot<m>(pb, SA[x], ph);
+          fmac_rot<m>(pa, DS[x], sh);
+          fmac_rot<m>(ph, DS[x], ah);
         }
-      }
+      };
+      step(IC<0>{}); step(IC<1>{}); step(IC<2>{}); step(IC<3>{});
       pr = quad_sum(pr) * g;
       pw = quad_sum(pw) * (g_prev * hs) * wsi;
       pk = quad_sum(pk) * hs;
@@ -381,6 +475,13 @@ __global__ __launch_bounds__(256) void key_kernel(
       ig *= wi;
       hs *= wi;
       ihs = ihs_prev;
+      if (kRecompute && tt == kChunk / 2) {
+        // S_7 from the forward rebuild: the backward walk rebuilds at most 8
+        // steps through 1/w
+#pragma unroll
+        for (int e = 0; e < E; ++e) Sh[e] = Mid[e];
+        g = ig = 1.0f;
+      }
     }
     if (it > 0) store_tile(slot ^ 1);
     __syncthreads();

@@ -33,14 +33,32 @@ def _randn(shape, g, scale, dtype, device="cuda"):
 
 
 # ----------------------------------------------------------------- pretrain
-@pytest.mark.parametrize("batch,tokens,heads,head_size",
-                         [(1, 16, 1, 64), (2, 32, 2, 64), (1, 64, 3, 64), (1, 16, 1, 128),
-                          (1, 16, 1, 256)])
-def test_pretrain_forward_matches_oracle(batch, tokens, heads, head_size):
+def _pretrain_inputs(shape, head_size, g, structured):
+    """structured=False: every input 0.05 * randn (the reference's
+    tests/tmix/wkv7/pretrain/test.py:25-41); True: O(1) inputs with the
+    model's operand structure (kk unit-norm per head, a = -kk,
+    b = kk * sigmoid(N(0,1)), logits ~ N(0, 1.5^2))."""
+    if not structured:
+        return tuple(_randn(shape, g, 0.05, torch.bfloat16) for _ in range(6))
+    B, T, C = shape
+    kk = torch.randn((B, T, C // head_size, head_size), generator=g)
+    kk = kk / kk.norm(dim=-1, keepdim=True)
+    gate = torch.sigmoid(torch.randn(kk.shape, generator=g))
+    r, k, v = (torch.randn(shape, generator=g) for _ in range(3))
+    w = torch.randn(shape, generator=g) * 1.5
+    vals = (r, w, k, v, (-kk).reshape(shape), (kk * gate).reshape(shape))
+    return tuple(t.to(torch.bfloat16).cuda() for t in vals)
+
+
+@pytest.mark.parametrize("batch,tokens,heads,head_size,structured",
+                         [(1, 16, 1, 64, False), (2, 32, 2, 64, False), (2, 32, 2, 64, True),
+                          (1, 64, 3, 64, True), (1, 272, 2, 64, True), (1, 16, 1, 128, False),
+                          (1, 48, 2, 128, True), (1, 16, 1, 256, False), (1, 32, 1, 256, True)])
+def test_pretrain_forward_matches_oracle(batch, tokens, heads, head_size, structured):
     C = require_gpu()
     g = torch.Generator().manual_seed(20260806 + batch + tokens + heads)
     shape = (batch, tokens, heads * head_size)
-    vals = tuple(_randn(shape, g, 0.5, torch.bfloat16) for _ in range(6))
+    vals = _pretrain_inputs(shape, head_size, g, structured)
     y = pretrain_tmix_wkv7_recurrent_bf16(*vals, head_size=head_size)
     torch.cuda.synchronize()
     assert y.shape == shape and y.dtype == torch.bfloat16
