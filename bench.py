@@ -230,6 +230,65 @@ def time_fp16_state_decode(torch, flashrwkv2_amd, w, steps: int, warmup: int):
     return ms, start.elapsed_time(end) / (steps * 4)
 
 
+def time_graph_decode(torch, flashrwkv2_amd, w, steps: int = 16, reps: int = 20):
+    """Serving-style decode loop on the graph-ticket path: `steps` consecutive
+    T=1 steps (device-side metadata validation + recurrence each) captured in
+    one HIP graph.  Returns per-step ms for graph replay and for the same
+    steps issued eagerly."""
+    from flashrwkv2_amd.tmix.wkv7 import (infer_tmix_wkv7_recurrent_fp32io16_forward_varlen as wkv7,
+                                          prepare_tmix_wkv7_recurrent_metadata as prep)
+
+    n = w.state_indices.numel()
+    dev = w.r.device
+    state0 = w.state_pool
+    state = state0.clone()
+    n_tok = torch.full((1,), w.total_tokens, device=dev, dtype=torch.int32)
+    n_seq = torch.full((1,), n, device=dev, dtype=torch.int32)
+    live = dict(state_pool_size=state.shape[0], token_capacity=w.total_tokens,
+                sequence_capacity=n, max_seqlen_capacity=1, num_active_tokens=n_tok,
+                num_active_sequences=n_seq)
+
+    def loop():
+        for _ in range(steps):
+            t = prep(w.cu_seqlens, w.state_indices, **live)
+            wkv7(*w.tokens, state_pool=state, cu_seqlens=w.cu_seqlens,
+                 state_indices=w.state_indices, validated_metadata=t)
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        loop()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        loop()
+    state.copy_(state0)
+    graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    g_ms = max(start.elapsed_time(end), (time.perf_counter() - t0) * 1e3) / (reps * steps)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(reps):
+        loop()
+    end.record()
+    torch.cuda.synchronize()
+    e_ms = max(start.elapsed_time(end), (time.perf_counter() - t0) * 1e3) / (reps * steps)
+    del graph
+    return {"workload": w.name + "_graph_loop", "steps_per_graph": steps,
+            "graph_ms_per_step": round(g_ms, 5), "eager_ms_per_step": round(e_ms, 5),
+            "graph_tokens_per_s": round(w.total_tokens / (g_ms * 1e-3), 1),
+            "eager_tokens_per_s": round(w.total_tokens / (e_ms * 1e-3), 1)}
+
+
 # FMAs per (token, head) element of the D x D state in the training backward:
 # 5 in the value-column pass (P += r dy^T, dv, dsa, P = w P + a dsa^T) and 9 in
 # the key-row pass (dr, two for the S rebuild, two P updates, dw dk db da)
@@ -408,6 +467,13 @@ def main() -> int:
             "kernel": "decode64_kernel<IoF16,StF16>",
             "roofline": roofline_obj(bytes3, f16_kms), "algorithmic_bytes": bytes3,
         }
+        # the same decode shape, and a small serving batch, as a captured
+        # graph of consecutive steps on the graph-ticket path
+        result["decode_graph"] = [
+            time_graph_decode(torch, flashrwkv2_amd, workloads.config(2, "cuda", dtype=torch.float16)),
+            time_graph_decode(torch, flashrwkv2_amd,
+                              workloads.config(2, "cuda", dtype=torch.float16, batch=8)),
+        ]
         if not result.get("metric"):
             result.update({"metric": METRIC, "value": result["decode"]["tokens_per_s"],
                            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
