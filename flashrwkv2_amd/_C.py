@@ -705,6 +705,211 @@ def rl_infctx_tmix_wkv7_chunk_fp32io16_backward_replay(chunk_token_starts, chunk
     N.check(rc, "rl_infctx_tmix_wkv7_chunk_fp32io16_backward_replay")
 
 
+# ---------------------------------------------------------------------------
+# producer / consumer stages of the layer: wkv_prepare and readout (fp16)
+# ---------------------------------------------------------------------------
+# The dense and low-rank projections are plain library GEMMs (torch matmul on
+# hipBLASLt, fp16 in, fp32 accumulate, fp16 out); every elementwise stage is
+# one of this library's HIP kernels.
+
+def _check_half(t, ref, name):
+    _check(isinstance(t, torch.Tensor) and t.is_cuda, name, " must be CUDA")
+    _check(t.is_contiguous(), name, " must be contiguous")
+    _check(t.dtype == torch.float16, name, " must be float16")
+    check_same_device(ref, t, name)
+
+
+def _check_scale(scale, what):
+    _check(math.isfinite(scale) and abs(scale) <= 3.4028234663852886e38,
+           what, " must be finite and representable as float32")
+
+
+def _project(x, weight, lora_a, lora_b, lora_scale):
+    """wkv_prepare_project_internal, infer_fp16_forward_varlen.cpp:192-232."""
+    _check(lora_a is None or lora_b is not None, "lora_a and lora_b must be provided together")
+    _check(lora_b is None or lora_a is not None, "lora_a and lora_b must be provided together")
+    _check_scale(lora_scale, "lora_scale")
+    out = torch.matmul(x, weight.t())
+    if lora_a is None:
+        return out
+    _check_half(lora_a, x, "lora_a")
+    _check_half(lora_b, x, "lora_b")
+    _check(lora_a.dim() == 2 and lora_a.size(0) > 0 and lora_a.size(1) == x.size(1),
+           "lora_a must have shape [R,K]")
+    _check(lora_a.size(0) <= 512, "LoRA projection requires R<=512")
+    _check(lora_b.dim() == 2 and lora_b.size(0) == weight.size(0)
+           and lora_b.size(1) == lora_a.size(0), "lora_b must have shape [N,R]")
+    if float(torch.tensor(lora_scale, dtype=torch.float32)) == 0.0:
+        return out
+    return torch.addmm(out, torch.matmul(x, lora_a.t()), lora_b.t(), alpha=float(lora_scale))
+
+
+def _rank_weights(x, runtime, original, rank_in):
+    """check_rank_dispatch, infer_fp16_forward_varlen.cpp:104-150."""
+    _check(runtime is not None or original is not None,
+           "one of weight or weight_t must be provided")
+    if runtime is not None:
+        _check_half(runtime, x, "weight")
+        _check(runtime.dim() == 2 and runtime.size(0) == x.size(1),
+               "rank-in runtime weight must have shape [input,rank]" if rank_in
+               else "rank-out runtime weight must have shape [rank,output]")
+    if original is not None:
+        _check_half(original, x, "weight_t")
+        _check(original.dim() == 2 and original.size(1) == x.size(1),
+               "rank-in original weight must have shape [rank,input]" if rank_in
+               else "rank-out original weight must have shape [output,rank]")
+    if runtime is not None and original is not None:
+        r_rank = runtime.size(1) if rank_in else runtime.size(0)
+        o_rank = original.size(0) if rank_in else original.size(1)
+        _check(r_rank == o_rank, "weight and weight_t must describe the same rank projection")
+    rank = ((runtime.size(1) if rank_in else runtime.size(0)) if runtime is not None
+            else (original.size(0) if rank_in else original.size(1)))
+    _check(rank <= 512, "low-rank projection requires R<=512")
+
+
+def _rank_mm(x, runtime, original, rank_in):
+    _rank_weights(x, runtime, original, rank_in)
+    return torch.matmul(x, runtime) if runtime is not None else torch.matmul(x, original.t())
+
+
+def _lowrank_activate(w1x, g1x):
+    tw, sg = torch.empty_like(w1x), torch.empty_like(g1x)
+    rc = N.load().fr2_tmix_lowrank_activate(w1x.numel(), w1x.data_ptr(), tw.data_ptr(),
+                                            g1x.numel(), g1x.data_ptr(), sg.data_ptr(),
+                                            _stream(w1x.device))
+    N.check(rc, "fr2_tmix_lowrank_activate")
+    return tw, sg
+
+
+def tmix_wkv_prepare_forward_varlen(
+        x_r, x_w, x_k, x_v, x_a, x_g, receptance_weight, key_weight, value_weight,
+        w1_t, a1_t, g1_t, v1_t, w2_t, a2_t, g2_t, v2_t, v0, k_k, a0, k_a,
+        v_first=None, w1=None, a1=None, g1=None, v1=None, w2=None, a2=None, g2=None, v2=None,
+        receptance_lora_a=None, receptance_lora_b=None, receptance_lora_scale=1.0,
+        key_lora_a=None, key_lora_b=None, key_lora_scale=1.0,
+        value_lora_a=None, value_lora_b=None, value_lora_scale=1.0,
+        head_size=64, batch_size=1, max_seqlen=1):
+    """tmix_wkv_prepare_forward_varlen, infer_fp16_forward_varlen.cpp:421-530.
+
+    Returns [receptance, decay logits, prepared key, value, a (= -kk),
+    b (= kk * a gate), output gate, v_first], each [total_tokens, C] fp16.
+    ``w1_t`` .. ``v2_t`` are the original ([rank,C] in, [C,rank] out)
+    layouts, ``w1`` .. ``v2`` the runtime ([C,rank] in, [rank,C] out) ones.
+    """
+    for t, name in ((x_r, "x_r"), (x_w, "x_w"), (x_k, "x_k"), (x_v, "x_v"), (x_a, "x_a"),
+                    (x_g, "x_g")):
+        _check_half(t, x_r, name)
+        _check(t.dim() == 2 and t.size(0) == x_r.size(0),
+               name, " must have packed shape [total_tokens,features]")
+        _check(t.shape == x_r.shape, name, " must match x_r's packed shape")
+    _check(head_size in (64, 128, 256), "head_size must be one of 64, 128, or 256")
+    T, C = x_r.shape
+    _check(C % head_size == 0, "channels must be divisible by head_size")
+    _check(batch_size > 0 and max_seqlen > 0, "batch_size and max_seqlen must be positive")
+    for t, name in ((receptance_weight, "receptance_weight"), (key_weight, "key_weight"),
+                    (value_weight, "value_weight")):
+        _check_half(t, x_r, name)
+        _check(t.dim() == 2 and t.size(0) == C and t.size(1) == C, name, " must have shape [C,C]")
+    receptance = _project(x_r, receptance_weight, receptance_lora_a, receptance_lora_b,
+                          receptance_lora_scale)
+    key = _project(x_k, key_weight, key_lora_a, key_lora_b, key_lora_scale)
+    value = _project(x_v, value_weight, value_lora_a, value_lora_b, value_lora_scale)
+    w1x = _rank_mm(x_w, w1, w1_t, True)
+    a1x = _rank_mm(x_a, a1, a1_t, True)
+    g1x = _rank_mm(x_g, g1, g1_t, True)
+    tw, sg = _lowrank_activate(w1x, g1x)
+    decay = _rank_mm(tw, w2, w2_t, False)
+    a12 = _rank_mm(a1x, a2, a2_t, False)
+    gate = _rank_mm(sg, g2, g2_t, False)
+    for t, name in ((decay, "w2"), (a12, "a2"), (gate, "g2")):
+        _check(t.size(1) == C, name, " runtime layout must have shape [R,C]")
+    if v_first is not None:
+        _check_half(v_first, x_r, "v_first")
+        _check(v_first.shape == value.shape, "v and v_first must have shape [total_tokens,C]")
+        _check_half(v0, x_r, "v0")
+        _check(v0.dim() == 1 and v0.size(0) == C, "v0 must have shape [C]")
+        v12 = _rank_mm(_rank_mm(x_v, v1, v1_t, True), v2, v2_t, False)
+        mixed = torch.empty_like(value)
+        rc = N.load().fr2_tmix_vres_forward(T, C, value.data_ptr(), v_first.data_ptr(),
+                                            v0.data_ptr(), v12.data_ptr(), mixed.data_ptr(),
+                                            _stream(x_r.device))
+        N.check(rc, "fr2_tmix_vres_forward")
+        value = mixed
+        returned_v_first = v_first
+    else:
+        # the first layer validates the value branch's layouts without running it
+        _rank_weights(x_v, v1, v1_t, True)
+        v_rank = v1.size(1) if v1 is not None else v1_t.size(0)
+        _check(v2 is not None or v2_t is not None, "v2 requires an original or runtime layout")
+        if v2_t is not None:
+            _check_half(v2_t, x_r, "v2")
+            _check(v2_t.dim() == 2 and v2_t.size(0) == C and v2_t.size(1) == v_rank,
+                   "v2 original layout must have shape [C,R]")
+        if v2 is not None:
+            _check_half(v2, x_r, "v2")
+            _check(v2.dim() == 2 and v2.size(0) == v_rank and v2.size(1) == C,
+                   "v2 runtime layout must have shape [R,C]")
+        returned_v_first = value
+    for t, name in ((k_k, "k_k"), (a0, "a0"), (k_a, "k_a")):
+        _check_half(t, x_r, name)
+        _check(t.dim() == 1 and t.size(0) == C, name, " must have shape [C]")
+    prepared_key, neg_kk, kka = (torch.empty_like(key) for _ in range(3))
+    rc = N.load().fr2_tmix_kk_a_gate_forward(
+        T, C // head_size, head_size, key.data_ptr(), k_k.data_ptr(), a0.data_ptr(),
+        a12.data_ptr(), k_a.data_ptr(), prepared_key.data_ptr(), neg_kk.data_ptr(),
+        kka.data_ptr(), _stream(x_r.device))
+    N.check(rc, "fr2_tmix_kk_a_gate_forward")
+    return [receptance, decay, prepared_key, value, neg_kk, kka, gate, returned_v_first]
+
+
+def tmix_readout_forward_varlen(wkv_output, receptance, key, value, r_k, ln_weight, ln_bias,
+                                gate, output_weight, output_lora_a=None, output_lora_b=None,
+                                output_lora_scale=1.0, head_size=64, batch_size=1, max_seqlen=1):
+    """tmix_readout_forward_varlen, csrc/sm120/tmix/readout/infer_fp16_forward_varlen.cpp:88-140:
+    the fused group-norm / r.k residual / gate stage (HIP) stored in fp16,
+    then the output projection (+ LoRA) as a library GEMM."""
+    x = wkv_output
+    _check_half(x, x, "x")
+    _check(head_size in (64, 128, 256), "head_size must be one of 64, 128, or 256")
+    _check(x.dim() == 2 and x.size(0) > 0 and x.size(1) > 0 and x.size(1) % head_size == 0,
+           "x must have packed shape [total_tokens,H*head_size]")
+    _check(batch_size > 0, "batch_size must be positive")
+    _check(max_seqlen > 0, "max_seqlen must be positive")
+    T, C = x.shape
+    for t, name in ((receptance, "r"), (key, "k"), (value, "v"), (gate, "g")):
+        _check_half(t, x, name)
+        _check(t.shape == x.shape, name, " must match x's packed shape")
+    for t, name in ((r_k, "r_k"), (ln_weight, "weight"), (ln_bias, "bias")):
+        _check_half(t, x, name)
+        _check(t.dim() == 1 and t.size(0) == C, name, " must have shape [C]")
+    pre = torch.empty_like(x)
+    rc = N.load().fr2_tmix_readout_prelinear_forward(
+        T, C // head_size, head_size, x.data_ptr(), receptance.data_ptr(), key.data_ptr(),
+        value.data_ptr(), r_k.data_ptr(), ln_weight.data_ptr(), ln_bias.data_ptr(),
+        gate.data_ptr(), pre.data_ptr(), _stream(x.device))
+    N.check(rc, "fr2_tmix_readout_prelinear_forward")
+    _check_half(output_weight, x, "output_weight")
+    _check(output_weight.dim() == 2 and output_weight.size(0) == C and output_weight.size(1) == C,
+           "output_weight must have shape [C,C]")
+    _check((output_lora_a is None) == (output_lora_b is None),
+           "output_lora_a and output_lora_b must be provided together")
+    _check_scale(output_lora_scale, "output_lora_scale")
+    out = torch.matmul(pre, output_weight.t())
+    if output_lora_a is None:
+        return out
+    _check_half(output_lora_a, x, "output_lora_a")
+    _check_half(output_lora_b, x, "output_lora_b")
+    _check(output_lora_a.dim() == 2 and output_lora_a.size(1) == C,
+           "output_lora_a must have shape [R,C]")
+    _check(0 < output_lora_a.size(0) <= 512, "output LoRA projection requires 0<R<=512")
+    _check(output_lora_b.dim() == 2 and output_lora_b.size(0) == C
+           and output_lora_b.size(1) == output_lora_a.size(0), "output_lora_b must have shape [C,R]")
+    if float(torch.tensor(output_lora_scale, dtype=torch.float32)) == 0.0:
+        return out
+    return torch.addmm(out, torch.matmul(pre, output_lora_a.t()), output_lora_b.t(),
+                       alpha=float(output_lora_scale))
+
+
 def exported_names() -> Sequence[str]:
     return (
         "prepare_tmix_wkv7_recurrent_metadata",
@@ -716,4 +921,6 @@ def exported_names() -> Sequence[str]:
         "infer_tmix_wkv7_chunk_bf16_forward_varlen",
         "rl_infctx_tmix_wkv7_chunk_fp32io16_forward",
         "rl_infctx_tmix_wkv7_chunk_fp32io16_backward_replay",
+        "tmix_wkv_prepare_forward_varlen",
+        "tmix_readout_forward_varlen",
     )

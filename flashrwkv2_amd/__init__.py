@@ -37,7 +37,12 @@ from .tmix.wkv7 import (  # noqa: E402
     rl_infctx_tmix_wkv7_chunk_fp32io16_factor_recompute,
 )
 
+from .tmix.readout import infer_tmix_readout_forward_varlen  # noqa: E402
+from .tmix.wkv_prepare import infer_tmix_wkv_prepare_forward_varlen  # noqa: E402
+
 __all__ = [
+    "infer_tmix_readout_forward_varlen",
+    "infer_tmix_wkv_prepare_forward_varlen",
     "infer_tmix_wkv7_chunk_bf16_forward_varlen",
     "infer_tmix_wkv7_recurrent_fp16_forward_varlen",
     "infer_tmix_wkv7_recurrent_fp32io16_forward_varlen",

@@ -68,6 +68,18 @@ SIGNATURES: dict[str, tuple] = {
         c_int32,
         [c_int32, c_int32, c_int32, c_int32] + [c_void_p] * 17,
     ),
+    "fr2_tmix_kk_a_gate_forward": (
+        c_int32, [c_int64, c_int32, c_int32] + [c_void_p] * 9,
+    ),
+    "fr2_tmix_lowrank_activate": (
+        c_int32, [c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p],
+    ),
+    "fr2_tmix_vres_forward": (
+        c_int32, [c_int64, c_int32] + [c_void_p] * 6,
+    ),
+    "fr2_tmix_readout_prelinear_forward": (
+        c_int32, [c_int64, c_int32, c_int32] + [c_void_p] * 10,
+    ),
     "fr2_wkv7_chunk_bf16_forward": (
         c_int32,
         [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int64, c_int32,

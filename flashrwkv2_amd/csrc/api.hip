@@ -275,3 +275,52 @@ extern "C" int fr2_wkv7_rl_infctx_replay(
   return fr2::launch_serial(head_size, dtype, false, p, num_chunks,
                             static_cast<hipStream_t>(stream));
 }
+
+// ---------------------------------------------------------------------------
+// producer / consumer stages of the layer (fp16)
+// ---------------------------------------------------------------------------
+extern "C" int fr2_tmix_kk_a_gate_forward(int64_t tokens, int32_t num_heads, int32_t head_size,
+                                          const void* k, const void* k_k, const void* a0,
+                                          const void* a12, const void* k_a, void* new_k,
+                                          void* neg_kk, void* kka, void* stream) {
+  if (!k || !k_k || !a0 || !a12 || !k_a || !new_k || !neg_kk || !kka)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (tokens <= 0 || num_heads <= 0) return FR2_ERR_INVALID_ARGUMENT;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return FR2_ERR_UNSUPPORTED;
+  return fr2::launch_kk_a_gate(tokens, num_heads, head_size, k, k_k, a0, a12, k_a, new_k, neg_kk,
+                               kka, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fr2_tmix_lowrank_activate(int64_t n_tanh, const void* tanh_in, void* tanh_out,
+                                         int64_t n_sigmoid, const void* sigmoid_in,
+                                         void* sigmoid_out, void* stream) {
+  if (n_tanh < 0 || n_sigmoid < 0) return FR2_ERR_INVALID_ARGUMENT;
+  if ((n_tanh > 0 && (!tanh_in || !tanh_out)) || (n_sigmoid > 0 && (!sigmoid_in || !sigmoid_out)))
+    return FR2_ERR_INVALID_ARGUMENT;
+  return fr2::launch_lowrank_act(n_tanh, tanh_in, tanh_out, n_sigmoid, sigmoid_in, sigmoid_out,
+                                 static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fr2_tmix_vres_forward(int64_t tokens, int32_t channels, const void* value,
+                                     const void* v_first, const void* v0, const void* v12,
+                                     void* output, void* stream) {
+  if (!value || !v_first || !v0 || !v12 || !output) return FR2_ERR_INVALID_ARGUMENT;
+  if (tokens <= 0 || channels <= 0 || channels % 8 != 0) return FR2_ERR_INVALID_ARGUMENT;
+  return fr2::launch_vres(tokens, channels, value, v_first, v0, v12, output,
+                          static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fr2_tmix_readout_prelinear_forward(int64_t tokens, int32_t num_heads,
+                                                  int32_t head_size, const void* wkv_output,
+                                                  const void* r, const void* k, const void* v,
+                                                  const void* r_k, const void* ln_weight,
+                                                  const void* ln_bias, const void* gate,
+                                                  void* output, void* stream) {
+  if (!wkv_output || !r || !k || !v || !r_k || !ln_weight || !ln_bias || !gate || !output)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (tokens <= 0 || num_heads <= 0) return FR2_ERR_INVALID_ARGUMENT;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return FR2_ERR_UNSUPPORTED;
+  return fr2::launch_readout_prelinear(tokens, num_heads, head_size, wkv_output, r, k, v, r_k,
+                                       ln_weight, ln_bias, gate, output,
+                                       static_cast<hipStream_t>(stream));
+}

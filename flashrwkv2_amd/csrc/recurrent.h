@@ -71,4 +71,16 @@ struct PretrainBwdArgs {
 };
 int launch_pretrain_backward(int D, const PretrainBwdArgs& p, hipStream_t s);
 
+// Elementwise producer / consumer stages of the layer (fp16 I/O).
+int launch_kk_a_gate(int64_t tokens, int H, int D, const void* k, const void* k_k, const void* a0,
+                     const void* a12, const void* k_a, void* new_k, void* neg_kk, void* kka,
+                     hipStream_t s);
+int launch_lowrank_act(int64_t n_t, const void* xt, void* yt, int64_t n_s, const void* xs, void* ys,
+                       hipStream_t s);
+int launch_vres(int64_t tokens, int C, const void* value, const void* v_first, const void* v0,
+                const void* v12, void* out, hipStream_t s);
+int launch_readout_prelinear(int64_t tokens, int H, int D, const void* x, const void* r,
+                             const void* k, const void* v, const void* r_k, const void* ln_w,
+                             const void* ln_b, const void* g, void* out, hipStream_t s);
+
 }  // namespace fr2

@@ -235,6 +235,57 @@ int fr2_wkv7_rl_infctx_replay(const int32_t* chunk_token_starts,
                               void* output, float* state_dot_a, float scale,
                               void* stream);
 
+/* ------------------------------------------------------------------------
+ * Producer and consumer stages of the WKV7 path (fp16 tensors, fp32 math).
+ * ---------------------------------------------------------------------- */
+
+/*
+ * Key / a-gate stage: per (token, head) of [tokens, H*D] fp16 rows,
+ *   u = k * k_k, kk = u / max(|u|, 1e-12), a = sigmoid(a0 + a12),
+ *   new_k = k * (1 + (a - 1) * k_a), neg_kk = -kk, kka = kk * a,
+ * with k_k, a0, k_a of shape [H*D].  Replaces tmix_kk_a_gate_forward_varlen_cuda
+ * (csrc/sm120/tmix/wkv_prepare/internal/kk_a_gate/infer_fp16_forward_varlen.cu,
+ *  called from csrc/sm120/tmix/wkv_prepare/infer_fp16_forward_varlen.cpp:520-528).
+ */
+int fr2_tmix_kk_a_gate_forward(int64_t tokens, int32_t num_heads, int32_t head_size,
+                               const void* k, const void* k_k, const void* a0,
+                               const void* a12, const void* k_a, void* new_k,
+                               void* neg_kk, void* kka, void* stream);
+
+/*
+ * Low-rank branch activations: tanh_out = tanh(tanh_in) over n_tanh values
+ * and sigmoid_out = sigmoid(sigmoid_in) over n_sigmoid values (fp16, one
+ * launch).  Replaces lowrank_tanh_f16_cuda / lowrank_sigmoid_f16_cuda
+ * (csrc/sm120/tmix/wkv_prepare/internal/lowrank/infer_fp16_forward_varlen.cu:423-448).
+ */
+int fr2_tmix_lowrank_activate(int64_t n_tanh, const void* tanh_in, void* tanh_out,
+                              int64_t n_sigmoid, const void* sigmoid_in, void* sigmoid_out,
+                              void* stream);
+
+/*
+ * Value residual of later layers over [tokens, C] fp16 (C % 8 == 0):
+ *   output = value + (v_first - value) * sigmoid(v0 + v12),  v0 of shape [C].
+ * Replaces wkv_prepare_vres_forward_varlen_cuda
+ * (csrc/sm120/tmix/wkv_prepare/internal/lowrank/infer_vres_fp16_forward_varlen.cu).
+ */
+int fr2_tmix_vres_forward(int64_t tokens, int32_t channels, const void* value,
+                          const void* v_first, const void* v0, const void* v12,
+                          void* output, void* stream);
+
+/*
+ * Readout before the output projection: per (token, head) of [tokens, H*D]
+ * fp16 rows, group norm of the WKV output (eps 64e-5) with ln_weight /
+ * ln_bias, plus sum(r * k * r_k) * v, times the gate; fp16 result.
+ * Replaces tmix_lnx_rkvres_xg_forward_varlen_cuda
+ * (csrc/sm120/tmix/readout/infer_fp16_forward_varlen.cu, called from
+ *  csrc/sm120/tmix/readout/infer_fp16_forward_varlen.cpp:44-86).
+ */
+int fr2_tmix_readout_prelinear_forward(int64_t tokens, int32_t num_heads, int32_t head_size,
+                                       const void* wkv_output, const void* r, const void* k,
+                                       const void* v, const void* r_k, const void* ln_weight,
+                                       const void* ln_bias, const void* gate, void* output,
+                                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,10 @@ adds numpy conveniences.  What each function restates:
   csrc/sm120/tmix/wkv7/pretrain_recurrent_bf16_forward.cu:163-286; pinned in
   tests/test_oracle_backward.py by central differences of ``wkv7_f64`` and
   by torch autograd of an fp64 per-token loop.
+* ``prepare`` (numpy, ``oracle/prepare.py``) — the producer / consumer
+  stages either side of the recurrence (wkv_prepare's kk / a gate, low-rank
+  branches and value residual; readout's group norm, residual, gate and
+  projection); pinned in tests/test_oracle_prepare.py.
 * ``wkv7_cpu_f32`` — the same recurrence in float, OpenMP over
   (sequence, head): the CPU baseline that bench.py times.
 * ``albatross_dither`` / ``wkv7_fp16_state`` (numpy) — the FP16-state
