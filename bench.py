@@ -289,6 +289,61 @@ def time_graph_decode(torch, flashrwkv2_amd, w, steps: int = 16, reps: int = 20)
             "eager_tokens_per_s": round(w.total_tokens / (e_ms * 1e-3), 1)}
 
 
+def time_layer_stages(torch, tokens: int, heads: int, steps: int = 20):
+    """HBM rates of the fused elementwise stages either side of the
+    recurrence on a config-1-sized token block ([tokens, heads*64] fp16):
+    kk/a gate (reads k, a12; writes key, a, b: 10 B per element), value
+    residual (reads value, v_first, v12; writes value: 8 B) and the readout
+    prelinear stage (reads wkv output, r, k, v, gate; writes 1: 12 B).
+    Per-launch times from HIP events around direct C-ABI launches."""
+    from flashrwkv2_amd import _native as N
+
+    D = 64
+    C = heads * D
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(3001)
+
+    def t(*shape):
+        return torch.randn(shape, generator=g, device=dev).half()
+
+    lib = N.load()
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+    k, a12, v, vf, v12, x, r, gt = (t(tokens, C) for _ in range(8))
+    kk, a0, ka, v0, rk, lw, lb = (t(C) for _ in range(7))
+    o1, o2, o3 = (torch.empty_like(k) for _ in range(3))
+    cases = {
+        "kk_a_gate_kernel<64>": (
+            10, lambda: lib.fr2_tmix_kk_a_gate_forward(
+                tokens, heads, D, k.data_ptr(), kk.data_ptr(), a0.data_ptr(), a12.data_ptr(),
+                ka.data_ptr(), o1.data_ptr(), o2.data_ptr(), o3.data_ptr(), sh)),
+        "vres_kernel": (
+            8, lambda: lib.fr2_tmix_vres_forward(tokens, C, v.data_ptr(), vf.data_ptr(),
+                                                 v0.data_ptr(), v12.data_ptr(), o1.data_ptr(), sh)),
+        "readout_prelinear_kernel<64>": (
+            12, lambda: lib.fr2_tmix_readout_prelinear_forward(
+                tokens, heads, D, x.data_ptr(), r.data_ptr(), k.data_ptr(), v.data_ptr(),
+                rk.data_ptr(), lw.data_ptr(), lb.data_ptr(), gt.data_ptr(), o2.data_ptr(), sh)),
+    }
+    out = {}
+    for name, (bpe, fn) in cases.items():
+        N.check(fn(), name)
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / steps
+        nbytes = bpe * tokens * C
+        out[name] = {"kernel_ms": round(ms, 5), "algorithmic_bytes": nbytes,
+                     "roofline": roofline_obj(nbytes, ms)}
+    return {"workload": f"cfg1_tokens{tokens}_C{C}_fp16", "kernels": out}
+
+
 # FMAs per (token, head) element of the D x D state in the training backward:
 # 5 in the value-column pass (P += r dy^T, dv, dsa, P = w P + a dsa^T) and 9 in
 # the key-row pass (dr, two for the S rebuild, two P updates, dw dk db da)
@@ -379,7 +434,7 @@ def main() -> int:
                     help="tokens per sequence in the CPU baseline sample")
     ap.add_argument("--no-train", action="store_true",
                     help="skip the training (forward + backward) leg")
-    ap.add_argument("--only", choices=["prefill", "decode", "train"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "train", "stages"], default=None,
                     help="run one leg only (profiling)")
     ap.add_argument("--config", type=int, default=1, choices=[1, 3, 4],
                     help="prefill workload (BASELINE config; the metric is quoted on 1)")
@@ -481,6 +536,8 @@ def main() -> int:
     if args.only in (None, "train") and not args.no_train:
         wt = pre.w if (pre is not None and args.config == 1) else workloads.config(1, "cuda")
         result["pretrain_training"] = time_pretrain_training(torch, wt, max(3, args.steps // 4))
+    if args.only in (None, "stages"):
+        result["layer_stages"] = time_layer_stages(torch, 8 * 4096, 32)
     if pre is not None and not args.no_cpu and args.config == 1:
         threads = min(16, os.cpu_count() or 1)
         tps, dt, n_tok, reps = cpu_baseline(pre.w, threads, args.cpu_sample_tokens)
