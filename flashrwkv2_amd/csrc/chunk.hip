@@ -274,11 +274,13 @@ struct KeyRegs {
 
 // kFull: every token of the chunk is inside the sequence (no masking).
 // nbias8 holds -log2(e) * decay_bias for the lane's keys.
-template <class Io, bool kVExact, bool kFull>
+// kUnitW: reverse mode, where unit_w marks a lane whose shifted retention
+// row lies past the segment (unit retention).
+template <class Io, bool kVExact, bool kFull, bool kUnitW = false>
 __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& op,
                                           const u32x4 (&raw)[6], const float (&nbias8)[8],
                                           bool valid, int mp, int cc, int hh, int i, int q,
-                                          KeyRegs& kr) {
+                                          KeyRegs& kr, bool unit_w = false) {
   const int kbase = 32 * hh + 8 * q;
   // tokens past the sequence end (their rows repeat the last token) carry
   // zero operands and a unit retention
@@ -300,6 +302,7 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
     const float ex = __builtin_amdgcn_exp2f(__builtin_fmaf(xl[e], -kLog2e, nbias8[e]));
     float lw2 = __builtin_amdgcn_rcpf(__builtin_fmaf(ex, kInvC, kInvC));
     if constexpr (!kFull) lw2 = valid ? lw2 : 0.0f;
+    if constexpr (kUnitW) lw2 = unit_w ? 0.0f : lw2;
     const float g2 = row_scan(lw2);
     const float gm = __builtin_amdgcn_exp2f(g2);      // gamma_t
     const float gp = row_prev(gm, 1.0f);              // gamma_{t-1}
@@ -469,13 +472,14 @@ __device__ __forceinline__ StateOps<kVExact> state_load(const ChunkOps<kVExact>&
   return o;
 }
 
-// With kTrain the chunk also writes its per-token sa rows (U, fp32) to
-// sa_col[token * row_stride] and its post-chunk state column to bnd_col[key * D].
+// With kTrain the chunk also writes its per-token sa rows (U, fp32) of tokens
+// 4q..4q+3 to sa_rows[0..3] and, when bnd_col is set, its post-chunk state
+// column to bnd_col[key * D].
 template <class Io, bool kVExact, bool kTrain = false>
 __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 (&S)[4],
                                               uint16_t (*yrows)[YP], int vcol, int i, int q,
-                                              float scale, float* sa_col = nullptr,
-                                              int64_t row_stride = 0, float* bnd_col = nullptr) {
+                                              float scale, float* const* sa_rows = nullptr,
+                                              float* bnd_col = nullptr) {
   using raw = typename Io::raw;
   // S split as B operand against the permuted A~ / R~ rows: K positions
   // 8q..8q+7 = rows 32m + 4q + (0..3) then 32m + 16 + 4q + (0..3)
@@ -502,7 +506,7 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
     Y = mm_ab(o.Mrb, Us, Y);
     if constexpr (kTrain) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sa_col[(4 * q + e) * row_stride] = Uf[e];
+      for (int e = 0; e < 4; ++e) *sa_rows[e] = Uf[e];
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -515,8 +519,10 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
       acc = mm_ax(o.Kt[kb], Vx, acc);
       S[kb] = acc * o.gl[kb];
       if constexpr (kTrain) {
+        if (bnd_col != nullptr) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bnd_col[(16 * kb + 4 * q + e) * D] = S[kb][e];
+          for (int e = 0; e < 4; ++e) bnd_col[(16 * kb + 4 * q + e) * D] = S[kb][e];
+        }
       }
     }
   } else {
@@ -532,7 +538,7 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
     Y = mm_ab(o.Mrb, Us, Y);
     if constexpr (kTrain) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sa_col[(4 * q + e) * row_stride] = Uf[e];
+      for (int e = 0; e < 4; ++e) *sa_rows[e] = Uf[e];
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -545,8 +551,10 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
       acc = mm_ab(o.Kt[kb], Vs, acc);
       S[kb] = acc * o.gl[kb];
       if constexpr (kTrain) {
+        if (bnd_col != nullptr) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bnd_col[(16 * kb + 4 * q + e) * D] = S[kb][e];
+          for (int e = 0; e < 4; ++e) bnd_col[(16 * kb + 4 * q + e) * D] = S[kb][e];
+        }
       }
     }
   }
@@ -590,7 +598,7 @@ __device__ __forceinline__ void wait_min_ge(int* c, int v) {
 // kTrain: the training-forward contract (pretrain path) also writes every
 // token's sa (p.sa_out) and the post-chunk state of every 16-token chunk
 // (p.boundary, [segment, H, boundary_per_seg, D, D]).
-template <class Io, bool kTrain>
+template <class Io, bool kTrain, bool kRev = false>
 __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
   using raw = typename Io::raw;
   constexpr bool kVExact = !__is_same(Io, IoF16);
@@ -654,28 +662,40 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
     // outputs of a finished group: 16-byte pieces of the staged rows, token
     // tid/8, elements 8*(tid%8).. (the four state waves cover the 32 rows)
     const int o_tok = tid >> 3, o_c8 = tid & 7;
-    raw* const ybase = yout + static_cast<int64_t>(t0 + o_tok) * row_stride + head_off + o_c8 * 8;
-    const int64_t gstride = static_cast<int64_t>(GT) * row_stride;
+    const int seg_len = t1 - t0;
     auto write_out = [&](int gi) {
       if (gi < 0) return;
       wait_min_ge(sm.consumed, gi + 1);       // every state wave staged its columns
-      if (t0 + gi * GT + o_tok < t1)
-        *reinterpret_cast<u32x4*>(ybase + static_cast<int64_t>(gi) * gstride) =
+      const int pos = gi * GT + o_tok;        // position in processing order
+      if (pos < seg_len) {
+        const int row = kRev ? t1 - 1 - pos : t0 + pos;
+        *reinterpret_cast<u32x4*>(yout + static_cast<int64_t>(row) * row_stride + head_off +
+                                  o_c8 * 8) =
             *reinterpret_cast<const u32x4*>(&sm.yb[gi & 1][o_tok][o_c8 * 8]);
+      }
       signal(&sm.drained[wv], gi + 1);
     };
     // training outputs: sa column of this lane and the boundary column
-    float* const sa_base =
-        kTrain ? p.sa_out + static_cast<int64_t>(t0) * row_stride + head_off + vcol : nullptr;
+    float* const sa_base = kTrain ? p.sa_out + head_off + vcol : nullptr;
     float* const bnd_base =
-        kTrain ? p.boundary + (static_cast<int64_t>(seg) * H + h) * p.boundary_per_seg * D * D + vcol
-               : nullptr;
+        (kTrain && p.boundary != nullptr)
+            ? p.boundary + (static_cast<int64_t>(seg) * H + h) * p.boundary_per_seg * D * D + vcol
+            : nullptr;
     auto chunk = [&](const StateOps<kVExact>& o, int gi, int c) {
       const int ci = gi * G + c;   // chunk index within the segment
+      float* sa_rows[4];
+      if constexpr (kTrain) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int pos = ci * L + 4 * q + e;
+          const int row = kRev ? t0 + (seg_len - pos) % seg_len : t0 + pos;
+          sa_rows[e] = sa_base + static_cast<int64_t>(row) * row_stride;
+        }
+      }
+      const int bi = kRev ? p.boundary_per_seg - 1 - ci : ci;
       state_compute<Io, kVExact, kTrain>(
-          o, S, &sm.yb[gi & 1][c * L], vcol, i, q, p.scale,
-          kTrain ? sa_base + static_cast<int64_t>(ci) * L * row_stride : nullptr, row_stride,
-          kTrain ? bnd_base + static_cast<int64_t>(ci) * D * D : nullptr);
+          o, S, &sm.yb[gi & 1][c * L], vcol, i, q, p.scale, sa_rows,
+          bnd_base != nullptr ? bnd_base + static_cast<int64_t>(bi) * D * D : nullptr);
     };
     auto group = [&](auto par_c, int gi) {
       constexpr int par = decltype(par_c)::value;
@@ -729,7 +749,7 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
     const int tok0 = t0 + cc * L + i;
     const raw* src[6];
     {
-      const int64_t off = static_cast<int64_t>(tok0) * row_stride + head_off + kbase;
+      const int64_t off = static_cast<int64_t>(kRev ? 0 : tok0) * row_stride + head_off + kbase;
       src[0] = static_cast<const raw*>(p.r) + off;
       src[1] = static_cast<const raw*>(p.logits) + off;
       src[2] = static_cast<const raw*>(p.k) + off;
@@ -744,11 +764,21 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
     // outstanding memory operation, the previous group's output stores
     // included, and a select right here would wait for the loads themselves.
     auto load_rows = [&](u32x4 (&dst)[6], int gi) {
-      const int tok = tok0 + gi * GT;
-      const int64_t off = static_cast<int64_t>(min(tok, t1 - 1) - tok0) * row_stride;
+      if constexpr (kRev) {
+        const int pos = cc * L + i + gi * GT;   // position in processing order
 #pragma unroll
-      for (int j = 0; j < 6; ++j)
-        dst[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src[j] + off));
+        for (int j = 0; j < 6; ++j) {
+          const int row = min(max(t1 - 1 - pos + ((p.shift_mask >> j) & 1), t0), t1 - 1);
+          dst[j] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4*>(src[j] + static_cast<int64_t>(row) * row_stride));
+        }
+      } else {
+        const int tok = tok0 + gi * GT;
+        const int64_t off = static_cast<int64_t>(min(tok, t1 - 1) - tok0) * row_stride;
+#pragma unroll
+        for (int j = 0; j < 6; ++j)
+          dst[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src[j] + off));
+      }
     };
     u32x4 rawA[6], rawB[6];
     KeyRegs kr;
@@ -761,12 +791,31 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
       if (gn + 1 < ngroups) load_rows(nxt, gn + 1);
       wait_min_ge(sm.consumed, gn - 1);             // group gn-2 no longer read
       const bool active = t0 + gn * GT + cc * L < t1;
-      if (t0 + gn * GT + cc * L + L <= t1)
-        key_part1<Io, kVExact, true>(sm, sm.ops[par][cc], cur, nbias8, true, par, cc, hh, i, q,
-                                     kr);
-      else if (active)
-        key_part1<Io, kVExact, false>(sm, sm.ops[par][cc], cur, nbias8, tok0 + gn * GT < t1,
-                                      par, cc, hh, i, q, kr);
+      if constexpr (kRev) {
+        // position 0 of the segment: the shifted rows lie past its end
+        const bool void_row = gn == 0 && cc == 0 && i == 0;
+        u32x4 rows[6];
+#pragma unroll
+        for (int j = 0; j < 6; ++j) {
+          const bool z = void_row && ((p.shift_mask >> j) & 1) && j != 1;
+          rows[j] = z ? u32x4{0u, 0u, 0u, 0u} : cur[j];
+        }
+        const bool unit_w = void_row && ((p.shift_mask >> 1) & 1);
+        if (t0 + gn * GT + cc * L + L <= t1)
+          key_part1<Io, kVExact, true, true>(sm, sm.ops[par][cc], rows, nbias8, true, par, cc,
+                                             hh, i, q, kr, unit_w);
+        else if (active)
+          key_part1<Io, kVExact, false, true>(sm, sm.ops[par][cc], rows, nbias8,
+                                              t0 + gn * GT + cc * L + i < t1, par, cc, hh, i, q,
+                                              kr, unit_w);
+      } else {
+        if (t0 + gn * GT + cc * L + L <= t1)
+          key_part1<Io, kVExact, true>(sm, sm.ops[par][cc], cur, nbias8, true, par, cc, hh, i,
+                                       q, kr);
+        else if (active)
+          key_part1<Io, kVExact, false>(sm, sm.ops[par][cc], cur, nbias8, tok0 + gn * GT < t1,
+                                        par, cc, hh, i, q, kr);
+      }
       signal(&sm.part1[kw], gn + 1);
       wait_ge(&sm.part1[partner], gn + 1);
       if (active) key_part2(sm, sm.ops[par][cc], par, cc, hh, i, q, kr);
@@ -783,16 +832,19 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
 
 int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen, hipStream_t s) {
   (void)max_seqlen;
-  const bool train = p.sa_out != nullptr || p.boundary != nullptr;
+  const bool train = p.sa_out != nullptr || p.boundary != nullptr || p.reverse;
   const dim3 grid(p.num_heads, nseg);
   if (train) {
     // the training contract: uniform segments whose length is a multiple of
     // the 16-token chunk, both outputs present, bf16 tokens
-    if (p.sa_out == nullptr || p.boundary == nullptr || p.boundary_len != L ||
+    if (p.sa_out == nullptr || (p.boundary == nullptr && !p.reverse) || p.boundary_len != L ||
         p.uniform_len <= 0 || p.uniform_len % L != 0 || p.state_in != nullptr ||
         dtype != FR2_DTYPE_BFLOAT16)
       return FR2_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL((chunk64_kernel<IoBF16, true>), grid, dim3(NT), 0, s, p);
+    if (p.reverse)
+      hipLaunchKernelGGL((chunk64_kernel<IoBF16, true, true>), grid, dim3(NT), 0, s, p);
+    else
+      hipLaunchKernelGGL((chunk64_kernel<IoBF16, true>), grid, dim3(NT), 0, s, p);
   } else if (dtype == FR2_DTYPE_BFLOAT16) {
     hipLaunchKernelGGL((chunk64_kernel<IoBF16, false>), grid, dim3(NT), 0, s, p);
   } else if (dtype == FR2_DTYPE_FLOAT16) {

@@ -15,9 +15,12 @@
 //
 // The only quantity that couples key rows is dsa, a column reduction of P
 // that feeds back into P's next step.  So:
-//   1. value_kernel: one workgroup per (batch, head) runs the column
-//      recurrence of P (4 lanes per value column, D/4 keys each, DPP quad
-//      reductions) backwards over T and writes dv and dsa;
+//   1. the value pass runs the column recurrence of P backwards over T and
+//      writes dv and dsa.  It is the forward recurrence in reverse time with
+//      (k, v, r, a, b, w) <- (r_t, dy_t, k_t, b_{t+1}, a_{t+1}, w_{t+1}), so
+//      at D = 64 it runs on the chunked MFMA kernel's reverse mode; other
+//      head sizes use value_kernel (one workgroup per (batch, head), 4 lanes
+//      per value column, D/4 keys each, DPP quad reductions);
 //   2. key_kernel: rows are then independent; each workgroup owns 64 key rows
 //      of one (batch, head) (4 lanes per row, D/4 values each) and walks T
 //      backwards carrying its rows of S and P, writing dr, dw, dk, db, da.
@@ -498,8 +501,33 @@ int launch_d(const PretrainBwdArgs& p, hipStream_t s) {
   const auto* b = static_cast<const uint16_t*>(p.b);
   const auto* dy = static_cast<const uint16_t*>(p.dy);
   const int bh = p.batch * p.heads;
-  hipLaunchKernelGGL(value_kernel<D>, dim3(bh), dim3(4 * D), 0, s, p.tokens, p.heads, r, w, k,
-                     a, b, dy, static_cast<uint16_t*>(p.dv), p.workspace);
+  if constexpr (D == 64) {
+    // The value pass is the forward recurrence run backwards in time with
+    // the roles (k, v, r, a, b, w) <- (r_t, dy_t, k_t, b_{t+1}, a_{t+1},
+    // w_{t+1}): its state is P, its output dv and its sa the next token's
+    // dsa.  At D = 64 it runs on the chunked MFMA kernel's reverse mode.
+    SegArgs v;
+    v.uniform_len = p.tokens;
+    v.num_heads = p.heads;
+    v.out_elems = static_cast<int64_t>(p.batch) * p.tokens * p.heads * D;
+    v.r = p.k;
+    v.logits = p.w;
+    v.k = p.r;
+    v.v = p.dy;
+    v.a = p.b;
+    v.b = p.a;
+    v.y = p.dv;
+    v.sa_out = p.workspace;
+    v.boundary_len = kChunk;
+    v.boundary_per_seg = p.tokens / kChunk;
+    v.reverse = true;
+    v.shift_mask = (1 << 1) | (1 << 4) | (1 << 5);
+    const int rc = launch_chunked(FR2_DTYPE_BFLOAT16, v, p.batch, p.tokens, s);
+    if (rc != FR2_OK) return rc;
+  } else {
+    hipLaunchKernelGGL(value_kernel<D>, dim3(bh), dim3(4 * D), 0, s, p.tokens, p.heads, r, w, k,
+                       a, b, dy, static_cast<uint16_t*>(p.dv), p.workspace);
+  }
   hipLaunchKernelGGL(key_kernel<D>, dim3(bh * (D / 64)), dim3(256), 0, s, p.tokens, p.heads, r,
                      w, k, v, a, b, dy, p.boundary, p.state_dot_a, p.workspace,
                      static_cast<uint16_t*>(p.dr), static_cast<uint16_t*>(p.dw),

@@ -41,6 +41,14 @@ struct SegArgs {
   // FP16-state (Albatross) mode: per-slot elapsed token counts (the dither
   // phase base); null for every other mode
   const int32_t* elapsed = nullptr;
+  // Reverse mode of the chunked kernel (the training backward's value pass):
+  // position p of a segment [t0, t1) reads token row t1-1-p, plus one row for
+  // tensor j when bit j of shift_mask is set (tensors r, logits, k, v, a, b
+  // = bits 0..5); a shifted row past t1-1 reads as zero operands with unit
+  // retention.  y rows go to t1-1-p, sa rows to t0 + (n-p) mod n (n = t1-t0)
+  // and the snapshot after chunk c to index boundary_per_seg-1-c.
+  bool reverse = false;
+  int shift_mask = 0;
 };
 
 int launch_serial(int D, int dtype, bool bf16_state, const SegArgs& p, int nseg,
