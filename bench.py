@@ -351,6 +351,12 @@ BWD_FMA_PER_ELEM = 14
 FP32_VECTOR_PEAK_TFLOPS = 157.3
 
 
+def lib_ws(B, T, H, D):
+    from flashrwkv2_amd import _native as N
+
+    return int(N.load().fr2_wkv7_pretrain_backward_workspace_floats(B, T, H, D))
+
+
 def time_pretrain_training(torch, w, steps: int):
     """The [B,T,H,D] training path on a config-1-shaped batch: per-launch
     times (ms) of the forward (y, state_dot_a, boundary) and of the backward
@@ -367,7 +373,7 @@ def time_pretrain_training(torch, w, steps: int):
     y = torch.empty_like(toks[3])
     boundary = torch.empty((B, H, T // 16, D, D), device=y.device, dtype=torch.float32)
     sa = torch.empty((B, T, H, D), device=y.device, dtype=torch.float32)
-    work = torch.empty_like(sa)
+    work = torch.empty(lib_ws(B, T, H, D), device=y.device, dtype=torch.float32)
     grads = [torch.empty_like(t) for t in toks]
     lib = N.load()
     stream = torch.cuda.current_stream()
@@ -405,8 +411,9 @@ def time_pretrain_training(torch, w, steps: int):
                               "peak": FP32_VECTOR_PEAK_TFLOPS, "unit": "TFLOP/s",
                               "frac": round(tf / FP32_VECTOR_PEAK_TFLOPS, 4)},
         "gradients_finite": ok,
-        "kernels": ["chunk64_kernel<IoBF16,true> (forward: y, sa, boundary)", "value_kernel<64>",
-                    "key_kernel<64>"],
+        "kernels": ["chunk64_kernel<IoBF16,true> (forward: y, sa, boundary)",
+                    "chunk64_kernel<IoBF16,true,true> (value pass: dv, dsa, P snapshots)",
+                    "key_chunk_kernel (key pass: dr, dw, dk, db, da)"],
     }
 
 

@@ -475,9 +475,10 @@ def pretrain_tmix_wkv7_recurrent_backward(r, w, k, v, a, b, grad_output, boundar
                                           grad_a, grad_b, head_size):
     """pretrain_recurrent_bf16_forward.cpp:29-46 (backward over bf16 [B,T,H,N]).
 
-    Fills the six bf16 gradient tensors in place.  The fp32 [B,T,H,N]
-    workspace that carries d(sa) between the two kernels is allocated here
-    (the reference allocates the same buffer for its N=256 path).
+    Fills the six bf16 gradient tensors in place.  The fp32 workspace that
+    carries d(sa) (and, at N=64, the value pass's gradient snapshots) between
+    the passes is allocated here (the reference allocates a d(sa) buffer for
+    its N=256 path).
     """
     _check(head_size in (64, 128, 256), "head_size must be one of 64, 128, or 256")
     _check(r.size(3) == head_size, "input head dimension must equal head_size")
@@ -499,7 +500,9 @@ def pretrain_tmix_wkv7_recurrent_backward(r, w, k, v, a, b, grad_output, boundar
            and boundary.dtype == torch.float32, "boundary must be float32 [B,H,T/16,N,N]")
     _check(state_dot_a.shape == r.shape and state_dot_a.dtype == torch.float32,
            "state_dot_a must be float32 [B,T,H,N]")
-    workspace = torch.empty(r.shape, device=r.device, dtype=torch.float32)
+    nws = N.load().fr2_wkv7_pretrain_backward_workspace_floats(B, T, H, head_size)
+    _check(nws > 0, "pretrain backward: unsupported shape")
+    workspace = torch.empty(nws, device=r.device, dtype=torch.float32)
     with torch.cuda.device(r.device):
         rc = N.load().fr2_wkv7_pretrain_backward(
             B, T, H, head_size, r.data_ptr(), w.data_ptr(), k.data_ptr(), v.data_ptr(),

@@ -64,6 +64,9 @@ SIGNATURES: dict[str, tuple] = {
         [c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
     ),
+    "fr2_wkv7_pretrain_backward_workspace_floats": (
+        c_int64, [c_int32, c_int32, c_int32, c_int32],
+    ),
     "fr2_wkv7_pretrain_backward": (
         c_int32,
         [c_int32, c_int32, c_int32, c_int32] + [c_void_p] * 17,

@@ -164,6 +164,14 @@ extern "C" int fr2_wkv7_pretrain_forward(int32_t batch, int32_t tokens,
                             static_cast<hipStream_t>(stream));
 }
 
+extern "C" int64_t fr2_wkv7_pretrain_backward_workspace_floats(int32_t batch, int32_t tokens,
+                                                               int32_t num_heads,
+                                                               int32_t head_size) {
+  if (batch <= 0 || tokens <= 0 || tokens % 16 != 0 || num_heads <= 0) return -1;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return -1;
+  return fr2::pretrain_backward_workspace_floats(batch, tokens, num_heads, head_size);
+}
+
 extern "C" int fr2_wkv7_pretrain_backward(
     int32_t batch, int32_t tokens, int32_t num_heads, int32_t head_size, const void* r,
     const void* w, const void* k, const void* v, const void* a, const void* b,

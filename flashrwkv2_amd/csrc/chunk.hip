@@ -36,6 +36,7 @@
 //     B-operand layout of B^^T U.
 // Operators are double-buffered in LDS by group parity; outputs are staged in
 // LDS and written back as full 128-byte rows by the key waves.
+#include "mfma.h"
 #include "recurrent.h"
 
 #include <cstddef>
@@ -43,11 +44,6 @@
 
 namespace fr2 {
 namespace {
-
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int D = 64;
 constexpr int L = 16;          // tokens per chunk
@@ -58,143 +54,6 @@ constexpr int MPP = L + 4;     // padded row of the partial token-token blocks
 constexpr int YP = D + 8;      // padded row of the staged outputs
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegExpHalf = -0.6065306597126334f;   // -exp(-1/2)
-
-__device__ __forceinline__ f32x4 mma32(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x16 __attribute__((ext_vector_type(16)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-// Two fp32 values rounded (nearest-even) to bf16 and packed: v_cvt_pk_bf16_f32.
-__device__ __forceinline__ uint32_t pack_bf16(float x0, float x1) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, bf16x2));
-}
-// hi/lo split of two values: hi = bf16(x), lo = bf16(x - hi), packed pairs
-// (three VALU instructions per value)
-__device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
-  hi = pack_bf16(x0, x1);
-  lo = pack_bf16(x0 - __uint_as_float(hi << 16), x1 - __uint_as_float(hi & 0xffff0000u));
-}
-
-struct Sp8 { bf16x8 hi, lo; };
-
-// split of eight values (a 16-byte hi vector and a 16-byte lo vector)
-__device__ __forceinline__ Sp8 split8(const float* x) {
-  u32x4 h, l;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t hj, lj;
-    split2(x[2 * j], x[2 * j + 1], hj, lj);
-    h[j] = hj;
-    l[j] = lj;
-  }
-  return Sp8{__builtin_bit_cast(bf16x8, h), __builtin_bit_cast(bf16x8, l)};
-}
-
-__device__ __forceinline__ f32x4 mma32x3(const Sp8& a, const Sp8& b, f32x4 c) {
-  c = mma32(a.lo, b.hi, c);
-  c = mma32(a.hi, b.lo, c);
-  return mma32(a.hi, b.hi, c);
-}
-
-// K = 16 products on the K = 32 instruction.  Lane group q supplies K
-// positions 8q..8q+7 = (first half's 4q..4q+3, second half's 4q..4q+3), so
-// [x | y] x [u ; v] = x u + y v.  Operand forms:
-//   AOp  (A side, split):   [hi | lo]                      one bf16x8
-//   BOp  (B side, split):   [lo | hi | 0 | 0], read through the windows
-//                           [lo | hi] and [hi | 0]
-//   BX   (B side, exact):   [v | v]
-// so  AOp x BOp = hi.lo + lo.hi, then hi.hi + lo.0  (two instructions) and
-//     AOp x BX  = hi.v + lo.v                        (one instruction).
-// Every product of the kernel runs on the one K = 32 opcode: with this
-// toolchain an accumulator produced by v_mfma_f32_16x16x32_bf16 and consumed
-// as src C by v_mfma_f32_16x16x16_bf16 gave wrong sums on gfx950.
-typedef bf16x8 AOp;
-typedef bf16x16 BOp;
-typedef bf16x8 BX;
-
-__device__ __forceinline__ f32x4 mm_ab(AOp a, BOp b, f32x4 c) {
-  c = mma32(a, __builtin_shufflevector(b, b, 0, 1, 2, 3, 4, 5, 6, 7), c);
-  return mma32(a, __builtin_shufflevector(b, b, 4, 5, 6, 7, 8, 9, 10, 11), c);
-}
-__device__ __forceinline__ f32x4 mm_ax(AOp a, BX b, f32x4 c) { return mma32(a, b, c); }
-
-// 16x16 matrices held in accumulator layout (lane l: column l%16, rows
-// 4(l/16)+e): the accumulator layout of X^T is the A-operand layout of X and
-// the accumulator layout of Y is the B-operand layout of Y.
-struct Split4 { uint32_t h0, h1, l0, l1; };
-__device__ __forceinline__ Split4 split4(f32x4 x) {
-  Split4 s;
-  split2(x[0], x[1], s.h0, s.l0);
-  split2(x[2], x[3], s.h1, s.l1);
-  return s;
-}
-__device__ __forceinline__ AOp as_a(const Split4& s) {
-  return __builtin_bit_cast(AOp, u32x4{s.h0, s.h1, s.l0, s.l1});
-}
-__device__ __forceinline__ BOp as_b(const Split4& s) {
-  typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
-  return __builtin_bit_cast(BOp, u32x8{s.l0, s.l1, s.h0, s.h1, 0u, 0u, 0u, 0u});
-}
-__device__ __forceinline__ BX as_bx(bf16x4 v) { return __builtin_shufflevector(v, v, 0, 1, 2, 3, 0, 1, 2, 3); }
-__device__ __forceinline__ BOp as_b(bf16x4 hi, bf16x4 lo) {
-  const bf16x4 z = {};
-  return __builtin_shufflevector(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7),
-                                 __builtin_shufflevector(z, z, 0, 1, 2, 3, 4, 5, 6, 7), 0, 1, 2,
-                                 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
-}
-
-// Inclusive prefix sum over the 16 lanes of a DPP row (the token axis).
-template <int N>
-__device__ __forceinline__ float row_shr(float x) {
-  return __int_as_float(
-      __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + N, 0xf, 0xf, true));
-}
-__device__ __forceinline__ float row_scan(float x) {
-  x += row_shr<1>(x);
-  x += row_shr<2>(x);
-  x += row_shr<4>(x);
-  x += row_shr<8>(x);
-  return x;
-}
-// x of the previous token in the DPP row; `first` for token 0
-__device__ __forceinline__ float row_prev(float x, float first) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(first), __float_as_int(x),
-                                                    0x111, 0xf, 0xf, false));
-}
-
-// Eight 16-bit token values packed in a 16-byte vector, widened to fp32.
-template <class Io>
-__device__ __forceinline__ void unpack8(u32x4 v, float* out) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t w = v[e];
-    if constexpr (__is_same(Io, IoBF16)) {
-      out[2 * e] = __uint_as_float(w << 16);
-      out[2 * e + 1] = __uint_as_float(w & 0xffff0000u);
-    } else {
-      out[2 * e] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w)));
-      out[2 * e + 1] =
-          static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
-    }
-  }
-}
-
-// LDS transpose read (ds_read_b64_tr_b16): within each 16-lane group G, lane
-// g receives item e = element g%4 of the 8-byte piece addressed by lane
-// 4e + g/4 of its group.  With lane g of group q addressing
-// &X[4q + g/4][c0 + 4(g%4)] of a row-major [token][column] array, lane g
-// receives X[4q+e][c0+g]: the K = 16 A-operand layout of X^T (row c0+g,
-// K = token), or equally the B-operand layout of X (K = token, column c0+g).
-__device__ __forceinline__ bf16x4 tr_rows(const __bf16* p) {
-  typedef short s16x4 __attribute__((ext_vector_type(4)));
-  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-  lds_s16x4* lp = (lds_s16x4*)(p);
-  return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(lp));
-}
 
 // Operators of one chunk consumed by the state path.  For bf16 tokens V is
 // exact in bf16 (no lo part) and the rows are padded for bank spread; fp16
@@ -677,9 +536,10 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
     };
     // training outputs: sa column of this lane and the boundary column
     float* const sa_base = kTrain ? p.sa_out + head_off + vcol : nullptr;
+    const int nsnap = (p.boundary_per_seg + p.boundary_every - 1) / p.boundary_every;
     float* const bnd_base =
         (kTrain && p.boundary != nullptr)
-            ? p.boundary + (static_cast<int64_t>(seg) * H + h) * p.boundary_per_seg * D * D + vcol
+            ? p.boundary + (static_cast<int64_t>(seg) * H + h) * nsnap * D * D + vcol
             : nullptr;
     auto chunk = [&](const StateOps<kVExact>& o, int gi, int c) {
       const int ci = gi * G + c;   // chunk index within the segment
@@ -693,9 +553,10 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
         }
       }
       const int bi = kRev ? p.boundary_per_seg - 1 - ci : ci;
+      const bool keep = bnd_base != nullptr && bi % p.boundary_every == 0;
       state_compute<Io, kVExact, kTrain>(
           o, S, &sm.yb[gi & 1][c * L], vcol, i, q, p.scale, sa_rows,
-          bnd_base != nullptr ? bnd_base + static_cast<int64_t>(bi) * D * D : nullptr);
+          keep ? bnd_base + static_cast<int64_t>(bi / p.boundary_every) * D * D : nullptr);
     };
     auto group = [&](auto par_c, int gi) {
       constexpr int par = decltype(par_c)::value;

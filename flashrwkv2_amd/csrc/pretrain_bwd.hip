@@ -505,7 +505,13 @@ int launch_d(const PretrainBwdArgs& p, hipStream_t s) {
     // The value pass is the forward recurrence run backwards in time with
     // the roles (k, v, r, a, b, w) <- (r_t, dy_t, k_t, b_{t+1}, a_{t+1},
     // w_{t+1}): its state is P, its output dv and its sa the next token's
-    // dsa.  At D = 64 it runs on the chunked MFMA kernel's reverse mode.
+    // dsa.  At D = 64 it runs on the chunked MFMA kernel's reverse mode and
+    // keeps P at the start of every span of chunks for the chunk-form key
+    // pass (csrc/pretrain_bwd_chunk.hip).
+    const int cps = key_chunk_span(p.tokens);
+    const int nchunk = p.tokens / kChunk;
+    const int nspan = (nchunk + cps - 1) / cps;
+    float* pbnd = p.workspace + static_cast<int64_t>(p.batch) * p.tokens * p.heads * D;
     SegArgs v;
     v.uniform_len = p.tokens;
     v.num_heads = p.heads;
@@ -518,12 +524,15 @@ int launch_d(const PretrainBwdArgs& p, hipStream_t s) {
     v.b = p.a;
     v.y = p.dv;
     v.sa_out = p.workspace;
+    v.boundary = pbnd;
     v.boundary_len = kChunk;
-    v.boundary_per_seg = p.tokens / kChunk;
+    v.boundary_per_seg = nchunk;
+    v.boundary_every = cps;
     v.reverse = true;
     v.shift_mask = (1 << 1) | (1 << 4) | (1 << 5);
     const int rc = launch_chunked(FR2_DTYPE_BFLOAT16, v, p.batch, p.tokens, s);
     if (rc != FR2_OK) return rc;
+    return launch_key_chunk(p, pbnd, nspan, cps, s);
   } else {
     hipLaunchKernelGGL(value_kernel<D>, dim3(bh), dim3(4 * D), 0, s, p.tokens, p.heads, r, w, k,
                        a, b, dy, static_cast<uint16_t*>(p.dv), p.workspace);
@@ -537,6 +546,16 @@ int launch_d(const PretrainBwdArgs& p, hipStream_t s) {
 }
 
 }  // namespace
+
+int64_t pretrain_backward_workspace_floats(int B, int T, int H, int D) {
+  int64_t n = static_cast<int64_t>(B) * T * H * D;
+  if (D == 64) {
+    const int cps = key_chunk_span(T);
+    const int nspan = (T / kChunk + cps - 1) / cps;
+    n += static_cast<int64_t>(B) * H * nspan * D * D;
+  }
+  return n;
+}
 
 int launch_pretrain_backward(int D, const PretrainBwdArgs& p, hipStream_t s) {
   switch (D) {

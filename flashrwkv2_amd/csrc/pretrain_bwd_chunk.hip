@@ -1,0 +1,406 @@
+// Key-row pass of the training backward in chunk form on the matrix cores
+// (D = 64).  With the value pass done (dsa known, and P snapshots every
+// kCps chunks), everything the key rows need inside a 16-token chunk is a
+// product of the chunk's start state S0, the carried gradient Pc (dL/dS of
+// the chunk's last token from the future) and 16x16 token blocks:
+//
+//   gamma_t = prod_{u<=t} w_u (per key row), gp_t = gamma_{t-1},
+//   B^ = b/gamma, K^ = k/gamma, R^ = r gamma/gamma_15, A^ = a gp/gamma_15,
+//   rho_t = gamma_15/gamma_t
+//   dr = gamma o (S0 DY^T + B^^T [SA DY^T]_{s<=t} + K^^T [V DY^T]_{s<=t})
+//   da = gp    o (S0 DSA^T + B^^T [SA DSA^T]_{s<t} + K^^T [V DSA^T]_{s<t})
+//   dk = rho   o (Pc V^T + R^^T [DY V^T]_{s>=t} + A^^T [DSA V^T]_{s>t})
+//   db = rho   o (Pc SA^T + R^^T [DY SA^T]_{s>=t} + A^^T [DSA SA^T]_{s>t})
+//   carry to the previous chunk: Pc' = gamma_15 o (Pc + R^^T DY + A^_{s>0}^T DSA)
+//                                      + a_0 dsa_0^T
+//
+// and dw needs no state product at all: with Z_t = rowsum(P_t o S_t),
+//   w_t dw_t = Z_t - b_t db_t - k_t dk_t,
+//   Z_{t-1}  = w_t dw_t + a_t da_t + r_{t-1} dr_{t-1},
+//   Z_15     = r_15 dr_15 + gamma_15 (rowsum(Pc o S0) + sum_s B^_s (Pc SA^T)_s
+//                                     + K^_s (Pc V^T)_s),
+// a per-row scan over the chunk's tokens.  Nothing walks backwards through
+// 1/w, so the pass does not depend on how the forward produced its
+// snapshots.
+//
+// Work layout: one 256-thread workgroup per (batch, head, span of kCps
+// chunks), walking its chunks backwards and carrying Pc in registers; it
+// starts from the value pass's snapshot of P at the span's end.  Wave w owns
+// key rows [16w, 16w+16).  Products over the 64 values use the K = 32
+// instruction with both operands in one permuted value order (lane group q
+// holds values 16vb+4q..16vb+4q+3 of every value block vb), the order in
+// which the accumulator of Pc^T already lies, so the carry feeds the next
+// chunk's products without a relayout.  Every fp32 operand is a bf16 hi/lo
+// split (fp32-level accuracy); bf16 token values (dy, v) are exact.
+#include "mfma.h"
+#include "recurrent.h"
+
+namespace fr2 {
+namespace {
+
+constexpr int kD = 64;
+constexpr int kL = 16;
+constexpr int kKNT = 256;
+constexpr float kLg2e = 1.4426950408889634f;
+constexpr float kNegEh = -0.6065306597126334f;   // -exp(-1/2)
+constexpr float kCl = kNegEh * kLg2e;            // log2(w) = kCl * sigmoid(x)
+
+struct KPassArgs {
+  int T, H, nspan, cps;
+  const uint16_t *r, *w, *k, *v, *a, *b, *dy;
+  const float *sa, *dsa, *bnd, *pbnd;
+  uint16_t *dr, *dw, *dk, *db, *da;
+};
+
+struct alignas(32) KSmem {
+  // per (key row, token) factors of the chunk: [key][token]
+  float bh[kD][kL], kh[kD][kL], rh[kD][kL], ah[kD][kL];
+  float gm[kD][kL], gp[kD][kL], rho[kD][kL], wsf[kD][kL];
+  float rr[kD][kL], kk[kD][kL], aa[kD][kL], bb[kD][kL];
+  // masked token-token blocks in B-operand form, one per lane
+  BOp gram[8][64];
+  // DY and DSA (hi, lo) of the chunk, [token][value], for transposed reads
+  __bf16 dyh[kL][kD], dsh[kL][kD], dsl[kL][kD];
+  float dsa0[kD];   // dsa of the chunk's first token (fp32)
+};
+
+__device__ __forceinline__ f32x4 mma32x2(const Sp8& a, bf16x8 b, f32x4 c) {
+  c = mma32(a.lo, b, c);
+  return mma32(a.hi, b, c);
+}
+__device__ __forceinline__ f32x4 mma32x2b(bf16x8 a, const Sp8& b, f32x4 c) {
+  c = mma32(a, b.lo, c);
+  return mma32(a, b.hi, c);
+}
+
+// full sum over the 16 lanes of a DPP row, in every lane of the row
+__device__ __forceinline__ float row_allsum(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x122, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x121, 0xf, 0xf, false));
+  return x;
+}
+// inclusive suffix sum over the 16 lanes of a DPP row (row_shl: lane l
+// reads lane l+N, zero past the row end)
+__device__ __forceinline__ float row_suffix(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x101, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x102, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x104, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x108, 0xf, 0xf, true));
+  return x;
+}
+
+__device__ __forceinline__ bf16x4 ld_bf4(const uint16_t* p) {
+  return __builtin_bit_cast(bf16x4, *reinterpret_cast<const u32x2*>(p));
+}
+__device__ __forceinline__ f32x4 ld_f4(const float* p) {
+  return *reinterpret_cast<const f32x4*>(p);
+}
+__device__ __forceinline__ f32x4 ld_f4_lds(const float* p) {
+  return *reinterpret_cast<const f32x4*>(p);
+}
+__device__ __forceinline__ bf16x8 cat8(bf16x4 x, bf16x4 y) {
+  return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+__device__ __forceinline__ float bf(uint16_t x) { return __uint_as_float(static_cast<uint32_t>(x) << 16); }
+
+__global__ __launch_bounds__(kKNT) void key_chunk_kernel(KPassArgs p) {
+  __shared__ KSmem sm;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int n = lane & 15, q = lane >> 4;
+  const int span = blockIdx.x % p.nspan;
+  const int bh = blockIdx.x / p.nspan;
+  const int bidx = bh / p.H, h = bh % p.H;
+  const int nchunk = p.T / kL;
+  const int64_t stride = static_cast<int64_t>(p.H) * kD;
+  const int64_t base0 = (static_cast<int64_t>(bidx) * p.T * p.H + h) * kD;
+  auto tok = [&](int t) { return base0 + static_cast<int64_t>(t) * stride; };
+  const int row = 16 * wv + n;              // key row of this lane (A / carry layout)
+  const int m_hi = min(p.cps * (span + 1), nchunk) - 1;
+  const int m_lo = p.cps * span;
+
+  // ---- carry into the span's last chunk: G_u^T P_u of the span's end token
+  f32x4 PcT[4];
+#pragma unroll
+  for (int vb = 0; vb < 4; ++vb) PcT[vb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (m_hi + 1 < nchunk) {
+    const int u = kL * (m_hi + 1);
+    const float* Pn = p.pbnd + (static_cast<int64_t>(bh) * p.nspan + span + 1) * kD * kD +
+                      static_cast<int64_t>(row) * kD;
+    const float x = bf(p.w[tok(u) + row]);
+    const float wu = __builtin_amdgcn_exp2f(kCl / (1.0f + __builtin_amdgcn_exp2f(-kLg2e * x)));
+    const float au = bf(p.a[tok(u) + row]);
+#pragma unroll
+    for (int vb = 0; vb < 4; ++vb) {
+      const int j0 = 16 * vb + 4 * q;
+      const f32x4 pn = ld_f4(Pn + j0);
+      const f32x4 du = ld_f4(p.dsa + tok(u) + j0);
+      PcT[vb] = wu * pn + au * du;
+    }
+  }
+
+  for (int m = m_hi; m >= m_lo; --m) {
+    const int t0 = kL * m;
+    // ---------------- per-lane operand rows (token n, permuted values)
+    bf16x4 DYb[4], Vb[4];
+    float SAf[16], DSf[16], S0f[16];
+#pragma unroll
+    for (int vb = 0; vb < 4; ++vb) {
+      const int j0 = 16 * vb + 4 * q;
+      DYb[vb] = ld_bf4(p.dy + tok(t0 + n) + j0);
+      Vb[vb] = ld_bf4(p.v + tok(t0 + n) + j0);
+      const f32x4 s4 = ld_f4(p.sa + tok(t0 + n) + j0);
+      const f32x4 d4 = ld_f4(p.dsa + tok(t0 + n) + j0);
+      f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+      if (m > 0)
+        z4 = ld_f4(p.bnd + (static_cast<int64_t>(bh) * nchunk + m - 1) * kD * kD +
+                   static_cast<int64_t>(row) * kD + j0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        SAf[4 * vb + e] = s4[e];
+        DSf[4 * vb + e] = d4[e];
+        S0f[4 * vb + e] = z4[e];
+      }
+    }
+    // ---------------- prep inputs: token tp, keys 4kg..4kg+3
+    const int tp = tid & 15, kg = tid >> 4;
+    const int64_t pbase = tok(t0 + tp) + 4 * kg;
+    const u32x2 rw = *reinterpret_cast<const u32x2*>(p.w + pbase);
+    const u32x2 rr = *reinterpret_cast<const u32x2*>(p.r + pbase);
+    const u32x2 rk = *reinterpret_cast<const u32x2*>(p.k + pbase);
+    const u32x2 ra = *reinterpret_cast<const u32x2*>(p.a + pbase);
+    const u32x2 rb = *reinterpret_cast<const u32x2*>(p.b + pbase);
+
+    // the previous chunk's readers are done with the shared tiles
+    __syncthreads();
+
+    // ---------------- prep: decays and scaled per-(key, token) factors
+    {
+      auto el = [](u32x2 v, int e) {
+        const uint32_t wd = v[e >> 1];
+        return __uint_as_float((e & 1) ? (wd & 0xffff0000u) : (wd << 16));
+      };
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = 4 * kg + e;
+        const float x = el(rw, e);
+        const float sg = 1.0f / (1.0f + __builtin_amdgcn_exp2f(-kLg2e * x));
+        const float lw2 = kCl * sg;
+        const float G = row_scan(lw2);
+        const float G15 = __shfl(G, (lane & 48) + 15);
+        const float Gp = G - lw2;
+        const float ig = __builtin_amdgcn_exp2f(-G);
+        sm.gm[key][tp] = __builtin_amdgcn_exp2f(G);
+        sm.gp[key][tp] = __builtin_amdgcn_exp2f(Gp);
+        sm.rho[key][tp] = __builtin_amdgcn_exp2f(G15 - G);
+        sm.wsf[key][tp] = kNegEh * sg * (1.0f - sg);
+        const float xr = el(rr, e), xk = el(rk, e), xa = el(ra, e), xb = el(rb, e);
+        sm.rr[key][tp] = xr;
+        sm.kk[key][tp] = xk;
+        sm.aa[key][tp] = xa;
+        sm.bb[key][tp] = xb;
+        sm.bh[key][tp] = xb * ig;
+        sm.kh[key][tp] = xk * ig;
+        sm.rh[key][tp] = xr * __builtin_amdgcn_exp2f(G - G15);
+        sm.ah[key][tp] = xa * __builtin_amdgcn_exp2f(Gp - G15);
+      }
+    }
+    // ---------------- value-side tiles for the transposed carry product
+    {
+      Sp8 ds0 = split8(&DSf[0]), ds1 = split8(&DSf[8]);
+      const u32x4 h0 = __builtin_bit_cast(u32x4, ds0.hi), l0 = __builtin_bit_cast(u32x4, ds0.lo);
+      const u32x4 h1 = __builtin_bit_cast(u32x4, ds1.hi), l1 = __builtin_bit_cast(u32x4, ds1.lo);
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb) {
+        const int j0 = 16 * vb + 4 * q;
+        *reinterpret_cast<bf16x4*>(&sm.dyh[n][j0]) = DYb[vb];
+        const u32x4& hh = vb < 2 ? h0 : h1;
+        const u32x4& ll = vb < 2 ? l0 : l1;
+        const int o = (vb & 1) * 2;
+        *reinterpret_cast<u32x2*>(&sm.dsh[n][j0]) = u32x2{hh[o], hh[o + 1]};
+        *reinterpret_cast<u32x2*>(&sm.dsl[n][j0]) = u32x2{ll[o], ll[o + 1]};
+        if (n == 0) *reinterpret_cast<f32x4*>(&sm.dsa0[j0]) =
+            f32x4{DSf[4 * vb], DSf[4 * vb + 1], DSf[4 * vb + 2], DSf[4 * vb + 3]};
+      }
+    }
+    // ---------------- operand blocks (K = 32: value blocks {2mb, 2mb+1})
+    const bf16x8 DY0 = cat8(DYb[0], DYb[1]), DY1 = cat8(DYb[2], DYb[3]);
+    const bf16x8 V0 = cat8(Vb[0], Vb[1]), V1 = cat8(Vb[2], Vb[3]);
+    const Sp8 SA0 = split8(&SAf[0]), SA1 = split8(&SAf[8]);
+    const Sp8 DS0 = split8(&DSf[0]), DS1 = split8(&DSf[8]);
+    // ---------------- token-token blocks, two per wave
+    {
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      f32x4 g0, g1;
+      int mode0, mode1;   // 0: s<=t, 1: s<t, 2: s>=t, 3: s>t
+      if (wv == 0) {        // SA DY^T, V DY^T  (dr)
+        g0 = mma32x2(SA1, DY1, mma32x2(SA0, DY0, z));
+        g1 = mma32(V1, DY1, mma32(V0, DY0, z));
+        mode0 = mode1 = 0;
+      } else if (wv == 1) { // SA DSA^T, V DSA^T  (da)
+        g0 = mma32x3(SA1, DS1, mma32x3(SA0, DS0, z));
+        g1 = mma32x2b(V1, DS1, mma32x2b(V0, DS0, z));
+        mode0 = mode1 = 1;
+      } else if (wv == 2) { // DY V^T, DSA V^T  (dk)
+        g0 = mma32(DY1, V1, mma32(DY0, V0, z));
+        g1 = mma32x2(DS1, V1, mma32x2(DS0, V0, z));
+        mode0 = 2;
+        mode1 = 3;
+      } else {              // DY SA^T, DSA SA^T  (db)
+        g0 = mma32x2b(DY1, SA1, mma32x2b(DY0, SA0, z));
+        g1 = mma32x3(DS1, SA1, mma32x3(DS0, SA0, z));
+        mode0 = 2;
+        mode1 = 3;
+      }
+      // accumulator: G[s][t] at lane t + 16 (s/4), item s%4
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int s = 4 * q + e, t = n;
+        auto keep = [&](int mode) {
+          return mode == 0 ? s <= t : mode == 1 ? s < t : mode == 2 ? s >= t : s > t;
+        };
+        g0[e] = keep(mode0) ? g0[e] : 0.f;
+        g1[e] = keep(mode1) ? g1[e] : 0.f;
+      }
+      sm.gram[2 * wv][lane] = as_b(split4(g0));
+      sm.gram[2 * wv + 1][lane] = as_b(split4(g1));
+    }
+    // ---------------- state-side products (rows of this wave)
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 DR, DA, DK0, DB0;
+    {
+      const Sp8 S00 = split8(&S0f[0]), S01 = split8(&S0f[8]);
+      DR = mma32x2(S01, DY1, mma32x2(S00, DY0, zero));
+      DA = mma32x3(S01, DS1, mma32x3(S00, DS0, zero));
+      float pc[16];
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pc[4 * vb + e] = PcT[vb][e];
+      const Sp8 P0 = split8(&pc[0]), P1 = split8(&pc[8]);
+      DK0 = mma32x2(P1, V1, mma32x2(P0, V0, zero));
+      DB0 = mma32x3(P1, SA1, mma32x3(P0, SA0, zero));
+    }
+    // rowsum(Pc o S0) for row `row`, gathered over the four lane groups
+    float pcs0 = 0.f;
+#pragma unroll
+    for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pcs0 = fmaf(PcT[vb][e], S0f[4 * vb + e], pcs0);
+    pcs0 += __shfl_xor(pcs0, 16);
+    pcs0 += __shfl_xor(pcs0, 32);
+
+    __syncthreads();
+
+    // ---------------- token-side products
+    const f32x4 bh4 = ld_f4_lds(&sm.bh[row][4 * q]), kh4 = ld_f4_lds(&sm.kh[row][4 * q]);
+    const f32x4 rh4 = ld_f4_lds(&sm.rh[row][4 * q]);
+    f32x4 ah4 = ld_f4_lds(&sm.ah[row][4 * q]);
+    const Split4 sBh = split4(bh4), sKh = split4(kh4), sRh = split4(rh4), sAh = split4(ah4);
+    DR = mm_ab(as_a(sKh), sm.gram[1][lane], mm_ab(as_a(sBh), sm.gram[0][lane], DR));
+    DA = mm_ab(as_a(sKh), sm.gram[3][lane], mm_ab(as_a(sBh), sm.gram[2][lane], DA));
+    f32x4 DK = mm_ab(as_a(sAh), sm.gram[5][lane], mm_ab(as_a(sRh), sm.gram[4][lane], DK0));
+    f32x4 DB = mm_ab(as_a(sAh), sm.gram[7][lane], mm_ab(as_a(sRh), sm.gram[6][lane], DB0));
+
+    // ---------------- outputs: accumulator lane (token n, rows 4q+e of the wave)
+    float dr[4], da[4], dk[4], db[4], dw[4];
+    {
+      const int t = n;
+      float zs[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int rk = 16 * wv + 4 * q + e;
+        dr[e] = sm.gm[rk][t] * DR[e];
+        da[e] = sm.gp[rk][t] * DA[e];
+        dk[e] = sm.rho[rk][t] * DK[e];
+        db[e] = sm.rho[rk][t] * DB[e];
+        // Z_15: r_15 dr_15 + gamma_15 (rowsum(Pc o S0) + sum_s B^_s DB0_s + K^_s DK0_s)
+        const float part = row_allsum(sm.bh[rk][t] * DB0[e] + sm.kh[rk][t] * DK0[e]);
+        const float rs0 = __shfl(pcs0, 4 * q + e);   // lanes 4q+e hold row 16wv+4q+e
+        const float dr15 = __shfl(dr[e], (lane & 48) + 15);
+        zs[e] = sm.rr[rk][15] * dr15 + sm.gm[rk][15] * (rs0 + part);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int rk = 16 * wv + 4 * q + e;
+        const float bd = sm.bb[rk][t] * db[e] + sm.kk[rk][t] * dk[e];
+        // inc_t = -b_t db_t - k_t dk_t + a_t da_t + r_{t-1} dr_{t-1}   (t >= 1)
+        const float drp = row_prev(dr[e], 0.0f);
+        const float rp = t > 0 ? sm.rr[rk][max(t - 1, 0)] : 0.0f;
+        const float inc = t > 0 ? -bd + sm.aa[rk][t] * da[e] + rp * drp : 0.0f;
+        const float z = zs[e] + row_suffix(inc) - inc;   // Z_t
+        dw[e] = (z - bd) * sm.wsf[rk][t];
+      }
+      const int64_t o = tok(t0 + t) + 16 * wv + 4 * q;
+      auto st4 = [&](uint16_t* dst, const float* x) {
+        u32x2 pk = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3])};
+        *reinterpret_cast<u32x2*>(dst + o) = pk;
+      };
+      st4(p.dr, dr);
+      st4(p.da, da);
+      st4(p.dk, dk);
+      st4(p.db, db);
+      st4(p.dw, dw);
+    }
+
+    // ---------------- carry to the previous chunk (A layout of Pc^T)
+    if (m > m_lo) {
+      // B operands over tokens s for this lane's row: R^ and A^ with s >= 1
+      if (q == 0) ah4[0] = 0.f;
+      const BOp bR = as_b(sRh), bA = as_b(split4(ah4));
+      const float g15 = sm.gm[row][15], a0 = sm.aa[row][0];
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb) {
+        // A = X^T (value 16vb+n, K = token 4q+e) through the transpose read
+        const __bf16* dyp = &sm.dyh[4 * q + (n >> 2)][16 * vb + 4 * (n & 3)];
+        const __bf16* dhp = &sm.dsh[4 * q + (n >> 2)][16 * vb + 4 * (n & 3)];
+        const __bf16* dlp = &sm.dsl[4 * q + (n >> 2)][16 * vb + 4 * (n & 3)];
+        const bf16x4 zz = {};
+        const AOp aDY = cat8(tr_rows(dyp), zz);
+        const AOp aDS = cat8(tr_rows(dhp), tr_rows(dlp));
+        // accumulator: D[value 16vb+4q+e][row n] at lane n + 16q, item e
+        f32x4 acc = mm_ab(aDS, bA, mm_ab(aDY, bR, PcT[vb]));
+        const f32x4 d0 = ld_f4_lds(&sm.dsa0[16 * vb + 4 * q]);
+        PcT[vb] = g15 * acc + a0 * d0;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+int key_chunk_span(int tokens) {
+  (void)tokens;
+  return 8;
+}
+
+int launch_key_chunk(const PretrainBwdArgs& a, const float* pbnd, int nspan, int cps,
+                     hipStream_t s) {
+  KPassArgs k;
+  k.T = a.tokens;
+  k.H = a.heads;
+  k.nspan = nspan;
+  k.cps = cps;
+  k.r = static_cast<const uint16_t*>(a.r);
+  k.w = static_cast<const uint16_t*>(a.w);
+  k.k = static_cast<const uint16_t*>(a.k);
+  k.v = static_cast<const uint16_t*>(a.v);
+  k.a = static_cast<const uint16_t*>(a.a);
+  k.b = static_cast<const uint16_t*>(a.b);
+  k.dy = static_cast<const uint16_t*>(a.dy);
+  k.sa = a.state_dot_a;
+  k.dsa = a.workspace;
+  k.bnd = a.boundary;
+  k.pbnd = pbnd;
+  k.dr = static_cast<uint16_t*>(a.dr);
+  k.dw = static_cast<uint16_t*>(a.dw);
+  k.dk = static_cast<uint16_t*>(a.dk);
+  k.db = static_cast<uint16_t*>(a.db);
+  k.da = static_cast<uint16_t*>(a.da);
+  const int64_t blocks = static_cast<int64_t>(a.batch) * a.heads * nspan;
+  hipLaunchKernelGGL(key_chunk_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kKNT), 0, s, k);
+  return record_launch();
+}
+
+}  // namespace fr2

@@ -49,6 +49,9 @@ struct SegArgs {
   // and the snapshot after chunk c to index boundary_per_seg-1-c.
   bool reverse = false;
   int shift_mask = 0;
+  // with boundary set: keep only the snapshots whose index is a multiple of
+  // boundary_every, at index / boundary_every
+  int boundary_every = 1;
 };
 
 int launch_serial(int D, int dtype, bool bf16_state, const SegArgs& p, int nseg,
@@ -78,6 +81,12 @@ struct PretrainBwdArgs {
        *db = nullptr;
 };
 int launch_pretrain_backward(int D, const PretrainBwdArgs& p, hipStream_t s);
+// fp32 elements of the backward's workspace: dsa [B,T,H,D], and at D = 64
+// the value pass's P snapshots [B,H,spans,D,D] (one per span of chunks)
+int64_t pretrain_backward_workspace_floats(int B, int T, int H, int D);
+int key_chunk_span(int tokens);
+int launch_key_chunk(const PretrainBwdArgs& a, const float* pbnd, int nspan, int cps,
+                     hipStream_t s);
 
 // Elementwise producer / consumer stages of the layer (fp16 I/O).
 int launch_kk_a_gate(int64_t tokens, int H, int D, const void* k, const void* k_k, const void* a0,

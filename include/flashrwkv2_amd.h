@@ -166,14 +166,24 @@ int fr2_wkv7_pretrain_forward(int32_t batch, int32_t tokens, int32_t num_heads,
  * Training backward of fr2_wkv7_pretrain_forward: gradients (bf16,
  * [B,T,H,D]) of sum(y * grad_output) with respect to r, the decay logits w,
  * k, v, a and b.  boundary and state_dot_a are the forward's outputs.
- * workspace holds batch*tokens*num_heads*head_size floats (the per-token
- * gradient of sa, passed from the value pass to the key pass); it needs no
- * initialisation.  Two kernels on `stream`.  Requires T % 16 == 0.
+ * workspace holds fr2_wkv7_pretrain_backward_workspace_floats(...) floats
+ * (the per-token gradient of sa, and at D = 64 the value pass's snapshots of
+ * dL/dS every few chunks); it needs no initialisation.  Kernels on `stream`.
+ * Requires T % 16 == 0.
  * Replaces backward / cuda_backward_v3 / cuda_backward_split /
  * cuda_backward_tiled256
  * (csrc/sm120/tmix/wkv7/pretrain_recurrent_bf16_forward.cpp:29-46,
  *  pretrain_recurrent_bf16_forward.cu:163-486).
  */
+/*
+ * fp32 elements of fr2_wkv7_pretrain_backward's workspace, or -1 for sizes
+ * that entry rejects.  No reference counterpart: the reference allocates its
+ * N = 256 workspace inside the binding
+ * (csrc/sm120/tmix/wkv7/pretrain_recurrent_bf16_forward.cpp:40-44).
+ */
+int64_t fr2_wkv7_pretrain_backward_workspace_floats(int32_t batch, int32_t tokens,
+                                                    int32_t num_heads, int32_t head_size);
+
 int fr2_wkv7_pretrain_backward(int32_t batch, int32_t tokens, int32_t num_heads,
                                int32_t head_size, const void* r, const void* w,
                                const void* k, const void* v, const void* a,

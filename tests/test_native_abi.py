@@ -16,7 +16,7 @@ HEADER = ROOT / "include" / "flashrwkv2_amd.h"
 
 def _declared() -> list[str]:
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(fr2_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:int|int64_t|const char\*)\s+(fr2_\w+)\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -68,6 +68,11 @@ def test_null_pointers_and_bad_sizes_are_rejected_before_any_launch(lib):
         1, 24, 1, 64, *([fake] * 16), nul) == N.FR2_ERR_INVALID_ARGUMENT
     assert lib.fr2_wkv7_pretrain_backward(
         1, 16, 1, 96, *([fake] * 16), nul) == N.FR2_ERR_UNSUPPORTED
+    # workspace: dsa [B,T,H,D] plus, at D = 64, one P snapshot per span of chunks
+    assert lib.fr2_wkv7_pretrain_backward_workspace_floats(2, 32, 3, 128) == 2 * 32 * 3 * 128
+    n64 = lib.fr2_wkv7_pretrain_backward_workspace_floats(2, 4096, 3, 64)
+    assert n64 > 2 * 4096 * 3 * 64 and (n64 - 2 * 4096 * 3 * 64) % (2 * 3 * 64 * 64) == 0
+    assert lib.fr2_wkv7_pretrain_backward_workspace_floats(1, 24, 1, 64) == -1
     assert lib.fr2_wkv7_recurrent_fp32_forward(
         fake, fake, fake, 1, 1, 32, 1, 1, N.FR2_DTYPE_BFLOAT16, *([fake] * 9), 1.0,
         nul) == N.FR2_ERR_UNSUPPORTED
