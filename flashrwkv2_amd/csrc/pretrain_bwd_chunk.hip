@@ -129,7 +129,7 @@ __global__ __launch_bounds__(kKNT) void key_chunk_kernel(KPassArgs p) {
     const float* Pn = p.pbnd + (static_cast<int64_t>(bh) * p.nspan + span + 1) * kD * kD +
                       static_cast<int64_t>(row) * kD;
     const float x = bf(p.w[tok(u) + row]);
-    const float wu = __builtin_amdgcn_exp2f(kCl / (1.0f + __builtin_amdgcn_exp2f(-kLg2e * x)));
+    const float wu = __builtin_amdgcn_exp2f(kCl * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLg2e * x)));
     const float au = bf(p.a[tok(u) + row]);
 #pragma unroll
     for (int vb = 0; vb < 4; ++vb) {
@@ -140,37 +140,52 @@ __global__ __launch_bounds__(kKNT) void key_chunk_kernel(KPassArgs p) {
     }
   }
 
-  for (int m = m_hi; m >= m_lo; --m) {
+  // global inputs of one chunk
+  struct In {
+    bf16x4 DYb[4], Vb[4];
+    f32x4 SA4[4], DS4[4], S04[4];
+    u32x2 rw, rr, rk, ra, rb;
+  };
+  const int tp = tid & 15, kg = tid >> 4;   // prep role: token tp, keys 4kg..4kg+3
+  auto load = [&](In& in, int m) {
     const int t0 = kL * m;
-    // ---------------- per-lane operand rows (token n, permuted values)
+#pragma unroll
+    for (int vb = 0; vb < 4; ++vb) {
+      const int j0 = 16 * vb + 4 * q;
+      in.DYb[vb] = ld_bf4(p.dy + tok(t0 + n) + j0);
+      in.Vb[vb] = ld_bf4(p.v + tok(t0 + n) + j0);
+      in.SA4[vb] = ld_f4(p.sa + tok(t0 + n) + j0);
+      in.DS4[vb] = ld_f4(p.dsa + tok(t0 + n) + j0);
+      // chunk 0 starts from the zero state (row 0 of the snapshot of chunk
+      // 0 is loaded and discarded: always in bounds)
+      in.S04[vb] = ld_f4(p.bnd + (static_cast<int64_t>(bh) * nchunk + max(m - 1, 0)) * kD * kD +
+                         static_cast<int64_t>(row) * kD + j0);
+    }
+    const int64_t pbase = tok(t0 + tp) + 4 * kg;
+    in.rw = *reinterpret_cast<const u32x2*>(p.w + pbase);
+    in.rr = *reinterpret_cast<const u32x2*>(p.r + pbase);
+    in.rk = *reinterpret_cast<const u32x2*>(p.k + pbase);
+    in.ra = *reinterpret_cast<const u32x2*>(p.a + pbase);
+    in.rb = *reinterpret_cast<const u32x2*>(p.b + pbase);
+  };
+  auto body = [&](int m) {
+    const int t0 = kL * m;
+    In in;
+    load(in, m);
     bf16x4 DYb[4], Vb[4];
     float SAf[16], DSf[16], S0f[16];
 #pragma unroll
     for (int vb = 0; vb < 4; ++vb) {
-      const int j0 = 16 * vb + 4 * q;
-      DYb[vb] = ld_bf4(p.dy + tok(t0 + n) + j0);
-      Vb[vb] = ld_bf4(p.v + tok(t0 + n) + j0);
-      const f32x4 s4 = ld_f4(p.sa + tok(t0 + n) + j0);
-      const f32x4 d4 = ld_f4(p.dsa + tok(t0 + n) + j0);
-      f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-      if (m > 0)
-        z4 = ld_f4(p.bnd + (static_cast<int64_t>(bh) * nchunk + m - 1) * kD * kD +
-                   static_cast<int64_t>(row) * kD + j0);
+      DYb[vb] = in.DYb[vb];
+      Vb[vb] = in.Vb[vb];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        SAf[4 * vb + e] = s4[e];
-        DSf[4 * vb + e] = d4[e];
-        S0f[4 * vb + e] = z4[e];
+        SAf[4 * vb + e] = in.SA4[vb][e];
+        DSf[4 * vb + e] = in.DS4[vb][e];
+        S0f[4 * vb + e] = m > 0 ? in.S04[vb][e] : 0.0f;
       }
     }
-    // ---------------- prep inputs: token tp, keys 4kg..4kg+3
-    const int tp = tid & 15, kg = tid >> 4;
-    const int64_t pbase = tok(t0 + tp) + 4 * kg;
-    const u32x2 rw = *reinterpret_cast<const u32x2*>(p.w + pbase);
-    const u32x2 rr = *reinterpret_cast<const u32x2*>(p.r + pbase);
-    const u32x2 rk = *reinterpret_cast<const u32x2*>(p.k + pbase);
-    const u32x2 ra = *reinterpret_cast<const u32x2*>(p.a + pbase);
-    const u32x2 rb = *reinterpret_cast<const u32x2*>(p.b + pbase);
+    const u32x2 rw = in.rw, rr = in.rr, rk = in.rk, ra = in.ra, rb = in.rb;
 
     // the previous chunk's readers are done with the shared tiles
     __syncthreads();
@@ -185,7 +200,7 @@ __global__ __launch_bounds__(kKNT) void key_chunk_kernel(KPassArgs p) {
       for (int e = 0; e < 4; ++e) {
         const int key = 4 * kg + e;
         const float x = el(rw, e);
-        const float sg = 1.0f / (1.0f + __builtin_amdgcn_exp2f(-kLg2e * x));
+        const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLg2e * x));
         const float lw2 = kCl * sg;
         const float G = row_scan(lw2);
         const float G15 = __shfl(G, (lane & 48) + 15);
@@ -233,35 +248,30 @@ __global__ __launch_bounds__(kKNT) void key_chunk_kernel(KPassArgs p) {
     {
       const f32x4 z = {0.f, 0.f, 0.f, 0.f};
       f32x4 g0, g1;
-      int mode0, mode1;   // 0: s<=t, 1: s<t, 2: s>=t, 3: s>t
-      if (wv == 0) {        // SA DY^T, V DY^T  (dr)
-        g0 = mma32x2(SA1, DY1, mma32x2(SA0, DY0, z));
-        g1 = mma32(V1, DY1, mma32(V0, DY0, z));
-        mode0 = mode1 = 0;
-      } else if (wv == 1) { // SA DSA^T, V DSA^T  (da)
-        g0 = mma32x3(SA1, DS1, mma32x3(SA0, DS0, z));
-        g1 = mma32x2b(V1, DS1, mma32x2b(V0, DS0, z));
-        mode0 = mode1 = 1;
-      } else if (wv == 2) { // DY V^T, DSA V^T  (dk)
-        g0 = mma32(DY1, V1, mma32(DY0, V0, z));
-        g1 = mma32x2(DS1, V1, mma32x2(DS0, V0, z));
-        mode0 = 2;
-        mode1 = 3;
-      } else {              // DY SA^T, DSA SA^T  (db)
-        g0 = mma32x2b(DY1, SA1, mma32x2b(DY0, SA0, z));
-        g1 = mma32x3(DS1, SA1, mma32x3(DS0, SA0, z));
-        mode0 = 2;
-        mode1 = 3;
-      }
-      // accumulator: G[s][t] at lane t + 16 (s/4), item s%4
+      // accumulator: G[s][t] at lane t + 16 (s/4), item s%4; the masks keep
+      // s <= t (dr), s < t (da), s >= t / s > t (dk, db)
+      auto mask = [&](f32x4 g, int lo) {   // keep s - t <= -lo (lo = 0 / 1) or
+        f32x4 r;                           // s - t >= lo - 2 (lo = 2 / 3)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int s = 4 * q + e, t = n;
-        auto keep = [&](int mode) {
-          return mode == 0 ? s <= t : mode == 1 ? s < t : mode == 2 ? s >= t : s > t;
-        };
-        g0[e] = keep(mode0) ? g0[e] : 0.f;
-        g1[e] = keep(mode1) ? g1[e] : 0.f;
+        for (int e = 0; e < 4; ++e) {
+          const int d = 4 * q + e - n;
+          const bool keep = lo < 2 ? d <= -lo : d >= lo - 2;
+          r[e] = keep ? g[e] : 0.f;
+        }
+        return r;
+      };
+      if (wv == 0) {        // SA DY^T, V DY^T  (dr)
+        g0 = mask(mma32x2(SA1, DY1, mma32x2(SA0, DY0, z)), 0);
+        g1 = mask(mma32(V1, DY1, mma32(V0, DY0, z)), 0);
+      } else if (wv == 1) { // SA DSA^T, V DSA^T  (da)
+        g0 = mask(mma32x3(SA1, DS1, mma32x3(SA0, DS0, z)), 1);
+        g1 = mask(mma32x2b(V1, DS1, mma32x2b(V0, DS0, z)), 1);
+      } else if (wv == 2) { // DY V^T, DSA V^T  (dk)
+        g0 = mask(mma32(DY1, V1, mma32(DY0, V0, z)), 2);
+        g1 = mask(mma32x2(DS1, V1, mma32x2(DS0, V0, z)), 3);
+      } else {              // DY SA^T, DSA SA^T  (db)
+        g0 = mask(mma32x2b(DY1, SA1, mma32x2b(DY0, SA0, z)), 2);
+        g1 = mask(mma32x3(DS1, SA1, mma32x3(DS0, SA0, z)), 3);
       }
       sm.gram[2 * wv][lane] = as_b(split4(g0));
       sm.gram[2 * wv + 1][lane] = as_b(split4(g1));
@@ -347,7 +357,7 @@ __global__ __launch_bounds__(kKNT) void key_chunk_kernel(KPassArgs p) {
     // ---------------- carry to the previous chunk (A layout of Pc^T)
     if (m > m_lo) {
       // B operands over tokens s for this lane's row: R^ and A^ with s >= 1
-      if (q == 0) ah4[0] = 0.f;
+      ah4[0] = q == 0 ? 0.f : ah4[0];
       const BOp bR = as_b(sRh), bA = as_b(split4(ah4));
       const float g15 = sm.gm[row][15], a0 = sm.aa[row][0];
 #pragma unroll
@@ -365,7 +375,8 @@ __global__ __launch_bounds__(kKNT) void key_chunk_kernel(KPassArgs p) {
         PcT[vb] = g15 * acc + a0 * d0;
       }
     }
-  }
+  };
+  for (int m = m_hi; m >= m_lo; --m) body(m);
 }
 
 }  // namespace
