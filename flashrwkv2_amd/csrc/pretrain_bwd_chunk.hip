@@ -55,14 +55,24 @@ struct KPassArgs {
 struct alignas(32) KSmem {
   // per (key row, token) factors of the chunk: [key][token]
   float bh[kD][kL], kh[kD][kL], rh[kD][kL], ah[kD][kL];
-  float gm[kD][kL], gp[kD][kL], rho[kD][kL], wsf[kD][kL];
-  float rr[kD][kL], kk[kD][kL], aa[kD][kL], bb[kD][kL];
-  // masked token-token blocks in B-operand form, one per lane
-  BOp gram[8][64];
+  float gm[kD][kL], gp[kD][kL], wsf[kD][kL];
+  __bf16 rr[kD][kL], kk[kD][kL], aa[kD][kL], bb[kD][kL];   // raw (exact) values
+  // masked token-token blocks in B-operand form, one per lane: the [lo | hi]
+  // half of the BOp (its upper half is zero)
+  bf16x8 gram[8][64];
   // DY and DSA (hi, lo) of the chunk, [token][value], for transposed reads
   __bf16 dyh[kL][kD], dsh[kL][kD], dsl[kL][kD];
   float dsa0[kD];   // dsa of the chunk's first token (fp32)
 };
+
+// the stored half of a BOp ([lo | hi]) and the full operand rebuilt from it
+__device__ __forceinline__ bf16x8 half_b(BOp b) {
+  return __builtin_shufflevector(b, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+__device__ __forceinline__ BOp full_b(bf16x8 h) {
+  const bf16x8 z = {};
+  return __builtin_shufflevector(h, z, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+}
 
 __device__ __forceinline__ f32x4 mma32x2(const Sp8& a, bf16x8 b, f32x4 c) {
   c = mma32(a.lo, b, c);
@@ -105,7 +115,7 @@ __device__ __forceinline__ bf16x8 cat8(bf16x4 x, bf16x4 y) {
 }
 __device__ __forceinline__ float bf(uint16_t x) { return __uint_as_float(static_cast<uint32_t>(x) << 16); }
 
-__global__ __launch_bounds__(kKNT) void key_chunk_kernel(KPassArgs p) {
+__global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
   __shared__ KSmem sm;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int n = lane & 15, q = lane >> 4;
@@ -208,13 +218,12 @@ __global__ __launch_bounds__(kKNT) void key_chunk_kernel(KPassArgs p) {
         const float ig = __builtin_amdgcn_exp2f(-G);
         sm.gm[key][tp] = __builtin_amdgcn_exp2f(G);
         sm.gp[key][tp] = __builtin_amdgcn_exp2f(Gp);
-        sm.rho[key][tp] = __builtin_amdgcn_exp2f(G15 - G);
         sm.wsf[key][tp] = kNegEh * sg * (1.0f - sg);
         const float xr = el(rr, e), xk = el(rk, e), xa = el(ra, e), xb = el(rb, e);
-        sm.rr[key][tp] = xr;
-        sm.kk[key][tp] = xk;
-        sm.aa[key][tp] = xa;
-        sm.bb[key][tp] = xb;
+        sm.rr[key][tp] = static_cast<__bf16>(xr);
+        sm.kk[key][tp] = static_cast<__bf16>(xk);
+        sm.aa[key][tp] = static_cast<__bf16>(xa);
+        sm.bb[key][tp] = static_cast<__bf16>(xb);
         sm.bh[key][tp] = xb * ig;
         sm.kh[key][tp] = xk * ig;
         sm.rh[key][tp] = xr * __builtin_amdgcn_exp2f(G - G15);
@@ -273,8 +282,8 @@ __global__ __launch_bounds__(kKNT) void key_chunk_kernel(KPassArgs p) {
         g0 = mask(mma32x2b(DY1, SA1, mma32x2b(DY0, SA0, z)), 2);
         g1 = mask(mma32x3(DS1, SA1, mma32x3(DS0, SA0, z)), 3);
       }
-      sm.gram[2 * wv][lane] = as_b(split4(g0));
-      sm.gram[2 * wv + 1][lane] = as_b(split4(g1));
+      sm.gram[2 * wv][lane] = half_b(as_b(split4(g0)));
+      sm.gram[2 * wv + 1][lane] = half_b(as_b(split4(g1)));
     }
     // ---------------- state-side products (rows of this wave)
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -308,10 +317,11 @@ __global__ __launch_bounds__(kKNT) void key_chunk_kernel(KPassArgs p) {
     const f32x4 rh4 = ld_f4_lds(&sm.rh[row][4 * q]);
     f32x4 ah4 = ld_f4_lds(&sm.ah[row][4 * q]);
     const Split4 sBh = split4(bh4), sKh = split4(kh4), sRh = split4(rh4), sAh = split4(ah4);
-    DR = mm_ab(as_a(sKh), sm.gram[1][lane], mm_ab(as_a(sBh), sm.gram[0][lane], DR));
-    DA = mm_ab(as_a(sKh), sm.gram[3][lane], mm_ab(as_a(sBh), sm.gram[2][lane], DA));
-    f32x4 DK = mm_ab(as_a(sAh), sm.gram[5][lane], mm_ab(as_a(sRh), sm.gram[4][lane], DK0));
-    f32x4 DB = mm_ab(as_a(sAh), sm.gram[7][lane], mm_ab(as_a(sRh), sm.gram[6][lane], DB0));
+    auto gram = [&](int g) { return full_b(sm.gram[g][lane]); };
+    DR = mm_ab(as_a(sKh), gram(1), mm_ab(as_a(sBh), gram(0), DR));
+    DA = mm_ab(as_a(sKh), gram(3), mm_ab(as_a(sBh), gram(2), DA));
+    f32x4 DK = mm_ab(as_a(sAh), gram(5), mm_ab(as_a(sRh), gram(4), DK0));
+    f32x4 DB = mm_ab(as_a(sAh), gram(7), mm_ab(as_a(sRh), gram(6), DB0));
 
     // ---------------- outputs: accumulator lane (token n, rows 4q+e of the wave)
     float dr[4], da[4], dk[4], db[4], dw[4];
@@ -323,22 +333,23 @@ __global__ __launch_bounds__(kKNT) void key_chunk_kernel(KPassArgs p) {
         const int rk = 16 * wv + 4 * q + e;
         dr[e] = sm.gm[rk][t] * DR[e];
         da[e] = sm.gp[rk][t] * DA[e];
-        dk[e] = sm.rho[rk][t] * DK[e];
-        db[e] = sm.rho[rk][t] * DB[e];
+        const float rho = sm.gm[rk][15] * __builtin_amdgcn_rcpf(sm.gm[rk][t]);   // gamma_15 / gamma_t
+        dk[e] = rho * DK[e];
+        db[e] = rho * DB[e];
         // Z_15: r_15 dr_15 + gamma_15 (rowsum(Pc o S0) + sum_s B^_s DB0_s + K^_s DK0_s)
         const float part = row_allsum(sm.bh[rk][t] * DB0[e] + sm.kh[rk][t] * DK0[e]);
         const float rs0 = __shfl(pcs0, 4 * q + e);   // lanes 4q+e hold row 16wv+4q+e
         const float dr15 = __shfl(dr[e], (lane & 48) + 15);
-        zs[e] = sm.rr[rk][15] * dr15 + sm.gm[rk][15] * (rs0 + part);
+        zs[e] = static_cast<float>(sm.rr[rk][15]) * dr15 + sm.gm[rk][15] * (rs0 + part);
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int rk = 16 * wv + 4 * q + e;
-        const float bd = sm.bb[rk][t] * db[e] + sm.kk[rk][t] * dk[e];
+        const float bd = static_cast<float>(sm.bb[rk][t]) * db[e] + static_cast<float>(sm.kk[rk][t]) * dk[e];
         // inc_t = -b_t db_t - k_t dk_t + a_t da_t + r_{t-1} dr_{t-1}   (t >= 1)
         const float drp = row_prev(dr[e], 0.0f);
-        const float rp = t > 0 ? sm.rr[rk][max(t - 1, 0)] : 0.0f;
-        const float inc = t > 0 ? -bd + sm.aa[rk][t] * da[e] + rp * drp : 0.0f;
+        const float rp = t > 0 ? static_cast<float>(sm.rr[rk][max(t - 1, 0)]) : 0.0f;
+        const float inc = t > 0 ? -bd + static_cast<float>(sm.aa[rk][t]) * da[e] + rp * drp : 0.0f;
         const float z = zs[e] + row_suffix(inc) - inc;   // Z_t
         dw[e] = (z - bd) * sm.wsf[rk][t];
       }
@@ -359,7 +370,7 @@ __global__ __launch_bounds__(kKNT) void key_chunk_kernel(KPassArgs p) {
       // B operands over tokens s for this lane's row: R^ and A^ with s >= 1
       ah4[0] = q == 0 ? 0.f : ah4[0];
       const BOp bR = as_b(sRh), bA = as_b(split4(ah4));
-      const float g15 = sm.gm[row][15], a0 = sm.aa[row][0];
+      const float g15 = sm.gm[row][15], a0 = static_cast<float>(sm.aa[row][0]);
 #pragma unroll
       for (int vb = 0; vb < 4; ++vb) {
         // A = X^T (value 16vb+n, K = token 4q+e) through the transpose read
