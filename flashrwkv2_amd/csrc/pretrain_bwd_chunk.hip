@@ -55,8 +55,7 @@ struct KPassArgs {
 struct alignas(32) KSmem {
   // per (key row, token) factors of the chunk: [key][token]
   float bh[kD][kL], kh[kD][kL], rh[kD][kL], ah[kD][kL];
-  float gm[kD][kL], gp[kD][kL], wsf[kD][kL];
-  __bf16 rr[kD][kL], kk[kD][kL], aa[kD][kL], bb[kD][kL];   // raw (exact) values
+  float gm[kD][kL], wsf[kD][kL];
   // masked token-token blocks in B-operand form, one per lane: the [lo | hi]
   // half of the BOp (its upper half is zero)
   bf16x8 gram[8][64];
@@ -217,13 +216,8 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
         const float Gp = G - lw2;
         const float ig = __builtin_amdgcn_exp2f(-G);
         sm.gm[key][tp] = __builtin_amdgcn_exp2f(G);
-        sm.gp[key][tp] = __builtin_amdgcn_exp2f(Gp);
         sm.wsf[key][tp] = kNegEh * sg * (1.0f - sg);
         const float xr = el(rr, e), xk = el(rk, e), xa = el(ra, e), xb = el(rb, e);
-        sm.rr[key][tp] = static_cast<__bf16>(xr);
-        sm.kk[key][tp] = static_cast<__bf16>(xk);
-        sm.aa[key][tp] = static_cast<__bf16>(xa);
-        sm.bb[key][tp] = static_cast<__bf16>(xb);
         sm.bh[key][tp] = xb * ig;
         sm.kh[key][tp] = xk * ig;
         sm.rh[key][tp] = xr * __builtin_amdgcn_exp2f(G - G15);
@@ -327,30 +321,31 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
     float dr[4], da[4], dk[4], db[4], dw[4];
     {
       const int t = n;
-      float zs[4];
 #pragma unroll
+      // raw per-(row, token) values are rebuilt from the stored scaled ones:
+      // b = B^ gamma, k = K^ gamma, r = R^ gamma_15 / gamma, a = A^ gamma_15 / gamma_{t-1}
       for (int e = 0; e < 4; ++e) {
         const int rk = 16 * wv + 4 * q + e;
-        dr[e] = sm.gm[rk][t] * DR[e];
-        da[e] = sm.gp[rk][t] * DA[e];
-        const float rho = sm.gm[rk][15] * __builtin_amdgcn_rcpf(sm.gm[rk][t]);   // gamma_15 / gamma_t
+        const float g = sm.gm[rk][t], g15 = sm.gm[rk][15];
+        const float gp = t > 0 ? sm.gm[rk][max(t - 1, 0)] : 1.0f;
+        const float rho = g15 * __builtin_amdgcn_rcpf(g);   // gamma_15 / gamma_t
+        dr[e] = g * DR[e];
+        da[e] = gp * DA[e];
         dk[e] = rho * DK[e];
         db[e] = rho * DB[e];
         // Z_15: r_15 dr_15 + gamma_15 (rowsum(Pc o S0) + sum_s B^_s DB0_s + K^_s DK0_s)
-        const float part = row_allsum(sm.bh[rk][t] * DB0[e] + sm.kh[rk][t] * DK0[e]);
+        const float bhv = sm.bh[rk][t], khv = sm.kh[rk][t];
+        const float part = row_allsum(bhv * DB0[e] + khv * DK0[e]);
         const float rs0 = __shfl(pcs0, 4 * q + e);   // lanes 4q+e hold row 16wv+4q+e
         const float dr15 = __shfl(dr[e], (lane & 48) + 15);
-        zs[e] = static_cast<float>(sm.rr[rk][15]) * dr15 + sm.gm[rk][15] * (rs0 + part);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int rk = 16 * wv + 4 * q + e;
-        const float bd = static_cast<float>(sm.bb[rk][t]) * db[e] + static_cast<float>(sm.kk[rk][t]) * dk[e];
+        const float z15 = sm.rh[rk][15] * dr15 + g15 * (rs0 + part);
+        const float bd = bhv * g * db[e] + khv * g * dk[e];
         // inc_t = -b_t db_t - k_t dk_t + a_t da_t + r_{t-1} dr_{t-1}   (t >= 1)
         const float drp = row_prev(dr[e], 0.0f);
-        const float rp = t > 0 ? static_cast<float>(sm.rr[rk][max(t - 1, 0)]) : 0.0f;
-        const float inc = t > 0 ? -bd + static_cast<float>(sm.aa[rk][t]) * da[e] + rp * drp : 0.0f;
-        const float z = zs[e] + row_suffix(inc) - inc;   // Z_t
+        const float rp = t > 0 ? sm.rh[rk][max(t - 1, 0)] * g15 * __builtin_amdgcn_rcpf(gp) : 0.0f;
+        const float av = sm.ah[rk][t] * g15 * __builtin_amdgcn_rcpf(gp);
+        const float inc = t > 0 ? -bd + av * da[e] + rp * drp : 0.0f;
+        const float z = z15 + row_suffix(inc) - inc;   // Z_t
         dw[e] = (z - bd) * sm.wsf[rk][t];
       }
       const int64_t o = tok(t0 + t) + 16 * wv + 4 * q;
@@ -370,7 +365,7 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
       // B operands over tokens s for this lane's row: R^ and A^ with s >= 1
       ah4[0] = q == 0 ? 0.f : ah4[0];
       const BOp bR = as_b(sRh), bA = as_b(split4(ah4));
-      const float g15 = sm.gm[row][15], a0 = static_cast<float>(sm.aa[row][0]);
+      const float g15 = sm.gm[row][15], a0 = sm.ah[row][0] * g15;   // gamma_{-1} = 1
 #pragma unroll
       for (int vb = 0; vb < 4; ++vb) {
         // A = X^T (value 16vb+n, K = token 4q+e) through the transpose read
