@@ -351,6 +351,40 @@ def time_layer_stages(torch, tokens: int, heads: int, steps: int = 20):
 BWD_BYTES_PER_TOKEN_HEAD = 7 * 128 + 256 + 64 * 64 * 4 // 16 + 6 * 128
 
 
+def time_chunk_bf16_state(torch, flashrwkv2_amd, w, steps: int):
+    """The bf16-state chunk entry (infer_tmix_wkv7_chunk_bf16_forward_varlen)
+    on a config-1-shaped batch with a bf16 state pool: public calls with a
+    reused ticket between HIP events."""
+    from flashrwkv2_amd.tmix.wkv7 import infer_tmix_wkv7_chunk_bf16_forward_varlen as fn
+
+    pool = w.state_pool.to(torch.bfloat16) if w.state_pool is not None else torch.zeros(
+        (w.state_indices.numel(), w.num_heads, 64, 64), device=w.r.device, dtype=torch.bfloat16)
+    ticket = flashrwkv2_amd.prepare_tmix_wkv7_recurrent_metadata(
+        w.cu_seqlens, w.state_indices, total_tokens=w.total_tokens, state_pool_size=pool.shape[0])
+
+    def call():
+        return fn(*w.tokens, state_pool=pool, cu_seqlens=w.cu_seqlens,
+                  state_indices=w.state_indices, validated_metadata=ticket)
+
+    call()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        call()
+    end.record()
+    torch.cuda.synchronize()
+    ms = max(start.elapsed_time(end), (time.perf_counter() - t0) * 1e3) / steps
+    nbytes = (w.total_tokens * w.num_heads * BYTES_PER_TOKEN_HEAD
+              + 2 * w.state_indices.numel() * w.num_heads * STATE_BYTES // 2)   # bf16 state
+    return {"workload": w.name + "_bf16_state", "ms_per_step": round(ms, 5),
+            "tokens_per_s": round(w.total_tokens / (ms * 1e-3), 1),
+            "kernel": "chunk64_kernel<IoBF16,false> (bf16 state load/store)",
+            "roofline": roofline_obj(nbytes, ms)}
+
+
 def lib_ws(B, T, H, D):
     from flashrwkv2_amd import _native as N
 
@@ -538,6 +572,9 @@ def main() -> int:
             result.update({"metric": METRIC, "value": result["decode"]["tokens_per_s"],
                            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
                            "warmup": args.warmup, "ms_per_step": round(dms, 5)})
+    if args.only in (None, "prefill") and args.config == 1 and pre is not None:
+        result["chunk_bf16_state"] = time_chunk_bf16_state(torch, flashrwkv2_amd, pre.w,
+                                                           max(5, args.steps // 2))
     if args.only in (None, "train") and not args.no_train:
         wt = pre.w if (pre is not None and args.config == 1) else workloads.config(1, "cuda")
         result["pretrain_training"] = time_pretrain_training(torch, wt, max(3, args.steps // 4))

@@ -206,7 +206,6 @@ extern "C" int fr2_wkv7_chunk_bf16_forward(
   if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 ||
       total_tokens <= 0 || chunk_size <= 0)
     return FR2_ERR_INVALID_ARGUMENT;
-  (void)max_seqlen;
   SegArgs p;
   p.bounds = query_start_loc;
   p.slots = state_indices;
@@ -219,6 +218,17 @@ extern "C" int fr2_wkv7_chunk_bf16_forward(
   p.a = a; p.b = b;
   p.y = output;
   p.scale = scale;
+  // The contract keeps the state in fp32 inside the call and rounds it to
+  // bf16 once at the end (infer_chunk_bf16_forward_varlen.cu:195-270), so long
+  // requests run on the chunked MFMA kernel with a bf16 state load / store;
+  // chunk_size only shapes the reference's workspace, not the arithmetic.
+  if (max_seqlen >= kChunkMinSeqlen) {
+    p.state_bf16 = true;
+    const int rc = fr2::launch_chunked(FR2_DTYPE_BFLOAT16, p, num_sequences, max_seqlen,
+                                       static_cast<hipStream_t>(stream));
+    if (rc != FR2_ERR_UNSUPPORTED) return rc;
+    p.state_bf16 = false;
+  }
   return fr2::launch_serial(64, FR2_DTYPE_BFLOAT16, true, p, num_sequences,
                             static_cast<hipStream_t>(stream));
 }

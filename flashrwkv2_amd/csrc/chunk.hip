@@ -512,11 +512,17 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) S[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (p.state_in != nullptr) {
+      // fp32 state, or (bf16-state contract) bf16 widened once; the state
+      // stays fp32 for the whole call and is rounded back once at the end
       const float* sin = static_cast<const float*>(p.state_in);
+      const uint16_t* sinb = static_cast<const uint16_t*>(p.state_in);
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) S[kb][e] = sin[sbase + (kb * 16 + 4 * q + e) * D + vcol];
+        for (int e = 0; e < 4; ++e) {
+          const int64_t at = sbase + (kb * 16 + 4 * q + e) * D + vcol;
+          S[kb][e] = p.state_bf16 ? IoBF16::to_f32(sinb[at]) : sin[at];
+        }
     }
     // outputs of a finished group: 16-byte pieces of the staged rows, token
     // tid/8, elements 8*(tid%8).. (the four state waves cover the 32 rows)
@@ -585,10 +591,17 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
     write_out(ngroups - 1);
     if (p.state_out != nullptr) {
       float* sout = static_cast<float*>(p.state_out);
+      uint16_t* soutb = static_cast<uint16_t*>(p.state_out);
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sout[sbase + (kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
+        for (int e = 0; e < 4; ++e) {
+          const int64_t at = sbase + (kb * 16 + 4 * q + e) * D + vcol;
+          if (p.state_bf16)
+            soutb[at] = IoBF16::from_f32(S[kb][e]);
+          else
+            sout[at] = S[kb][e];
+        }
     }
   } else {
     // ---------------- key waves: chunk cc of each group, key half hh

@@ -25,6 +25,7 @@ struct SegArgs {
   int64_t out_elems = 0;            // for the fail-closed NaN fill
   const void* state_in = nullptr;   // null: zero initial state
   void* state_out = nullptr;        // null: final state not written
+  bool state_bf16 = false;          // chunked kernel: state_in/out hold bf16
   const void* r = nullptr;
   const void* logits = nullptr;
   const void* bias = nullptr;       // [H, D] or null

@@ -131,6 +131,56 @@ def test_chunk_bf16_ragged_tail_and_slot_update(chunk_size):
     assert torch.equal(pool[[1, 4]], before[[1, 4]])
 
 
+def test_chunk_bf16_long_requests_on_the_chunked_kernel():
+    """max_seqlen >= 128 runs the chunked MFMA kernel with a bf16 state load
+    and store (the state stays fp32 inside the call, as the reference's K2
+    keeps it, infer_chunk_bf16_forward_varlen.cu:195-270); checked against the
+    oracle and against the token-serial path on the same inputs."""
+    require_gpu()
+    g = torch.Generator().manual_seed(12)
+    lengths = [130, 1, 300, 77]
+    total, h, d = sum(lengths), 2, 64
+    cu_list = [0]
+    for n in lengths:
+        cu_list.append(cu_list[-1] + n)
+    kk = torch.randn((total, h, d), generator=g)
+    kk = kk / kk.norm(dim=-1, keepdim=True)
+    gate = torch.sigmoid(torch.randn((total, h, d), generator=g))
+    inputs = [(torch.randn((total, h, d), generator=g) * s).to(torch.bfloat16).cuda()
+              for s in (1.0, 1.5, 1.0, 1.0)]
+    inputs = inputs[:4] + [(-kk).to(torch.bfloat16).cuda(), (kk * gate).to(torch.bfloat16).cuda()]
+    cu = torch.tensor(cu_list, device="cuda", dtype=torch.int32)
+    slots = torch.tensor([4, 0, 2, 5], device="cuda", dtype=torch.int32)
+    pool = _randn((6, h, d, d), g, 0.1, torch.bfloat16)
+    before = pool.clone()
+    y_ref, pool_ref = _chunk_reference(inputs, pool, cu, slots, 1.0)
+    out = infer_tmix_wkv7_chunk_bf16_forward_varlen(
+        *inputs, state_pool=pool, cu_seqlens=cu, state_indices=slots, max_seqlen=300)
+    torch.cuda.synchronize()
+    assert_output_close(out, y_ref)
+    active = [4, 0, 2, 5]
+    assert_state_close(pool[active], pool_ref[active], rmse=4e-3, fro=4e-3)
+    assert torch.equal(pool[[1, 3]], before[[1, 3]])
+    # the same call forced token-serial (max_seqlen below the chunked threshold
+    # is only a dispatch hint here: it is resolved from the ticket otherwise)
+    pool2 = before.clone()
+    from flashrwkv2_amd import _native as N
+    import flashrwkv2_amd
+    C = flashrwkv2_amd._C
+    out2 = torch.empty_like(out)
+    lq, ls, status, _, keep = C._resolve_launch_metadata(cu, slots, total, 6, 300, None)
+    rc = N.load().fr2_wkv7_chunk_bf16_forward(
+        lq.data_ptr(), ls.data_ptr(), status.data_ptr(), 4, h, total, 16, 64,
+        pool2.data_ptr(), *(t.data_ptr() for t in inputs[:2]), None,
+        *(t.data_ptr() for t in inputs[2:]), out2.data_ptr(), 1.0,
+        torch.cuda.current_stream().cuda_stream)
+    N.check(rc, "fr2_wkv7_chunk_bf16_forward")
+    torch.cuda.synchronize()
+    del keep
+    assert_output_close(out2, y_ref)
+    assert_state_close(pool2[active], pool_ref[active], rmse=4e-3, fro=4e-3)
+
+
 def test_chunk_bf16_rejects_non_bf16_and_duplicate_slots_without_state_write():
     require_gpu()
     tensors = [torch.zeros((2, 1, 64), device="cuda", dtype=torch.bfloat16) for _ in range(6)]
