@@ -339,8 +339,9 @@ def time_layer_stages(torch, tokens: int, heads: int, steps: int = 20):
         torch.cuda.synchronize()
         ms = start.elapsed_time(end) / steps
         nbytes = bpe * tokens * C
+        wl = f"cfg1_tokens{tokens}_C{C}_fp16"
         out[name] = {"kernel_ms": round(ms, 5), "algorithmic_bytes": nbytes,
-                     "roofline": roofline_obj(nbytes, ms)}
+                     "roofline": roofline_obj(nbytes, ms, measured_traffic(name, wl))}
     return {"workload": f"cfg1_tokens{tokens}_C{C}_fp16", "kernels": out}
 
 
@@ -383,6 +384,14 @@ def time_chunk_bf16_state(torch, flashrwkv2_amd, w, steps: int):
             "tokens_per_s": round(w.total_tokens / (ms * 1e-3), 1),
             "kernel": "chunk64_kernel<IoBF16,false> (bf16 state load/store)",
             "roofline": roofline_obj(nbytes, ms)}
+
+
+def _bwd_traffic(B, T, H):
+    """Measured HBM bytes of the two backward kernels (PMC, committed), when
+    the workload is the measured one."""
+    wl = f"cfg1_shape_training_B{B}_T{T}_H{H}"
+    parts = [measured_traffic(k, wl) for k in ("chunk64_kernel<IoBF16,true,true>", "key_chunk_kernel")]
+    return None if any(x is None for x in parts) else sum(parts)
 
 
 def lib_ws(B, T, H, D):
@@ -441,7 +450,7 @@ def time_pretrain_training(torch, w, steps: int):
         "train_tokens_per_s": round(B * T / ((fwd_ms + bwd_ms) * 1e-3), 1),
         "backward_tokens_per_s": round(B * T / (bwd_ms * 1e-3), 1),
         "backward_algorithmic_bytes": bwd_bytes,
-        "backward_roofline": roofline_obj(bwd_bytes, bwd_ms),
+        "backward_roofline": roofline_obj(bwd_bytes, bwd_ms, _bwd_traffic(B, T, H)),
         "gradients_finite": ok,
         "kernels": ["chunk64_kernel<IoBF16,true> (forward: y, sa, boundary)",
                     "chunk64_kernel<IoBF16,true,true> (value pass: dv, dsa, P snapshots)",
