@@ -14,6 +14,8 @@ Reference bindings mirrored:
   csrc/sm120/tmix/wkv7/infer_chunk_bf16_forward_varlen.cpp:44-204
   csrc/sm120/tmix/wkv7/rl_infctx_chunk_fp32io16_forward.cpp:73-241
   csrc/sm120/tmix/wkv7/rl_infctx_chunk_fp32io16_backward.cpp:22-135
+  csrc/sm120/tmix/wkv7/statetune_recurrent_fp32io16_forward.cpp:26-56
+  csrc/sm120/tmix/wkv7/statetune_recurrent_fp32io16_backward.cpp:34-82
 """
 
 from __future__ import annotations
@@ -514,6 +516,118 @@ def pretrain_tmix_wkv7_recurrent_backward(r, w, k, v, a, b, grad_output, boundar
 
 
 # ---------------------------------------------------------------------------
+# StateTune (trainable initial state over a chunk list)
+# ---------------------------------------------------------------------------
+def _statetune_check(sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, state,
+                     tokens):
+    for t, name in ((sequence_chunk_offsets, "sequence_chunk_offsets"),
+                    (chunk_token_starts, "chunk_token_starts"),
+                    (chunk_token_ends, "chunk_token_ends"), (state, "state")):
+        check_cuda_contiguous(t, name)
+        check_same_device(state, t, name)
+    for t in (sequence_chunk_offsets, chunk_token_starts, chunk_token_ends):
+        _check(t.dtype == torch.int32, "chunk metadata must be int32")
+    _check(state.dtype == torch.float32 and state.dim() == 4
+           and state.size(2) == state.size(3), "state must be float32 [B,H,D,D]")
+    D = state.size(3)
+    _check(D in (64, 128, 256), "head_size must be one of 64, 128, or 256")
+    r = tokens[0][0]
+    _check(r.dtype in _TOKEN_DTYPES, "token tensors must be float16 or bfloat16")
+    for t, name in tokens:
+        check_cuda_contiguous(t, name)
+        check_same_device(state, t, name)
+        _check(t.dtype == r.dtype, name, " must have the dtype of r")
+        _check(t.shape == r.shape, name, " must match r shape")
+    _check(r.dim() == 3 and r.size(1) == state.size(1) and r.size(2) == D,
+           "token tensors must have shape [total_tokens,H,D]")
+    _check(sequence_chunk_offsets.numel() == state.size(0) + 1,
+           "sequence_chunk_offsets must have shape [B+1]")
+    _check(chunk_token_starts.numel() > 0
+           and chunk_token_ends.numel() == chunk_token_starts.numel(),
+           "chunk token metadata must have matching shape [C]")
+    return state.size(0), chunk_token_starts.numel(), r.size(0), state.size(1), D
+
+
+def statetune_tmix_wkv7_recurrent_fp32io16_forward(sequence_chunk_offsets, chunk_token_starts,
+                                                   chunk_token_ends, state, r, decay_logits,
+                                                   k, v, a, b, output, boundary, state_dot_a,
+                                                   scale=1.0):
+    """statetune_recurrent_fp32io16_forward.cpp:26-56: runs every sequence's
+    chunks from ``state`` (updated in place to the final state) and fills
+    ``output``, ``boundary`` (start-of-chunk states) and ``state_dot_a``."""
+    B, C, T, H, D = _statetune_check(
+        sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, state,
+        ((r, "r"), (decay_logits, "decay_logits"), (k, "k"), (v, "v"), (a, "a"), (b, "b"),
+         (output, "output")))
+    check_cuda_contiguous(boundary, "boundary")
+    check_cuda_contiguous(state_dot_a, "state_dot_a")
+    _check(boundary.dtype == torch.float32 and tuple(boundary.shape) == (C, H, D, D),
+           "boundary must be float32 [C,H,D,D]")
+    _check(state_dot_a.dtype == torch.float32 and state_dot_a.shape == r.shape,
+           "state_dot_a must be float32 [total_tokens,H,D]")
+    with torch.cuda.device(state.device):
+        rc = N.load().fr2_wkv7_statetune_forward(
+            sequence_chunk_offsets.data_ptr(), chunk_token_starts.data_ptr(),
+            chunk_token_ends.data_ptr(), B, C, T, H, D, _dtype_code(r), state.data_ptr(),
+            r.data_ptr(), decay_logits.data_ptr(), k.data_ptr(), v.data_ptr(), a.data_ptr(),
+            b.data_ptr(), output.data_ptr(), boundary.data_ptr(), state_dot_a.data_ptr(),
+            float(scale), _stream(state.device))
+    N.check(rc, "statetune_tmix_wkv7_recurrent_fp32io16_forward")
+
+
+def statetune_tmix_wkv7_recurrent_fp32io16_backward(sequence_chunk_offsets, chunk_token_starts,
+                                                    chunk_token_ends, final_state, r,
+                                                    decay_logits, k, v, a, b, state_dot_a,
+                                                    grad_output, grad_final_state, boundary,
+                                                    grad_r, grad_decay_logits, grad_k, grad_v,
+                                                    grad_a, grad_b, grad_initial_state,
+                                                    scale=1.0):
+    """statetune_recurrent_fp32io16_backward.cpp:34-82: fills the six token
+    gradients and ``grad_initial_state`` in place.  ``grad_output`` and
+    ``grad_final_state`` may be None (zero).  ``final_state`` is checked but
+    not read: chunk-end states are rebuilt from ``boundary``.  The fp32
+    workspace (d(sa) per token and the replayed in-chunk states) is
+    allocated here."""
+    grads = ((grad_r, "grad_r"), (grad_decay_logits, "grad_decay_logits"), (grad_k, "grad_k"),
+             (grad_v, "grad_v"), (grad_a, "grad_a"), (grad_b, "grad_b"))
+    toks = [(r, "r"), (decay_logits, "decay_logits"), (k, "k"), (v, "v"), (a, "a"), (b, "b"),
+            *grads]
+    if grad_output is not None:
+        toks.append((grad_output, "grad_output"))
+    B, C, T, H, D = _statetune_check(sequence_chunk_offsets, chunk_token_starts,
+                                     chunk_token_ends, final_state, tuple(toks))
+    for t, name in ((boundary, "boundary"), (state_dot_a, "state_dot_a"),
+                    (grad_initial_state, "grad_initial_state")):
+        check_cuda_contiguous(t, name)
+        check_same_device(final_state, t, name)
+    _check(boundary.dtype == torch.float32 and tuple(boundary.shape) == (C, H, D, D),
+           "boundary must be float32 [C,H,D,D]")
+    _check(state_dot_a.dtype == torch.float32 and state_dot_a.shape == r.shape,
+           "state_dot_a must be float32 [total_tokens,H,D]")
+    _check(grad_initial_state.dtype == torch.float32
+           and grad_initial_state.shape == final_state.shape,
+           "grad_initial_state must be float32 [B,H,D,D]")
+    if grad_final_state is not None:
+        check_cuda_contiguous(grad_final_state, "grad_final_state")
+        _check(grad_final_state.dtype == torch.float32
+               and grad_final_state.shape == final_state.shape,
+               "grad_final_state must be float32 [B,H,D,D]")
+    nws = N.load().fr2_wkv7_statetune_backward_workspace_floats(T, H, D)
+    _check(nws > 0, "statetune backward: unsupported shape")
+    workspace = torch.empty(nws, device=r.device, dtype=torch.float32)
+    ptr = lambda t: None if t is None else t.data_ptr()
+    with torch.cuda.device(final_state.device):
+        rc = N.load().fr2_wkv7_statetune_backward(
+            sequence_chunk_offsets.data_ptr(), chunk_token_starts.data_ptr(),
+            chunk_token_ends.data_ptr(), B, C, T, H, D, _dtype_code(r), r.data_ptr(),
+            decay_logits.data_ptr(), k.data_ptr(), v.data_ptr(), a.data_ptr(), b.data_ptr(),
+            state_dot_a.data_ptr(), ptr(grad_output), ptr(grad_final_state), boundary.data_ptr(),
+            workspace.data_ptr(), *(g.data_ptr() for g, _ in grads),
+            grad_initial_state.data_ptr(), float(scale), _stream(final_state.device))
+    N.check(rc, "statetune_tmix_wkv7_recurrent_fp32io16_backward")
+
+
+# ---------------------------------------------------------------------------
 # bf16-state packed chunk inference
 # ---------------------------------------------------------------------------
 def _check_bf16(t, ref, name):
@@ -921,6 +1035,8 @@ def exported_names() -> Sequence[str]:
         "tmix_wkv7_recurrent_fp16_from_decay_logits",
         "pretrain_tmix_wkv7_recurrent_forward",
         "pretrain_tmix_wkv7_recurrent_backward",
+        "statetune_tmix_wkv7_recurrent_fp32io16_forward",
+        "statetune_tmix_wkv7_recurrent_fp32io16_backward",
         "infer_tmix_wkv7_chunk_bf16_forward_varlen",
         "rl_infctx_tmix_wkv7_chunk_fp32io16_forward",
         "rl_infctx_tmix_wkv7_chunk_fp32io16_backward_replay",

@@ -35,6 +35,7 @@ from .tmix.wkv7 import (  # noqa: E402
     pretrain_tmix_wkv7_recurrent_bf16,
     rl_infctx_tmix_wkv7_chunk_fp32io16,
     rl_infctx_tmix_wkv7_chunk_fp32io16_factor_recompute,
+    statetune_tmix_wkv7_recurrent_fp32io16,
 )
 
 from .tmix.readout import infer_tmix_readout_forward_varlen  # noqa: E402
@@ -50,6 +51,7 @@ __all__ = [
     "pretrain_tmix_wkv7_recurrent_bf16",
     "rl_infctx_tmix_wkv7_chunk_fp32io16",
     "rl_infctx_tmix_wkv7_chunk_fp32io16_factor_recompute",
+    "statetune_tmix_wkv7_recurrent_fp32io16",
 ]
 
 __version__ = "0.1.0"

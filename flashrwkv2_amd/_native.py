@@ -71,6 +71,19 @@ SIGNATURES: dict[str, tuple] = {
         c_int32,
         [c_int32, c_int32, c_int32, c_int32] + [c_void_p] * 17,
     ),
+    "fr2_wkv7_statetune_forward": (
+        c_int32,
+        [c_void_p] * 3 + [c_int32, c_int32, c_int64, c_int32, c_int32, c_int32]
+        + [c_void_p] * 10 + [c_float, c_void_p],
+    ),
+    "fr2_wkv7_statetune_backward_workspace_floats": (
+        c_int64, [c_int64, c_int32, c_int32],
+    ),
+    "fr2_wkv7_statetune_backward": (
+        c_int32,
+        [c_void_p] * 3 + [c_int32, c_int32, c_int64, c_int32, c_int32, c_int32]
+        + [c_void_p] * 18 + [c_float, c_void_p],
+    ),
     "fr2_tmix_kk_a_gate_forward": (
         c_int32, [c_int64, c_int32, c_int32] + [c_void_p] * 9,
     ),

@@ -295,6 +295,95 @@ extern "C" int fr2_wkv7_rl_infctx_replay(
 }
 
 // ---------------------------------------------------------------------------
+// StateTune (trainable initial state over a chunk list)
+// ---------------------------------------------------------------------------
+namespace {
+
+bool statetune_sizes_ok(int32_t num_sequences, int32_t num_chunks, int64_t total_tokens,
+                        int32_t num_heads) {
+  return num_sequences > 0 && num_chunks > 0 && num_heads > 0 && total_tokens > 0 &&
+         total_tokens < (int64_t{1} << 31);
+}
+
+}  // namespace
+
+extern "C" int fr2_wkv7_statetune_forward(
+    const int32_t* sequence_chunk_offsets, const int32_t* chunk_token_starts,
+    const int32_t* chunk_token_ends, int32_t num_sequences, int32_t num_chunks,
+    int64_t total_tokens, int32_t num_heads, int32_t head_size, int32_t dtype, float* state,
+    const void* r, const void* decay_logits, const void* k, const void* v, const void* a,
+    const void* b, void* output, float* boundary, float* state_dot_a, float scale,
+    void* stream) {
+  if (!sequence_chunk_offsets || !chunk_token_starts || !chunk_token_ends || !state ||
+      !tokens_ok(r, decay_logits, k, v, a, b, output) || !boundary || !state_dot_a)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (!statetune_sizes_ok(num_sequences, num_chunks, total_tokens, num_heads))
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return FR2_ERR_UNSUPPORTED;
+  if (dtype != FR2_DTYPE_FLOAT16 && dtype != FR2_DTYPE_BFLOAT16) return FR2_ERR_UNSUPPORTED;
+  fr2::StateTuneArgs p;
+  p.offsets = sequence_chunk_offsets;
+  p.starts = chunk_token_starts;
+  p.ends = chunk_token_ends;
+  p.num_seq = num_sequences;
+  p.num_chunks = num_chunks;
+  p.heads = num_heads;
+  p.tokens = total_tokens;
+  p.r = r; p.w = decay_logits; p.k = k; p.v = v; p.a = a; p.b = b;
+  p.scale = scale;
+  p.state = state;
+  p.y = output;
+  p.sa = state_dot_a;
+  p.boundary = boundary;
+  return fr2::launch_statetune_forward(head_size, dtype, p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t fr2_wkv7_statetune_backward_workspace_floats(int64_t total_tokens,
+                                                                int32_t num_heads,
+                                                                int32_t head_size) {
+  if (total_tokens <= 0 || total_tokens >= (int64_t{1} << 31) || num_heads <= 0) return -1;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return -1;
+  return fr2::statetune_backward_workspace_floats(total_tokens, num_heads, head_size);
+}
+
+extern "C" int fr2_wkv7_statetune_backward(
+    const int32_t* sequence_chunk_offsets, const int32_t* chunk_token_starts,
+    const int32_t* chunk_token_ends, int32_t num_sequences, int32_t num_chunks,
+    int64_t total_tokens, int32_t num_heads, int32_t head_size, int32_t dtype, const void* r,
+    const void* decay_logits, const void* k, const void* v, const void* a, const void* b,
+    const float* state_dot_a, const void* grad_output, const float* grad_final_state,
+    const float* boundary, float* workspace, void* grad_r, void* grad_decay_logits,
+    void* grad_k, void* grad_v, void* grad_a, void* grad_b, float* grad_initial_state,
+    float scale, void* stream) {
+  if (!sequence_chunk_offsets || !chunk_token_starts || !chunk_token_ends || !r ||
+      !decay_logits || !k || !v || !a || !b || !state_dot_a || !boundary || !workspace)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (!statetune_sizes_ok(num_sequences, num_chunks, total_tokens, num_heads))
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return FR2_ERR_UNSUPPORTED;
+  if (dtype != FR2_DTYPE_FLOAT16 && dtype != FR2_DTYPE_BFLOAT16) return FR2_ERR_UNSUPPORTED;
+  fr2::StateTuneArgs p;
+  p.offsets = sequence_chunk_offsets;
+  p.starts = chunk_token_starts;
+  p.ends = chunk_token_ends;
+  p.num_seq = num_sequences;
+  p.num_chunks = num_chunks;
+  p.heads = num_heads;
+  p.tokens = total_tokens;
+  p.r = r; p.w = decay_logits; p.k = k; p.v = v; p.a = a; p.b = b;
+  p.scale = scale;
+  p.sa = const_cast<float*>(state_dot_a);
+  p.boundary = const_cast<float*>(boundary);
+  p.dy = grad_output;
+  p.dfinal = grad_final_state;
+  p.dr = grad_r; p.dw = grad_decay_logits; p.dk = grad_k; p.dv = grad_v;
+  p.da = grad_a; p.db = grad_b;
+  p.dstate0 = grad_initial_state;
+  return fr2::launch_statetune_backward(head_size, dtype, p, workspace,
+                                        static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
 // producer / consumer stages of the layer (fp16)
 // ---------------------------------------------------------------------------
 extern "C" int fr2_tmix_kk_a_gate_forward(int64_t tokens, int32_t num_heads, int32_t head_size,

@@ -89,6 +89,37 @@ int key_chunk_span(int tokens);
 int launch_key_chunk(const PretrainBwdArgs& a, const float* pbnd, int nspan, int cps,
                      hipStream_t s);
 
+// StateTune: the recurrence from a trainable initial state over a chunk
+// list, and its backward (token I/O fp16 or bf16, fp32 state).
+struct StateTuneArgs {
+  const int32_t* offsets = nullptr;  // [B+1] chunk range of each sequence
+  const int32_t* starts = nullptr;   // [C] first token row of each chunk
+  const int32_t* ends = nullptr;     // [C] one past its last token row
+  int num_seq = 0, num_chunks = 0, heads = 0;
+  int64_t tokens = 0;
+  const void *r = nullptr, *w = nullptr, *k = nullptr, *v = nullptr, *a = nullptr,
+             *b = nullptr;
+  float scale = 1.0f;
+  // forward
+  float* state = nullptr;      // [B,H,D,D] initial state in, final state out
+  void* y = nullptr;           // [T,H,D]
+  float* sa = nullptr;         // state_dot_a [T,H,D] (written forward, read backward)
+  float* boundary = nullptr;   // [C,H,D,D] state at the start of each chunk
+  // backward
+  const void* dy = nullptr;        // [T,H,D] or null (zero)
+  const float* dfinal = nullptr;   // [B,H,D,D] or null (zero)
+  float* snap = nullptr;           // [ceil(T/TT),H,D,D] replay snapshots
+  float* dsa = nullptr;            // [T,H,D]
+  void *dr = nullptr, *dw = nullptr, *dk = nullptr, *dv = nullptr, *da = nullptr,
+       *db = nullptr;              // [T,H,D] each, nullable
+  float* dstate0 = nullptr;        // [B,H,D,D], nullable
+};
+int launch_statetune_forward(int D, int dtype, const StateTuneArgs& p, hipStream_t s);
+// workspace: dsa [T,H,D] then the replay snapshots [ceil(T/TT),H,D,D]
+int launch_statetune_backward(int D, int dtype, StateTuneArgs p, float* workspace,
+                              hipStream_t s);
+int64_t statetune_backward_workspace_floats(int64_t T, int H, int D);
+
 // Elementwise producer / consumer stages of the layer (fp16 I/O).
 int launch_kk_a_gate(int64_t tokens, int H, int D, const void* k, const void* k_k, const void* a0,
                      const void* a12, const void* k_a, void* new_k, void* neg_kk, void* kka,

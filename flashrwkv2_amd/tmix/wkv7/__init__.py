@@ -254,8 +254,10 @@ from .rl_infctx import (  # noqa: E402
     rl_infctx_tmix_wkv7_chunk_fp32io16,
     rl_infctx_tmix_wkv7_chunk_fp32io16_factor_recompute,
 )
+from .statetune import statetune_tmix_wkv7_recurrent_fp32io16  # noqa: E402
 
 __all__ += [
+    "statetune_tmix_wkv7_recurrent_fp32io16",
     "pretrain_tmix_wkv7_recurrent_bf16",
     "infer_tmix_wkv7_chunk_bf16_forward_varlen",
     "rl_infctx_tmix_wkv7_chunk_fp32io16",

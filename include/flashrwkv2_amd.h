@@ -246,6 +246,65 @@ int fr2_wkv7_rl_infctx_replay(const int32_t* chunk_token_starts,
                               void* stream);
 
 /* ------------------------------------------------------------------------
+ * StateTune: the recurrence from a trainable fp32 initial state over a chunk
+ * list, and its training backward.
+ *
+ * Sequence s runs chunks sequence_chunk_offsets[s] .. [s+1]-1 in order;
+ * chunk c covers token rows [chunk_token_starts[c], chunk_token_ends[c]) of
+ * the packed [total_tokens, H, D] tensors (fp16 or bf16, one dtype for all).
+ * Chunks must not overlap; rows outside every chunk are not written.
+ * ---------------------------------------------------------------------- */
+
+/*
+ * Forward: state [B,H,D,D] fp32 holds the initial state on entry and the
+ * final state on return.  Writes output = scale * S_t^T r_t (token dtype),
+ * state_dot_a [T,H,D] fp32 (pre-update sa) and boundary [C,H,D,D] fp32, the
+ * state at the start of every chunk.
+ * Replaces statetune_tmix_wkv7_recurrent_fp32io16_forward
+ * (csrc/sm120/tmix/wkv7/statetune_recurrent_fp32io16_forward.cpp:26-44,
+ *  statetune_recurrent_fp32io16_forward.cu:32-131).
+ */
+int fr2_wkv7_statetune_forward(const int32_t* sequence_chunk_offsets,
+                               const int32_t* chunk_token_starts,
+                               const int32_t* chunk_token_ends, int32_t num_sequences,
+                               int32_t num_chunks, int64_t total_tokens, int32_t num_heads,
+                               int32_t head_size, int32_t dtype, float* state, const void* r,
+                               const void* decay_logits, const void* k, const void* v,
+                               const void* a, const void* b, void* output, float* boundary,
+                               float* state_dot_a, float scale, void* stream);
+
+/*
+ * fp32 elements of fr2_wkv7_statetune_backward's workspace, or -1 for sizes
+ * it rejects.  No reference counterpart: the reference's backward rebuilds
+ * states by dividing by the decay over whole chunks and needs no workspace.
+ */
+int64_t fr2_wkv7_statetune_backward_workspace_floats(int64_t total_tokens, int32_t num_heads,
+                                                     int32_t head_size);
+
+/*
+ * Backward: gradients of sum(output * grad_output) + sum(S_final *
+ * grad_final_state) with respect to r, decay_logits, k, v, a, b (token dtype,
+ * [T,H,D]) and the initial state (grad_initial_state, fp32 [B,H,D,D]).
+ * grad_output / grad_final_state may be NULL (zero cotangent); every
+ * gradient pointer may be NULL (not written).  state_dot_a and boundary are
+ * the forward's outputs; the workspace needs no initialisation.  The
+ * reference's final_state argument is not taken: chunk-end states are
+ * rebuilt from the boundaries.
+ * Replaces statetune_tmix_wkv7_recurrent_fp32io16_backward
+ * (csrc/sm120/tmix/wkv7/statetune_recurrent_fp32io16_backward.cpp:34-67,
+ *  statetune_recurrent_fp32io16_backward.cu:49-255, 317-502).
+ */
+int fr2_wkv7_statetune_backward(
+    const int32_t* sequence_chunk_offsets, const int32_t* chunk_token_starts,
+    const int32_t* chunk_token_ends, int32_t num_sequences, int32_t num_chunks,
+    int64_t total_tokens, int32_t num_heads, int32_t head_size, int32_t dtype, const void* r,
+    const void* decay_logits, const void* k, const void* v, const void* a, const void* b,
+    const float* state_dot_a, const void* grad_output, const float* grad_final_state,
+    const float* boundary, float* workspace, void* grad_r, void* grad_decay_logits,
+    void* grad_k, void* grad_v, void* grad_a, void* grad_b, float* grad_initial_state,
+    float scale, void* stream);
+
+/* ------------------------------------------------------------------------
  * Producer and consumer stages of the WKV7 path (fp16 tensors, fp32 math).
  * ---------------------------------------------------------------------- */
 

@@ -18,6 +18,13 @@ adds numpy conveniences.  What each function restates:
   csrc/sm120/tmix/wkv7/pretrain_recurrent_bf16_forward.cu:163-286; pinned in
   tests/test_oracle_backward.py by central differences of ``wkv7_f64`` and
   by torch autograd of an fp64 per-token loop.
+* ``statetune_f64`` — the trainable-initial-state recurrence over a chunk
+  list, csrc/sm120/tmix/wkv7/statetune_recurrent_fp32io16_forward.cu:32-131
+  (start-of-chunk boundary, state_dot_a, scale) and the gradients its
+  backward (statetune_recurrent_fp32io16_backward.cu:50-240) returns,
+  including the initial state's; pinned in tests/test_oracle_statetune.py
+  by the pretrain oracle (zero state, one chunk), chunk-split invariance,
+  state linearity, central differences and torch autograd.
 * ``prepare`` (numpy, ``oracle/prepare.py``) — the producer / consumer
   stages either side of the recurrence (wkv_prepare's kk / a gate, low-rank
   branches and value residual; readout's group norm, residual, gate and
@@ -77,6 +84,9 @@ def _load() -> ctypes.CDLL:
             c_double, c_void_p, c_int]
         lib.wkv7_oracle_pretrain_bwd_f64.restype = None
         lib.wkv7_oracle_pretrain_bwd_f64.argtypes = [c_int] * 4 + [c_void_p] * 13
+        lib.wkv7_oracle_statetune_f64.restype = None
+        lib.wkv7_oracle_statetune_f64.argtypes = [c_int] * 4 + [c_void_p] * 10 + [
+            c_double] + [c_void_p] * 13
         lib.wkv7_cpu_max_threads.restype = c_int
         lib.wkv7_cpu_max_threads.argtypes = []
         _lib = lib
@@ -157,6 +167,38 @@ def pretrain_backward_f64(r, logits, k, v, a, b, dy):
     _load().wkv7_oracle_pretrain_bwd_f64(B, T, H, D, *(_p(t) for t in arrs),
                                          *(_p(o) for o in outs))
     return tuple(outs)
+
+
+def statetune_f64(state0, offsets, starts, ends, r, logits, k, v, a, b, *, scale=1.0,
+                  dy=None, dfinal=None):
+    """fp64 StateTune forward and backward over a chunk list.
+
+    ``state0`` is ``[B,H,D,D]``, the token tensors ``[T,H,D]``; ``offsets``
+    ``[B+1]`` index the chunk list ``starts`` / ``ends`` ``[C]``.  Returns a
+    dict with ``y``, ``sa``, ``boundary`` (start-of-chunk states), ``state``
+    (final) and the gradients ``dr, dw, dk, dv, da, db, dstate0`` of
+    ``sum(y * dy) + sum(state * dfinal)`` (token rows outside every chunk
+    are zero in every per-token output).
+    """
+    arrs = [_f32(t) for t in (r, logits, k, v, a, b)]
+    T, H, D = arrs[0].shape
+    s0 = _f32(state0)
+    B = s0.shape[0]
+    off, st, en = _i32(offsets), _i32(starts), _i32(ends)
+    C = st.size
+    tok = lambda: np.zeros((T, H, D), dtype=np.float64)
+    out = {"y": tok(), "sa": tok(), "boundary": np.zeros((C, H, D, D)),
+           "state": np.zeros((B, H, D, D))}
+    grads = {n: tok() for n in ("dr", "dw", "dk", "dv", "da", "db")}
+    grads["dstate0"] = np.zeros((B, H, D, D))
+    dyf = None if dy is None else _f32(dy)
+    dff = None if dfinal is None else _f32(dfinal)
+    _load().wkv7_oracle_statetune_f64(
+        B, T, H, D, _p(off), _p(st), _p(en), _p(s0), *(_p(t) for t in arrs), float(scale),
+        _p(dyf), _p(dff), _p(out["y"]), _p(out["sa"]), _p(out["boundary"]), _p(out["state"]),
+        *(_p(grads[n]) for n in ("dr", "dw", "dk", "dv", "da", "db", "dstate0")))
+    out.update(grads)
+    return out
 
 
 def cpu_threads() -> int:

@@ -225,3 +225,130 @@ void wkv7_oracle_pretrain_bwd_f64(int B, int T, int H, int D, const float* r,
   free(sa);
   free(dsa);
 }
+
+/*
+ * StateTune: the recurrence with a trainable initial state, walked over a
+ * chunk list (csrc/sm120/tmix/wkv7/statetune_recurrent_fp32io16_forward.cu:32-131,
+ * the reference test's _reference loop tests/tmix/wkv7/statetune/test.py:43-91).
+ * Sequence s runs its chunks offsets[s] .. offsets[s+1]-1 in order, chunk c
+ * covering tokens [starts[c], ends[c]) of the packed [T,H,D] tensors, from
+ * state0[s] ([B,H,D,D], k rows, v columns).  Forward outputs:
+ *   y         [T,H,D]   scale * S_t^T r_t           (rows of chunk tokens only)
+ *   sa        [T,H,D]   S_{t-1}^T a_t
+ *   boundary  [C,H,D,D] the state at the start of chunk c
+ *   state_out [B,H,D,D] the state after the sequence's last chunk
+ * Backward (dy and/or dfinal may be NULL = zero cotangent): the gradients of
+ * L = sum(y * dy) + sum(S_final * dfinal) with respect to r, the decay
+ * logits, k, v, a, b (rows of chunk tokens only) and state0 (dstate0), with
+ * the adjoint of the pretrain backward above plus
+ *   P_final = dfinal,  dr_t = scale * S_t dy_t,  P_t += scale * r_t dy_t^T,
+ *   dstate0 = (diag(w_first) + a_first b_first^T) P_first
+ * (P carried to before the sequence's first token).  Every state of a
+ * sequence is kept; no division.  Double precision throughout.
+ */
+void wkv7_oracle_statetune_f64(int B, int T, int H, int D, const int32_t* offsets,
+                               const int32_t* starts, const int32_t* ends,
+                               const float* state0, const float* r, const float* logits,
+                               const float* k, const float* v, const float* a,
+                               const float* b, double scale, const float* dy,
+                               const float* dfinal, double* y, double* sa_out,
+                               double* boundary, double* state_out, double* dr,
+                               double* dlogit, double* dk, double* dv, double* da,
+                               double* db, double* dstate0) {
+  const int64_t DD = (int64_t)D * D;
+  int32_t* toks = (int32_t*)malloc(sizeof(int32_t) * (T > 0 ? T : 1));
+  double* S = (double*)malloc(sizeof(double) * DD * (T + 1));
+  double* P = (double*)malloc(sizeof(double) * DD);
+  double* w = (double*)malloc(sizeof(double) * D);
+  double* sa = (double*)malloc(sizeof(double) * (int64_t)(T > 0 ? T : 1) * D);
+  double* dsa = (double*)malloc(sizeof(double) * D);
+  for (int s = 0; s < B; ++s)
+    for (int h = 0; h < H; ++h) {
+      /* the sequence's tokens in execution order */
+      int n = 0;
+      for (int c = offsets[s]; c < offsets[s + 1]; ++c)
+        for (int t = starts[c]; t < ends[c]; ++t) toks[n++] = t;
+      const float* s0 = state0 + ((int64_t)s * H + h) * DD;
+      for (int64_t e = 0; e < DD; ++e) S[e] = s0[e];
+      int m = 0;
+      for (int c = offsets[s]; c < offsets[s + 1]; ++c) {
+        memcpy(boundary + ((int64_t)c * H + h) * DD, S + DD * m, sizeof(double) * DD);
+        for (int t = starts[c]; t < ends[c]; ++t, ++m) {
+          const int64_t o = ((int64_t)t * H + h) * D;
+          const double* Sp = S + DD * m;
+          double* Sn = S + DD * (m + 1);
+          for (int i = 0; i < D; ++i) w[i] = wkv7_oracle_retention(logits[o + i]);
+          for (int j = 0; j < D; ++j) {
+            double acc = 0;
+            for (int i = 0; i < D; ++i) acc += Sp[(int64_t)i * D + j] * a[o + i];
+            sa[(int64_t)m * D + j] = acc;
+            sa_out[o + j] = acc;
+          }
+          for (int i = 0; i < D; ++i)
+            for (int j = 0; j < D; ++j)
+              Sn[(int64_t)i * D + j] = w[i] * Sp[(int64_t)i * D + j] +
+                                       b[o + i] * sa[(int64_t)m * D + j] +
+                                       (double)k[o + i] * v[o + j];
+          for (int j = 0; j < D; ++j) {
+            double acc = 0;
+            for (int i = 0; i < D; ++i) acc += (double)r[o + i] * Sn[(int64_t)i * D + j];
+            y[o + j] = scale * acc;
+          }
+        }
+      }
+      memcpy(state_out + ((int64_t)s * H + h) * DD, S + DD * n, sizeof(double) * DD);
+      /* backward */
+      for (int64_t e = 0; e < DD; ++e)
+        P[e] = dfinal ? dfinal[((int64_t)s * H + h) * DD + e] : 0.0;
+      for (m = n - 1; m >= 0; --m) {
+        const int t = toks[m];
+        const int64_t o = ((int64_t)t * H + h) * D;
+        const double* Sp = S + DD * m;
+        const double* Sn = S + DD * (m + 1);
+        for (int i = 0; i < D; ++i) w[i] = wkv7_oracle_retention(logits[o + i]);
+        if (dy)
+          for (int i = 0; i < D; ++i)
+            for (int j = 0; j < D; ++j)
+              P[(int64_t)i * D + j] += scale * (double)r[o + i] * dy[o + j];
+        for (int i = 0; i < D; ++i) {
+          double gr = 0, gk = 0, gb = 0, gw = 0;
+          for (int j = 0; j < D; ++j) {
+            const double p = P[(int64_t)i * D + j];
+            if (dy) gr += Sn[(int64_t)i * D + j] * dy[o + j];
+            gk += p * v[o + j];
+            gb += p * sa[(int64_t)m * D + j];
+            gw += p * Sp[(int64_t)i * D + j];
+          }
+          const double sg = 1.0 / (1.0 + exp(-(double)logits[o + i]));
+          dr[o + i] = scale * gr;
+          dk[o + i] = gk;
+          db[o + i] = gb;
+          dlogit[o + i] = gw * w[i] * (-exp(-0.5)) * sg * (1.0 - sg);
+        }
+        for (int j = 0; j < D; ++j) {
+          double gv = 0, gs = 0;
+          for (int i = 0; i < D; ++i) {
+            gv += P[(int64_t)i * D + j] * k[o + i];
+            gs += P[(int64_t)i * D + j] * b[o + i];
+          }
+          dv[o + j] = gv;
+          dsa[j] = gs;
+        }
+        for (int i = 0; i < D; ++i) {
+          double g = 0;
+          for (int j = 0; j < D; ++j) g += Sp[(int64_t)i * D + j] * dsa[j];
+          da[o + i] = g;
+        }
+        for (int i = 0; i < D; ++i)
+          for (int j = 0; j < D; ++j)
+            P[(int64_t)i * D + j] = w[i] * P[(int64_t)i * D + j] + a[o + i] * dsa[j];
+      }
+      memcpy(dstate0 + ((int64_t)s * H + h) * DD, P, sizeof(double) * DD);
+    }
+  free(toks);
+  free(S);
+  free(P);
+  free(w);
+  free(sa);
+  free(dsa);
+}

@@ -1,0 +1,218 @@
+"""GPU parity of StateTune (trainable initial state over a chunk list)
+against the fp64 oracle (oracle.statetune_f64, pinned in
+test_oracle_statetune.py).
+
+The first test is the reference's own case and bounds
+(tests/tmix/wkv7/statetune/test.py:93-165): B=2, H=1, five tokens in chunks
+[0,1) [1,3) | [3,5), state and tokens 0.01 * randn, scale 0.75, the loss
+sum(y^2) + sum(S_final^2); forward atol = rtol = 8e-3 (bf16) / 3e-4 (fp16),
+gradients atol 8e-3 / 3e-4 and rtol 1e-2 / 3e-3, for D in {64, 128, 256}.
+The oracle is fed the cotangents the backward actually received
+(dy = 2y rounded to the token dtype, dS_final = 2 S_final).
+
+The others widen the cases: ragged, empty and long chunks, gaps, several
+heads, O(1) inputs in the model's operand structure (there the gradients
+meet a relative RMSE bound and the allclose bound with its absolute part
+scaled by the gradient's RMS), zero cotangents, determinism, and that the
+caller's initial state is not modified.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from wkv7_testlib import relative_rmse, require_gpu, to_np
+
+pytestmark = pytest.mark.gpu
+
+from flashrwkv2_amd.tmix.wkv7 import statetune_tmix_wkv7_recurrent_fp32io16  # noqa: E402
+
+TOKEN_GRADS = ("dr", "dw", "dk", "dv", "da", "db")
+
+
+def _meta(offsets, starts, ends):
+    return [torch.tensor(x, dtype=torch.int32, device="cuda") for x in (offsets, starts, ends)]
+
+
+def _run(state, meta, vals, scale):
+    state = state.clone().requires_grad_()
+    vals = [v.clone().requires_grad_() for v in vals]
+    out = statetune_tmix_wkv7_recurrent_fp32io16(state, *meta, *vals, scale=scale)
+    return state, vals, out
+
+
+def _grads(state, vals):
+    return {"dstate0": state.grad, **{n: v.grad for n, v in zip(TOKEN_GRADS, vals)}}
+
+
+def _oracle(state, meta, vals, scale, dy=None, dfinal=None):
+    return oracle.statetune_f64(to_np(state), *(m.cpu().numpy() for m in meta),
+                                *(to_np(v) for v in vals), scale=scale,
+                                dy=None if dy is None else to_np(dy),
+                                dfinal=None if dfinal is None else to_np(dfinal))
+
+
+def _allclose(actual, expected, atol, rtol, what):
+    a = to_np(actual).astype(np.float64)
+    assert np.isfinite(a).all(), what
+    worst = float(np.max(np.abs(a - expected) - (atol + rtol * np.abs(expected))))
+    assert worst <= 0.0, (what, worst)
+
+
+@pytest.mark.parametrize("head_size", [64, 128, 256])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_statetune_reference_case(dtype, head_size):
+    require_gpu()
+    g = torch.Generator().manual_seed(20260805 + head_size)
+    B, H, T = 2, 1, 5
+    state0 = (torch.randn((B, H, head_size, head_size), generator=g) * 0.01).cuda()
+    vals = [(torch.randn((T, H, head_size), generator=g) * 0.01).to(dtype).cuda()
+            for _ in range(6)]
+    meta = _meta([0, 2, 3], [0, 1, 3], [1, 3, 5])
+    snapshot = state0.clone()
+    state, leaves, (y, fin, boundary, sa) = _run(state0, meta, vals, 0.75)
+    torch.cuda.synchronize()
+    ref = _oracle(state0, meta, vals, 0.75)
+    tol = 8e-3 if dtype == torch.bfloat16 else 3e-4
+    assert y.dtype == dtype and fin.dtype == torch.float32
+    assert tuple(boundary.shape) == (3, H, head_size, head_size)
+    for got, key in ((y, "y"), (fin, "state"), (boundary, "boundary"), (sa, "sa")):
+        _allclose(got, ref[key], tol, tol, key)
+
+    (y.float().square().sum() + fin.square().sum()).backward()
+    torch.cuda.synchronize()
+    dy = (2.0 * y.detach().float()).to(dtype)
+    ref = _oracle(state0, meta, vals, 0.75, dy=dy, dfinal=2.0 * fin.detach())
+    rtol = 1e-2 if dtype == torch.bfloat16 else 3e-3
+    got = _grads(state, leaves)
+    for key in ("dstate0", *TOKEN_GRADS):
+        _allclose(got[key], ref[key], tol, rtol, key)
+    assert got["dstate0"].dtype == torch.float32 and got["dr"].dtype == dtype
+    assert torch.equal(state0, snapshot)
+
+
+def _structured(T, H, D, dtype, g, logit_scale=1.0):
+    """The model's operand structure at O(1) scale: r, k, v ~ N(0,1),
+    kk = L2-normalised N(0,1), a = -kk, b = kk * sigmoid(N(0,1))."""
+    vals = [torch.randn((T, H, D), generator=g) for _ in range(6)]
+    kk = torch.randn((T, H, D), generator=g)
+    kk = kk / kk.norm(dim=-1, keepdim=True)
+    vals[1] = torch.randn((T, H, D), generator=g) * logit_scale
+    vals[4] = -kk
+    vals[5] = kk * torch.sigmoid(torch.randn((T, H, D), generator=g))
+    return [v.to(dtype).cuda() for v in vals]
+
+
+def _check_strong(got, ref, keys, rel=1e-2, atol=0.03, rtol=0.05):
+    for key in keys:
+        a, e = to_np(got[key]).astype(np.float64), ref[key]
+        assert np.isfinite(a).all(), key
+        assert relative_rmse(a, e) <= rel, (key, relative_rmse(a, e))
+        bound = atol * max(1.0, float(np.sqrt(np.mean(e * e)))) + rtol * np.abs(e)
+        assert float(np.max(np.abs(a - e) - bound)) <= 0.0, key
+
+
+@pytest.mark.parametrize("head_size", [64, 128, 256])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_statetune_ragged_chunks_gaps_and_empty_chunks(dtype, head_size):
+    """Sequence 0: chunks of 1, 17, 0 and 40 tokens; tokens 58..60 belong to
+    no chunk; sequence 1: chunks of 33 and 7 tokens; sequence 2: no chunks."""
+    require_gpu()
+    g = torch.Generator().manual_seed(7 * head_size + (dtype == torch.float16))
+    H, T = 2, 101
+    D = head_size
+    vals = _structured(T, H, D, dtype, g)
+    state0 = (torch.randn((3, H, D, D), generator=g) * 0.5).cuda()
+    meta = _meta([0, 4, 6, 6], [0, 1, 18, 18, 61, 94], [1, 18, 18, 58, 94, 101])
+    state, leaves, (y, fin, boundary, sa) = _run(state0, meta, vals, 0.5)
+    dy = torch.randn((T, H, D), generator=g).to(dtype).cuda()
+    dfin = torch.randn((3, H, D, D), generator=g).cuda()
+    torch.autograd.backward([y, fin], [dy, dfin])
+    torch.cuda.synchronize()
+    ref = _oracle(state0, meta, vals, 0.5, dy=dy, dfinal=dfin)
+    used = np.r_[0:58, 61:101]
+    fwd = {"y": y[used], "sa": sa[used]}
+    _check_strong(fwd, {k: ref[k][used] for k in ("y", "sa")}, ("y", "sa"), rel=5e-3)
+    for got, key in ((fin, "state"), (boundary, "boundary")):
+        assert relative_rmse(to_np(got), ref[key]) <= 2e-3, key
+    # the sequence without chunks keeps its state and passes dS_final through
+    assert torch.equal(fin[2], state0[2])
+    got = _grads(state, leaves)
+    assert torch.equal(got["dstate0"][2], dfin[2])
+    _check_strong({k: got[k][used] for k in TOKEN_GRADS}, {k: ref[k][used] for k in TOKEN_GRADS},
+                  TOKEN_GRADS)
+    _check_strong(got, ref, ("dstate0",))
+
+
+@pytest.mark.parametrize("head_size", [64, 256])
+def test_statetune_long_chunk(head_size):
+    """One 600-token chunk per sequence: the key pass restarts from the
+    replay snapshots every 16 (8 at D = 256) tokens."""
+    require_gpu()
+    g = torch.Generator().manual_seed(600 + head_size)
+    H, L, D = 2, 600, head_size
+    vals = _structured(2 * L, H, D, torch.bfloat16, g, logit_scale=1.5)
+    state0 = (torch.randn((2, H, D, D), generator=g) * 0.3).cuda()
+    meta = _meta([0, 1, 2], [0, L], [L, 2 * L])
+    state, leaves, (y, fin, _, _) = _run(state0, meta, vals, 1.0)
+    dy = torch.randn((2 * L, H, D), generator=g).to(torch.bfloat16).cuda()
+    dfin = (torch.randn((2, H, D, D), generator=g) * 0.1).cuda()
+    torch.autograd.backward([y, fin], [dy, dfin])
+    torch.cuda.synchronize()
+    ref = _oracle(state0, meta, vals, 1.0, dy=dy, dfinal=dfin)
+    _check_strong({"y": y}, ref, ("y",), rel=5e-3)
+    _check_strong(_grads(state, leaves), ref, ("dstate0", *TOKEN_GRADS))
+
+
+def test_statetune_zero_cotangents_through_native_entry():
+    """grad_output / grad_final_state = None through the native backward
+    (the reference's nullptr paths) against the oracle with zero cotangents
+    on the other input."""
+    C = require_gpu()
+    g = torch.Generator().manual_seed(11)
+    H, T, D = 1, 40, 64
+    vals = _structured(T, H, D, torch.bfloat16, g)
+    state0 = (torch.randn((1, H, D, D), generator=g) * 0.5).cuda()
+    meta = _meta([0, 2], [0, 13], [13, 40])
+    st = state0.clone()
+    y = torch.empty_like(vals[3])
+    boundary = torch.empty((2, H, D, D), device="cuda")
+    sa = torch.empty((T, H, D), device="cuda")
+    C.statetune_tmix_wkv7_recurrent_fp32io16_forward(*meta, st, *vals, y, boundary, sa, 1.0)
+    dy = torch.randn((T, H, D), generator=g).to(torch.bfloat16).cuda()
+    dfin = torch.randn((1, H, D, D), generator=g).cuda()
+    for gy, gf in ((dy, None), (None, dfin)):
+        grads = [torch.empty_like(v) for v in vals]
+        g0 = torch.empty_like(st)
+        C.statetune_tmix_wkv7_recurrent_fp32io16_backward(*meta, st, *vals, sa, gy, gf, boundary,
+                                                          *grads, g0, 1.0)
+        torch.cuda.synchronize()
+        ref = _oracle(state0, meta, vals, 1.0, dy=gy, dfinal=gf)
+        got = {"dstate0": g0, **dict(zip(TOKEN_GRADS, grads))}
+        _check_strong(got, ref, ("dstate0", *TOKEN_GRADS))
+
+
+def test_statetune_is_deterministic_and_validates():
+    require_gpu()
+    g = torch.Generator().manual_seed(5)
+    H, T, D = 2, 50, 128
+    vals = _structured(T, H, D, torch.float16, g)
+    state0 = (torch.randn((2, H, D, D), generator=g) * 0.2).cuda()
+    meta = _meta([0, 1, 2], [0, 20], [20, 50])
+    runs = []
+    for _ in range(2):
+        state, leaves, (y, fin, _, _) = _run(state0, meta, vals, 0.9)
+        (y.float().square().sum() + fin.square().sum()).backward()
+        runs.append([y, fin, state.grad, *(v.grad for v in leaves)])
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    with pytest.raises(TypeError, match="dtype of r"):
+        statetune_tmix_wkv7_recurrent_fp32io16(state0, *meta, vals[0], vals[1].bfloat16(),
+                                               *vals[2:])
+    with pytest.raises(ValueError, match=r"shape \[B\+1\]"):
+        statetune_tmix_wkv7_recurrent_fp32io16(state0, meta[0][:2], *meta[1:], *vals)
+    with pytest.raises(ValueError, match="scale must be finite"):
+        statetune_tmix_wkv7_recurrent_fp32io16(state0, *meta, *vals, scale=float("nan"))
