@@ -458,6 +458,102 @@ def time_pretrain_training(torch, w, steps: int):
     }
 
 
+# StateTune HBM bytes per (token, head) at D = 64 with 16-bit tokens:
+#   forward  r w k a b v in (6 x 128 B), y out (128 B), state_dot_a out (256 B)
+#   backward replay: r w k a b v in (768 B); value pass: r w k a b dy in
+#            (768 B), dv (128 B) + dsa (256 B) out; key pass: dy v (256 B),
+#            sa dsa (512 B), r w k a b (640 B) in, five gradients (640 B) out
+# plus, per chunk and head, the 16 KiB boundary (written forward, read twice
+# backward) and, per 16 tokens and head, the 16 KiB replay snapshot (written
+# and read once).
+ST_FWD_BYTES_PER_TOKEN_HEAD = 6 * 128 + 128 + 256
+ST_BWD_BYTES_PER_TOKEN_HEAD = 768 + 768 + 128 + 256 + 256 + 512 + 640 + 640
+
+
+def time_statetune_training(torch, w, steps: int, chunk_len: int = 1024):
+    """StateTune on the config-1 shape: B sequences of T tokens, each run as
+    T/chunk_len chunks from a trainable fp32 initial state ~ N(0, 0.1);
+    per-call times (ms) of the forward and of the backward (replay, value
+    and key passes) through the C ABI between HIP events on the launch
+    stream."""
+    from flashrwkv2_amd import _native as N
+
+    B, T, H = w.info["B"], w.info["T"], w.info["H"]
+    D = 64
+    dev = w.tokens[0].device
+    toks = list(w.tokens)
+    nck = T // chunk_len
+    offsets = torch.arange(B + 1, dtype=torch.int32, device=dev) * nck
+    starts = torch.arange(B * nck, dtype=torch.int32, device=dev) * chunk_len
+    ends = starts + chunk_len
+    C = B * nck
+    g = torch.Generator(device=dev)
+    g.manual_seed(2002)
+    state0 = torch.randn((B, H, D, D), generator=g, device=dev) * 0.1
+    state = state0.clone()
+    dy = torch.randn((B * T, H, D), generator=g, device=dev).to(torch.bfloat16)
+    dfin = torch.randn((B, H, D, D), generator=g, device=dev)
+    y = torch.empty_like(toks[3])
+    boundary = torch.empty((C, H, D, D), device=dev, dtype=torch.float32)
+    sa = torch.empty((B * T, H, D), device=dev, dtype=torch.float32)
+    lib = N.load()
+    work = torch.empty(int(lib.fr2_wkv7_statetune_backward_workspace_floats(B * T, H, D)),
+                       device=dev, dtype=torch.float32)
+    grads = [torch.empty_like(t) for t in toks]
+    g0 = torch.empty_like(state)
+    stream = torch.cuda.current_stream()
+    meta = (offsets.data_ptr(), starts.data_ptr(), ends.data_ptr(), B, C, B * T, H, D,
+            N.FR2_DTYPE_BFLOAT16)
+    ptrs = [t.data_ptr() for t in toks]
+
+    def fwd():
+        state.copy_(state0)   # the forward updates the state in place
+        return lib.fr2_wkv7_statetune_forward(*meta, state.data_ptr(), *ptrs, y.data_ptr(),
+                                              boundary.data_ptr(), sa.data_ptr(), 1.0,
+                                              stream.cuda_stream)
+
+    def bwd():
+        return lib.fr2_wkv7_statetune_backward(
+            *meta, *ptrs, sa.data_ptr(), dy.data_ptr(), dfin.data_ptr(), boundary.data_ptr(),
+            work.data_ptr(), *(t.data_ptr() for t in grads), g0.data_ptr(), 1.0,
+            stream.cuda_stream)
+
+    def timed(fn, name):
+        N.check(fn(), name)
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            rc = fn()
+            if rc:
+                N.check(rc, name)
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
+
+    fwd_ms = timed(fwd, "fr2_wkv7_statetune_forward")
+    bwd_ms = timed(bwd, "fr2_wkv7_statetune_backward")
+    ok = all(bool(torch.isfinite(t).all()) for t in (*grads, g0))
+    th = B * T * H
+    state_bytes = D * D * 4
+    fwd_bytes = ST_FWD_BYTES_PER_TOKEN_HEAD * th + (C + 2 * B) * H * state_bytes
+    bwd_bytes = (ST_BWD_BYTES_PER_TOKEN_HEAD * th + 3 * C * H * state_bytes
+                 + 2 * (th // 16) * state_bytes + 2 * B * H * state_bytes)
+    return {
+        "workload": f"cfg1_shape_statetune_B{B}_T{T}_H{H}_chunk{chunk_len}",
+        "forward_ms": round(fwd_ms, 4), "backward_ms": round(bwd_ms, 4),
+        "train_tokens_per_s": round(B * T / ((fwd_ms + bwd_ms) * 1e-3), 1),
+        "forward_roofline": roofline_obj(fwd_bytes, fwd_ms),
+        "backward_roofline": roofline_obj(bwd_bytes, bwd_ms),
+        "gradients_finite": ok,
+        "kernels": ["st_forward_kernel<64,IoBF16,false> (y, sa, boundary, final state)",
+                    "st_forward_kernel<64,IoBF16,true> (replay: in-chunk snapshots)",
+                    "st_value_kernel<64,IoBF16> (dv, dsa)",
+                    "st_key_kernel<64,IoBF16> (dr, dw, dk, db, da, dS0)"],
+    }
+
+
 def mfma_obj(w, kernel_ms: float):
     """Matrix-core use of the chunked kernel: issued bf16 MFMA flops (hi/lo
     split products included) over the launch time, against the dense bf16 peak."""
@@ -587,6 +683,7 @@ def main() -> int:
     if args.only in (None, "train") and not args.no_train:
         wt = pre.w if (pre is not None and args.config == 1) else workloads.config(1, "cuda")
         result["pretrain_training"] = time_pretrain_training(torch, wt, max(3, args.steps // 4))
+        result["statetune_training"] = time_statetune_training(torch, wt, max(3, args.steps // 4))
     if args.only in (None, "stages"):
         result["layer_stages"] = time_layer_stages(torch, 8 * 4096, 32)
     if pre is not None and not args.no_cpu and args.config == 1:

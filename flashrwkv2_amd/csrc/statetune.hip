@@ -40,11 +40,14 @@ namespace {
 
 constexpr float kWScale = -0.6065306597126334f;  // -exp(-1/2)
 constexpr int kThreads = 256;
-constexpr int E = 16;                             // elements per lane
 
 template <int D>
 struct St {
-  static constexpr int L = D / 16;                // lanes per line
+  // lanes per line (16 elements each); 16 lanes per line at every D (D/16
+  // elements each) measured ~6 % slower at D = 64: the per-token chain is
+  // reduction and LDS latency, not element work
+  static constexpr int L = D / 16;
+  static constexpr int E = D / L;                 // elements per lane
   static constexpr int LINES = kThreads / L;      // lines per workgroup
   static constexpr int G = D / LINES;             // workgroups per (seq, head)
   static constexpr int TT = D == 256 ? 8 : 16;    // tokens per tile
@@ -62,6 +65,7 @@ __device__ __forceinline__ float line_sum(float x) {
   return x;
 }
 
+template <int E>
 __device__ __forceinline__ void lds16(const float* src, float* dst) {
 #pragma unroll
   for (int x = 0; x < E; x += 4) {
@@ -70,6 +74,7 @@ __device__ __forceinline__ void lds16(const float* src, float* dst) {
   }
 }
 
+template <int E>
 __device__ __forceinline__ void store16(float* dst, const float* src) {
 #pragma unroll
   for (int x = 0; x < E; x += 4) {
@@ -118,7 +123,7 @@ __device__ __forceinline__ void seq_chunks(const StateTuneArgs& p, int seq, int&
 template <int D, class Io, bool kReplay>
 __global__ __launch_bounds__(kThreads) void st_forward_kernel(StateTuneArgs p) {
   using C = St<D>;
-  constexpr int L = C::L, LINES = C::LINES, G = C::G, TT = C::TT;
+  constexpr int L = C::L, E = C::E, LINES = C::LINES, G = C::G, TT = C::TT;
   constexpr int UF = D / 8, UP = LINES / 8, UT = 5 * UF + UP;
   __shared__ __align__(16) float tok[TT][5][D];   // r, w (retention), k, a, b
   __shared__ __align__(16) float vv[TT][LINES];   // v on this group's columns
@@ -188,20 +193,20 @@ __global__ __launch_bounds__(kThreads) void st_forward_kernel(StateTuneArgs p) {
       __syncthreads();
       for (int tt = 0; tt < n; ++tt) {
         float A[E], W[E], B[E], K[E];
-        lds16(&tok[tt][3][q * E], A);
+        lds16<E>(&tok[tt][3][q * E], A);
         float sp = 0.0f;
 #pragma unroll
         for (int x = 0; x < E; ++x) sp = fmaf(A[x], S[x], sp);
         const float sa = line_sum<L>(sp);
-        lds16(&tok[tt][1][q * E], W);
-        lds16(&tok[tt][4][q * E], B);
-        lds16(&tok[tt][2][q * E], K);
+        lds16<E>(&tok[tt][1][q * E], W);
+        lds16<E>(&tok[tt][4][q * E], B);
+        lds16<E>(&tok[tt][2][q * E], K);
         const float vj = vv[tt][line];
 #pragma unroll
         for (int x = 0; x < E; ++x) S[x] = fmaf(K[x], vj, fmaf(B[x], sa, W[x] * S[x]));
         if constexpr (!kReplay) {
           float R[E];
-          lds16(&tok[tt][0][q * E], R);
+          lds16<E>(&tok[tt][0][q * E], R);
           float yp = 0.0f;
 #pragma unroll
           for (int x = 0; x < E; ++x) yp = fmaf(R[x], S[x], yp);
@@ -227,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void st_forward_kernel(StateTuneArgs p) {
 template <int D, class Io>
 __global__ __launch_bounds__(kThreads) void st_value_kernel(StateTuneArgs p) {
   using C = St<D>;
-  constexpr int L = C::L, LINES = C::LINES, G = C::G, TT = C::TT;
+  constexpr int L = C::L, E = C::E, LINES = C::LINES, G = C::G, TT = C::TT;
   constexpr int UF = D / 8, UP = LINES / 8, UT = 5 * UF + UP;
   __shared__ __align__(16) float tok[TT][5][D];   // r, w (retention), k, a, b
   __shared__ __align__(16) float dyv[TT][LINES];  // dy on this group's columns
@@ -284,12 +289,12 @@ __global__ __launch_bounds__(kThreads) void st_value_kernel(StateTuneArgs p) {
       __syncthreads();
       for (int tt = n - 1; tt >= 0; --tt) {
         float R[E], K[E], B[E];
-        lds16(&tok[tt][0][q * E], R);
+        lds16<E>(&tok[tt][0][q * E], R);
         const float sdy = p.scale * dyv[tt][line];
 #pragma unroll
         for (int x = 0; x < E; ++x) P[x] = fmaf(R[x], sdy, P[x]);
-        lds16(&tok[tt][2][q * E], K);
-        lds16(&tok[tt][4][q * E], B);
+        lds16<E>(&tok[tt][2][q * E], K);
+        lds16<E>(&tok[tt][4][q * E], B);
         float vp = 0.0f, dp = 0.0f;
 #pragma unroll
         for (int x = 0; x < E; ++x) {
@@ -302,8 +307,8 @@ __global__ __launch_bounds__(kThreads) void st_value_kernel(StateTuneArgs p) {
         if (q == 0 && p.dv != nullptr) static_cast<raw*>(p.dv)[o] = Io::from_f32(dvj);
         if (q == 1) p.dsa[o] = dsj;
         float W[E], A[E];
-        lds16(&tok[tt][1][q * E], W);
-        lds16(&tok[tt][3][q * E], A);
+        lds16<E>(&tok[tt][1][q * E], W);
+        lds16<E>(&tok[tt][3][q * E], A);
 #pragma unroll
         for (int x = 0; x < E; ++x) P[x] = fmaf(W[x], P[x], A[x] * dsj);
       }
@@ -318,7 +323,7 @@ __global__ __launch_bounds__(kThreads) void st_value_kernel(StateTuneArgs p) {
 template <int D, class Io>
 __global__ __launch_bounds__(kThreads) void st_key_kernel(StateTuneArgs p) {
   using C = St<D>;
-  constexpr int L = C::L, LINES = C::LINES, G = C::G, TT = C::TT;
+  constexpr int L = C::L, E = C::E, LINES = C::LINES, G = C::G, TT = C::TT;
   constexpr int UB = D / 8, UF = D / 4, UR = LINES / 8;
   constexpr int UT = 2 * UB + 2 * UF + 5 * UR;
   __shared__ __align__(16) float vec[TT][4][D];       // dy, v, sa, dsa
@@ -337,7 +342,7 @@ __global__ __launch_bounds__(kThreads) void st_key_kernel(StateTuneArgs p) {
   const int64_t rowoff = static_cast<int64_t>(i) * D + q * E;   // element (i, qE)
   float P[E];
   if (p.dfinal != nullptr) {
-    lds16(p.dfinal + (static_cast<int64_t>(seq) * p.heads + h) * DD + rowoff, P);
+    lds16<E>(p.dfinal + (static_cast<int64_t>(seq) * p.heads + h) * DD + rowoff, P);
   } else {
 #pragma unroll
     for (int x = 0; x < E; ++x) P[x] = 0.0f;
@@ -394,7 +399,7 @@ __global__ __launch_bounds__(kThreads) void st_key_kernel(StateTuneArgs p) {
           ? p.boundary + (static_cast<int64_t>(c) * p.heads + h) * DD + rowoff
           : p.snap + (static_cast<int64_t>(t0 / TT) * p.heads + h) * DD + rowoff;
       float Org[E], Mid[E], S[E];
-      lds16(org, Org);
+      lds16<E>(org, Org);
       // rebuild forwards (the forward's own arithmetic), keeping the state
       // after token m-1
       const int m = n / 2;
@@ -406,8 +411,8 @@ __global__ __launch_bounds__(kThreads) void st_key_kernel(StateTuneArgs p) {
       for (int tt = 0; tt < n; ++tt) {
         const float wi = rows[tt][1][line], ki = rows[tt][2][line], bi = rows[tt][4][line];
         float V[E], SA[E];
-        lds16(&vec[tt][1][q * E], V);
-        lds16(&vec[tt][2][q * E], SA);
+        lds16<E>(&vec[tt][1][q * E], V);
+        lds16<E>(&vec[tt][2][q * E], SA);
 #pragma unroll
         for (int x = 0; x < E; ++x) S[x] = fmaf(ki, V[x], fmaf(bi, SA[x], wi * S[x]));
         if (tt == m - 1) {
@@ -421,10 +426,10 @@ __global__ __launch_bounds__(kThreads) void st_key_kernel(StateTuneArgs p) {
         const float ki = rows[tt][2][line], ai = rows[tt][3][line];
         const float bi = rows[tt][4][line], wsi = rows[tt][5][line];
         float DY[E], V[E], SA[E], DS[E];
-        lds16(&vec[tt][0][q * E], DY);
-        lds16(&vec[tt][1][q * E], V);
-        lds16(&vec[tt][2][q * E], SA);
-        lds16(&vec[tt][3][q * E], DS);
+        lds16<E>(&vec[tt][0][q * E], DY);
+        lds16<E>(&vec[tt][1][q * E], V);
+        lds16<E>(&vec[tt][2][q * E], SA);
+        lds16<E>(&vec[tt][3][q * E], DS);
         const float sri = p.scale * ri;
         float pr = 0.0f, pk = 0.0f, pb = 0.0f;
 #pragma unroll
@@ -474,7 +479,7 @@ __global__ __launch_bounds__(kThreads) void st_key_kernel(StateTuneArgs p) {
     }
   }
   if (p.dstate0 != nullptr)
-    store16(p.dstate0 + (static_cast<int64_t>(seq) * p.heads + h) * DD + rowoff, P);
+    store16<E>(p.dstate0 + (static_cast<int64_t>(seq) * p.heads + h) * DD + rowoff, P);
 }
 
 template <int D, class Io>
