@@ -473,9 +473,11 @@ ST_BWD_BYTES_PER_TOKEN_HEAD = 768 + 768 + 128 + 256 + 256 + 512 + 640 + 640
 def time_statetune_training(torch, w, steps: int, chunk_len: int = 1024):
     """StateTune on the config-1 shape: B sequences of T tokens, each run as
     T/chunk_len chunks from a trainable fp32 initial state ~ N(0, 0.1);
-    per-call times (ms) of the forward and of the backward (replay, value
-    and key passes) through the C ABI between HIP events on the launch
-    stream."""
+    per-call times (ms) of the forward and of the backward through the C ABI
+    between HIP events on the launch stream.  This chunk list is the uniform
+    layout, so the public entry runs the chunked MFMA kernels
+    (`fr2_wkv7_statetune_uniform_*`); the token-serial kernels that serve
+    every other chunk list (`fr2_wkv7_statetune_*`) are timed on it too."""
     from flashrwkv2_amd import _native as N
 
     B, T, H = w.info["B"], w.info["T"], w.info["H"]
@@ -496,27 +498,44 @@ def time_statetune_training(torch, w, steps: int, chunk_len: int = 1024):
     y = torch.empty_like(toks[3])
     boundary = torch.empty((C, H, D, D), device=dev, dtype=torch.float32)
     sa = torch.empty((B * T, H, D), device=dev, dtype=torch.float32)
+    snaps = torch.empty((B, H, T // 16, D, D), device=dev, dtype=torch.float32)
     lib = N.load()
-    work = torch.empty(int(lib.fr2_wkv7_statetune_backward_workspace_floats(B * T, H, D)),
-                       device=dev, dtype=torch.float32)
+    work_s = torch.empty(int(lib.fr2_wkv7_statetune_backward_workspace_floats(B * T, H, D)),
+                         device=dev, dtype=torch.float32)
+    work_u = torch.empty(int(lib.fr2_wkv7_statetune_uniform_backward_workspace_floats(B, T, H)),
+                         device=dev, dtype=torch.float32)
     grads = [torch.empty_like(t) for t in toks]
     g0 = torch.empty_like(state)
     stream = torch.cuda.current_stream()
+    hs = stream.cuda_stream
     meta = (offsets.data_ptr(), starts.data_ptr(), ends.data_ptr(), B, C, B * T, H, D,
             N.FR2_DTYPE_BFLOAT16)
     ptrs = [t.data_ptr() for t in toks]
+    gptrs = [t.data_ptr() for t in grads]
 
-    def fwd():
-        state.copy_(state0)   # the forward updates the state in place
+    # each forward first restores the initial state (it is updated in place):
+    # an 8 MiB copy, about 2 us, inside the forward's timing
+    def fwd_uniform():
+        state.copy_(state0)
+        return lib.fr2_wkv7_statetune_uniform_forward(
+            B, T, H, chunk_len, state.data_ptr(), *ptrs, y.data_ptr(), boundary.data_ptr(),
+            sa.data_ptr(), snaps.data_ptr(), 1.0, hs)
+
+    def bwd_uniform():
+        return lib.fr2_wkv7_statetune_uniform_backward(
+            B, T, H, chunk_len, *ptrs, sa.data_ptr(), dy.data_ptr(), dfin.data_ptr(),
+            boundary.data_ptr(), snaps.data_ptr(), work_u.data_ptr(), *gptrs, g0.data_ptr(), 1.0,
+            hs)
+
+    def fwd_serial():
+        state.copy_(state0)
         return lib.fr2_wkv7_statetune_forward(*meta, state.data_ptr(), *ptrs, y.data_ptr(),
-                                              boundary.data_ptr(), sa.data_ptr(), 1.0,
-                                              stream.cuda_stream)
+                                              boundary.data_ptr(), sa.data_ptr(), 1.0, hs)
 
-    def bwd():
+    def bwd_serial():
         return lib.fr2_wkv7_statetune_backward(
             *meta, *ptrs, sa.data_ptr(), dy.data_ptr(), dfin.data_ptr(), boundary.data_ptr(),
-            work.data_ptr(), *(t.data_ptr() for t in grads), g0.data_ptr(), 1.0,
-            stream.cuda_stream)
+            work_s.data_ptr(), *gptrs, g0.data_ptr(), 1.0, hs)
 
     def timed(fn, name):
         N.check(fn(), name)
@@ -532,25 +551,38 @@ def time_statetune_training(torch, w, steps: int, chunk_len: int = 1024):
         torch.cuda.synchronize()
         return start.elapsed_time(end) / steps
 
-    fwd_ms = timed(fwd, "fr2_wkv7_statetune_forward")
-    bwd_ms = timed(bwd, "fr2_wkv7_statetune_backward")
+    sf = timed(fwd_serial, "fr2_wkv7_statetune_forward")
+    sb = timed(bwd_serial, "fr2_wkv7_statetune_backward")
+    uf = timed(fwd_uniform, "fr2_wkv7_statetune_uniform_forward")
+    ub = timed(bwd_uniform, "fr2_wkv7_statetune_uniform_backward")
     ok = all(bool(torch.isfinite(t).all()) for t in (*grads, g0))
     th = B * T * H
     state_bytes = D * D * 4
+    # token-serial: boundaries written forward and read by replay and key
+    # pass; replay snapshots written and read once
     fwd_bytes = ST_FWD_BYTES_PER_TOKEN_HEAD * th + (C + 2 * B) * H * state_bytes
     bwd_bytes = (ST_BWD_BYTES_PER_TOKEN_HEAD * th + 3 * C * H * state_bytes
                  + 2 * (th // 16) * state_bytes + 2 * B * H * state_bytes)
+    # chunked: the forward also writes the post-16-token snapshots, which the
+    # backward's key pass reads; the backward is the pretrain one's 2 944 B
+    # per token-head plus dL/dS_final in and dL/dS_initial out
+    ufwd_bytes = fwd_bytes + (th // 16) * state_bytes
+    ubwd_bytes = BWD_BYTES_PER_TOKEN_HEAD * th + 2 * B * H * state_bytes
     return {
         "workload": f"cfg1_shape_statetune_B{B}_T{T}_H{H}_chunk{chunk_len}",
-        "forward_ms": round(fwd_ms, 4), "backward_ms": round(bwd_ms, 4),
-        "train_tokens_per_s": round(B * T / ((fwd_ms + bwd_ms) * 1e-3), 1),
-        "forward_roofline": roofline_obj(fwd_bytes, fwd_ms),
-        "backward_roofline": roofline_obj(bwd_bytes, bwd_ms),
+        "forward_ms": round(uf, 4), "backward_ms": round(ub, 4),
+        "train_tokens_per_s": round(B * T / ((uf + ub) * 1e-3), 1),
+        "forward_roofline": roofline_obj(ufwd_bytes, uf),
+        "backward_roofline": roofline_obj(ubwd_bytes, ub),
+        "token_serial": {"forward_ms": round(sf, 4), "backward_ms": round(sb, 4),
+                         "train_tokens_per_s": round(B * T / ((sf + sb) * 1e-3), 1),
+                         "forward_roofline": roofline_obj(fwd_bytes, sf),
+                         "backward_roofline": roofline_obj(bwd_bytes, sb)},
         "gradients_finite": ok,
-        "kernels": ["st_forward_kernel<64,IoBF16,false> (y, sa, boundary, final state)",
-                    "st_forward_kernel<64,IoBF16,true> (replay: in-chunk snapshots)",
-                    "st_value_kernel<64,IoBF16> (dv, dsa)",
-                    "st_key_kernel<64,IoBF16> (dr, dw, dk, db, da, dS0)"],
+        "kernels": ["chunk64_kernel<IoBF16,true> (forward) + st_gather_kernel (boundaries)",
+                    "chunk64_kernel<IoBF16,true,true> + first_token_kernel + key_chunk_kernel "
+                    "(backward)",
+                    "token-serial: st_forward_kernel, st_value_kernel, st_key_kernel"],
     }
 
 

@@ -548,13 +548,37 @@ def _statetune_check(sequence_chunk_offsets, chunk_token_starts, chunk_token_end
     return state.size(0), chunk_token_starts.numel(), r.size(0), state.size(1), D
 
 
+def _statetune_uniform_chunk_len(offsets, starts, ends, B, C, T, D, dtype):
+    """The chunk length when the chunk list is B sequences of equal length
+    packed back to back, each cut into equal chunks of a multiple of 16
+    tokens (D = 64, bf16): the layout the chunked MFMA kernels take.
+    Reads the (small) chunk metadata on the host."""
+    if D != 64 or dtype != torch.bfloat16 or C % B or T % B:
+        return None
+    nck, per_seq = C // B, T // B
+    if per_seq % nck or (per_seq // nck) % 16:
+        return None
+    length = per_seq // nck
+    dev = starts.device
+    want = torch.arange(C + 1, dtype=torch.int32, device=dev) * length
+    ok = (torch.equal(offsets, torch.arange(B + 1, dtype=torch.int32, device=dev) * nck)
+          and torch.equal(starts, want[:-1]) and torch.equal(ends, want[1:]))
+    return length if ok else None
+
+
 def statetune_tmix_wkv7_recurrent_fp32io16_forward(sequence_chunk_offsets, chunk_token_starts,
                                                    chunk_token_ends, state, r, decay_logits,
                                                    k, v, a, b, output, boundary, state_dot_a,
                                                    scale=1.0):
     """statetune_recurrent_fp32io16_forward.cpp:26-56: runs every sequence's
     chunks from ``state`` (updated in place to the final state) and fills
-    ``output``, ``boundary`` (start-of-chunk states) and ``state_dot_a``."""
+    ``output``, ``boundary`` (start-of-chunk states) and ``state_dot_a``.
+
+    When the chunk list is the uniform layout (D = 64, bf16, equal sequences
+    packed back to back, equal chunks of a multiple of 16 tokens) it runs on
+    the chunked MFMA kernels and returns the fp32 post-16-token state
+    snapshots ``[B,H,T/16,64,64]`` that the fast backward takes; otherwise it
+    runs token-serial and returns None (the reference returns None)."""
     B, C, T, H, D = _statetune_check(
         sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, state,
         ((r, "r"), (decay_logits, "decay_logits"), (k, "k"), (v, "v"), (a, "a"), (b, "b"),
@@ -565,7 +589,20 @@ def statetune_tmix_wkv7_recurrent_fp32io16_forward(sequence_chunk_offsets, chunk
            "boundary must be float32 [C,H,D,D]")
     _check(state_dot_a.dtype == torch.float32 and state_dot_a.shape == r.shape,
            "state_dot_a must be float32 [total_tokens,H,D]")
+    length = _statetune_uniform_chunk_len(sequence_chunk_offsets, chunk_token_starts,
+                                          chunk_token_ends, B, C, T, D, r.dtype)
     with torch.cuda.device(state.device):
+        if length is not None:
+            per_seq = T // B
+            snapshots = torch.empty((B, H, per_seq // 16, D, D), device=state.device,
+                                    dtype=torch.float32)
+            rc = N.load().fr2_wkv7_statetune_uniform_forward(
+                B, per_seq, H, length, state.data_ptr(), r.data_ptr(), decay_logits.data_ptr(),
+                k.data_ptr(), v.data_ptr(), a.data_ptr(), b.data_ptr(), output.data_ptr(),
+                boundary.data_ptr(), state_dot_a.data_ptr(), snapshots.data_ptr(), float(scale),
+                _stream(state.device))
+            N.check(rc, "statetune_tmix_wkv7_recurrent_fp32io16_forward")
+            return snapshots
         rc = N.load().fr2_wkv7_statetune_forward(
             sequence_chunk_offsets.data_ptr(), chunk_token_starts.data_ptr(),
             chunk_token_ends.data_ptr(), B, C, T, H, D, _dtype_code(r), state.data_ptr(),
@@ -573,6 +610,7 @@ def statetune_tmix_wkv7_recurrent_fp32io16_forward(sequence_chunk_offsets, chunk
             b.data_ptr(), output.data_ptr(), boundary.data_ptr(), state_dot_a.data_ptr(),
             float(scale), _stream(state.device))
     N.check(rc, "statetune_tmix_wkv7_recurrent_fp32io16_forward")
+    return None
 
 
 def statetune_tmix_wkv7_recurrent_fp32io16_backward(sequence_chunk_offsets, chunk_token_starts,
@@ -581,13 +619,15 @@ def statetune_tmix_wkv7_recurrent_fp32io16_backward(sequence_chunk_offsets, chun
                                                     grad_output, grad_final_state, boundary,
                                                     grad_r, grad_decay_logits, grad_k, grad_v,
                                                     grad_a, grad_b, grad_initial_state,
-                                                    scale=1.0):
+                                                    scale=1.0, snapshots=None):
     """statetune_recurrent_fp32io16_backward.cpp:34-82: fills the six token
     gradients and ``grad_initial_state`` in place.  ``grad_output`` and
     ``grad_final_state`` may be None (zero).  ``final_state`` is checked but
     not read: chunk-end states are rebuilt from ``boundary``.  The fp32
     workspace (d(sa) per token and the replayed in-chunk states) is
-    allocated here."""
+    allocated here.  ``snapshots`` (not in the reference) is what the
+    forward returned on the uniform layout: with it and a ``grad_output``
+    the backward runs on the chunked MFMA kernels."""
     grads = ((grad_r, "grad_r"), (grad_decay_logits, "grad_decay_logits"), (grad_k, "grad_k"),
              (grad_v, "grad_v"), (grad_a, "grad_a"), (grad_b, "grad_b"))
     toks = [(r, "r"), (decay_logits, "decay_logits"), (k, "k"), (v, "v"), (a, "a"), (b, "b"),
@@ -612,10 +652,32 @@ def statetune_tmix_wkv7_recurrent_fp32io16_backward(sequence_chunk_offsets, chun
         _check(grad_final_state.dtype == torch.float32
                and grad_final_state.shape == final_state.shape,
                "grad_final_state must be float32 [B,H,D,D]")
+    ptr = lambda t: None if t is None else t.data_ptr()
+    if snapshots is not None and grad_output is not None:
+        per_seq = T // B
+        _check(T % B == 0 and C % B == 0 and T % C == 0,
+               "snapshots are only for the uniform chunk layout")
+        length = T // C
+        check_cuda_contiguous(snapshots, "snapshots")
+        _check(snapshots.dtype == torch.float32
+               and tuple(snapshots.shape) == (B, H, per_seq // 16, D, D)
+               and D == 64 and r.dtype == torch.bfloat16 and length % 16 == 0
+               and per_seq % length == 0, "snapshots do not match the uniform chunk layout")
+        nws = N.load().fr2_wkv7_statetune_uniform_backward_workspace_floats(B, per_seq, H)
+        _check(nws > 0, "statetune backward: unsupported shape")
+        workspace = torch.empty(nws, device=r.device, dtype=torch.float32)
+        with torch.cuda.device(final_state.device):
+            rc = N.load().fr2_wkv7_statetune_uniform_backward(
+                B, per_seq, H, length, r.data_ptr(), decay_logits.data_ptr(), k.data_ptr(),
+                v.data_ptr(), a.data_ptr(), b.data_ptr(), state_dot_a.data_ptr(),
+                grad_output.data_ptr(), ptr(grad_final_state), boundary.data_ptr(),
+                snapshots.data_ptr(), workspace.data_ptr(), *(g.data_ptr() for g, _ in grads),
+                grad_initial_state.data_ptr(), float(scale), _stream(final_state.device))
+        N.check(rc, "statetune_tmix_wkv7_recurrent_fp32io16_backward")
+        return
     nws = N.load().fr2_wkv7_statetune_backward_workspace_floats(T, H, D)
     _check(nws > 0, "statetune backward: unsupported shape")
     workspace = torch.empty(nws, device=r.device, dtype=torch.float32)
-    ptr = lambda t: None if t is None else t.data_ptr()
     with torch.cuda.device(final_state.device):
         rc = N.load().fr2_wkv7_statetune_backward(
             sequence_chunk_offsets.data_ptr(), chunk_token_starts.data_ptr(),

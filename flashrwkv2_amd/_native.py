@@ -84,6 +84,15 @@ SIGNATURES: dict[str, tuple] = {
         [c_void_p] * 3 + [c_int32, c_int32, c_int64, c_int32, c_int32, c_int32]
         + [c_void_p] * 18 + [c_float, c_void_p],
     ),
+    "fr2_wkv7_statetune_uniform_forward": (
+        c_int32, [c_int32] * 4 + [c_void_p] * 11 + [c_float, c_void_p],
+    ),
+    "fr2_wkv7_statetune_uniform_backward_workspace_floats": (
+        c_int64, [c_int32] * 3,
+    ),
+    "fr2_wkv7_statetune_uniform_backward": (
+        c_int32, [c_int32] * 4 + [c_void_p] * 19 + [c_float, c_void_p],
+    ),
     "fr2_tmix_kk_a_gate_forward": (
         c_int32, [c_int64, c_int32, c_int32] + [c_void_p] * 9,
     ),

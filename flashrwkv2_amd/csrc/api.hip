@@ -383,6 +383,73 @@ extern "C" int fr2_wkv7_statetune_backward(
                                         static_cast<hipStream_t>(stream));
 }
 
+namespace {
+
+bool statetune_uniform_ok(int32_t batch, int32_t tokens, int32_t num_heads, int32_t chunk_len) {
+  return batch > 0 && num_heads > 0 && tokens > 0 && chunk_len > 0 && chunk_len % 16 == 0 &&
+         tokens % chunk_len == 0 &&
+         static_cast<int64_t>(batch) * num_heads <= (int64_t{1} << 30) / 4 &&
+         static_cast<int64_t>(batch) * tokens < (int64_t{1} << 31);
+}
+
+}  // namespace
+
+extern "C" int fr2_wkv7_statetune_uniform_forward(
+    int32_t batch, int32_t tokens, int32_t num_heads, int32_t chunk_len, float* state,
+    const void* r, const void* decay_logits, const void* k, const void* v, const void* a,
+    const void* b, void* output, float* boundary, float* state_dot_a, float* snapshots,
+    float scale, void* stream) {
+  if (!state || !tokens_ok(r, decay_logits, k, v, a, b, output) || !boundary || !state_dot_a ||
+      !snapshots)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (!statetune_uniform_ok(batch, tokens, num_heads, chunk_len)) return FR2_ERR_INVALID_ARGUMENT;
+  fr2::StateTuneArgs p;
+  p.heads = num_heads;
+  p.r = r; p.w = decay_logits; p.k = k; p.v = v; p.a = a; p.b = b;
+  p.scale = scale;
+  p.state = state;
+  p.y = output;
+  p.sa = state_dot_a;
+  p.boundary = boundary;
+  return fr2::launch_statetune_uniform_forward(batch, tokens, num_heads, chunk_len, p, snapshots,
+                                               static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t fr2_wkv7_statetune_uniform_backward_workspace_floats(int32_t batch,
+                                                                        int32_t tokens,
+                                                                        int32_t num_heads) {
+  if (batch <= 0 || tokens <= 0 || tokens % 16 != 0 || num_heads <= 0) return -1;
+  return fr2::pretrain_backward_workspace_floats(batch, tokens, num_heads, 64) +
+         static_cast<int64_t>(batch) * num_heads * 64 * 64;
+}
+
+extern "C" int fr2_wkv7_statetune_uniform_backward(
+    int32_t batch, int32_t tokens, int32_t num_heads, int32_t chunk_len, const void* r,
+    const void* decay_logits, const void* k, const void* v, const void* a, const void* b,
+    const float* state_dot_a, const void* grad_output, const float* grad_final_state,
+    const float* boundary, const float* snapshots, float* workspace, void* grad_r,
+    void* grad_decay_logits, void* grad_k, void* grad_v, void* grad_a, void* grad_b,
+    float* grad_initial_state, float scale, void* stream) {
+  if (!r || !decay_logits || !k || !v || !a || !b || !state_dot_a || !grad_output || !boundary ||
+      !snapshots || !workspace || !grad_r || !grad_decay_logits || !grad_k || !grad_v ||
+      !grad_a || !grad_b || !grad_initial_state)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (!statetune_uniform_ok(batch, tokens, num_heads, chunk_len)) return FR2_ERR_INVALID_ARGUMENT;
+  fr2::StateTuneArgs p;
+  p.heads = num_heads;
+  p.r = r; p.w = decay_logits; p.k = k; p.v = v; p.a = a; p.b = b;
+  p.scale = scale;
+  p.sa = const_cast<float*>(state_dot_a);
+  p.boundary = const_cast<float*>(boundary);
+  p.dy = grad_output;
+  p.dfinal = grad_final_state;
+  p.dr = grad_r; p.dw = grad_decay_logits; p.dk = grad_k; p.dv = grad_v;
+  p.da = grad_a; p.db = grad_b;
+  p.dstate0 = grad_initial_state;
+  return fr2::launch_statetune_uniform_backward(batch, tokens, num_heads, chunk_len, p, snapshots,
+                                                workspace, static_cast<hipStream_t>(stream));
+}
+
 // ---------------------------------------------------------------------------
 // producer / consumer stages of the layer (fp16)
 // ---------------------------------------------------------------------------

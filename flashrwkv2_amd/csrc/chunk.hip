@@ -139,7 +139,8 @@ template <class Io, bool kVExact, bool kFull, bool kUnitW = false>
 __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& op,
                                           const u32x4 (&raw)[6], const float (&nbias8)[8],
                                           bool valid, int mp, int cc, int hh, int i, int q,
-                                          KeyRegs& kr, bool unit_w = false) {
+                                          KeyRegs& kr, bool unit_w = false,
+                                          float kscale = 1.0f) {
   const int kbase = 32 * hh + 8 * q;
   // tokens past the sequence end (their rows repeat the last token) carry
   // zero operands and a unit retention
@@ -170,6 +171,7 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
     rt[e] = xr[e] * gm;
     bh[e] = xb[e] * ig;
     kh[e] = xk[e] * ig;
+    if constexpr (kUnitW) kh[e] *= kscale;   // reverse mode: k is r_t, times scale
     if (i == L - 1) op.gl[kbase + e] = gm;
   }
   kr.As = split8(at);
@@ -677,11 +679,11 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
         const bool unit_w = void_row && ((p.shift_mask >> 1) & 1);
         if (t0 + gn * GT + cc * L + L <= t1)
           key_part1<Io, kVExact, true, true>(sm, sm.ops[par][cc], rows, nbias8, true, par, cc,
-                                             hh, i, q, kr, unit_w);
+                                             hh, i, q, kr, unit_w, p.kv_scale);
         else if (active)
           key_part1<Io, kVExact, false, true>(sm, sm.ops[par][cc], rows, nbias8,
                                               t0 + gn * GT + cc * L + i < t1, par, cc, hh, i, q,
-                                              kr, unit_w);
+                                              kr, unit_w, p.kv_scale);
       } else {
         if (t0 + gn * GT + cc * L + L <= t1)
           key_part1<Io, kVExact, true>(sm, sm.ops[par][cc], cur, nbias8, true, par, cc, hh, i,
@@ -710,10 +712,10 @@ int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen, hipStr
   const dim3 grid(p.num_heads, nseg);
   if (train) {
     // the training contract: uniform segments whose length is a multiple of
-    // the 16-token chunk, both outputs present, bf16 tokens
+    // the 16-token chunk, both outputs present, bf16 tokens (an initial
+    // state, or in reverse mode an initial dL/dS, may be given)
     if (p.sa_out == nullptr || (p.boundary == nullptr && !p.reverse) || p.boundary_len != L ||
-        p.uniform_len <= 0 || p.uniform_len % L != 0 || p.state_in != nullptr ||
-        dtype != FR2_DTYPE_BFLOAT16)
+        p.uniform_len <= 0 || p.uniform_len % L != 0 || dtype != FR2_DTYPE_BFLOAT16)
       return FR2_ERR_UNSUPPORTED;
     if (p.reverse)
       hipLaunchKernelGGL((chunk64_kernel<IoBF16, true, true>), grid, dim3(NT), 0, s, p);

@@ -491,6 +491,29 @@ __global__ __launch_bounds__(256) void key_kernel(
   }
 }
 
+// StateTune: the value pass ends with P at each sequence's first token t0
+// (pfirst) but does not form dsa_t0 = P^T b_t0 (it writes zero there: with a
+// zero initial state nothing reads it).  With a trainable initial state
+// da_t0 = S_init dsa_t0 does, and dL/dS_init = diag(w_t0) P + a_t0 dsa_t0^T.
+// One workgroup per (sequence, head), lane j = value column.
+__global__ __launch_bounds__(64) void first_token_kernel(int T, int H, const uint16_t* wl,
+                                                         const uint16_t* a, const uint16_t* b,
+                                                         const float* pfirst, float* dsa,
+                                                         float* dstate0) {
+  constexpr int D = 64;
+  const int bh = blockIdx.x, bidx = bh / H, h = bh % H, j = threadIdx.x;
+  const int64_t row = (static_cast<int64_t>(bidx) * T * H + h) * D;   // token t0
+  const float* P = pfirst + static_cast<int64_t>(bh) * D * D;
+  float ds = 0.0f;
+  for (int i = 0; i < D; ++i) ds = fmaf(P[i * D + j], IoBF16::to_f32(b[row + i]), ds);
+  dsa[row + j] = ds;
+  float* out = dstate0 + static_cast<int64_t>(bh) * D * D;
+  for (int i = 0; i < D; ++i) {
+    const float w = retention_from_logit(IoBF16::to_f32(wl[row + i]));
+    out[i * D + j] = fmaf(w, P[i * D + j], IoBF16::to_f32(a[row + i]) * ds);
+  }
+}
+
 template <int D>
 int launch_d(const PretrainBwdArgs& p, hipStream_t s) {
   const auto* r = static_cast<const uint16_t*>(p.r);
@@ -530,8 +553,14 @@ int launch_d(const PretrainBwdArgs& p, hipStream_t s) {
     v.boundary_every = cps;
     v.reverse = true;
     v.shift_mask = (1 << 1) | (1 << 4) | (1 << 5);
+    v.state_in = p.dfinal;     // P after the last token (StateTune), or zero
+    v.kv_scale = p.scale;
+    v.state_out = p.pfirst;    // P at token 0 (StateTune), or not written
     const int rc = launch_chunked(FR2_DTYPE_BFLOAT16, v, p.batch, p.tokens, s);
     if (rc != FR2_OK) return rc;
+    if (p.pfirst != nullptr && p.dstate0 != nullptr)
+      hipLaunchKernelGGL(first_token_kernel, dim3(bh), dim3(64), 0, s, p.tokens, p.heads, w, a, b,
+                         p.pfirst, p.workspace, p.dstate0);
     return launch_key_chunk(p, pbnd, nspan, cps, s);
   } else {
     hipLaunchKernelGGL(value_kernel<D>, dim3(bh), dim3(4 * D), 0, s, p.tokens, p.heads, r, w, k,

@@ -50,6 +50,13 @@ struct KPassArgs {
   const uint16_t *r, *w, *k, *v, *a, *b, *dy;
   const float *sa, *dsa, *bnd, *pbnd;
   uint16_t *dr, *dw, *dk, *db, *da;
+  // StateTune: y = scale * S^T r, the start state of chunk 0 (sequence b at
+  // state0 + b * state0_stride, [H,D,D]; null: zero) and dL/dS_final
+  // ([B,H,D,D]; null: zero)
+  float scale;
+  const float* state0;
+  int64_t state0_stride;
+  const float* dfinal;
 };
 
 struct alignas(32) KSmem {
@@ -147,6 +154,10 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
       const f32x4 du = ld_f4(p.dsa + tok(u) + j0);
       PcT[vb] = wu * pn + au * du;
     }
+  } else if (p.dfinal != nullptr) {
+    const float* Pf = p.dfinal + (static_cast<int64_t>(bh) * kD + row) * kD;
+#pragma unroll
+    for (int vb = 0; vb < 4; ++vb) PcT[vb] = ld_f4(Pf + 16 * vb + 4 * q);
   }
 
   // global inputs of one chunk
@@ -165,10 +176,14 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
       in.Vb[vb] = ld_bf4(p.v + tok(t0 + n) + j0);
       in.SA4[vb] = ld_f4(p.sa + tok(t0 + n) + j0);
       in.DS4[vb] = ld_f4(p.dsa + tok(t0 + n) + j0);
-      // chunk 0 starts from the zero state (row 0 of the snapshot of chunk
-      // 0 is loaded and discarded: always in bounds)
-      in.S04[vb] = ld_f4(p.bnd + (static_cast<int64_t>(bh) * nchunk + max(m - 1, 0)) * kD * kD +
-                         static_cast<int64_t>(row) * kD + j0);
+      // chunk 0 starts from state0, or from the zero state (then row 0 of
+      // the snapshot of chunk 0 is loaded and discarded: always in bounds)
+      const float* s0 =
+          (m == 0 && p.state0 != nullptr)
+              ? p.state0 + static_cast<int64_t>(bidx) * p.state0_stride +
+                    static_cast<int64_t>(h) * kD * kD
+              : p.bnd + (static_cast<int64_t>(bh) * nchunk + max(m - 1, 0)) * kD * kD;
+      in.S04[vb] = ld_f4(s0 + static_cast<int64_t>(row) * kD + j0);
     }
     const int64_t pbase = tok(t0 + tp) + 4 * kg;
     in.rw = *reinterpret_cast<const u32x2*>(p.w + pbase);
@@ -191,7 +206,7 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
       for (int e = 0; e < 4; ++e) {
         SAf[4 * vb + e] = in.SA4[vb][e];
         DSf[4 * vb + e] = in.DS4[vb][e];
-        S0f[4 * vb + e] = m > 0 ? in.S04[vb][e] : 0.0f;
+        S0f[4 * vb + e] = (m > 0 || p.state0 != nullptr) ? in.S04[vb][e] : 0.0f;
       }
     }
     const u32x2 rw = in.rw, rr = in.rr, rk = in.rk, ra = in.ra, rb = in.rb;
@@ -310,7 +325,9 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
     const f32x4 bh4 = ld_f4_lds(&sm.bh[row][4 * q]), kh4 = ld_f4_lds(&sm.kh[row][4 * q]);
     const f32x4 rh4 = ld_f4_lds(&sm.rh[row][4 * q]);
     f32x4 ah4 = ld_f4_lds(&sm.ah[row][4 * q]);
-    const Split4 sBh = split4(bh4), sKh = split4(kh4), sRh = split4(rh4), sAh = split4(ah4);
+    // R^ enters P (and so dk, db and the carry) times the output scale
+    const Split4 sBh = split4(bh4), sKh = split4(kh4), sRh = split4(p.scale * rh4),
+                 sAh = split4(ah4);
     auto gram = [&](int g) { return full_b(sm.gram[g][lane]); };
     DR = mm_ab(as_a(sKh), gram(1), mm_ab(as_a(sBh), gram(0), DR));
     DA = mm_ab(as_a(sKh), gram(3), mm_ab(as_a(sBh), gram(2), DA));
@@ -329,7 +346,7 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
         const float g = sm.gm[rk][t], g15 = sm.gm[rk][15];
         const float gp = t > 0 ? sm.gm[rk][max(t - 1, 0)] : 1.0f;
         const float rho = g15 * __builtin_amdgcn_rcpf(g);   // gamma_15 / gamma_t
-        dr[e] = g * DR[e];
+        dr[e] = p.scale * g * DR[e];
         da[e] = gp * DA[e];
         dk[e] = rho * DK[e];
         db[e] = rho * DB[e];
@@ -415,6 +432,10 @@ int launch_key_chunk(const PretrainBwdArgs& a, const float* pbnd, int nspan, int
   k.dk = static_cast<uint16_t*>(a.dk);
   k.db = static_cast<uint16_t*>(a.db);
   k.da = static_cast<uint16_t*>(a.da);
+  k.scale = a.scale;
+  k.state0 = a.state0;
+  k.state0_stride = a.state0_stride;
+  k.dfinal = a.dfinal;
   const int64_t blocks = static_cast<int64_t>(a.batch) * a.heads * nspan;
   hipLaunchKernelGGL(key_chunk_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kKNT), 0, s, k);
   return record_launch();

@@ -50,6 +50,9 @@ struct SegArgs {
   // and the snapshot after chunk c to index boundary_per_seg-1-c.
   bool reverse = false;
   int shift_mask = 0;
+  // reverse mode: factor on the k operand (the value pass's r_t), i.e. the
+  // forward's output scale
+  float kv_scale = 1.0f;
   // with boundary set: keep only the snapshots whose index is a multiple of
   // boundary_every, at index / boundary_every
   int boundary_every = 1;
@@ -80,6 +83,16 @@ struct PretrainBwdArgs {
   float* workspace = nullptr;
   void *dr = nullptr, *dw = nullptr, *dk = nullptr, *dv = nullptr, *da = nullptr,
        *db = nullptr;
+  // StateTune at D = 64 (uniform layout): y = scale * S^T r, the start state
+  // of each sequence (state0 + b * state0_stride, [H,D,D]), dL/dS_final
+  // [B,H,D,D], the output dL/dS_initial [B,H,D,D] and an fp32 [B,H,D,D]
+  // buffer for dL/dS at each sequence's first token; null / 1 for pretrain
+  float scale = 1.0f;
+  const float* state0 = nullptr;
+  int64_t state0_stride = 0;
+  const float* dfinal = nullptr;
+  float* dstate0 = nullptr;
+  float* pfirst = nullptr;
 };
 int launch_pretrain_backward(int D, const PretrainBwdArgs& p, hipStream_t s);
 // fp32 elements of the backward's workspace: dsa [B,T,H,D], and at D = 64
@@ -119,6 +132,14 @@ int launch_statetune_forward(int D, int dtype, const StateTuneArgs& p, hipStream
 int launch_statetune_backward(int D, int dtype, StateTuneArgs p, float* workspace,
                               hipStream_t s);
 int64_t statetune_backward_workspace_floats(int64_t T, int H, int D);
+// D = 64, bf16, B sequences of T tokens each as T / chunk_len chunks
+// (chunk_len % 16 == 0): the chunked MFMA kernels.  snap holds the
+// post-16-token states [B,H,T/16,64,64]; the backward's workspace is
+// pretrain_backward_workspace_floats(B, T, H, 64) + B*H*64*64 floats.
+int launch_statetune_uniform_forward(int B, int T, int H, int chunk_len, const StateTuneArgs& a,
+                                     float* snap, hipStream_t s);
+int launch_statetune_uniform_backward(int B, int T, int H, int chunk_len, const StateTuneArgs& a,
+                                      const float* snap, float* workspace, hipStream_t s);
 
 // Elementwise producer / consumer stages of the layer (fp16 I/O).
 int launch_kk_a_gate(int64_t tokens, int H, int D, const void* k, const void* k_k, const void* a0,

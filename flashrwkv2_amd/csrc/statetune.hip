@@ -504,7 +504,72 @@ int backward_d(const StateTuneArgs& p, hipStream_t s) {
   return record_launch();
 }
 
+// boundary[b * nck + j] (the state at the start of chunk j of sequence b,
+// chunks of chunk_len tokens): j = 0 from state (before the forward runs),
+// j > 0 from the post-16-token snapshot that ends at token j * chunk_len
+__global__ __launch_bounds__(256) void st_gather_kernel(int H, int nck, int chunk_len,
+                                                         bool first, const float* state,
+                                                         const float* snap, int snaps_per_seq,
+                                                         float* boundary) {
+  constexpr int DD = 64 * 64;
+  const int c = blockIdx.x / H, h = blockIdx.x % H;
+  const int b = c / nck, j = c % nck;
+  if ((j == 0) != first) return;
+  const float* src =
+      j == 0 ? state + (static_cast<int64_t>(b) * H + h) * DD
+             : snap + ((static_cast<int64_t>(b) * H + h) * snaps_per_seq + j * chunk_len / 16 - 1) *
+                          DD;
+  float* dst = boundary + static_cast<int64_t>(blockIdx.x) * DD;
+  for (int x = threadIdx.x; x < DD / 4; x += 256)
+    reinterpret_cast<f4*>(dst)[x] = reinterpret_cast<const f4*>(src)[x];
+}
+
 }  // namespace
+
+int launch_statetune_uniform_forward(int B, int T, int H, int chunk_len, const StateTuneArgs& a,
+                                     float* snap, hipStream_t s) {
+  const int nck = T / chunk_len;
+  const int64_t blocks = static_cast<int64_t>(B) * nck * H;
+  if (blocks > 0x7fffffff) return FR2_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(st_gather_kernel, dim3(blocks), dim3(256), 0, s, H, nck, chunk_len, true,
+                     a.state, snap, T / 16, a.boundary);
+  SegArgs v;
+  v.uniform_len = T;
+  v.num_heads = H;
+  v.out_elems = static_cast<int64_t>(B) * T * H * 64;
+  v.state_in = a.state;
+  v.state_out = a.state;
+  v.r = a.r; v.logits = a.w; v.k = a.k; v.v = a.v; v.a = a.a; v.b = a.b;
+  v.y = a.y;
+  v.sa_out = a.sa;
+  v.boundary = snap;
+  v.boundary_len = 16;
+  v.boundary_per_seg = T / 16;
+  v.scale = a.scale;
+  const int rc = launch_chunked(FR2_DTYPE_BFLOAT16, v, B, T, s);
+  if (rc != FR2_OK) return rc;
+  hipLaunchKernelGGL(st_gather_kernel, dim3(blocks), dim3(256), 0, s, H, nck, chunk_len, false,
+                     a.state, snap, T / 16, a.boundary);
+  return record_launch();
+}
+
+int launch_statetune_uniform_backward(int B, int T, int H, int chunk_len, const StateTuneArgs& a,
+                                      const float* snap, float* workspace, hipStream_t s) {
+  PretrainBwdArgs p;
+  p.batch = B; p.tokens = T; p.heads = H;
+  p.r = a.r; p.w = a.w; p.k = a.k; p.v = a.v; p.a = a.a; p.b = a.b; p.dy = a.dy;
+  p.boundary = snap;
+  p.state_dot_a = a.sa;
+  p.workspace = workspace;
+  p.dr = a.dr; p.dw = a.dw; p.dk = a.dk; p.dv = a.dv; p.da = a.da; p.db = a.db;
+  p.scale = a.scale;
+  p.state0 = a.boundary;   // chunk 0 of sequence b is boundary[b * nck]
+  p.state0_stride = static_cast<int64_t>(T / chunk_len) * H * 64 * 64;
+  p.dfinal = a.dfinal;
+  p.dstate0 = a.dstate0;
+  p.pfirst = workspace + pretrain_backward_workspace_floats(B, T, H, 64);
+  return launch_pretrain_backward(64, p, s);
+}
 
 int64_t statetune_backward_workspace_floats(int64_t T, int H, int D) {
   const int TT = D == 256 ? 8 : 16;

@@ -82,19 +82,26 @@ class _StateTune(torch.autograd.Function):
             (chunk_token_starts.numel(), state.shape[1], state.shape[2], state.shape[3]),
             device=state.device, dtype=torch.float32)
         state_dot_a = torch.empty_like(r, dtype=torch.float32)
-        _extension().statetune_tmix_wkv7_recurrent_fp32io16_forward(
+        # on the uniform layout (D = 64, bf16, equal sequences and chunks) the
+        # native forward runs the chunked MFMA kernels and also returns the
+        # post-16-token state snapshots its backward reads
+        snapshots = _extension().statetune_tmix_wkv7_recurrent_fp32io16_forward(
             sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, state, r,
             decay_logits, k, v, a, b, output, boundary, state_dot_a, float(scale))
+        ctx.has_snapshots = snapshots is not None
         ctx.save_for_backward(sequence_chunk_offsets, chunk_token_starts, chunk_token_ends,
-                              state, r, decay_logits, k, v, a, b, state_dot_a, boundary)
+                              state, r, decay_logits, k, v, a, b, state_dot_a, boundary,
+                              *(() if snapshots is None else (snapshots,)))
         ctx.scale = float(scale)
         ctx.mark_non_differentiable(boundary, state_dot_a)
         return output, state, boundary, state_dot_a
 
     @staticmethod
     def backward(ctx, grad_output, grad_final_state, _grad_boundary, _grad_state_dot_a):  # type: ignore[override]
+        saved = ctx.saved_tensors
         (offsets, starts, ends, final_state, r, decay_logits, k, v, a, b, state_dot_a,
-         boundary) = ctx.saved_tensors
+         boundary) = saved[:12]
+        snapshots = saved[12] if ctx.has_snapshots else None
         if grad_output is not None:
             grad_output = grad_output.contiguous().to(v.dtype)
         if grad_final_state is not None:
@@ -103,7 +110,8 @@ class _StateTune(torch.autograd.Function):
         grad_initial = torch.empty_like(final_state)
         _extension().statetune_tmix_wkv7_recurrent_fp32io16_backward(
             offsets, starts, ends, final_state, r, decay_logits, k, v, a, b, state_dot_a,
-            grad_output, grad_final_state, boundary, *gradients, grad_initial, ctx.scale)
+            grad_output, grad_final_state, boundary, *gradients, grad_initial, ctx.scale,
+            snapshots=snapshots)
         return (grad_initial, None, None, None, *gradients, None)
 
 

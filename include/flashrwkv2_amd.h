@@ -304,6 +304,45 @@ int fr2_wkv7_statetune_backward(
     void* grad_k, void* grad_v, void* grad_a, void* grad_b, float* grad_initial_state,
     float scale, void* stream);
 
+/*
+ * StateTune on the chunked MFMA kernels, for the common layout: D = 64, bf16
+ * tokens, `batch` sequences of `tokens` rows each, packed back to back
+ * ([batch*tokens, H, 64]), each run as tokens / chunk_len chunks of
+ * chunk_len rows (chunk_len % 16 == 0).  That is the chunk list
+ * sequence_chunk_offsets[s] = s * nck, chunk_token_starts[c] = c * chunk_len,
+ * chunk_token_ends[c] = (c + 1) * chunk_len of fr2_wkv7_statetune_forward,
+ * with the same outputs, plus `snapshots` [batch, H, tokens/16, 64, 64] fp32:
+ * the state after every 16 tokens, which the backward reads.
+ * Same reference interface as fr2_wkv7_statetune_forward.
+ */
+int fr2_wkv7_statetune_uniform_forward(int32_t batch, int32_t tokens, int32_t num_heads,
+                                       int32_t chunk_len, float* state, const void* r,
+                                       const void* decay_logits, const void* k, const void* v,
+                                       const void* a, const void* b, void* output,
+                                       float* boundary, float* state_dot_a, float* snapshots,
+                                       float scale, void* stream);
+
+/*
+ * fp32 elements of fr2_wkv7_statetune_uniform_backward's workspace, or -1.
+ * No reference counterpart (see fr2_wkv7_statetune_backward_workspace_floats).
+ */
+int64_t fr2_wkv7_statetune_uniform_backward_workspace_floats(int32_t batch, int32_t tokens,
+                                                             int32_t num_heads);
+
+/*
+ * Backward of fr2_wkv7_statetune_uniform_forward (same gradients as
+ * fr2_wkv7_statetune_backward; grad_output and every gradient are required,
+ * grad_final_state may be NULL).  snapshots are the forward's.
+ * Same reference interface as fr2_wkv7_statetune_backward.
+ */
+int fr2_wkv7_statetune_uniform_backward(
+    int32_t batch, int32_t tokens, int32_t num_heads, int32_t chunk_len, const void* r,
+    const void* decay_logits, const void* k, const void* v, const void* a, const void* b,
+    const float* state_dot_a, const void* grad_output, const float* grad_final_state,
+    const float* boundary, const float* snapshots, float* workspace, void* grad_r,
+    void* grad_decay_logits, void* grad_k, void* grad_v, void* grad_a, void* grad_b,
+    float* grad_initial_state, float scale, void* stream);
+
 /* ------------------------------------------------------------------------
  * Producer and consumer stages of the WKV7 path (fp16 tensors, fp32 math).
  * ---------------------------------------------------------------------- */

@@ -216,3 +216,94 @@ def test_statetune_is_deterministic_and_validates():
         statetune_tmix_wkv7_recurrent_fp32io16(state0, meta[0][:2], *meta[1:], *vals)
     with pytest.raises(ValueError, match="scale must be finite"):
         statetune_tmix_wkv7_recurrent_fp32io16(state0, *meta, *vals, scale=float("nan"))
+
+
+# ------------------------------------------------ uniform layout: MFMA kernels
+def _uniform_meta(B, per_seq, length):
+    nck = per_seq // length
+    starts = [c * length for c in range(B * nck)]
+    return _meta([s * nck for s in range(B + 1)], starts, [s + length for s in starts])
+
+
+@pytest.mark.parametrize("B,per_seq,length,scale", [
+    (3, 128, 32, 1.0),
+    (2, 256, 16, 0.75),
+    (1, 64, 64, 1.0),
+    (2, 1024, 256, 1.0),     # several 8-chunk spans of the key pass
+])
+def test_statetune_uniform_layout_runs_chunked_kernels(B, per_seq, length, scale):
+    """D = 64, bf16, equal sequences cut into equal chunks of a multiple of 16
+    tokens: the forward runs the chunked MFMA kernel (it returns the
+    post-16-token snapshots) and the backward the chunked value and key
+    passes; both against the fp64 oracle and against the token-serial
+    kernels on the same inputs."""
+    C = require_gpu()
+    g = torch.Generator().manual_seed(B * 1000 + per_seq + length)
+    H, D, T = 2, 64, B * per_seq
+    vals = _structured(T, H, D, torch.bfloat16, g, logit_scale=1.5)
+    state0 = (torch.randn((B, H, D, D), generator=g) * 0.5).cuda()
+    meta = _uniform_meta(B, per_seq, length)
+    nck = B * (per_seq // length)
+    dy = torch.randn((T, H, D), generator=g).to(torch.bfloat16).cuda()
+    dfin = torch.randn((B, H, D, D), generator=g).cuda()
+
+    outs = {}
+    for name in ("chunked", "serial"):
+        st = state0.clone()
+        y = torch.empty_like(vals[3])
+        bnd = torch.empty((nck, H, D, D), device="cuda")
+        sa = torch.empty((T, H, D), device="cuda")
+        if name == "chunked":
+            snaps = C.statetune_tmix_wkv7_recurrent_fp32io16_forward(*meta, st, *vals, y, bnd, sa,
+                                                                     scale)
+            assert snaps is not None and tuple(snaps.shape) == (B, H, per_seq // 16, D, D)
+        else:
+            snaps = None
+            from flashrwkv2_amd import _native as Nn
+            rc = Nn.load().fr2_wkv7_statetune_forward(
+                *(m.data_ptr() for m in meta), B, nck, T, H, D, Nn.FR2_DTYPE_BFLOAT16,
+                st.data_ptr(), *(v.data_ptr() for v in vals), y.data_ptr(), bnd.data_ptr(),
+                sa.data_ptr(), scale, torch.cuda.current_stream().cuda_stream)
+            Nn.check(rc, "fr2_wkv7_statetune_forward")
+        grads = [torch.empty_like(v) for v in vals]
+        g0 = torch.empty_like(st)
+        C.statetune_tmix_wkv7_recurrent_fp32io16_backward(*meta, st, *vals, sa, dy, dfin, bnd,
+                                                          *grads, g0, scale, snapshots=snaps)
+        torch.cuda.synchronize()
+        outs[name] = {"y": y, "state": st, "boundary": bnd, "sa": sa, "dstate0": g0,
+                      **dict(zip(TOKEN_GRADS, grads))}
+
+    ref = _oracle(state0, meta, vals, scale, dy=dy, dfinal=dfin)
+    got = outs["chunked"]
+    _check_strong(got, ref, ("y", "sa"), rel=5e-3)
+    for key in ("state", "boundary"):
+        assert relative_rmse(to_np(got[key]), ref[key]) <= 2e-3, key
+    _check_strong(got, ref, ("dstate0", *TOKEN_GRADS))
+    # the two kernel families agree with each other as closely as with fp64
+    for key in ("y", "state", "dstate0", *TOKEN_GRADS):
+        assert relative_rmse(to_np(got[key]), to_np(outs["serial"][key])) <= 1e-2, key
+
+
+def test_statetune_uniform_autograd_and_fallbacks():
+    """The public function takes the chunked path on the uniform layout
+    (its results match the oracle); an fp16 or a ragged layout of the same
+    tokens falls back to the token-serial kernels with the same results."""
+    require_gpu()
+    g = torch.Generator().manual_seed(77)
+    B, per_seq, length, H, D = 2, 96, 32, 2, 64
+    T = B * per_seq
+    vals = _structured(T, H, D, torch.bfloat16, g)
+    state0 = (torch.randn((B, H, D, D), generator=g) * 0.5).cuda()
+    dy = torch.randn((T, H, D), generator=g).to(torch.bfloat16).cuda()
+    dfin = torch.randn((B, H, D, D), generator=g).cuda()
+    runs = {}
+    for name, meta in (("uniform", _uniform_meta(B, per_seq, length)),
+                       ("ragged", _meta([0, 2, 5], [0, 32, 96, 100, 150], [32, 96, 100, 150, 192]))):
+        state, leaves, (y, fin, _, _) = _run(state0, meta, vals, 1.0)
+        torch.autograd.backward([y, fin], [dy, dfin])
+        torch.cuda.synchronize()
+        runs[name] = {"y": y, "state": fin, **_grads(state, leaves)}
+        ref = _oracle(state0, meta, vals, 1.0, dy=dy, dfinal=dfin)
+        _check_strong(runs[name], ref, ("y", "dstate0", *TOKEN_GRADS))
+    for key in ("y", "state", "dstate0", *TOKEN_GRADS):
+        assert relative_rmse(to_np(runs["uniform"][key]), to_np(runs["ragged"][key])) <= 1e-2, key
