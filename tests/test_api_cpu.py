@@ -15,6 +15,7 @@ from flashrwkv2_amd.tmix.wkv7 import (
     infer_tmix_wkv7_recurrent_fp32io16_forward_varlen,
     pretrain_tmix_wkv7_recurrent_bf16,
     rl_infctx_tmix_wkv7_chunk_fp32io16,
+    statetune_tmix_wkv7_recurrent_fp32io16,
 )
 
 EXPECTED = {
@@ -25,6 +26,7 @@ EXPECTED = {
     "pretrain_tmix_wkv7_recurrent_bf16",
     "rl_infctx_tmix_wkv7_chunk_fp32io16",
     "rl_infctx_tmix_wkv7_chunk_fp32io16_factor_recompute",
+    "statetune_tmix_wkv7_recurrent_fp32io16",
 }
 
 
@@ -115,3 +117,47 @@ def test_fp16_public_signature_is_raw_only_and_has_no_elapsed_alias():
     for name in ("log_decay", "elapsed_t"):
         assert name not in params
     assert params["scale"].default == 1.0 and params["decay_bias"].default is None
+
+
+def test_statetune_signature_and_python_checks():
+    """statetune.py:202-236 of the reference: keyword-only scale, the
+    reference's check order and messages (CPU tensors are rejected before
+    anything reaches the native layer)."""
+    sig = inspect.signature(statetune_tmix_wkv7_recurrent_fp32io16)
+    assert tuple(sig.parameters)[:10] == (
+        "initial_state", "sequence_chunk_offsets", "chunk_token_starts", "chunk_token_ends",
+        "r", "decay_logits", "k", "v", "a", "b")
+    assert sig.parameters["scale"].kind is inspect.Parameter.KEYWORD_ONLY
+    assert sig.parameters["scale"].default == 1.0
+    t = torch.zeros((5, 1, 64), dtype=torch.bfloat16)
+    meta = [torch.tensor(x, dtype=torch.int32) for x in ([0, 1], [0], [5])]
+    with pytest.raises(ValueError, match="state must be contiguous CUDA"):
+        statetune_tmix_wkv7_recurrent_fp32io16(torch.zeros((1, 1, 64, 64)), *meta, *(t,) * 6)
+    with pytest.raises(TypeError, match="state must be a torch.Tensor"):
+        statetune_tmix_wkv7_recurrent_fp32io16(None, *meta, *(t,) * 6)
+
+
+def test_statetune_uniform_layout_detection():
+    """The chunk lists the chunked MFMA StateTune kernels take: equal
+    sequences packed back to back, equal chunks of a multiple of 16 tokens,
+    D = 64, bf16 (checked on CPU metadata; the same code reads it on the
+    device)."""
+    import importlib
+
+    C = importlib.import_module("flashrwkv2_amd._C")
+    detect = C._statetune_uniform_chunk_len
+    i32 = lambda x: torch.tensor(x, dtype=torch.int32)
+    bf = torch.bfloat16
+    # 2 sequences x 64 tokens as chunks of 32
+    assert detect(i32([0, 2, 4]), i32([0, 32, 64, 96]), i32([32, 64, 96, 128]), 2, 4, 128, 64,
+                  bf) == 32
+    assert detect(i32([0, 1, 2]), i32([0, 64]), i32([64, 128]), 2, 2, 128, 64, bf) == 64
+    # not a multiple of 16, unequal chunks, a gap, fp16, D = 128
+    assert detect(i32([0, 2, 4]), i32([0, 8, 16, 24]), i32([8, 16, 24, 32]), 2, 4, 32, 64,
+                  bf) is None
+    assert detect(i32([0, 2, 4]), i32([0, 16, 64, 96]), i32([16, 64, 96, 128]), 2, 4, 128, 64,
+                  bf) is None
+    assert detect(i32([0, 1, 2]), i32([0, 80]), i32([64, 144]), 2, 2, 128, 64, bf) is None
+    assert detect(i32([0, 1, 2]), i32([0, 64]), i32([64, 128]), 2, 2, 128, 64,
+                  torch.float16) is None
+    assert detect(i32([0, 1, 2]), i32([0, 64]), i32([64, 128]), 2, 2, 128, 128, bf) is None
