@@ -333,13 +333,28 @@ __device__ __forceinline__ StateOps<kVExact> state_load(const ChunkOps<kVExact>&
   return o;
 }
 
+// Where the sa rows 4q+e (e = 0..3) of a chunk go: row row0 + dir*e of the
+// column pointer col (rows of row_stride floats), except that e = 0 goes to
+// row `wrap` when wrap >= 0 (the reverse mode's position 0).  Kept as a few
+// integers and formed at the store, so that no per-row pointers stay live
+// across the chain.
+struct SaRows {
+  float* col = nullptr;
+  int64_t row_stride = 0;
+  int row0 = 0, dir = 1, wrap = -1;
+  __device__ __forceinline__ float* at(int e) const {
+    const int row = (e == 0 && wrap >= 0) ? wrap : row0 + dir * e;
+    return col + static_cast<int64_t>(row) * row_stride;
+  }
+};
+
 // With kTrain the chunk also writes its per-token sa rows (U, fp32) of tokens
-// 4q..4q+3 to sa_rows[0..3] and, when bnd_col is set, its post-chunk state
+// 4q..4q+3 to sa_rows.at(0..3) and, when bnd_col is set, its post-chunk state
 // column to bnd_col[key * D].
 template <class Io, bool kVExact, bool kTrain = false>
 __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 (&S)[4],
                                               uint16_t (*yrows)[YP], int vcol, int i, int q,
-                                              float scale, float* const* sa_rows = nullptr,
+                                              float scale, const SaRows& sa_rows = SaRows{},
                                               float* bnd_col = nullptr) {
   using raw = typename Io::raw;
   // S split as B operand against the permuted A~ / R~ rows: K positions
@@ -367,7 +382,7 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
     Y = mm_ab(o.Mrb, Us, Y);
     if constexpr (kTrain) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) *sa_rows[e] = Uf[e];
+      for (int e = 0; e < 4; ++e) *sa_rows.at(e) = Uf[e];
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -399,7 +414,7 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
     Y = mm_ab(o.Mrb, Us, Y);
     if constexpr (kTrain) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) *sa_rows[e] = Uf[e];
+      for (int e = 0; e < 4; ++e) *sa_rows.at(e) = Uf[e];
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -551,14 +566,16 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
             : nullptr;
     auto chunk = [&](const StateOps<kVExact>& o, int gi, int c) {
       const int ci = gi * G + c;   // chunk index within the segment
-      float* sa_rows[4];
+      SaRows sa_rows;
       if constexpr (kTrain) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int pos = ci * L + 4 * q + e;
-          const int row = kRev ? t0 + (seg_len - pos) % seg_len : t0 + pos;
-          sa_rows[e] = sa_base + static_cast<int64_t>(row) * row_stride;
-        }
+        // forward: rows t0 + pos; reverse: t0 + (n - pos) mod n, which is
+        // t1 - pos except at pos = 0
+        const int pos0 = ci * L + 4 * q;
+        sa_rows.col = sa_base;
+        sa_rows.row_stride = row_stride;
+        sa_rows.row0 = kRev ? t1 - pos0 : t0 + pos0;
+        sa_rows.dir = kRev ? -1 : 1;
+        sa_rows.wrap = (kRev && pos0 == 0) ? t0 : -1;
       }
       const int bi = kRev ? p.boundary_per_seg - 1 - ci : ci;
       const bool keep = bnd_base != nullptr && bi % p.boundary_every == 0;
@@ -570,9 +587,10 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
       constexpr int par = decltype(par_c)::value;
       wait_min_ge(sm.ready, gi + 1);          // operators of group gi stored
       wait_min_ge(sm.drained, gi - 1);        // outputs of group gi-2 written back
-      if (t0 + gi * GT + GT <= t1) {
+      if (!kTrain && t0 + gi * GT + GT <= t1) {
         // both chunks: the second chunk's first-needed operand reads (the
         // S-side rows and V-side blocks) go out before the first chunk's chain
+        // (not in training mode, whose extra outputs would then spill)
         const StateOps<kVExact> o0 = state_load(sm.ops[par][0], vcol, i, q);
         StateOps<kVExact> o1;
         state_load_early(o1, sm.ops[par][1], vcol, i, q);
