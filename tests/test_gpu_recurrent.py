@@ -372,9 +372,12 @@ def test_baseline_configs_match_fp64_oracle(cfg, overrides):
 @pytest.mark.parametrize("cfg,overrides", [
     (1, dict(batch=2, tokens=1024, heads=2)),
     (4, dict(tokens=8192, heads=1)),
+    (4, dict(heads=8)),
 ])
 def test_chunked_kernel_long_sequences_match_fp64_oracle(cfg, overrides):
-    """Chunked MFMA form over many chunks (fp32 carry drift vs fp64)."""
+    """Chunked MFMA form over many chunks (fp32 carry drift vs fp64); the
+    last case is BASELINE config 4 at its full length (65 536 tokens, 4 096
+    chunks, long-memory decays) on eight of its heads."""
     C = require_gpu()
     from flashrwkv2_amd import workloads
 
