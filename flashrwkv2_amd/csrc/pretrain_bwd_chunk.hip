@@ -59,15 +59,23 @@ struct KPassArgs {
   const float* dfinal;
 };
 
+// LDS row pitches chosen against bank conflicts (64 banks of 4 bytes): a
+// [key][token] row of 20 floats puts keys 4 apart 16 banks apart, so the
+// [4q+e][n] scalar reads, the [4kg+e][tp] stores and the [n][4q] 16-byte
+// reads all spread over the 64 banks; a [token][value] row of 72 bf16
+// (36 banks) does the same for the 8-byte tile stores [n][16vb+4q].
+constexpr int kFP = 20;
+constexpr int kTP = 72;
+
 struct alignas(32) KSmem {
   // per (key row, token) factors of the chunk: [key][token]
-  float bh[kD][kL], kh[kD][kL], rh[kD][kL], ah[kD][kL];
-  float gm[kD][kL], wsf[kD][kL];
+  float bh[kD][kFP], kh[kD][kFP], rh[kD][kFP], ah[kD][kFP];
+  float gm[kD][kFP], wsf[kD][kFP];
   // masked token-token blocks in B-operand form, one per lane: the [lo | hi]
   // half of the BOp (its upper half is zero)
   bf16x8 gram[8][64];
   // DY and DSA (hi, lo) of the chunk, [token][value], for transposed reads
-  __bf16 dyh[kL][kD], dsh[kL][kD], dsl[kL][kD];
+  __bf16 dyh[kL][kTP], dsh[kL][kTP], dsl[kL][kTP];
   float dsa0[kD];   // dsa of the chunk's first token (fp32)
 };
 
