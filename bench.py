@@ -132,7 +132,7 @@ class Runner:
         return "serial_kernel<64,IoBF16,StF32>"
 
 
-def cpu_baseline(w, threads: int, sample_tokens: int | None, min_seconds: float = 3.0):
+def cpu_baseline(w, threads: int, sample_tokens: int | None, min_seconds: float = 12.0):
     """fp32 C recurrence on the host over the first `sample_tokens` tokens of
     every sequence (all heads), repeated until `min_seconds` of CPU time."""
     import numpy as np
@@ -350,6 +350,37 @@ def time_layer_stages(torch, tokens: int, heads: int, steps: int = 20):
 # boundary snapshot amortised over its 16 tokens (4 D^2 / 16); writes the six
 # bf16 gradients (6 x 2D).
 BWD_BYTES_PER_TOKEN_HEAD = 7 * 128 + 256 + 64 * 64 * 4 // 16 + 6 * 128
+
+
+def time_long_context(torch, flashrwkv2_amd, steps: int):
+    """BASELINE config 4 at full size (B=1, T=65536, H=64): the public call,
+    which cuts the sequence into pieces (summary pass, combine, pieces), and
+    the unsplit chunked kernel (one block per head) through the C ABI."""
+    from flashrwkv2_amd import _C as CC
+    from flashrwkv2_amd import workloads
+
+    w = workloads.config(4, "cuda")
+    run = Runner(w, torch, flashrwkv2_amd)
+    ms = run.time_steps(steps, 2)
+    unsplit_ms = run.time_kernel(max(2, steps // 2))
+    pieces, piece_len, ws = CC.split_plan(w.state_indices.numel(), w.num_heads, 64,
+                                          run.ticket._max_seqlen())
+    nbytes = algorithmic_bytes(w.total_tokens, w.num_heads, w.state_indices.numel())
+    out = {
+        "workload": w.name, "ms_per_step": round(ms, 4),
+        "tokens_per_s": round(w.total_tokens / (ms * 1e-3), 1),
+        "kernels": "chunk64_kernel summary pass + split_combine_kernel + chunk64_kernel pieces",
+        "pieces": pieces, "piece_len": piece_len, "workspace_bytes": ws,
+        "roofline": roofline_obj(nbytes, ms),
+        "unsplit": {"ms_per_step": round(unsplit_ms, 4),
+                    "tokens_per_s": round(w.total_tokens / (unsplit_ms * 1e-3), 1),
+                    "kernel": "chunk64_kernel<IoBF16,false> (one block per head)",
+                    "roofline": roofline_obj(nbytes, unsplit_ms)},
+        "algorithmic_bytes": nbytes,
+    }
+    del run, w
+    torch.cuda.empty_cache()
+    return out
 
 
 def time_chunk_bf16_state(torch, flashrwkv2_amd, w, steps: int):
@@ -603,14 +634,14 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode (config 2) leg")
     ap.add_argument("--cpu-sample-tokens", type=int, default=4096,
                     help="tokens per sequence in the CPU baseline sample")
     ap.add_argument("--no-train", action="store_true",
                     help="skip the training (forward + backward) leg")
-    ap.add_argument("--only", choices=["prefill", "decode", "train", "stages"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "long", "train", "stages"], default=None,
                     help="run one leg only (profiling)")
     ap.add_argument("--config", type=int, default=1, choices=[1, 3, 4],
                     help="prefill workload (BASELINE config; the metric is quoted on 1)")
@@ -712,6 +743,8 @@ def main() -> int:
     if args.only in (None, "prefill") and args.config == 1 and pre is not None:
         result["chunk_bf16_state"] = time_chunk_bf16_state(torch, flashrwkv2_amd, pre.w,
                                                            max(5, args.steps // 2))
+    if args.only in (None, "long") and args.config == 1:
+        result["long_context"] = time_long_context(torch, flashrwkv2_amd, max(4, args.steps // 4))
     if args.only in (None, "train") and not args.no_train:
         wt = pre.w if (pre is not None and args.config == 1) else workloads.config(1, "cuda")
         result["pretrain_training"] = time_pretrain_training(torch, wt, max(3, args.steps // 4))

@@ -20,6 +20,7 @@ Reference bindings mirrored:
 
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Sequence
 
@@ -330,7 +331,7 @@ def _resolve_launch_metadata(qsl, slots, total_tokens, pool_size, max_seqlen, ti
 
 
 def _recurrent_launch(kernel, qsl, slots, state, r, decay_logits, k, v, a, b, output,
-                      scale, decay_bias, validated_metadata, max_seqlen):
+                      scale, decay_bias, validated_metadata, max_seqlen, split_pieces=None):
     n, h, d = check_recurrent_layout(qsl, slots, state, r, decay_logits, k, v, a, b,
                                      output, scale)
     if decay_bias is not None:
@@ -343,13 +344,47 @@ def _recurrent_launch(kernel, qsl, slots, state, r, decay_logits, k, v, a, b, ou
               int(max_seqlen), _dtype_code(r), state.data_ptr(), r.data_ptr(),
               decay_logits.data_ptr(), N.ptr(decay_bias), k.data_ptr(), v.data_ptr(),
               a.data_ptr(), b.data_ptr(), output.data_ptr(), float(scale))
+    pieces, piece_len, ws_bytes = 1, 0, 0
+    if kernel is None or kernel == N.KERNEL_SPLIT:
+        # the forced split without a known max_seqlen bounds it by the token count
+        ms = int(max_seqlen) if (kernel is None or int(max_seqlen) > 0) else r.size(0)
+        pieces, piece_len, ws_bytes = split_plan(n, h, d, ms, split_pieces)
+        if kernel == N.KERNEL_SPLIT and pieces < 2:
+            raise RuntimeError("sequence split needs head size 64 and at least two pieces")
     with torch.cuda.device(state.device):
         stream = _stream(state.device)
-        if kernel is None:
+        if pieces > 1:
+            # workspace from the caching allocator on this stream: it is only
+            # handed out again to work queued later on the same stream
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=state.device)
+            rc = lib.fr2_wkv7_recurrent_fp32_forward_split(*common, pieces, piece_len,
+                                                           ws.data_ptr(), ws_bytes, stream)
+            del ws
+        elif kernel is None:
             rc = lib.fr2_wkv7_recurrent_fp32_forward(*common, stream)
         else:
             rc = lib.fr2_wkv7_recurrent_fp32_forward_kernel(int(kernel), *common, stream)
     N.check(rc, "tmix_wkv7_recurrent_fp32_from_decay_logits")
+
+
+def split_plan(num_sequences: int, num_heads: int, head_size: int, max_seqlen: int,
+               pieces: int | None = None) -> tuple[int, int, int]:
+    """(pieces, piece_len, workspace_bytes) of the chunked prefill's sequence
+    split: the library's plan, or `pieces` pieces when given (tests)."""
+    lib = N.load()
+    if pieces is None:
+        pc, pl, wb = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+        N.check(lib.fr2_wkv7_recurrent_fp32_split_plan(num_sequences, num_heads, head_size,
+                                                       max_seqlen, ctypes.byref(pc),
+                                                       ctypes.byref(pl), ctypes.byref(wb)),
+                "fr2_wkv7_recurrent_fp32_split_plan")
+        return pc.value, pl.value, wb.value
+    if head_size != 64 or pieces < 2:
+        return 1, max_seqlen, 0
+    plen = -(-max(max_seqlen, 1) // pieces)
+    plen = -(-plen // 32) * 32
+    ws = num_sequences * (3 * pieces - 2) * num_heads * 64 * 64 * 4
+    return pieces, plen, ws
     # Implicit validation buffers (`keep`) are released after the launch; the
     # caching allocator only hands them out again to work queued later on this
     # same stream, which runs after the kernels that read them.
@@ -368,11 +403,14 @@ def tmix_wkv7_recurrent_fp32_from_decay_logits(query_start_loc, state_indices, s
 def tmix_wkv7_recurrent_fp32_kernel_forced(kernel, query_start_loc, state_indices, state, r,
                                            decay_logits, k, v, a, b, output, scale,
                                            decay_bias=None, validated_metadata=None,
-                                           max_seqlen=-1):
+                                           max_seqlen=-1, split_pieces=None):
     """Same contract with the kernel family forced (0 serial, 1 decode,
-    2 chunked MFMA).  No reference counterpart: used to pin each kernel."""
+    2 chunked MFMA, 3 chunked with the sequence split, `split_pieces` pieces
+    or the library's plan).  No reference counterpart: used to pin each
+    kernel."""
     _recurrent_launch(int(kernel), query_start_loc, state_indices, state, r, decay_logits,
-                      k, v, a, b, output, scale, decay_bias, validated_metadata, max_seqlen)
+                      k, v, a, b, output, scale, decay_bias, validated_metadata, max_seqlen,
+                      split_pieces)
 
 
 # ---------------------------------------------------------------------------

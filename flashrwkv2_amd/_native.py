@@ -28,6 +28,7 @@ FR2_DTYPE_BFLOAT16 = 1
 KERNEL_SERIAL = 0
 KERNEL_DECODE = 1
 KERNEL_CHUNKED = 2
+KERNEL_SPLIT = 3   # chunked, long sequences cut into pieces (Python-side selector)
 
 _i32p = POINTER(c_int32)
 
@@ -52,6 +53,16 @@ SIGNATURES: dict[str, tuple] = {
         [c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32,
          c_int64, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_void_p],
+    ),
+    "fr2_wkv7_recurrent_fp32_split_plan": (
+        c_int32, [c_int32, c_int32, c_int32, c_int32, _i32p, _i32p, POINTER(c_int64)],
+    ),
+    "fr2_wkv7_recurrent_fp32_forward_split": (
+        c_int32,
+        [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64,
+         c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32,
+         c_void_p, c_int64, c_void_p],
     ),
     "fr2_wkv7_recurrent_fp16_forward": (
         c_int32,

@@ -3,6 +3,8 @@
 // segment descriptor and enqueues the chosen kernel family on `stream`.
 #include "recurrent.h"
 
+#include <algorithm>
+
 namespace {
 
 using fr2::SegArgs;
@@ -101,6 +103,74 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kernel(
                         num_sequences, num_heads, head_size, total_tokens,
                         max_seqlen, dtype, state, r, decay_logits, decay_bias, k,
                         v, a, b, output, scale, stream);
+}
+
+// Sequence split of the chunked prefill.  With few (sequence, head) units
+// the chunked kernel leaves most CUs idle (one block per unit, one block per
+// CU), so long sequences are cut into pieces: a summary pass (one block per
+// piece but the last), a combine kernel and the real pass over every piece.
+// Both passes run one block per CU, so a sequence gets 256/units pieces
+// (neither pass then needs a second round of blocks) of at least 1024
+// tokens; split only when that gives three pieces or more (at most 85 units:
+// with two pieces the summary pass costs what the split saves).
+constexpr int kSplitMaxUnits = 85;
+constexpr int kSplitMinPiece = 1024;
+constexpr int kSplitAlign = 32;
+
+extern "C" int fr2_wkv7_recurrent_fp32_split_plan(int32_t num_sequences, int32_t num_heads,
+                                                  int32_t head_size, int32_t max_seqlen,
+                                                  int32_t* pieces, int32_t* piece_len,
+                                                  int64_t* workspace_bytes) {
+  if (!pieces || !piece_len || !workspace_bytes || num_sequences <= 0 || num_heads <= 0)
+    return FR2_ERR_INVALID_ARGUMENT;
+  *pieces = 1;
+  *piece_len = max_seqlen;
+  *workspace_bytes = 0;
+  const int64_t units = static_cast<int64_t>(num_sequences) * num_heads;
+  if (head_size != 64 || max_seqlen < kChunkMinSeqlen || units > kSplitMaxUnits) return FR2_OK;
+  int P = static_cast<int>(std::min<int64_t>(256 / units, max_seqlen / kSplitMinPiece));
+  if (P < 3) return FR2_OK;
+  int len = (max_seqlen + P - 1) / P;
+  len = (len + kSplitAlign - 1) / kSplitAlign * kSplitAlign;
+  P = (max_seqlen + len - 1) / len;
+  if (P < 3 || static_cast<int64_t>(num_sequences) * P * 2 > 65535) return FR2_OK;
+  *pieces = P;
+  *piece_len = len;
+  *workspace_bytes = fr2::split_workspace_floats(num_sequences, num_heads, P) * 4;
+  return FR2_OK;
+}
+
+extern "C" int fr2_wkv7_recurrent_fp32_forward_split(
+    const int32_t* query_start_loc, const int32_t* state_indices, const int32_t* status,
+    int32_t num_sequences, int32_t num_heads, int32_t head_size, int64_t total_tokens,
+    int32_t max_seqlen, int32_t dtype, float* state, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a, const void* b,
+    void* output, float scale, int32_t pieces, int32_t piece_len, void* workspace,
+    int64_t workspace_bytes, void* stream) {
+  (void)max_seqlen;
+  if (!query_start_loc || !state_indices || !status || !state || !workspace ||
+      !tokens_ok(r, decay_logits, k, v, a, b, output))
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 || total_tokens <= 0)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (head_size != 64) return FR2_ERR_UNSUPPORTED;
+  if (pieces < 2 || workspace_bytes < fr2::split_workspace_floats(num_sequences, num_heads,
+                                                                   pieces) * 4)
+    return FR2_ERR_INVALID_ARGUMENT;
+  SegArgs p;
+  p.bounds = query_start_loc;
+  p.slots = state_indices;
+  p.status = status;
+  p.num_heads = num_heads;
+  p.out_elems = total_tokens * num_heads * head_size;
+  p.state_in = state;
+  p.state_out = state;
+  p.r = r; p.logits = decay_logits; p.bias = decay_bias; p.k = k; p.v = v; p.a = a; p.b = b;
+  p.y = output;
+  p.scale = scale;
+  return fr2::launch_chunked_split(dtype, p, num_sequences, pieces, piece_len,
+                                   static_cast<float*>(workspace),
+                                   static_cast<hipStream_t>(stream));
 }
 
 extern "C" int fr2_wkv7_recurrent_fp16_forward(

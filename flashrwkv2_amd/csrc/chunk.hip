@@ -92,7 +92,8 @@ struct alignas(16) Smem {
   // progress counters, each written by one wave only: groups whose operators
   // key wave w has stored, groups whose part-1 partials it has stored, and
   // groups state wave w has finished / whose output rows it has written back
-  int ready[4], part1[4], drained[4], consumed[4];
+  // (consumed has a slot for each of the summary pass's eight state waves)
+  int ready[4], part1[4], drained[4], consumed[8];
 };
 
 // Column position of key k in the A~ / R~ rows: for each half m = k/32 the 32
@@ -135,7 +136,8 @@ struct KeyRegs {
 // nbias8 holds -log2(e) * decay_bias for the lane's keys.
 // kUnitW: reverse mode, where unit_w marks a lane whose shifted retention
 // row lies past the segment (unit retention).
-template <class Io, bool kVExact, bool kFull, bool kUnitW = false>
+// kSum: summary pass (no R~ operands, no R-side blocks).
+template <class Io, bool kVExact, bool kFull, bool kUnitW = false, bool kSum = false>
 __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& op,
                                           const u32x4 (&raw)[6], const float (&nbias8)[8],
                                           bool valid, int mp, int cc, int hh, int i, int q,
@@ -147,7 +149,7 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
   auto tok = [&](int j) { return (kFull || valid) ? raw[j] : zero4; };
   float xr[8], xl[8], xk[8], xa[8], xb[8];
-  unpack8<Io>(tok(0), xr);
+  if constexpr (!kSum) unpack8<Io>(tok(0), xr);
   unpack8<Io>(raw[1], xl);
   unpack8<Io>(tok(2), xk);
   unpack8<Io>(tok(4), xa);
@@ -168,50 +170,55 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
     const float gp = row_prev(gm, 1.0f);              // gamma_{t-1}
     const float ig = __builtin_amdgcn_exp2f(-g2);     // 1 / gamma_t
     at[e] = xa[e] * gp;
-    rt[e] = xr[e] * gm;
+    if constexpr (!kSum) rt[e] = xr[e] * gm;
     bh[e] = xb[e] * ig;
     kh[e] = xk[e] * ig;
     if constexpr (kUnitW) kh[e] *= kscale;   // reverse mode: k is r_t, times scale
     if (i == L - 1) op.gl[kbase + e] = gm;
   }
   kr.As = split8(at);
-  kr.Rs = split8(rt);
+  if constexpr (!kSum) kr.Rs = split8(rt);
   kr.Bs = split8(bh);
   kr.Ks = split8(kh);
+  const u32x4 vraw = tok(3);
   if constexpr (kVExact) {
-    kr.Vs.hi = __builtin_bit_cast(bf16x8, tok(3));     // bf16 values are exact
+    kr.Vs.hi = __builtin_bit_cast(bf16x8, vraw);       // bf16 values are exact
   } else {
     float xv[8];
-    unpack8<Io>(tok(3), xv);
+    unpack8<Io>(vraw, xv);
     kr.Vs = split8(xv);
   }
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   const f32x4 pab = mma32x3(kr.As, kr.Bs, zero);
   const f32x4 pak = mma32x3(kr.As, kr.Ks, zero);
-  const f32x4 prb = mma32x3(kr.Rs, kr.Bs, zero);
-  const f32x4 prk = mma32x3(kr.Rs, kr.Ks, zero);
   // lane (i, q) holds P[4q+e][i]: one 16-byte store per block
   *reinterpret_cast<f32x4*>(&sm.mpart[mp][cc][hh][0][i][4 * q]) = pab;
   *reinterpret_cast<f32x4*>(&sm.mpart[mp][cc][hh][1][i][4 * q]) = pak;
-  *reinterpret_cast<f32x4*>(&sm.mpart[mp][cc][hh][2][i][4 * q]) = prb;
-  *reinterpret_cast<f32x4*>(&sm.mpart[mp][cc][hh][3][i][4 * q]) = prk;
+  if constexpr (!kSum) {
+    const f32x4 prb = mma32x3(kr.Rs, kr.Bs, zero);
+    const f32x4 prk = mma32x3(kr.Rs, kr.Ks, zero);
+    *reinterpret_cast<f32x4*>(&sm.mpart[mp][cc][hh][2][i][4 * q]) = prb;
+    *reinterpret_cast<f32x4*>(&sm.mpart[mp][cc][hh][3][i][4 * q]) = prk;
+  }
 }
 
 // ---------------------------------------------------------------------------
 // key side, part 2: store the operands; hh = 0 forms T, hh = 1 the masked
 // Mak, Mrb, Mrk
 // ---------------------------------------------------------------------------
-template <bool kVExact>
+template <bool kVExact, bool kSum = false>
 __device__ __forceinline__ void key_part2(Smem<kVExact>& sm, ChunkOps<kVExact>& op, int mp,
                                           int cc, int hh, int i, int q, const KeyRegs& kr) {
   const int kbase = 32 * hh + 8 * q;
   {
     // keys kbase..kbase+7 land in two 4-key runs of the permuted rows
     const int p0 = key_pos(kbase), p1 = key_pos(kbase + 4);
-    *reinterpret_cast<bf16x4*>(&op.r_h[i][p0]) = kr.Rs.hi.lo;
-    *reinterpret_cast<bf16x4*>(&op.r_h[i][p1]) = kr.Rs.hi.hi;
-    *reinterpret_cast<bf16x4*>(&op.r_l[i][p0]) = kr.Rs.lo.lo;
-    *reinterpret_cast<bf16x4*>(&op.r_l[i][p1]) = kr.Rs.lo.hi;
+    if constexpr (!kSum) {
+      *reinterpret_cast<bf16x4*>(&op.r_h[i][p0]) = kr.Rs.hi.lo;
+      *reinterpret_cast<bf16x4*>(&op.r_h[i][p1]) = kr.Rs.hi.hi;
+      *reinterpret_cast<bf16x4*>(&op.r_l[i][p0]) = kr.Rs.lo.lo;
+      *reinterpret_cast<bf16x4*>(&op.r_l[i][p1]) = kr.Rs.lo.hi;
+    }
     *reinterpret_cast<bf16x4*>(&op.at_h[i][p0]) = kr.As.hi.lo;
     *reinterpret_cast<bf16x4*>(&op.at_h[i][p1]) = kr.As.hi.hi;
     *reinterpret_cast<bf16x4*>(&op.at_l[i][p0]) = kr.As.lo.lo;
@@ -262,15 +269,19 @@ __device__ __forceinline__ void key_part2(Smem<kVExact>& sm, ChunkOps<kVExact>& 
     for (int e = 0; e < 4; ++e) {
       const int s = 4 * q + e;       // A-operand layout: row i, K = s
       const float v1 = mp0[0][1][s][i] + mp0[1][1][s][i];
-      const float v2 = mp0[0][2][s][i] + mp0[1][2][s][i];
-      const float v3 = mp0[0][3][s][i] + mp0[1][3][s][i];
       mak[e] = (i > s) ? v1 : 0.f;
-      mrb[e] = (i >= s) ? v2 : 0.f;
-      mrk[e] = (i >= s) ? v3 : 0.f;
+      if constexpr (!kSum) {
+        const float v2 = mp0[0][2][s][i] + mp0[1][2][s][i];
+        const float v3 = mp0[0][3][s][i] + mp0[1][3][s][i];
+        mrb[e] = (i >= s) ? v2 : 0.f;
+        mrk[e] = (i >= s) ? v3 : 0.f;
+      }
     }
     store_aop(op.mak, i, q, as_a(split4(mak)));
-    store_aop(op.mrb, i, q, as_a(split4(mrb)));
-    store_aop(op.mrk, i, q, as_a(split4(mrk)));
+    if constexpr (!kSum) {
+      store_aop(op.mrb, i, q, as_a(split4(mrb)));
+      store_aop(op.mrk, i, q, as_a(split4(mrk)));
+    }
   }
 }
 
@@ -289,11 +300,11 @@ struct StateOps {
 };
 
 // operands the chain needs first: Mak, Mrk, V and the A~ / R~ rows
-template <bool kVExact>
+template <bool kVExact, bool kSum = false>
 __device__ __forceinline__ void state_load_early(StateOps<kVExact>& o, const ChunkOps<kVExact>& op,
                                                  int vcol, int i, int q) {
   o.Mak = load_aop(op.mak, i, q);
-  o.Mrk = load_aop(op.mrk, i, q);
+  if constexpr (!kSum) o.Mrk = load_aop(op.mrk, i, q);
   // transposed operands straight from the token rows (see tr_rows)
   const int trow = 4 * q + (i >> 2), tcol = 4 * (i & 3);
   const int vc0 = 16 * (vcol >> 4) + tcol;
@@ -301,16 +312,18 @@ __device__ __forceinline__ void state_load_early(StateOps<kVExact>& o, const Chu
   if constexpr (!kVExact) o.vl = tr_rows(&op.v_l[trow][vc0]);
   o.Aa0 = rows_vs_state(op.at_h, op.at_l, 0, i, q);
   o.Aa1 = rows_vs_state(op.at_h, op.at_l, 1, i, q);
-  o.Ra0 = rows_vs_state(op.r_h, op.r_l, 0, i, q);
-  o.Ra1 = rows_vs_state(op.r_h, op.r_l, 1, i, q);
+  if constexpr (!kSum) {
+    o.Ra0 = rows_vs_state(op.r_h, op.r_l, 0, i, q);
+    o.Ra1 = rows_vs_state(op.r_h, op.r_l, 1, i, q);
+  }
 }
 // the rest: T, Mrb, B^^T, K^^T and gamma_L
-template <bool kVExact>
+template <bool kVExact, bool kSum = false>
 __device__ __forceinline__ void state_load_late(StateOps<kVExact>& o, const ChunkOps<kVExact>& op,
                                                 int vcol, int i, int q) {
   (void)vcol;
   o.Ta = load_aop(op.t, i, q);
-  o.Mrb = load_aop(op.mrb, i, q);
+  if constexpr (!kSum) o.Mrb = load_aop(op.mrb, i, q);
   const int trow = 4 * q + (i >> 2), tcol = 4 * (i & 3);
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
@@ -324,12 +337,12 @@ __device__ __forceinline__ void state_load_late(StateOps<kVExact>& o, const Chun
     o.gl[kb] = *reinterpret_cast<const f32x4*>(&op.gl[kb * 16 + 4 * q]);
   }
 }
-template <bool kVExact>
+template <bool kVExact, bool kSum = false>
 __device__ __forceinline__ StateOps<kVExact> state_load(const ChunkOps<kVExact>& op, int vcol,
                                                         int i, int q) {
   StateOps<kVExact> o;
-  state_load_early(o, op, vcol, i, q);
-  state_load_late(o, op, vcol, i, q);
+  state_load_early<kVExact, kSum>(o, op, vcol, i, q);
+  state_load_late<kVExact, kSum>(o, op, vcol, i, q);
   return o;
 }
 
@@ -351,11 +364,13 @@ struct SaRows {
 // With kTrain the chunk also writes its per-token sa rows (U, fp32) of tokens
 // 4q..4q+3 to sa_rows.at(0..3) and, when bnd_col is set, its post-chunk state
 // column to bnd_col[key * D].
-template <class Io, bool kVExact, bool kTrain = false>
+// kSum (summary pass): the state update only, no outputs; with no_v the
+// value rows count as zero (the transition of the chunk).
+template <class Io, bool kVExact, bool kTrain = false, bool kSum = false>
 __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 (&S)[4],
                                               uint16_t (*yrows)[YP], int vcol, int i, int q,
                                               float scale, const SaRows& sa_rows = SaRows{},
-                                              float* bnd_col = nullptr) {
+                                              float* bnd_col = nullptr, bool no_v = false) {
   using raw = typename Io::raw;
   // S split as B operand against the permuted A~ / R~ rows: K positions
   // 8q..8q+7 = rows 32m + 4q + (0..3) then 32m + 16 + 4q + (0..3)
@@ -369,7 +384,26 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   // X = A~ S0 + Mak V,  U = T X,  Y = R~ S0 + Mrb U + Mrk V
   f32x4 X, Y;
-  if constexpr (kVExact) {
+  if constexpr (kSum) {
+    // X = A~ S0 + Mak V, U = T X, S_L = diag(gamma_L) (S0 + B^^T U + K^^T V)
+    (void)yrows; (void)scale; (void)Y;
+    // A x V for the token-indexed A operand (exact bf16 V: one instruction)
+    auto times_v = [&](AOp a, f32x4 c) {
+      if (no_v) return c;
+      if constexpr (kVExact) return mm_ax(a, as_bx(o.vh), c);
+      else return mm_ab(a, as_b(o.vh, o.vl), c);
+    };
+    X = times_v(o.Mak, zero);
+    X = mma32x3(o.Aa0, Sb[0], X);
+    X = mma32x3(o.Aa1, Sb[1], X);
+    const BOp Us = as_b(split4(mm_ab(o.Ta, as_b(split4(X)), zero)));
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      f32x4 acc = mm_ab(o.Bt[kb], Us, S[kb]);
+      acc = times_v(o.Kt[kb], acc);
+      S[kb] = acc * o.gl[kb];
+    }
+  } else if constexpr (kVExact) {
     const BX Vx = as_bx(o.vh);
     X = mm_ax(o.Mak, Vx, zero);
     Y = mm_ax(o.Mrk, Vx, zero);
@@ -460,11 +494,13 @@ __device__ __forceinline__ void wait_ge(int* c, int v) {
   for (int it = 0; it < kSpinLimit && peek(c) < v; ++it) __builtin_amdgcn_s_sleep(1);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
-// wait until all four counters c[0..3] reach v
+// wait until all four counters c[0..3] (kEight: c[0..7]) reach v
+template <bool kEight = false>
 __device__ __forceinline__ void wait_min_ge(int* c, int v) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   for (int it = 0; it < kSpinLimit; ++it) {
-    const int m = min(min(peek(c), peek(c + 1)), min(peek(c + 2), peek(c + 3)));
+    int m = min(min(peek(c), peek(c + 1)), min(peek(c + 2), peek(c + 3)));
+    if constexpr (kEight) m = min(m, min(min(peek(c + 4), peek(c + 5)), min(peek(c + 6), peek(c + 7))));
     if (m >= v) break;
     __builtin_amdgcn_s_sleep(1);
   }
@@ -474,8 +510,15 @@ __device__ __forceinline__ void wait_min_ge(int* c, int v) {
 // kTrain: the training-forward contract (pretrain path) also writes every
 // token's sa (p.sa_out) and the post-chunk state of every 16-token chunk
 // (p.boundary, [segment, H, boundary_per_seg, D, D]).
-template <class Io, bool kTrain, bool kRev = false>
-__global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
+// kSum: the summary pass of a sequence split: block y = n * (pieces - 1) + j
+// summarises piece j < last of sequence n with 12 waves.  The four key waves
+// prepare the operators once; state waves 0-3 carry the piece's final state
+// from a zero start (F) and state waves 4-7 its transition, the state from
+// an identity start with V = 0 (Phi), to split_summary[(n * (pieces - 1) +
+// j) * 2 + {0: F, 1: Phi}, H, D, D].  Nothing else is written.
+constexpr int NT_SUM = 768;
+template <class Io, bool kTrain, bool kRev = false, bool kSum = false>
+__global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) {
   using raw = typename Io::raw;
   constexpr bool kVExact = !__is_same(Io, IoF16);
   __shared__ Smem<kVExact> sm;
@@ -489,17 +532,39 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
   const int q = lane >> 4;
   const int H = p.num_heads;
 
+  // sequence split: which sequence, piece and (summary) kind this block is
+  const int npc = p.split_pieces;
+  int seq = seg, piece = 0;
+  if constexpr (kSum) {
+    seq = seg / (npc - 1);
+    piece = seg % (npc - 1);
+  } else if (npc > 0) {
+    seq = seg / npc;
+    piece = seg % npc;
+  }
   if (p.status != nullptr) {
     if (p.status[0] != 0) {
-      fill_output_nan<Io>(static_cast<raw*>(p.y), p.out_elems,
-                          static_cast<int64_t>(seg) * gridDim.x + h,
-                          static_cast<int64_t>(gridDim.x) * gridDim.y);
+      if constexpr (!kSum)
+        fill_output_nan<Io>(static_cast<raw*>(p.y), p.out_elems,
+                            static_cast<int64_t>(seg) * gridDim.x + h,
+                            static_cast<int64_t>(gridDim.x) * gridDim.y);
       return;
     }
-    if (seg >= p.status[2]) return;
+    if (seq >= p.status[2]) return;
   }
   int t0, t1;
-  if (p.uniform_len > 0) {
+  bool last_piece = true;
+  if (kSum || npc > 0) {
+    const int q0 = p.bounds[seq], q1 = p.bounds[seq + 1];
+    const int len = q1 - q0;
+    const int last = len > 0 ? (len - 1) / p.split_len : 0;
+    // pieces past the sequence's last have nothing to do; the summary pass
+    // covers the pieces before the last only
+    if (piece > last || (kSum && piece >= last)) return;
+    last_piece = piece == last;
+    t0 = q0 + piece * p.split_len;
+    t1 = min(t0 + p.split_len, q1);
+  } else if (p.uniform_len > 0) {
     t0 = seg * p.uniform_len;
     t1 = t0 + p.uniform_len;
   } else if (p.chunk_offsets != nullptr) {
@@ -512,23 +577,42 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
     t0 = p.bounds[seg];
     t1 = p.bounds[seg + 1];
   }
-  const int slot = p.slots ? p.slots[seg] : seg;
+  const int slot = p.slots ? p.slots[seq] : seq;
   const int64_t head_off = static_cast<int64_t>(h) * D;
   const int64_t row_stride = static_cast<int64_t>(H) * D;
   const int ngroups = (t1 - t0 + GT - 1) / GT;
   raw* yout = static_cast<raw*>(p.y);
 
-  if (tid < 16) (&sm.ready[0])[tid] = 0;
+  if (tid < 20) (&sm.ready[0])[tid] = 0;
   __syncthreads();   // the only workgroup barrier: counters are zero
 
-  if (wv < 4) {
-    // ---------------- state waves: columns [16wv, 16wv+16)
-    const int vcol = 16 * wv + i;
+  constexpr int kStateWaves = kSum ? 8 : 4;
+  if (wv < kStateWaves) {
+    // ---------------- state waves: columns [16wv, 16wv+16); in the summary
+    // pass waves 4-7 repeat the columns for the transition (kind 1)
+    const int vcol = 16 * (wv & 3) + i;
+    const int kind = kSum ? (wv >> 2) : 0;
     const int64_t sbase = (static_cast<int64_t>(slot) * H + h) * D * D;
     f32x4 S[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) S[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (p.state_in != nullptr) {
+    // state of a piece after the first (real split pass): the combined
+    // start state; the summary pass starts from zero (F) or identity (Phi)
+    const int64_t pbase = (static_cast<int64_t>(seq) * (npc > 0 ? npc : 1) + piece) * H + h;
+    if constexpr (kSum) {
+      if (kind == 1) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) S[kb][e] = (kb * 16 + 4 * q + e == vcol) ? 1.0f : 0.0f;
+      }
+    } else if (npc > 0) {
+      const float* sin = p.split_state + pbase * D * D;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[kb][e] = sin[(kb * 16 + 4 * q + e) * D + vcol];
+    } else if (p.state_in != nullptr) {
       // fp32 state, or (bf16-state contract) bf16 widened once; the state
       // stays fp32 for the whole call and is rounded back once at the end
       const float* sin = static_cast<const float*>(p.state_in);
@@ -583,9 +667,20 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
           o, S, &sm.yb[gi & 1][c * L], vcol, i, q, p.scale, sa_rows,
           keep ? bnd_base + static_cast<int64_t>(bi / p.boundary_every) * D * D : nullptr);
     };
+    auto chunk_sum = [&](const StateOps<kVExact>& o) {
+      state_compute<Io, kVExact, false, true>(o, S, nullptr, vcol, i, q, 1.0f, SaRows{},
+                                              nullptr, kind == 1);
+    };
     auto group = [&](auto par_c, int gi) {
       constexpr int par = decltype(par_c)::value;
       wait_min_ge(sm.ready, gi + 1);          // operators of group gi stored
+      if constexpr (kSum) {
+        // state update only: no outputs to stage or drain
+        chunk_sum(state_load<kVExact, true>(sm.ops[par][0], vcol, i, q));
+        if (t0 + gi * GT + L < t1) chunk_sum(state_load<kVExact, true>(sm.ops[par][1], vcol, i, q));
+        signal(&sm.consumed[wv], gi + 1);
+        return;
+      }
       wait_min_ge(sm.drained, gi - 1);        // outputs of group gi-2 written back
       if (!kTrain && t0 + gi * GT + GT <= t1) {
         // both chunks: the second chunk's first-needed operand reads (the
@@ -608,8 +703,20 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
       group(std::integral_constant<int, 0>{}, gi);
       if (gi + 1 < ngroups) group(std::integral_constant<int, 1>{}, gi + 1);
     }
-    write_out(ngroups - 1);
-    if (p.state_out != nullptr) {
+    if constexpr (kSum) {
+      float* sout = p.split_summary + ((static_cast<int64_t>(seg) * 2 + kind) * H + h) * D * D;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
+      return;
+    } else {
+      write_out(ngroups - 1);
+    }
+    if (!last_piece) {
+      // a piece before the last hands on nothing: its successor started
+      // from the combined state
+    } else if (p.state_out != nullptr) {
       float* sout = static_cast<float*>(p.state_out);
       uint16_t* soutb = static_cast<uint16_t*>(p.state_out);
 #pragma unroll
@@ -670,8 +777,14 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
         const int tok = tok0 + gi * GT;
         const int64_t off = static_cast<int64_t>(min(tok, t1 - 1) - tok0) * row_stride;
 #pragma unroll
-        for (int j = 0; j < 6; ++j)
+        for (int j = 0; j < 6; ++j) {
+          // the summary pass reads no r
+          if (kSum && j == 0) {
+            dst[j] = u32x4{0u, 0u, 0u, 0u};
+            continue;
+          }
           dst[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src[j] + off));
+        }
       }
     };
     u32x4 rawA[6], rawB[6];
@@ -683,7 +796,7 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
     auto iter = [&](auto par_c, u32x4 (&cur)[6], u32x4 (&nxt)[6], int gn) {
       constexpr int par = decltype(par_c)::value;   // parity of gn
       if (gn + 1 < ngroups) load_rows(nxt, gn + 1);
-      wait_min_ge(sm.consumed, gn - 1);             // group gn-2 no longer read
+      wait_min_ge<kSum>(sm.consumed, gn - 1);       // group gn-2 no longer read
       const bool active = t0 + gn * GT + cc * L < t1;
       if constexpr (kRev) {
         // position 0 of the segment: the shifted rows lie past its end
@@ -704,15 +817,15 @@ __global__ __launch_bounds__(NT) void chunk64_kernel(SegArgs p) {
                                               kr, unit_w, p.kv_scale);
       } else {
         if (t0 + gn * GT + cc * L + L <= t1)
-          key_part1<Io, kVExact, true>(sm, sm.ops[par][cc], cur, nbias8, true, par, cc, hh, i,
-                                       q, kr);
+          key_part1<Io, kVExact, true, false, kSum>(sm, sm.ops[par][cc], cur, nbias8, true, par,
+                                                    cc, hh, i, q, kr);
         else if (active)
-          key_part1<Io, kVExact, false>(sm, sm.ops[par][cc], cur, nbias8, tok0 + gn * GT < t1,
-                                        par, cc, hh, i, q, kr);
+          key_part1<Io, kVExact, false, false, kSum>(sm, sm.ops[par][cc], cur, nbias8,
+                                                     tok0 + gn * GT < t1, par, cc, hh, i, q, kr);
       }
       signal(&sm.part1[kw], gn + 1);
       wait_ge(&sm.part1[partner], gn + 1);
-      if (active) key_part2(sm, sm.ops[par][cc], par, cc, hh, i, q, kr);
+      if (active) key_part2<kVExact, kSum>(sm, sm.ops[par][cc], par, cc, hh, i, q, kr);
       signal(&sm.ready[kw], gn + 1);
     };
     for (int gn = 0; gn < ngroups; gn += 2) {
@@ -743,6 +856,90 @@ int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen, hipStr
     hipLaunchKernelGGL((chunk64_kernel<IoBF16, false>), grid, dim3(NT), 0, s, p);
   } else if (dtype == FR2_DTYPE_FLOAT16) {
     hipLaunchKernelGGL((chunk64_kernel<IoF16, false>), grid, dim3(NT), 0, s, p);
+  } else {
+    return FR2_ERR_UNSUPPORTED;
+  }
+  return record_launch();
+}
+
+namespace {
+
+// Start states of the pieces of a split sequence: S(0) = the slot state,
+// S(j+1) = Phi_j S(j) + F_j, written to split_state[n * pieces + j] (S(0)
+// too: the real pass's last piece overwrites the slot while its first piece
+// may not have read it yet, so every piece starts from this copy).
+// One 256-thread block per (head, sequence); thread t owns column t % 64 of
+// rows 16 (t / 64) .. +15.
+__global__ __launch_bounds__(256) void split_combine_kernel(SegArgs p) {
+  __shared__ float phi[D][D + 1];
+  __shared__ float st[D][D + 1];
+  const int h = blockIdx.x, n = blockIdx.y, tid = threadIdx.x, H = p.num_heads;
+  if (p.status != nullptr && (p.status[0] != 0 || n >= p.status[2])) return;
+  const int len = p.bounds[n + 1] - p.bounds[n];
+  const int last = len > 0 ? (len - 1) / p.split_len : 0;
+  const int c = tid & 63, r0 = (tid >> 6) * 16;
+  const int slot = p.slots ? p.slots[n] : n;
+  const float* s0 = static_cast<const float*>(p.state_in) + (static_cast<int64_t>(slot) * H + h) * D * D;
+  float* out0 = p.split_state + (static_cast<int64_t>(n) * p.split_pieces * H + h) * D * D;
+  for (int r = r0; r < r0 + 16; ++r) {
+    st[r][c] = s0[r * D + c];
+    out0[r * D + c] = st[r][c];
+  }
+  const int np1 = p.split_pieces - 1;
+  for (int j = 0; j < last; ++j) {
+    const int64_t pair = static_cast<int64_t>(n) * np1 + j;
+    const float* f = p.split_summary + ((pair * 2) * H + h) * D * D;
+    const float* ph = p.split_summary + ((pair * 2 + 1) * H + h) * D * D;
+    for (int r = r0; r < r0 + 16; ++r) phi[r][c] = ph[r * D + c];
+    __syncthreads();
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = f[(r0 + e) * D + c];
+    for (int k = 0; k < D; ++k) {
+      const float sk = st[k][c];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = __builtin_fmaf(phi[r0 + e][k], sk, acc[e]);
+    }
+    __syncthreads();   // every thread is done reading st and phi
+    float* out = p.split_state +
+                 ((static_cast<int64_t>(n) * p.split_pieces + j + 1) * H + h) * D * D;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      st[r0 + e][c] = acc[e];
+      out[(r0 + e) * D + c] = acc[e];
+    }
+  }
+}
+
+}  // namespace
+
+int64_t split_workspace_floats(int nseg, int H, int pieces) {
+  return static_cast<int64_t>(nseg) * (3 * pieces - 2) * H * D * D;
+}
+
+int launch_chunked_split(int dtype, SegArgs p, int nseg, int pieces, int piece_len,
+                         float* workspace, hipStream_t s) {
+  if (p.sa_out != nullptr || p.boundary != nullptr || p.reverse || p.state_bf16 ||
+      p.uniform_len > 0 || p.ends != nullptr || p.chunk_offsets != nullptr)
+    return FR2_ERR_UNSUPPORTED;
+  if (pieces < 2 || piece_len <= 0 || piece_len % GT != 0 || workspace == nullptr ||
+      p.state_in == nullptr || p.state_out != p.state_in ||
+      static_cast<int64_t>(nseg) * pieces > 65535)
+    return FR2_ERR_INVALID_ARGUMENT;
+  p.split_pieces = pieces;
+  p.split_len = piece_len;
+  p.split_summary = workspace;
+  p.split_state = workspace + static_cast<int64_t>(nseg) * (pieces - 1) * 2 * p.num_heads * D * D;
+  const dim3 gsum(p.num_heads, nseg * (pieces - 1)), gcomb(p.num_heads, nseg),
+      greal(p.num_heads, nseg * pieces);
+  if (dtype == FR2_DTYPE_BFLOAT16) {
+    hipLaunchKernelGGL((chunk64_kernel<IoBF16, false, false, true>), gsum, dim3(NT_SUM), 0, s, p);
+    hipLaunchKernelGGL(split_combine_kernel, gcomb, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((chunk64_kernel<IoBF16, false>), greal, dim3(NT), 0, s, p);
+  } else if (dtype == FR2_DTYPE_FLOAT16) {
+    hipLaunchKernelGGL((chunk64_kernel<IoF16, false, false, true>), gsum, dim3(NT_SUM), 0, s, p);
+    hipLaunchKernelGGL(split_combine_kernel, gcomb, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((chunk64_kernel<IoF16, false>), greal, dim3(NT), 0, s, p);
   } else {
     return FR2_ERR_UNSUPPORTED;
   }

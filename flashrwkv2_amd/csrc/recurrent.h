@@ -56,6 +56,18 @@ struct SegArgs {
   // with boundary set: keep only the snapshots whose index is a multiple of
   // boundary_every, at index / boundary_every
   int boundary_every = 1;
+  // Sequence split of the chunked kernel (few long sequences).  Sequence n
+  // is cut into pieces of split_len tokens (the last one shorter); piece j
+  // covers [q0 + j*split_len, min(q0 + (j+1)*split_len, q1)).
+  //   real pass (split_pieces > 0, grid y = N * split_pieces): piece j of
+  //     sequence n is segment n*split_pieces + j; it starts from the slot
+  //     state (j = 0) or from split_state[(n*split_pieces + j), H, D, D],
+  //     and only the sequence's last piece writes the slot;
+  //   summary pass (chunk64_kernel with kSum): see launch_split_summary.
+  int split_pieces = 0;
+  int split_len = 0;
+  float* split_state = nullptr;
+  float* split_summary = nullptr;
 };
 
 int launch_serial(int D, int dtype, bool bf16_state, const SegArgs& p, int nseg,
@@ -69,6 +81,12 @@ int launch_fp16_state(int D, const SegArgs& p, int nseg, int max_seqlen, int32_t
 // for contracts it does not cover (sa output / boundaries / bf16 state).
 int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen,
                    hipStream_t s);
+// Sequence-split chunked prefill (D = 64, fp32 state, plain contract):
+// `pieces` pieces of `piece_len` tokens per sequence.  workspace holds
+// split_workspace_floats(nseg, H, pieces) floats.
+int64_t split_workspace_floats(int nseg, int H, int pieces);
+int launch_chunked_split(int dtype, SegArgs p, int nseg, int pieces, int piece_len,
+                         float* workspace, hipStream_t s);
 
 // Training backward of the [B,T,H,D] zero-state path: bf16 token tensors and
 // gradients, the forward's fp32 boundary [B,H,T/16,D,D] and state_dot_a

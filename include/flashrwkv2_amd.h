@@ -122,6 +122,43 @@ int fr2_wkv7_recurrent_fp32_forward_kernel(
     float scale, void* stream);
 
 /*
+ * Sequence-split plan for the chunked prefill (head_size 64).  With few
+ * (sequence, head) units one block per unit leaves most of the GPU idle; the
+ * plan cuts every sequence into *pieces pieces of *piece_len tokens (a
+ * multiple of 32; the last piece of a sequence is shorter) and reports the
+ * device workspace fr2_wkv7_recurrent_fp32_forward_split needs.  *pieces is
+ * 1 when splitting does not pay (fewer than three pieces of 256/units, or
+ * pieces shorter than 1024 tokens).  No reference counterpart: the reference runs one CUDA block
+ * per (sequence, head) in launch_recurrent_fp32
+ * (csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:393-453).
+ */
+int fr2_wkv7_recurrent_fp32_split_plan(int32_t num_sequences, int32_t num_heads,
+                                       int32_t head_size, int32_t max_seqlen,
+                                       int32_t* pieces, int32_t* piece_len,
+                                       int64_t* workspace_bytes);
+
+/*
+ * fr2_wkv7_recurrent_fp32_forward with the sequence split of a plan (same
+ * results within fp32 rounding): a summary pass computes each piece's
+ * zero-start final state F and its transition Phi (identity start, V = 0),
+ * a combine kernel chains S(j+1) = Phi_j S(j) + F_j from the slot state, and
+ * the chunked kernel then runs every piece from its start state; the last
+ * piece of each sequence writes the slot.  workspace: device memory of at
+ * least the plan's workspace_bytes, owned by the caller, not read after the
+ * call's kernels finish.  Replaces, for long sequences, the single-block-
+ * per-(sequence, head) launch of tmix_wkv7_recurrent_fp32_from_decay_logits
+ * (…fp32io16_forward_varlen.cpp:330-387).
+ */
+int fr2_wkv7_recurrent_fp32_forward_split(
+    const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, int32_t num_sequences, int32_t num_heads,
+    int32_t head_size, int64_t total_tokens, int32_t max_seqlen, int32_t dtype,
+    float* state, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a,
+    const void* b, void* output, float scale, int32_t pieces, int32_t piece_len,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Packed varlen recurrence with an FP16 state pool [slots,H,D,D] updated in
  * place (the "Albatross" FP16-state contract, fp16 token tensors only):
  *   delta  = fp16(w - 1 + dither(phase)),

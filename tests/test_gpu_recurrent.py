@@ -390,6 +390,14 @@ def test_chunked_kernel_long_sequences_match_fp64_oracle(cfg, overrides):
     out = _run_kernel(C, CHUNKED, case, pool)
     assert_output_close(out, y_ref)
     assert_state_close(pool, pool_ref)
+    # the public entry on the same inputs: with few (sequence, head) units it
+    # cuts the sequence into pieces (summary, combine, pieces)
+    pool2 = w.state_pool.clone()
+    out2 = wkv7(*w.tokens, state_pool=pool2, cu_seqlens=w.cu_seqlens,
+                state_indices=w.state_indices)
+    torch.cuda.synchronize()
+    assert_output_close(out2, y_ref)
+    assert_state_close(pool2, pool_ref)
 
 
 def test_chunked_and_serial_agree_at_full_prefill_size():
