@@ -371,7 +371,8 @@ def time_long_context(torch, flashrwkv2_amd, steps: int):
         "tokens_per_s": round(w.total_tokens / (ms * 1e-3), 1),
         "kernels": "chunk64_kernel summary pass + split_combine_kernel + chunk64_kernel pieces",
         "pieces": pieces, "piece_len": piece_len, "workspace_bytes": ws,
-        "roofline": roofline_obj(nbytes, ms),
+        "roofline": roofline_obj(nbytes, ms, measured_traffic(
+            "split:chunk64_summary+combine+pieces", w.name)),
         "unsplit": {"ms_per_step": round(unsplit_ms, 4),
                     "tokens_per_s": round(w.total_tokens / (unsplit_ms * 1e-3), 1),
                     "kernel": "chunk64_kernel<IoBF16,false> (one block per head)",
@@ -634,7 +635,7 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode (config 2) leg")
     ap.add_argument("--cpu-sample-tokens", type=int, default=4096,
