@@ -618,6 +618,25 @@ def time_statetune_training(torch, w, steps: int, chunk_len: int = 1024):
     }
 
 
+def device_info(torch) -> dict:
+    """Name and CU count of device 0, plus rocm-smi's current clock levels
+    when the tool is present (the effective shader clock under the prefill
+    kernel, from GRBM_GUI_ACTIVE, is in profiles/mfma_counters.json)."""
+    import subprocess
+
+    props = torch.cuda.get_device_properties(0)
+    info = {"name": props.name, "arch": getattr(props, "gcnArchName", ""),
+            "cus": props.multi_processor_count}
+    try:
+        out = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True, text=True,
+                             timeout=20).stdout
+        info["rocm_smi_clocks"] = [ln.split(":", 1)[1].strip() for ln in out.splitlines()
+                                   if "clock level" in ln]
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return info
+
+
 def mfma_obj(w, kernel_ms: float):
     """Matrix-core use of the chunked kernel: issued bf16 MFMA flops (hi/lo
     split products included) over the launch time, against the dense bf16 peak."""
@@ -627,8 +646,17 @@ def mfma_obj(w, kernel_ms: float):
     chunks = int(((lens + 15) // 16).sum()) * w.num_heads
     flops = chunks * MFMA_PER_CHUNK * MFMA_FLOPS
     tf = flops / (kernel_ms * 1e-3) / 1e12
-    return {"issued_tflops": round(tf, 2), "peak_tflops": MFMA_PEAK_TFLOPS,
-            "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "instructions": chunks * MFMA_PER_CHUNK}
+    out = {"issued_tflops": round(tf, 2), "peak_tflops": MFMA_PEAK_TFLOPS,
+           "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "instructions": chunks * MFMA_PER_CHUNK}
+    # PMC-measured matrix-core use of the same kernel and workload
+    # (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs), the MfmaUtil metric)
+    path = ROOT / "profiles" / "mfma_counters.json"
+    if path.exists():
+        m = json.loads(path.read_text()).get("chunk64_kernel<IoBF16,false>")
+        if m is not None and m.get("workload") == w.name:
+            out["measured_util"] = m["mfma_util"]
+            out["measured_sclk_mhz"] = m["effective_sclk_mhz"]
+    return out
 
 
 def main() -> int:
@@ -752,6 +780,7 @@ def main() -> int:
         result["statetune_training"] = time_statetune_training(torch, wt, max(3, args.steps // 4))
     if args.only in (None, "stages"):
         result["layer_stages"] = time_layer_stages(torch, 8 * 4096, 32)
+    result["device"] = device_info(torch)
     if pre is not None and not args.no_cpu and args.config == 1:
         threads = min(16, os.cpu_count() or 1)
         tps, dt, n_tok, reps = cpu_baseline(pre.w, threads, args.cpu_sample_tokens)
