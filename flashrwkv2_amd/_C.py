@@ -736,6 +736,11 @@ def _check_bf16(t, ref, name):
     _check(t.dtype == torch.bfloat16, name, " must be bf16")
 
 
+# pieces of the bf16-state chunk entry's sequence split: None = the library's
+# plan; tests set a count to force the split on small cases
+_chunk_split_pieces = None
+
+
 def infer_tmix_wkv7_chunk_bf16_forward_varlen(r, decay_logits, k, v, a, b, state_pool,
                                               cu_seqlens, state_indices, chunk_size=16,
                                               max_seqlen=-1, scale=1.0, decay_bias=None,
@@ -775,13 +780,22 @@ def infer_tmix_wkv7_chunk_bf16_forward_varlen(r, decay_logits, k, v, a, b, state
     lq, ls, status, max_seqlen, keep = _resolve_launch_metadata(
         cu_seqlens, state_indices, r.size(0), state_pool.size(0), int(max_seqlen),
         validated_metadata)
-    with torch.cuda.device(r.device):
-        rc = N.load().fr2_wkv7_chunk_bf16_forward(
-            lq.data_ptr(), ls.data_ptr(), status.data_ptr(), state_indices.numel(), h,
+    args = (lq.data_ptr(), ls.data_ptr(), status.data_ptr(), state_indices.numel(), h,
             r.size(0), int(chunk_size), int(max_seqlen), state_pool.data_ptr(),
             r.data_ptr(), decay_logits.data_ptr(), N.ptr(decay_bias), k.data_ptr(),
-            v.data_ptr(), a.data_ptr(), b.data_ptr(), output.data_ptr(), float(scale),
-            _stream(r.device))
+            v.data_ptr(), a.data_ptr(), b.data_ptr(), output.data_ptr(), float(scale))
+    pieces, piece_len, ws_bytes = split_plan(state_indices.numel(), h, 64, int(max_seqlen),
+                                             _chunk_split_pieces)
+    with torch.cuda.device(r.device):
+        if pieces > 1:
+            # few long sequences: the sequence split (workspace on this stream)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=r.device)
+            rc = N.load().fr2_wkv7_chunk_bf16_forward_split(*args, pieces, piece_len,
+                                                            ws.data_ptr(), ws_bytes,
+                                                            _stream(r.device))
+            del ws
+        else:
+            rc = N.load().fr2_wkv7_chunk_bf16_forward(*args, _stream(r.device))
     N.check(rc, "infer_tmix_wkv7_chunk_bf16_forward_varlen")
     del keep
     return output, state_pool

@@ -122,6 +122,13 @@ SIGNATURES: dict[str, tuple] = {
          c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
          c_void_p, c_void_p, c_void_p, c_float, c_void_p],
     ),
+    "fr2_wkv7_chunk_bf16_forward_split": (
+        c_int32,
+        [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int64, c_int32,
+         c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32, c_void_p,
+         c_int64, c_void_p],
+    ),
     "fr2_wkv7_rl_infctx_forward": (
         c_int32,
         [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,

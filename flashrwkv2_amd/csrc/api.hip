@@ -303,6 +303,42 @@ extern "C" int fr2_wkv7_chunk_bf16_forward(
                             static_cast<hipStream_t>(stream));
 }
 
+extern "C" int fr2_wkv7_chunk_bf16_forward_split(
+    const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, int32_t num_sequences, int32_t num_heads,
+    int64_t total_tokens, int32_t chunk_size, int32_t max_seqlen,
+    uint16_t* state_bf16, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a,
+    const void* b, void* output, float scale, int32_t pieces, int32_t piece_len,
+    void* workspace, int64_t workspace_bytes, void* stream) {
+  (void)max_seqlen;
+  if (!query_start_loc || !state_indices || !status || !state_bf16 || !workspace ||
+      !tokens_ok(r, decay_logits, k, v, a, b, output))
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 ||
+      total_tokens <= 0 || chunk_size <= 0)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (pieces < 2 || workspace_bytes < fr2::split_workspace_floats(num_sequences, num_heads,
+                                                                   pieces) * 4)
+    return FR2_ERR_INVALID_ARGUMENT;
+  SegArgs p;
+  p.bounds = query_start_loc;
+  p.slots = state_indices;
+  p.status = status;
+  p.num_heads = num_heads;
+  p.out_elems = total_tokens * num_heads * 64;
+  p.state_in = state_bf16;
+  p.state_out = state_bf16;
+  p.state_bf16 = true;
+  p.r = r; p.logits = decay_logits; p.bias = decay_bias; p.k = k; p.v = v;
+  p.a = a; p.b = b;
+  p.y = output;
+  p.scale = scale;
+  return fr2::launch_chunked_split(FR2_DTYPE_BFLOAT16, p, num_sequences, pieces, piece_len,
+                                   static_cast<float*>(workspace),
+                                   static_cast<hipStream_t>(stream));
+}
+
 extern "C" int fr2_wkv7_rl_infctx_forward(
     const int32_t* sequence_chunk_offsets, const int32_t* chunk_token_starts,
     const int32_t* chunk_token_ends, int32_t num_sequences, int32_t num_chunks,

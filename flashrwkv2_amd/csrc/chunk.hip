@@ -879,10 +879,13 @@ __global__ __launch_bounds__(256) void split_combine_kernel(SegArgs p) {
   const int last = len > 0 ? (len - 1) / p.split_len : 0;
   const int c = tid & 63, r0 = (tid >> 6) * 16;
   const int slot = p.slots ? p.slots[n] : n;
-  const float* s0 = static_cast<const float*>(p.state_in) + (static_cast<int64_t>(slot) * H + h) * D * D;
+  // the slot state: fp32, or (bf16-state contract) bf16 widened once
+  const int64_t s0 = (static_cast<int64_t>(slot) * H + h) * D * D;
+  const float* s0f = static_cast<const float*>(p.state_in) + s0;
+  const uint16_t* s0b = static_cast<const uint16_t*>(p.state_in) + s0;
   float* out0 = p.split_state + (static_cast<int64_t>(n) * p.split_pieces * H + h) * D * D;
   for (int r = r0; r < r0 + 16; ++r) {
-    st[r][c] = s0[r * D + c];
+    st[r][c] = p.state_bf16 ? IoBF16::to_f32(s0b[r * D + c]) : s0f[r * D + c];
     out0[r * D + c] = st[r][c];
   }
   const int np1 = p.split_pieces - 1;
@@ -919,7 +922,7 @@ int64_t split_workspace_floats(int nseg, int H, int pieces) {
 
 int launch_chunked_split(int dtype, SegArgs p, int nseg, int pieces, int piece_len,
                          float* workspace, hipStream_t s) {
-  if (p.sa_out != nullptr || p.boundary != nullptr || p.reverse || p.state_bf16 ||
+  if (p.sa_out != nullptr || p.boundary != nullptr || p.reverse ||
       p.uniform_len > 0 || p.ends != nullptr || p.chunk_offsets != nullptr)
     return FR2_ERR_UNSUPPORTED;
   if (pieces < 2 || piece_len <= 0 || piece_len % GT != 0 || workspace == nullptr ||

@@ -246,6 +246,24 @@ int fr2_wkv7_chunk_bf16_forward(
     const void* b, void* output, float scale, void* stream);
 
 /*
+ * fr2_wkv7_chunk_bf16_forward with the sequence split of
+ * fr2_wkv7_recurrent_fp32_split_plan (head_size 64): the same three passes as
+ * fr2_wkv7_recurrent_fp32_forward_split, the bf16 slot state widened once by
+ * the combine kernel and rounded once by each sequence's last piece.  Replaces,
+ * for few long sequences, the one-block-per-(sequence, head) launch of
+ * infer_tmix_wkv7_chunk_bf16_forward_varlen_cuda
+ * (…/infer_chunk_bf16_forward_varlen.cu:276-340).
+ */
+int fr2_wkv7_chunk_bf16_forward_split(
+    const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, int32_t num_sequences, int32_t num_heads,
+    int64_t total_tokens, int32_t chunk_size, int32_t max_seqlen,
+    uint16_t* state_bf16, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a,
+    const void* b, void* output, float scale, int32_t pieces, int32_t piece_len,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * RL/Infctx fp32-state chunked forward over chunk metadata
  * (sequence_chunk_offsets [N+1], chunk_token_starts/ends [C]).  `state` is the
  * working pool [N,H,D,D] (slot i = sequence i), updated in place to the final

@@ -181,6 +181,54 @@ def test_chunk_bf16_long_requests_on_the_chunked_kernel():
     assert_state_close(pool2[active], pool_ref[active], rmse=4e-3, fro=4e-3)
 
 
+@pytest.mark.parametrize("pieces", [2, 3])
+def test_chunk_bf16_sequence_split(monkeypatch, pieces):
+    """The bf16-state chunk entry with the sequence split forced (summary
+    pass, combine from the widened bf16 slot state, pieces; each sequence's
+    last piece rounds the slot once): the oracle's values and the unsplit
+    call's, untouched slots unchanged."""
+    require_gpu()
+    import flashrwkv2_amd
+
+    g = torch.Generator().manual_seed(31)
+    lengths = [700, 5, 260, 64]
+    total, h, d = sum(lengths), 3, 64
+    cu_list = [0]
+    for n in lengths:
+        cu_list.append(cu_list[-1] + n)
+    kk = torch.randn((total, h, d), generator=g)
+    kk = kk / kk.norm(dim=-1, keepdim=True)
+    gate = torch.sigmoid(torch.randn((total, h, d), generator=g))
+    inputs = [(torch.randn((total, h, d), generator=g) * s).to(torch.bfloat16).cuda()
+              for s in (1.0, 1.5, 1.0, 1.0)]
+    inputs = inputs[:4] + [(-kk).to(torch.bfloat16).cuda(), (kk * gate).to(torch.bfloat16).cuda()]
+    cu = torch.tensor(cu_list, device="cuda", dtype=torch.int32)
+    slots = torch.tensor([4, 0, 2, 5], device="cuda", dtype=torch.int32)
+    pool = _randn((6, h, d, d), g, 0.1, torch.bfloat16)
+    before = pool.clone()
+    y_ref, pool_ref = _chunk_reference(inputs, pool, cu, slots, 0.5)
+    monkeypatch.setattr(flashrwkv2_amd._C, "_chunk_split_pieces", pieces)
+    out = infer_tmix_wkv7_chunk_bf16_forward_varlen(
+        *inputs, state_pool=pool, cu_seqlens=cu, state_indices=slots, max_seqlen=700,
+        scale=0.5)
+    torch.cuda.synchronize()
+    assert_output_close(out, y_ref)
+    active = [4, 0, 2, 5]
+    assert_state_close(pool[active], pool_ref[active], rmse=4e-3, fro=4e-3)
+    assert torch.equal(pool[[1, 3]], before[[1, 3]])
+    monkeypatch.setattr(flashrwkv2_amd._C, "_chunk_split_pieces", None)
+    pool2 = before.clone()
+    out2 = infer_tmix_wkv7_chunk_bf16_forward_varlen(
+        *inputs, state_pool=pool2, cu_seqlens=cu, state_indices=slots, max_seqlen=700,
+        scale=0.5)
+    torch.cuda.synchronize()
+    dy = out.float() - out2.float()
+    assert (dy.square().mean().sqrt() / out2.float().square().mean().sqrt()).item() <= 2e-3
+    # both round the same fp32 state once; a split can move a value across a
+    # bf16 rounding boundary, so the pools agree to one bf16 ulp
+    assert ((pool.float() - pool2.float()).abs() <= pool2.float().abs() * 2 ** -7 + 1e-30).all()
+
+
 def test_chunk_bf16_rejects_non_bf16_and_duplicate_slots_without_state_write():
     require_gpu()
     tensors = [torch.zeros((2, 1, 64), device="cuda", dtype=torch.bfloat16) for _ in range(6)]
