@@ -120,3 +120,70 @@ def test_split_fails_closed_on_invalid_metadata():
     torch.cuda.synchronize()
     assert torch.isnan(out.float()).all()
     assert torch.equal(pool, before)
+
+
+@pytest.mark.cuda_graph
+def test_split_under_graph_capture_with_live_metadata():
+    """Graph ticket (live cu_seqlens / counts, capacity-sized plan): the split
+    path is captured once (its workspace comes from the graph's pool) and
+    every replay equals the eager call on the same ticket kind and the
+    oracle; a replay after the live metadata changed follows the new
+    sequences."""
+    C = require_gpu()
+    from flashrwkv2_amd import _C as CC
+
+    dev = torch.device("cuda")
+    case = make_case(dtype=torch.bfloat16, head_size=64, lengths=(3000, 1000), num_heads=2,
+                     seed=11)
+    packed = tokens(case)
+    slots_n = case["state_pool"].shape[0]
+    initial = case["state_pool"].clone()
+    cu = torch.tensor([0, 3000, 4000], device=dev, dtype=torch.int32)
+    idx = case["state_indices"].clone()
+    n_tok = torch.full((1,), 4000, device=dev, dtype=torch.int32)
+    n_seq = torch.full((1,), 2, device=dev, dtype=torch.int32)
+    live = dict(state_pool_size=slots_n, token_capacity=4000, sequence_capacity=2,
+                max_seqlen_capacity=4000, num_active_tokens=n_tok, num_active_sequences=n_seq)
+    assert CC.split_plan(2, 2, 64, 4000)[0] == 3           # the capacity plan splits
+    y_ref, pool_ref = oracle_expect(case)
+    active = case["state_indices"].long()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        eager_state = initial.clone()
+        t_eager = prepare_tmix_wkv7_recurrent_metadata(cu, idx, **live)
+        eager = wkv7(*packed, state_pool=eager_state, cu_seqlens=cu, state_indices=idx,
+                     validated_metadata=t_eager)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    assert_output_close(eager, y_ref)
+    assert_state_close(eager_state[active], pool_ref[active.cpu().numpy()])
+    state = initial.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        ticket = prepare_tmix_wkv7_recurrent_metadata(cu, idx, **live)
+        graph_out = wkv7(*packed, state_pool=state, cu_seqlens=cu, state_indices=idx,
+                         validated_metadata=ticket)
+    for _ in range(3):
+        state.copy_(initial)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(graph_out, eager)
+        assert torch.equal(state, eager_state)
+    # one live sequence of 2500 tokens: the replay follows the new metadata
+    state.copy_(initial)
+    cu.copy_(torch.tensor([0, 2500, -1], device=dev, dtype=torch.int32))
+    n_tok.fill_(2500)
+    n_seq.fill_(1)
+    graph.replay()
+    torch.cuda.synchronize()
+    one = dict(case)
+    one.update({n: t[:2500] for n, t in zip(("r", "decay_logits", "k", "v", "a", "b"), packed)})
+    one["cu_seqlens"] = torch.tensor([0, 2500], device=dev, dtype=torch.int32)
+    one["state_indices"] = idx[:1].clone()
+    y1, p1 = oracle_expect(one, state_pool=initial)
+    assert_output_close(graph_out[:2500], y1)
+    s0 = int(idx[0])
+    assert_state_close(state[s0:s0 + 1], p1[s0:s0 + 1])
+    others = [i for i in range(slots_n) if i != s0]
+    assert torch.equal(state[others], initial[others])
