@@ -203,8 +203,9 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
 }
 
 // ---------------------------------------------------------------------------
-// key side, part 2: store the operands; hh = 0 forms T, hh = 1 the masked
-// Mak, Mrb, Mrk
+// key side, part 2: store the operands; the wave whose key half hh equals
+// the group parity mp forms T, the other one the masked Mak, Mrb, Mrk (the
+// T chain is the heavier role: alternating it spreads it over all four SIMDs)
 // ---------------------------------------------------------------------------
 template <bool kVExact, bool kSum = false>
 __device__ __forceinline__ void key_part2(Smem<kVExact>& sm, ChunkOps<kVExact>& op, int mp,
@@ -234,7 +235,7 @@ __device__ __forceinline__ void key_part2(Smem<kVExact>& sm, ChunkOps<kVExact>& 
   // mp0[0][b][s][t] + mp0[1][b][s][t]
   const float (*mp0)[4][L][MPP] = sm.mpart[mp][cc];
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  if (hh == 0) {
+  if (hh == mp) {
     // M[e] = Mab[4q+e][i] (accumulator layout), Mt[e] = Mab[i][4q+e]
     const f32x4 m4 = *reinterpret_cast<const f32x4*>(&mp0[0][0][i][4 * q]) +
                      *reinterpret_cast<const f32x4*>(&mp0[1][0][i][4 * q]);
