@@ -384,6 +384,28 @@ def time_long_context(torch, flashrwkv2_amd, steps: int):
     return out
 
 
+def time_varlen(torch, flashrwkv2_amd, steps: int):
+    """BASELINE config 3 (64 packed sequences of seeded lengths U{1..2048},
+    H = 64, per-sequence fp32 states): the public call with a reused ticket,
+    and the kernel's per-launch time through the C ABI."""
+    from flashrwkv2_amd import workloads
+
+    w = workloads.config(3, "cuda")
+    run = Runner(w, torch, flashrwkv2_amd)
+    ms = run.time_steps(steps, 5)
+    kms = run.time_kernel(steps)
+    nbytes = algorithmic_bytes(w.total_tokens, w.num_heads, w.state_indices.numel())
+    out = {
+        "workload": w.name, "total_tokens": w.total_tokens,
+        "ms_per_step": round(ms, 4), "tokens_per_s": round(w.total_tokens / (ms * 1e-3), 1),
+        "kernel_ms": round(kms, 4), "kernel": run.kernel_name(),
+        "roofline": roofline_obj(nbytes, kms), "algorithmic_bytes": nbytes,
+    }
+    del run, w
+    torch.cuda.empty_cache()
+    return out
+
+
 def time_chunk_bf16_state(torch, flashrwkv2_amd, w, steps: int):
     """The bf16-state chunk entry (infer_tmix_wkv7_chunk_bf16_forward_varlen)
     on a config-1-shaped batch with a bf16 state pool: public calls with a
@@ -773,6 +795,7 @@ def main() -> int:
         result["chunk_bf16_state"] = time_chunk_bf16_state(torch, flashrwkv2_amd, pre.w,
                                                            max(5, args.steps // 2))
     if args.only in (None, "long") and args.config == 1:
+        result["varlen_prefill"] = time_varlen(torch, flashrwkv2_amd, max(5, args.steps // 2))
         result["long_context"] = time_long_context(torch, flashrwkv2_amd, max(4, args.steps // 4))
     if args.only in (None, "train") and not args.no_train:
         wt = pre.w if (pre is not None and args.config == 1) else workloads.config(1, "cuda")
