@@ -363,16 +363,17 @@ def time_long_context(torch, flashrwkv2_amd, steps: int):
     run = Runner(w, torch, flashrwkv2_amd)
     ms = run.time_steps(steps, 2)
     unsplit_ms = run.time_kernel(max(2, steps // 2))
-    pieces, piece_len, ws = CC.split_plan(w.state_indices.numel(), w.num_heads, 64,
-                                          run.ticket._max_seqlen())
+    pieces, piece_len, lead_len, ws = CC.split_plan(w.state_indices.numel(), w.num_heads, 64,
+                                                    run.ticket._max_seqlen())
     nbytes = algorithmic_bytes(w.total_tokens, w.num_heads, w.state_indices.numel())
     out = {
         "workload": w.name, "ms_per_step": round(ms, 4),
         "tokens_per_s": round(w.total_tokens / (ms * 1e-3), 1),
-        "kernels": "chunk64_kernel summary pass + split_combine_kernel + chunk64_kernel pieces",
-        "pieces": pieces, "piece_len": piece_len, "workspace_bytes": ws,
+        "kernels": "chunk64_kernel piece 0 (second stream) concurrent with the summary pass, "
+                   "split_combine_kernel, chunk64_kernel pieces 1..P-1",
+        "pieces": pieces, "piece_len": piece_len, "lead_len": lead_len, "workspace_bytes": ws,
         "roofline": roofline_obj(nbytes, ms, measured_traffic(
-            "split:chunk64_summary+combine+pieces", w.name)),
+            "split:lead+summary+combine+pieces", w.name)),
         "unsplit": {"ms_per_step": round(unsplit_ms, 4),
                     "tokens_per_s": round(w.total_tokens / (unsplit_ms * 1e-3), 1),
                     "kernel": "chunk64_kernel<IoBF16,false> (one block per head)",

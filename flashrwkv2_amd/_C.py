@@ -57,6 +57,21 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_aux_streams: dict[int, torch.cuda.Stream] = {}
+
+
+def _aux_stream(device: torch.device) -> int:
+    """The second stream of the pipelined sequence split (piece 0 runs on it
+    next to the summary pass), one per device, default priority.  The library
+    orders it against the caller's stream with events, so it joins a graph
+    capture of the caller's stream."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    s = _aux_streams.get(idx)
+    if s is None:
+        s = _aux_streams[idx] = torch.cuda.Stream(device=idx)
+    return s.cuda_stream
+
+
 def _dtype_code(t: torch.Tensor) -> int:
     return _TOKEN_DTYPES[t.dtype]
 
@@ -344,11 +359,11 @@ def _recurrent_launch(kernel, qsl, slots, state, r, decay_logits, k, v, a, b, ou
               int(max_seqlen), _dtype_code(r), state.data_ptr(), r.data_ptr(),
               decay_logits.data_ptr(), N.ptr(decay_bias), k.data_ptr(), v.data_ptr(),
               a.data_ptr(), b.data_ptr(), output.data_ptr(), float(scale))
-    pieces, piece_len, ws_bytes = 1, 0, 0
+    pieces, piece_len, lead_len, ws_bytes = 1, 0, 0, 0
     if kernel is None or kernel == N.KERNEL_SPLIT:
         # the forced split without a known max_seqlen bounds it by the token count
         ms = int(max_seqlen) if (kernel is None or int(max_seqlen) > 0) else r.size(0)
-        pieces, piece_len, ws_bytes = split_plan(n, h, d, ms, split_pieces)
+        pieces, piece_len, lead_len, ws_bytes = split_plan(n, h, d, ms, split_pieces)
         if kernel == N.KERNEL_SPLIT and pieces < 2:
             raise RuntimeError("sequence split needs head size 64 and at least two pieces")
     with torch.cuda.device(state.device):
@@ -357,8 +372,9 @@ def _recurrent_launch(kernel, qsl, slots, state, r, decay_logits, k, v, a, b, ou
             # workspace from the caching allocator on this stream: it is only
             # handed out again to work queued later on the same stream
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=state.device)
-            rc = lib.fr2_wkv7_recurrent_fp32_forward_split(*common, pieces, piece_len,
-                                                           ws.data_ptr(), ws_bytes, stream)
+            aux = _aux_stream(state.device) if lead_len > 0 else None
+            rc = lib.fr2_wkv7_recurrent_fp32_forward_split(*common, pieces, piece_len, lead_len,
+                                                           ws.data_ptr(), ws_bytes, stream, aux)
             del ws
         elif kernel is None:
             rc = lib.fr2_wkv7_recurrent_fp32_forward(*common, stream)
@@ -368,23 +384,33 @@ def _recurrent_launch(kernel, qsl, slots, state, r, decay_logits, k, v, a, b, ou
 
 
 def split_plan(num_sequences: int, num_heads: int, head_size: int, max_seqlen: int,
-               pieces: int | None = None) -> tuple[int, int, int]:
-    """(pieces, piece_len, workspace_bytes) of the chunked prefill's sequence
-    split: the library's plan, or `pieces` pieces when given (tests)."""
+               pieces=None) -> tuple[int, int, int, int]:
+    """(pieces, piece_len, lead_len, workspace_bytes) of the chunked prefill's
+    sequence split: the library's plan (the pipelined split), or, for tests,
+    `pieces` equal pieces of the classic split (lead_len 0) or, with
+    `pieces=(P, lead_len)`, P pieces of the pipelined split whose piece 0 has
+    lead_len tokens."""
     lib = N.load()
     if pieces is None:
-        pc, pl, wb = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+        pc, pl, ll, wb = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
         N.check(lib.fr2_wkv7_recurrent_fp32_split_plan(num_sequences, num_heads, head_size,
                                                        max_seqlen, ctypes.byref(pc),
-                                                       ctypes.byref(pl), ctypes.byref(wb)),
+                                                       ctypes.byref(pl), ctypes.byref(ll),
+                                                       ctypes.byref(wb)),
                 "fr2_wkv7_recurrent_fp32_split_plan")
-        return pc.value, pl.value, wb.value
+        return pc.value, pl.value, ll.value, wb.value
+    lead = 0
+    if isinstance(pieces, tuple):
+        pieces, lead = pieces
     if head_size != 64 or pieces < 2:
-        return 1, max_seqlen, 0
-    plen = -(-max(max_seqlen, 1) // pieces)
+        return 1, max_seqlen, 0, 0
+    if lead > 0:
+        plen = -(-max(max_seqlen - lead, 1) // (pieces - 1))
+    else:
+        plen = -(-max(max_seqlen, 1) // pieces)
     plen = -(-plen // 32) * 32
     ws = num_sequences * (3 * pieces - 2) * num_heads * 64 * 64 * 4
-    return pieces, plen, ws
+    return pieces, plen, lead, ws
     # Implicit validation buffers (`keep`) are released after the launch; the
     # caching allocator only hands them out again to work queued later on this
     # same stream, which runs after the kernels that read them.
@@ -784,15 +810,16 @@ def infer_tmix_wkv7_chunk_bf16_forward_varlen(r, decay_logits, k, v, a, b, state
             r.size(0), int(chunk_size), int(max_seqlen), state_pool.data_ptr(),
             r.data_ptr(), decay_logits.data_ptr(), N.ptr(decay_bias), k.data_ptr(),
             v.data_ptr(), a.data_ptr(), b.data_ptr(), output.data_ptr(), float(scale))
-    pieces, piece_len, ws_bytes = split_plan(state_indices.numel(), h, 64, int(max_seqlen),
-                                             _chunk_split_pieces)
+    pieces, piece_len, lead_len, ws_bytes = split_plan(state_indices.numel(), h, 64,
+                                                       int(max_seqlen), _chunk_split_pieces)
     with torch.cuda.device(r.device):
         if pieces > 1:
             # few long sequences: the sequence split (workspace on this stream)
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=r.device)
-            rc = N.load().fr2_wkv7_chunk_bf16_forward_split(*args, pieces, piece_len,
+            aux = _aux_stream(r.device) if lead_len > 0 else None
+            rc = N.load().fr2_wkv7_chunk_bf16_forward_split(*args, pieces, piece_len, lead_len,
                                                             ws.data_ptr(), ws_bytes,
-                                                            _stream(r.device))
+                                                            _stream(r.device), aux)
             del ws
         else:
             rc = N.load().fr2_wkv7_chunk_bf16_forward(*args, _stream(r.device))

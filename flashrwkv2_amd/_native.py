@@ -55,14 +55,14 @@ SIGNATURES: dict[str, tuple] = {
          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_void_p],
     ),
     "fr2_wkv7_recurrent_fp32_split_plan": (
-        c_int32, [c_int32, c_int32, c_int32, c_int32, _i32p, _i32p, POINTER(c_int64)],
+        c_int32, [c_int32, c_int32, c_int32, c_int32, _i32p, _i32p, _i32p, POINTER(c_int64)],
     ),
     "fr2_wkv7_recurrent_fp32_forward_split": (
         c_int32,
         [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64,
          c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
          c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32,
-         c_void_p, c_int64, c_void_p],
+         c_int32, c_void_p, c_int64, c_void_p, c_void_p],
     ),
     "fr2_wkv7_recurrent_fp16_forward": (
         c_int32,
@@ -126,8 +126,8 @@ SIGNATURES: dict[str, tuple] = {
         c_int32,
         [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int64, c_int32,
          c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-         c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32, c_void_p,
-         c_int64, c_void_p],
+         c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32, c_int32,
+         c_void_p, c_int64, c_void_p, c_void_p],
     ),
     "fr2_wkv7_rl_infctx_forward": (
         c_int32,

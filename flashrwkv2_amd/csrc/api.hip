@@ -107,35 +107,52 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kernel(
 
 // Sequence split of the chunked prefill.  With few (sequence, head) units
 // the chunked kernel leaves most CUs idle (one block per unit, one block per
-// CU), so long sequences are cut into pieces: a summary pass (one block per
-// piece but the last), a combine kernel and the real pass over every piece.
-// Both passes run one block per CU, so a sequence gets 256/units pieces
-// (neither pass then needs a second round of blocks) of at least 1024
-// tokens; split only when that gives three pieces or more (at most 85 units:
-// with two pieces the summary pass costs what the split saves).
-constexpr int kSplitMaxUnits = 85;
+// CU), so long sequences are cut into pieces.  The plan is the pipelined
+// ("lead") split: piece 0 runs from the slot state concurrently with a
+// summary pass over pieces 1..P-2 (one block per unit and piece), then a
+// combine kernel chains the start states and pieces 1..P-1 run.  With
+// Q = 256/units and P = Q + 1 pieces, both phases hold one block per CU.  A
+// summary block costs ~1.3x a real block per token when the two run side by
+// side (config 4: 96 vs 73 ns per token), but the lead piece's block also
+// slows down next to it; piece 0 gets 1.2x the tokens of the others (the
+// best of 1.15x-1.33x measured at config 4); Q is also capped so that pieces keep at least
+// 1024 tokens.  Split only when Q >= 2 (at most 128 units).
+constexpr int kSplitMaxUnits = 128;
 constexpr int kSplitMinPiece = 1024;
 constexpr int kSplitAlign = 32;
+constexpr float kSplitLeadRatio = 1.2f;
 
 extern "C" int fr2_wkv7_recurrent_fp32_split_plan(int32_t num_sequences, int32_t num_heads,
                                                   int32_t head_size, int32_t max_seqlen,
                                                   int32_t* pieces, int32_t* piece_len,
-                                                  int64_t* workspace_bytes) {
-  if (!pieces || !piece_len || !workspace_bytes || num_sequences <= 0 || num_heads <= 0)
+                                                  int32_t* lead_len, int64_t* workspace_bytes) {
+  if (!pieces || !piece_len || !lead_len || !workspace_bytes || num_sequences <= 0 ||
+      num_heads <= 0)
     return FR2_ERR_INVALID_ARGUMENT;
   *pieces = 1;
   *piece_len = max_seqlen;
+  *lead_len = 0;
   *workspace_bytes = 0;
   const int64_t units = static_cast<int64_t>(num_sequences) * num_heads;
   if (head_size != 64 || max_seqlen < kChunkMinSeqlen || units > kSplitMaxUnits) return FR2_OK;
-  int P = static_cast<int>(std::min<int64_t>(256 / units, max_seqlen / kSplitMinPiece));
-  if (P < 3) return FR2_OK;
-  int len = (max_seqlen + P - 1) / P;
+  // pieces after the lead piece: one block per CU in each phase, and pieces
+  // of at least kSplitMinPiece tokens
+  const int Q = static_cast<int>(std::min<int64_t>(
+      256 / units,
+      static_cast<int64_t>(static_cast<float>(max_seqlen) / kSplitMinPiece - kSplitLeadRatio)));
+  if (Q < 2) return FR2_OK;
+  int len = static_cast<int>(max_seqlen / (Q + kSplitLeadRatio));
   len = (len + kSplitAlign - 1) / kSplitAlign * kSplitAlign;
-  P = (max_seqlen + len - 1) / len;
+  if (len < kSplitMinPiece) return FR2_OK;
+  int lead = max_seqlen - Q * len;
+  lead = (lead + kSplitAlign - 1) / kSplitAlign * kSplitAlign;
+  if (lead < len) lead = len;
+  // pieces the longest sequence actually has with these lengths
+  const int P = max_seqlen <= lead ? 1 : 2 + (max_seqlen - lead - 1) / len;
   if (P < 3 || static_cast<int64_t>(num_sequences) * P * 2 > 65535) return FR2_OK;
   *pieces = P;
   *piece_len = len;
+  *lead_len = lead;
   *workspace_bytes = fr2::split_workspace_floats(num_sequences, num_heads, P) * 4;
   return FR2_OK;
 }
@@ -145,8 +162,8 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_split(
     int32_t num_sequences, int32_t num_heads, int32_t head_size, int64_t total_tokens,
     int32_t max_seqlen, int32_t dtype, float* state, const void* r, const void* decay_logits,
     const void* decay_bias, const void* k, const void* v, const void* a, const void* b,
-    void* output, float scale, int32_t pieces, int32_t piece_len, void* workspace,
-    int64_t workspace_bytes, void* stream) {
+    void* output, float scale, int32_t pieces, int32_t piece_len, int32_t lead_len,
+    void* workspace, int64_t workspace_bytes, void* stream, void* aux_stream) {
   (void)max_seqlen;
   if (!query_start_loc || !state_indices || !status || !state || !workspace ||
       !tokens_ok(r, decay_logits, k, v, a, b, output))
@@ -168,9 +185,10 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_split(
   p.r = r; p.logits = decay_logits; p.bias = decay_bias; p.k = k; p.v = v; p.a = a; p.b = b;
   p.y = output;
   p.scale = scale;
-  return fr2::launch_chunked_split(dtype, p, num_sequences, pieces, piece_len,
+  return fr2::launch_chunked_split(dtype, p, num_sequences, pieces, piece_len, lead_len,
                                    static_cast<float*>(workspace),
-                                   static_cast<hipStream_t>(stream));
+                                   static_cast<hipStream_t>(stream),
+                                   static_cast<hipStream_t>(aux_stream));
 }
 
 extern "C" int fr2_wkv7_recurrent_fp16_forward(
@@ -310,7 +328,8 @@ extern "C" int fr2_wkv7_chunk_bf16_forward_split(
     uint16_t* state_bf16, const void* r, const void* decay_logits,
     const void* decay_bias, const void* k, const void* v, const void* a,
     const void* b, void* output, float scale, int32_t pieces, int32_t piece_len,
-    void* workspace, int64_t workspace_bytes, void* stream) {
+    int32_t lead_len, void* workspace, int64_t workspace_bytes, void* stream,
+    void* aux_stream) {
   (void)max_seqlen;
   if (!query_start_loc || !state_indices || !status || !state_bf16 || !workspace ||
       !tokens_ok(r, decay_logits, k, v, a, b, output))
@@ -335,8 +354,9 @@ extern "C" int fr2_wkv7_chunk_bf16_forward_split(
   p.y = output;
   p.scale = scale;
   return fr2::launch_chunked_split(FR2_DTYPE_BFLOAT16, p, num_sequences, pieces, piece_len,
-                                   static_cast<float*>(workspace),
-                                   static_cast<hipStream_t>(stream));
+                                   lead_len, static_cast<float*>(workspace),
+                                   static_cast<hipStream_t>(stream),
+                                   static_cast<hipStream_t>(aux_stream));
 }
 
 extern "C" int fr2_wkv7_rl_infctx_forward(

@@ -15,7 +15,7 @@ int record_launch() {
 }
 }  // namespace fr2
 
-extern "C" int fr2_abi_version(void) { return 100; }
+extern "C" int fr2_abi_version(void) { return 200; }
 
 extern "C" const char* fr2_status_string(int status) {
   switch (status) {

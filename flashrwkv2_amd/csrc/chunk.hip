@@ -536,12 +536,10 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
   // sequence split: which sequence, piece and (summary) kind this block is
   const int npc = p.split_pieces;
   int seq = seg, piece = 0;
-  if constexpr (kSum) {
-    seq = seg / (npc - 1);
-    piece = seg % (npc - 1);
-  } else if (npc > 0) {
-    seq = seg / npc;
-    piece = seg % npc;
+  if (kSum || npc > 0) {
+    const int cnt = p.split_count > 0 ? p.split_count : (kSum ? npc - 1 : npc);
+    seq = seg / cnt;
+    piece = p.split_first + seg % cnt;
   }
   if (p.status != nullptr) {
     if (p.status[0] != 0) {
@@ -557,14 +555,14 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
   bool last_piece = true;
   if (kSum || npc > 0) {
     const int q0 = p.bounds[seq], q1 = p.bounds[seq + 1];
-    const int len = q1 - q0;
-    const int last = len > 0 ? (len - 1) / p.split_len : 0;
+    int start, plen, last;
+    split_piece(p, q1 - q0, piece, start, plen, last);
     // pieces past the sequence's last have nothing to do; the summary pass
     // covers the pieces before the last only
     if (piece > last || (kSum && piece >= last)) return;
     last_piece = piece == last;
-    t0 = q0 + piece * p.split_len;
-    t1 = min(t0 + p.split_len, q1);
+    t0 = q0 + start;
+    t1 = min(t0 + plen, q1);
   } else if (p.uniform_len > 0) {
     t0 = seg * p.uniform_len;
     t1 = t0 + p.uniform_len;
@@ -607,7 +605,7 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
 #pragma unroll
           for (int e = 0; e < 4; ++e) S[kb][e] = (kb * 16 + 4 * q + e == vcol) ? 1.0f : 0.0f;
       }
-    } else if (npc > 0) {
+    } else if (npc > 0 && !(piece == 0 && p.split_lead_pass)) {
       const float* sin = p.split_state + pbase * D * D;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
@@ -715,8 +713,16 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
       write_out(ngroups - 1);
     }
     if (!last_piece) {
-      // a piece before the last hands on nothing: its successor started
-      // from the combined state
+      // a piece before the last hands on nothing (its successor starts from
+      // the combined state), except the lead pass's piece 0, whose end state
+      // is piece 1's start
+      if (p.split_lead_pass && piece == 0) {
+        float* sout = p.split_state + (pbase + H) * D * D;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
+      }
     } else if (p.state_out != nullptr) {
       float* sout = static_cast<float*>(p.state_out);
       uint16_t* soutb = static_cast<uint16_t*>(p.state_out);
@@ -865,10 +871,14 @@ int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen, hipStr
 
 namespace {
 
-// Start states of the pieces of a split sequence: S(0) = the slot state,
-// S(j+1) = Phi_j S(j) + F_j, written to split_state[n * pieces + j] (S(0)
-// too: the real pass's last piece overwrites the slot while its first piece
-// may not have read it yet, so every piece starts from this copy).
+// Start states of the pieces of a split sequence: S(j+1) = Phi_j S(j) + F_j,
+// written to split_state[n * pieces + j + 1].  Classic split (split_first
+// 0): S(0) = the slot state, also copied to split_state[n * pieces] (the real
+// pass's last piece overwrites the slot while its first piece may not have
+// read it yet, so every piece starts from this copy).  Lead split
+// (split_first 1): S(1) is piece 0's end state, already in
+// split_state[n * pieces + 1] from the lead pass.  The summaries of pieces
+// split_first.. are at index n * split_count + (j - split_first).
 // One 256-thread block per (head, sequence); thread t owns column t % 64 of
 // rows 16 (t / 64) .. +15.
 __global__ __launch_bounds__(256) void split_combine_kernel(SegArgs p) {
@@ -876,22 +886,32 @@ __global__ __launch_bounds__(256) void split_combine_kernel(SegArgs p) {
   __shared__ float st[D][D + 1];
   const int h = blockIdx.x, n = blockIdx.y, tid = threadIdx.x, H = p.num_heads;
   if (p.status != nullptr && (p.status[0] != 0 || n >= p.status[2])) return;
-  const int len = p.bounds[n + 1] - p.bounds[n];
-  const int last = len > 0 ? (len - 1) / p.split_len : 0;
+  int start, plen, last;
+  split_piece(p, p.bounds[n + 1] - p.bounds[n], 0, start, plen, last);
   const int c = tid & 63, r0 = (tid >> 6) * 16;
-  const int slot = p.slots ? p.slots[n] : n;
-  // the slot state: fp32, or (bf16-state contract) bf16 widened once
-  const int64_t s0 = (static_cast<int64_t>(slot) * H + h) * D * D;
-  const float* s0f = static_cast<const float*>(p.state_in) + s0;
-  const uint16_t* s0b = static_cast<const uint16_t*>(p.state_in) + s0;
-  float* out0 = p.split_state + (static_cast<int64_t>(n) * p.split_pieces * H + h) * D * D;
-  for (int r = r0; r < r0 + 16; ++r) {
-    st[r][c] = p.state_bf16 ? IoBF16::to_f32(s0b[r * D + c]) : s0f[r * D + c];
-    out0[r * D + c] = st[r][c];
+  const int j0 = p.split_first;
+  if (j0 == 0) {
+    const int slot = p.slots ? p.slots[n] : n;
+    // the slot state: fp32, or (bf16-state contract) bf16 widened once
+    const int64_t s0 = (static_cast<int64_t>(slot) * H + h) * D * D;
+    const float* s0f = static_cast<const float*>(p.state_in) + s0;
+    const uint16_t* s0b = static_cast<const uint16_t*>(p.state_in) + s0;
+    float* out0 = p.split_state + (static_cast<int64_t>(n) * p.split_pieces * H + h) * D * D;
+    for (int r = r0; r < r0 + 16; ++r) {
+      st[r][c] = p.state_bf16 ? IoBF16::to_f32(s0b[r * D + c]) : s0f[r * D + c];
+      out0[r * D + c] = st[r][c];
+    }
+  } else {
+    // pieces 0 and 1 need no combined start: the lead pass handed piece 1 its
+    // start directly
+    if (last <= 1) return;
+    const float* s1 =
+        p.split_state + ((static_cast<int64_t>(n) * p.split_pieces + 1) * H + h) * D * D;
+    for (int r = r0; r < r0 + 16; ++r) st[r][c] = s1[r * D + c];
   }
-  const int np1 = p.split_pieces - 1;
-  for (int j = 0; j < last; ++j) {
-    const int64_t pair = static_cast<int64_t>(n) * np1 + j;
+  const int cnt = p.split_count > 0 ? p.split_count : p.split_pieces - 1;
+  for (int j = j0; j < last; ++j) {
+    const int64_t pair = static_cast<int64_t>(n) * cnt + (j - j0);
     const float* f = p.split_summary + ((pair * 2) * H + h) * D * D;
     const float* ph = p.split_summary + ((pair * 2 + 1) * H + h) * D * D;
     for (int r = r0; r < r0 + 16; ++r) phi[r][c] = ph[r * D + c];
@@ -921,32 +941,79 @@ int64_t split_workspace_floats(int nseg, int H, int pieces) {
   return static_cast<int64_t>(nseg) * (3 * pieces - 2) * H * D * D;
 }
 
+namespace {
+
+template <class Io>
+void launch_split_kernels(const SegArgs& p, int nseg, int pieces, hipStream_t s,
+                          hipStream_t aux) {
+  const int H = p.num_heads;
+  if (p.split_lead <= 0) {
+    // classic: summaries of pieces 0..P-2, combine from the slot, every piece
+    const dim3 gsum(H, nseg * (pieces - 1)), gcomb(H, nseg), greal(H, nseg * pieces);
+    hipLaunchKernelGGL((chunk64_kernel<Io, false, false, true>), gsum, dim3(NT_SUM), 0, s, p);
+    hipLaunchKernelGGL(split_combine_kernel, gcomb, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((chunk64_kernel<Io, false>), greal, dim3(NT), 0, s, p);
+    return;
+  }
+  // lead: piece 0 (from the slot) on the aux stream, concurrently with the
+  // summaries of pieces 1..P-2; then the combine from piece 0's end state and
+  // pieces 1..P-1
+  hipEvent_t fork = nullptr, join = nullptr;
+  if (aux != nullptr) {
+    if (hipEventCreateWithFlags(&fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&join, hipEventDisableTiming) != hipSuccess ||
+        hipEventRecord(fork, s) != hipSuccess || hipStreamWaitEvent(aux, fork, 0) != hipSuccess)
+      aux = nullptr;   // fall back to one stream (same results, no overlap)
+  }
+  const hipStream_t s_lead = aux != nullptr ? aux : s;
+  SegArgs pl = p;
+  pl.split_first = 0;
+  pl.split_count = 1;
+  pl.split_lead_pass = true;
+  hipLaunchKernelGGL((chunk64_kernel<Io, false>), dim3(H, nseg), dim3(NT), 0, s_lead, pl);
+  SegArgs ps = p;
+  ps.split_first = 1;
+  ps.split_count = pieces - 2;
+  if (pieces > 2)
+    hipLaunchKernelGGL((chunk64_kernel<Io, false, false, true>), dim3(H, nseg * (pieces - 2)),
+                       dim3(NT_SUM), 0, s, ps);
+  if (aux != nullptr) {
+    if (hipEventRecord(join, aux) != hipSuccess || hipStreamWaitEvent(s, join, 0) != hipSuccess)
+      hipStreamSynchronize(aux);   // cannot order the streams: wait on the host
+  }
+  if (pieces > 2) hipLaunchKernelGGL(split_combine_kernel, dim3(H, nseg), dim3(256), 0, s, ps);
+  SegArgs pr = p;
+  pr.split_first = 1;
+  pr.split_count = pieces - 1;
+  hipLaunchKernelGGL((chunk64_kernel<Io, false>), dim3(H, nseg * (pieces - 1)), dim3(NT), 0, s,
+                     pr);
+  // destroying an event with pending waits is legal: the runtime keeps it
+  // until they complete
+  if (fork != nullptr) hipEventDestroy(fork);
+  if (join != nullptr) hipEventDestroy(join);
+}
+
+}  // namespace
+
 int launch_chunked_split(int dtype, SegArgs p, int nseg, int pieces, int piece_len,
-                         float* workspace, hipStream_t s) {
+                         int lead_len, float* workspace, hipStream_t s, hipStream_t aux) {
   if (p.sa_out != nullptr || p.boundary != nullptr || p.reverse ||
       p.uniform_len > 0 || p.ends != nullptr || p.chunk_offsets != nullptr)
     return FR2_ERR_UNSUPPORTED;
-  if (pieces < 2 || piece_len <= 0 || piece_len % GT != 0 || workspace == nullptr ||
-      p.state_in == nullptr || p.state_out != p.state_in ||
-      static_cast<int64_t>(nseg) * pieces > 65535)
+  if (pieces < 2 || piece_len <= 0 || piece_len % GT != 0 || lead_len < 0 ||
+      lead_len % GT != 0 || workspace == nullptr || p.state_in == nullptr ||
+      p.state_out != p.state_in || static_cast<int64_t>(nseg) * pieces > 65535)
     return FR2_ERR_INVALID_ARGUMENT;
+  if (dtype != FR2_DTYPE_BFLOAT16 && dtype != FR2_DTYPE_FLOAT16) return FR2_ERR_UNSUPPORTED;
   p.split_pieces = pieces;
   p.split_len = piece_len;
+  p.split_lead = lead_len;
   p.split_summary = workspace;
   p.split_state = workspace + static_cast<int64_t>(nseg) * (pieces - 1) * 2 * p.num_heads * D * D;
-  const dim3 gsum(p.num_heads, nseg * (pieces - 1)), gcomb(p.num_heads, nseg),
-      greal(p.num_heads, nseg * pieces);
-  if (dtype == FR2_DTYPE_BFLOAT16) {
-    hipLaunchKernelGGL((chunk64_kernel<IoBF16, false, false, true>), gsum, dim3(NT_SUM), 0, s, p);
-    hipLaunchKernelGGL(split_combine_kernel, gcomb, dim3(256), 0, s, p);
-    hipLaunchKernelGGL((chunk64_kernel<IoBF16, false>), greal, dim3(NT), 0, s, p);
-  } else if (dtype == FR2_DTYPE_FLOAT16) {
-    hipLaunchKernelGGL((chunk64_kernel<IoF16, false, false, true>), gsum, dim3(NT_SUM), 0, s, p);
-    hipLaunchKernelGGL(split_combine_kernel, gcomb, dim3(256), 0, s, p);
-    hipLaunchKernelGGL((chunk64_kernel<IoF16, false>), greal, dim3(NT), 0, s, p);
-  } else {
-    return FR2_ERR_UNSUPPORTED;
-  }
+  if (dtype == FR2_DTYPE_BFLOAT16)
+    launch_split_kernels<IoBF16>(p, nseg, pieces, s, aux);
+  else
+    launch_split_kernels<IoF16>(p, nseg, pieces, s, aux);
   return record_launch();
 }
 

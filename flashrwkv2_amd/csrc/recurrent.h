@@ -68,7 +68,28 @@ struct SegArgs {
   int split_len = 0;
   float* split_state = nullptr;
   float* split_summary = nullptr;
+  // Pipelined ("lead") split: piece 0 has split_lead tokens (0: split_len)
+  // and pieces j >= 1 cover [q0 + lead + (j-1)*split_len, ...).  A launch's
+  // grid covers pieces split_first .. split_first + split_count - 1 of every
+  // sequence (split_count 0: every piece, or every piece but the last in the
+  // summary pass).  split_lead_pass: piece 0 starts from the slot state and,
+  // unless it is the sequence's last piece, hands its end state to
+  // split_state[n * split_pieces + 1].
+  int split_lead = 0;
+  int split_first = 0;
+  int split_count = 0;
+  bool split_lead_pass = false;
 };
+
+// Token range [start, start + len) of piece j of a split sequence of n
+// tokens, and the index of the sequence's last piece.
+__host__ __device__ inline void split_piece(const SegArgs& p, int n, int j, int& start,
+                                            int& len, int& last) {
+  const int lead = p.split_lead > 0 ? p.split_lead : p.split_len;
+  last = n <= lead ? 0 : 1 + (n - lead - 1) / p.split_len;
+  start = j == 0 ? 0 : lead + (j - 1) * p.split_len;
+  len = j == 0 ? lead : p.split_len;
+}
 
 int launch_serial(int D, int dtype, bool bf16_state, const SegArgs& p, int nseg,
                   hipStream_t s);
@@ -82,11 +103,13 @@ int launch_fp16_state(int D, const SegArgs& p, int nseg, int max_seqlen, int32_t
 int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen,
                    hipStream_t s);
 // Sequence-split chunked prefill (D = 64, fp32 state, plain contract):
-// `pieces` pieces of `piece_len` tokens per sequence.  workspace holds
-// split_workspace_floats(nseg, H, pieces) floats.
+// `pieces` pieces per sequence, of `piece_len` tokens except piece 0, which
+// has lead_len tokens when lead_len > 0 (the pipelined split: piece 0 runs on
+// `aux` concurrently with the summary pass; aux null runs it on s).
+// workspace holds split_workspace_floats(nseg, H, pieces) floats.
 int64_t split_workspace_floats(int nseg, int H, int pieces);
 int launch_chunked_split(int dtype, SegArgs p, int nseg, int pieces, int piece_len,
-                         float* workspace, hipStream_t s);
+                         int lead_len, float* workspace, hipStream_t s, hipStream_t aux);
 
 // Training backward of the [B,T,H,D] zero-state path: bf16 token tensors and
 // gradients, the forward's fp32 boundary [B,H,T/16,D,D] and state_dot_a

@@ -124,30 +124,40 @@ int fr2_wkv7_recurrent_fp32_forward_kernel(
 /*
  * Sequence-split plan for the chunked prefill (head_size 64).  With few
  * (sequence, head) units one block per unit leaves most of the GPU idle; the
- * plan cuts every sequence into *pieces pieces of *piece_len tokens (a
- * multiple of 32; the last piece of a sequence is shorter) and reports the
- * device workspace fr2_wkv7_recurrent_fp32_forward_split needs.  *pieces is
- * 1 when splitting does not pay (fewer than three pieces of 256/units, or
- * pieces shorter than 1024 tokens).  No reference counterpart: the reference runs one CUDA block
- * per (sequence, head) in launch_recurrent_fp32
+ * plan cuts every sequence into up to *pieces pieces: piece 0 of *lead_len
+ * tokens, the others of *piece_len tokens (multiples of 32; a sequence's last
+ * piece is shorter), and reports the device workspace
+ * fr2_wkv7_recurrent_fp32_forward_split needs.  The plan is the pipelined
+ * split (see below): 256/units + 1 pieces, piece 0 about 1.2x the others.
+ * *pieces is 1 when splitting does not pay (more than 128 units, or pieces
+ * shorter than 1024 tokens).  No reference counterpart: the reference runs
+ * one CUDA block per (sequence, head) in launch_recurrent_fp32
  * (csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:393-453).
  */
 int fr2_wkv7_recurrent_fp32_split_plan(int32_t num_sequences, int32_t num_heads,
                                        int32_t head_size, int32_t max_seqlen,
                                        int32_t* pieces, int32_t* piece_len,
-                                       int64_t* workspace_bytes);
+                                       int32_t* lead_len, int64_t* workspace_bytes);
 
 /*
  * fr2_wkv7_recurrent_fp32_forward with the sequence split of a plan (same
- * results within fp32 rounding): a summary pass computes each piece's
- * zero-start final state F and its transition Phi (identity start, V = 0),
- * a combine kernel chains S(j+1) = Phi_j S(j) + F_j from the slot state, and
- * the chunked kernel then runs every piece from its start state; the last
- * piece of each sequence writes the slot.  workspace: device memory of at
- * least the plan's workspace_bytes, owned by the caller, not read after the
- * call's kernels finish.  Replaces, for long sequences, the single-block-
- * per-(sequence, head) launch of tmix_wkv7_recurrent_fp32_from_decay_logits
- * (…fp32io16_forward_varlen.cpp:330-387).
+ * results within fp32 rounding).  A summary pass computes a piece's
+ * zero-start final state F and its transition Phi (identity start, V = 0), a
+ * combine kernel chains S(j+1) = Phi_j S(j) + F_j, and the chunked kernel
+ * runs each piece from its start state; the last piece of each sequence
+ * writes the slot.
+ *   lead_len == 0 (classic): pieces of piece_len tokens; summaries of pieces
+ *     0..P-2, the chain starts from the slot state, then every piece runs.
+ *   lead_len > 0 (pipelined): piece 0 has lead_len tokens and runs from the
+ *     slot state on aux_stream, concurrently with the summaries of pieces
+ *     1..P-2 on stream (events order the two streams; under graph capture
+ *     aux_stream joins the capture); the chain starts from piece 0's end
+ *     state, then pieces 1..P-1 run.  aux_stream NULL runs piece 0 on stream
+ *     too (same results, no overlap).
+ * workspace: device memory of at least the plan's workspace_bytes, owned by
+ * the caller, not read after the call's kernels finish.  Replaces, for long
+ * sequences, the single-block-per-(sequence, head) launch of
+ * tmix_wkv7_recurrent_fp32_from_decay_logits (…fp32io16_forward_varlen.cpp:330-387).
  */
 int fr2_wkv7_recurrent_fp32_forward_split(
     const int32_t* query_start_loc, const int32_t* state_indices,
@@ -156,7 +166,8 @@ int fr2_wkv7_recurrent_fp32_forward_split(
     float* state, const void* r, const void* decay_logits,
     const void* decay_bias, const void* k, const void* v, const void* a,
     const void* b, void* output, float scale, int32_t pieces, int32_t piece_len,
-    void* workspace, int64_t workspace_bytes, void* stream);
+    int32_t lead_len, void* workspace, int64_t workspace_bytes, void* stream,
+    void* aux_stream);
 
 /*
  * Packed varlen recurrence with an FP16 state pool [slots,H,D,D] updated in
@@ -247,9 +258,10 @@ int fr2_wkv7_chunk_bf16_forward(
 
 /*
  * fr2_wkv7_chunk_bf16_forward with the sequence split of
- * fr2_wkv7_recurrent_fp32_split_plan (head_size 64): the same three passes as
- * fr2_wkv7_recurrent_fp32_forward_split, the bf16 slot state widened once by
- * the combine kernel and rounded once by each sequence's last piece.  Replaces,
+ * fr2_wkv7_recurrent_fp32_split_plan (head_size 64): the same passes, classic
+ * or pipelined, as fr2_wkv7_recurrent_fp32_forward_split; the bf16 slot state
+ * is widened once (by the combine kernel, or by piece 0 in the pipelined
+ * split) and rounded once by each sequence's last piece.  Replaces,
  * for few long sequences, the one-block-per-(sequence, head) launch of
  * infer_tmix_wkv7_chunk_bf16_forward_varlen_cuda
  * (…/infer_chunk_bf16_forward_varlen.cu:276-340).
@@ -261,7 +273,8 @@ int fr2_wkv7_chunk_bf16_forward_split(
     uint16_t* state_bf16, const void* r, const void* decay_logits,
     const void* decay_bias, const void* k, const void* v, const void* a,
     const void* b, void* output, float scale, int32_t pieces, int32_t piece_len,
-    void* workspace, int64_t workspace_bytes, void* stream);
+    int32_t lead_len, void* workspace, int64_t workspace_bytes, void* stream,
+    void* aux_stream);
 
 /*
  * RL/Infctx fp32-state chunked forward over chunk metadata

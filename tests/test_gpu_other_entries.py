@@ -181,7 +181,7 @@ def test_chunk_bf16_long_requests_on_the_chunked_kernel():
     assert_state_close(pool2[active], pool_ref[active], rmse=4e-3, fro=4e-3)
 
 
-@pytest.mark.parametrize("pieces", [2, 3])
+@pytest.mark.parametrize("pieces", [2, 3, (3, 320), (2, 96)])
 def test_chunk_bf16_sequence_split(monkeypatch, pieces):
     """The bf16-state chunk entry with the sequence split forced (summary
     pass, combine from the widened bf16 slot state, pieces; each sequence's
@@ -421,7 +421,7 @@ def test_backend_is_the_in_tree_hip_library():
 
     assert flashrwkv2_amd._C is not None
     lib = _native.load()
-    assert lib.fr2_abi_version() == 100
+    assert lib.fr2_abi_version() == 200
     with open("/proc/self/maps") as fh:
         maps = fh.read()
     assert str(_native.LIB_PATH) in maps or _native.LIB_PATH.name in maps

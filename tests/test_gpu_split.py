@@ -3,7 +3,9 @@
 A split run cuts every sequence into pieces: a summary pass computes each
 piece's zero-start final state F and transition Phi, a combine kernel chains
 S(j+1) = Phi_j S(j) + F_j, and the chunked kernel runs the pieces from those
-start states.  The results must match the fp64 oracle on exactly the
+start states.  The classic split (equal pieces) chains from the slot state;
+the pipelined split runs piece 0 (its own length) from the slot state on a
+second stream next to the summary pass and chains from its end state.  The results must match the fp64 oracle on exactly the
 kernel's inputs with the same gates as the unsplit kernels (relative RMSE
 2e-3 from tests/fixtures/tolerances-v1.json:9-12 of the reference, plus
 |dy| <= 2e-2 max(1, |y|) and ||dS|| / ||S|| <= 1e-3 per (slot, head)), and
@@ -61,6 +63,12 @@ def _close_to_unsplit(y_split, y_chunk, p_split, p_chunk, active):
     ((700, 64, 1, 129, 1024), 4),       # sequences of 1..4 pieces, ragged last pieces
     ((2000, 33), 3),
     ((96, 96, 96), 3),                  # pieces of 32 tokens
+    # pipelined split: (pieces, piece 0's length)
+    ((1024,), (2, 512)),                # no summary pass, no combine
+    ((1024,), (4, 352)),
+    ((700, 64, 1, 129, 1024), (4, 320)),   # sequences ending inside piece 0 and later
+    ((2000, 33), (3, 1024)),
+    ((96, 96, 96), (3, 32)),
 ])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_split_matches_oracle_and_unsplit(lengths, pieces, dtype):
@@ -92,7 +100,10 @@ def test_public_call_splits_a_long_single_sequence():
     C = require_gpu()
     from flashrwkv2_amd import _C as CC
 
-    assert CC.split_plan(1, 4, 64, 8192)[:2] == (8, 1024)
+    pieces, plen, lead, _ = CC.split_plan(1, 4, 64, 8192)
+    assert pieces >= 3 and plen >= 1024 and lead >= plen and lead % 32 == 0 == plen % 32
+    assert lead + (pieces - 2) * plen < 8192 <= lead + (pieces - 1) * plen
+    assert CC.split_plan(1, 64, 64, 65536)[:3] == (5, 12608, 15104)   # config 4
     assert CC.split_plan(8, 32, 64, 4096)[0] == 1      # config 1: 256 units, no split
     case = make_case(dtype=torch.bfloat16, head_size=64, lengths=(8192,), num_heads=4,
                      seed=7)
@@ -115,11 +126,13 @@ def test_split_fails_closed_on_invalid_metadata():
     slots = torch.tensor([0], device="cuda", dtype=torch.int32)
     out = torch.zeros_like(case["v"])
     before = pool.clone()
-    C.tmix_wkv7_recurrent_fp32_kernel_forced(SPLIT, bad_cu, slots, pool, *tokens(case), out,
-                                             1.0, None, None, split_pieces=4)
-    torch.cuda.synchronize()
-    assert torch.isnan(out.float()).all()
-    assert torch.equal(pool, before)
+    for pieces in (4, (4, 640)):
+        out.zero_()
+        C.tmix_wkv7_recurrent_fp32_kernel_forced(SPLIT, bad_cu, slots, pool, *tokens(case),
+                                                 out, 1.0, None, None, split_pieces=pieces)
+        torch.cuda.synchronize()
+        assert torch.isnan(out.float()).all()
+        assert torch.equal(pool, before)
 
 
 @pytest.mark.cuda_graph

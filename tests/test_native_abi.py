@@ -41,7 +41,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_version_and_status_strings(lib):
-    assert lib.fr2_abi_version() == 100
+    assert lib.fr2_abi_version() == 200
     assert lib.fr2_status_string(N.FR2_OK) == b"ok"
     assert lib.fr2_status_string(N.FR2_ERR_INVALID_ARGUMENT) == b"invalid argument"
     assert lib.fr2_status_string(N.FR2_ERR_UNSUPPORTED) == b"unsupported configuration"
