@@ -115,10 +115,13 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kernel(
 // summary block costs ~1.3x a real block per token when the two run side by
 // side (config 4: 96 vs 73 ns per token), but the lead piece's block also
 // slows down next to it; piece 0 gets 1.2x the tokens of the others (the
-// best of 1.15x-1.33x measured at config 4); Q is also capped so that pieces keep at least
-// 1024 tokens.  Split only when Q >= 2 (at most 128 units).
+// best of 1.15x-1.33x measured at config 4).  Q is also capped so that
+// pieces keep at least 384 tokens: shorter pieces lose to the fixed cost of
+// the extra passes (1024 tokens on 32 units: 3 pieces 0.095 ms, unsplit
+// 0.083 ms; 2048 tokens: 5 pieces 0.120 ms, unsplit 0.164 ms).  Split only
+// when Q >= 2 (at most 128 units).
 constexpr int kSplitMaxUnits = 128;
-constexpr int kSplitMinPiece = 1024;
+constexpr int kSplitMinPiece = 384;
 constexpr int kSplitAlign = 32;
 constexpr float kSplitLeadRatio = 1.2f;
 

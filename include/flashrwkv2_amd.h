@@ -130,7 +130,7 @@ int fr2_wkv7_recurrent_fp32_forward_kernel(
  * fr2_wkv7_recurrent_fp32_forward_split needs.  The plan is the pipelined
  * split (see below): 256/units + 1 pieces, piece 0 about 1.2x the others.
  * *pieces is 1 when splitting does not pay (more than 128 units, or pieces
- * shorter than 1024 tokens).  No reference counterpart: the reference runs
+ * shorter than 384 tokens).  No reference counterpart: the reference runs
  * one CUDA block per (sequence, head) in launch_recurrent_fp32
  * (csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:393-453).
  */

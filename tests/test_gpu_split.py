@@ -96,12 +96,12 @@ def test_split_matches_oracle_and_unsplit(lengths, pieces, dtype):
 
 def test_public_call_splits_a_long_single_sequence():
     """B = 1 prefill (4 heads): the public entry takes the split by itself
-    (the plan gives 8 pieces of 1024 tokens) and matches the oracle."""
+    (the plan cuts it into pieces of at least 384 tokens) and matches the oracle."""
     C = require_gpu()
     from flashrwkv2_amd import _C as CC
 
     pieces, plen, lead, _ = CC.split_plan(1, 4, 64, 8192)
-    assert pieces >= 3 and plen >= 1024 and lead >= plen and lead % 32 == 0 == plen % 32
+    assert pieces >= 3 and plen >= 384 and lead >= plen and lead % 32 == 0 == plen % 32
     assert lead + (pieces - 2) * plen < 8192 <= lead + (pieces - 1) * plen
     assert CC.split_plan(1, 64, 64, 65536)[:3] == (5, 12608, 15104)   # config 4
     assert CC.split_plan(8, 32, 64, 4096)[0] == 1      # config 1: 256 units, no split
@@ -157,7 +157,7 @@ def test_split_under_graph_capture_with_live_metadata():
     n_seq = torch.full((1,), 2, device=dev, dtype=torch.int32)
     live = dict(state_pool_size=slots_n, token_capacity=4000, sequence_capacity=2,
                 max_seqlen_capacity=4000, num_active_tokens=n_tok, num_active_sequences=n_seq)
-    assert CC.split_plan(2, 2, 64, 4000)[0] == 3           # the capacity plan splits
+    assert CC.split_plan(2, 2, 64, 4000)[0] >= 3           # the capacity plan splits
     y_ref, pool_ref = oracle_expect(case)
     active = case["state_indices"].long()
     stream = torch.cuda.Stream()
