@@ -650,6 +650,12 @@ def device_info(torch) -> dict:
     props = torch.cuda.get_device_properties(0)
     info = {"name": props.name, "arch": getattr(props, "gcnArchName", ""),
             "cus": props.multi_processor_count}
+    # under a profiler (its library preloaded, the GPU initialised before
+    # main) a child that execs another interpreter is refused: skip the tool
+    profiled = any(k.startswith("ROCPROF") for k in os.environ) or \
+        "rocprof" in os.environ.get("LD_PRELOAD", "")
+    if profiled:
+        return info
     try:
         out = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True, text=True,
                              timeout=20).stdout
