@@ -422,7 +422,8 @@ def time_chunk_bf16_state(torch, flashrwkv2_amd, w, steps: int):
         return fn(*w.tokens, state_pool=pool, cu_seqlens=w.cu_seqlens,
                   state_indices=w.state_indices, validated_metadata=ticket)
 
-    call()
+    for _ in range(20):   # warm-up: the first calls after the decode legs run slower
+        call()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
