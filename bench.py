@@ -422,7 +422,9 @@ def time_chunk_bf16_state(torch, flashrwkv2_amd, w, steps: int):
         return fn(*w.tokens, state_pool=pool, cu_seqlens=w.cu_seqlens,
                   state_indices=w.state_indices, validated_metadata=ticket)
 
-    for _ in range(20):   # warm-up: the first calls after the decode legs run slower
+    # warm-up as long as the prefill leg's (~70 ms): after the short decode
+    # legs the clocks need that long to come back up
+    for _ in range(200):
         call()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
