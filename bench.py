@@ -407,6 +407,111 @@ def time_varlen(torch, flashrwkv2_amd, steps: int):
     return out
 
 
+def _events_ms(torch, fn, launches: int, warmup: int = 5) -> float:
+    """Average duration (ms) of `fn` over `launches` back-to-back calls on the
+    current stream, HIP events on both sides (and the wall clock, whichever
+    is longer)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(launches):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return max(start.elapsed_time(end), (time.perf_counter() - t0) * 1e3) / launches
+
+
+VALU_FP32_PEAK_TFLOPS = 157.3      # vendor figure (packed fp32)
+FLOPS_PER_TOKEN_HEAD = 5 * 64 * 64 * 2   # recurrence form: 5 x D x D FMA
+
+
+def time_other_paths(torch, flashrwkv2_amd, w, steps: int):
+    """The remaining forward paths on the config-1 batch, through the C ABI
+    on the current stream: the token-serial kernel forced (what D = 128/256
+    and mid-length sequences run), and the rl_infctx forward (chunk list of
+    16-token chunks, one block per sequence) and its backward replay (every
+    chunk from its start-of-chunk state, sa written)."""
+    from flashrwkv2_amd import _native as N
+    from flashrwkv2_amd.tmix.wkv7.rl_infctx import _make_chunk_metadata
+
+    lib = N.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    B, H, T = w.state_indices.numel(), w.num_heads, w.total_tokens
+    toks = [t.data_ptr() for t in w.tokens]
+    out = torch.empty_like(w.v)
+    ticket = flashrwkv2_amd.prepare_tmix_wkv7_recurrent_metadata(
+        w.cu_seqlens, w.state_indices, total_tokens=T, state_pool_size=B)
+    state = torch.zeros((B, H, 64, 64), device="cuda", dtype=torch.float32)
+    meta = (ticket._query_start_loc_snapshot().data_ptr(),
+            ticket._state_indices_snapshot().data_ptr(), ticket._status().data_ptr())
+
+    def serial():
+        N.check(lib.fr2_wkv7_recurrent_fp32_forward_kernel(
+            N.KERNEL_SERIAL, *meta, B, H, 64, T, ticket._max_seqlen(), N.FR2_DTYPE_BFLOAT16,
+            state.data_ptr(), toks[0], toks[1], None, *toks[2:], out.data_ptr(), 1.0, stream),
+            "serial")
+
+    offsets = w.cu_seqlens.cpu().tolist()
+    seq_chunks, starts, ends = _make_chunk_metadata(offsets, 16, w.r.device)
+    nchunks = starts.numel()
+
+    def rl_forward():
+        N.check(lib.fr2_wkv7_rl_infctx_forward(
+            seq_chunks.data_ptr(), starts.data_ptr(), ends.data_ptr(), B, nchunks, H, 64, T,
+            max(hi - lo for lo, hi in zip(offsets[:-1], offsets[1:])), 16, 1,
+            N.FR2_DTYPE_BFLOAT16, state.data_ptr(), toks[0], toks[1], None, *toks[2:],
+            out.data_ptr(), 1.0, stream), "rl_infctx forward")
+
+    g = torch.Generator(device="cuda").manual_seed(5)
+    boundary = torch.randn((nchunks, H, 64, 64), device="cuda", generator=g) * 0.1
+    sa = torch.empty((T, H, 64), device="cuda", dtype=torch.float32)
+
+    def rl_replay():
+        N.check(lib.fr2_wkv7_rl_infctx_replay(
+            starts.data_ptr(), ends.data_ptr(), nchunks, H, 64, T, N.FR2_DTYPE_BFLOAT16,
+            boundary.data_ptr(), toks[0], toks[1], None, *toks[2:], out.data_ptr(),
+            sa.data_ptr(), 1.0, stream), "rl_infctx replay")
+
+    n = max(5, steps // 2)
+    s_ms = _events_ms(torch, serial, n)
+    f_ms = _events_ms(torch, rl_forward, n)
+    r_ms = _events_ms(torch, rl_replay, n)
+    io = T * H * BYTES_PER_TOKEN_HEAD
+    flops = T * H * FLOPS_PER_TOKEN_HEAD
+    replay_bytes = io + T * H * 64 * 4 + nchunks * H * STATE_BYTES   # + sa, + boundary reads
+    out_obj = {
+        "workload": w.name,
+        "token_serial": {
+            "kernel": "serial_kernel<64,IoBF16,StF32>", "kernel_ms": round(s_ms, 4),
+            "tokens_per_s": round(T / (s_ms * 1e-3), 1),
+            "roofline": roofline_obj(io + 2 * B * H * STATE_BYTES, s_ms),
+            "valu": {"achieved_tflops": round(flops / (s_ms * 1e-3) / 1e12, 2),
+                     "peak_tflops": VALU_FP32_PEAK_TFLOPS,
+                     "frac": round(flops / (s_ms * 1e-3) / 1e12 / VALU_FP32_PEAK_TFLOPS, 4),
+                     "flops_per_token_head": FLOPS_PER_TOKEN_HEAD},
+        },
+        "rl_infctx_forward": {
+            "kernel": "chunk64_kernel<IoBF16,false> over each sequence's chunk list",
+            "chunk_size": 16, "kernel_ms": round(f_ms, 4),
+            "tokens_per_s": round(T / (f_ms * 1e-3), 1),
+            "roofline": roofline_obj(io + 2 * B * H * STATE_BYTES, f_ms),
+        },
+        "rl_infctx_replay": {
+            "kernel": "serial_kernel<64,IoBF16,StF32> per 16-token chunk (sa written)",
+            "chunks": nchunks, "kernel_ms": round(r_ms, 4),
+            "tokens_per_s": round(T / (r_ms * 1e-3), 1),
+            "roofline": roofline_obj(replay_bytes, r_ms), "algorithmic_bytes": replay_bytes,
+        },
+    }
+    del boundary, sa, out, state
+    torch.cuda.empty_cache()
+    return out_obj
+
+
 def time_chunk_bf16_state(torch, flashrwkv2_amd, w, steps: int):
     """The bf16-state chunk entry (infer_tmix_wkv7_chunk_bf16_forward_varlen)
     on a config-1-shaped batch with a bf16 state pool: public calls with a
@@ -804,6 +909,8 @@ def main() -> int:
     if args.only in (None, "prefill") and args.config == 1 and pre is not None:
         result["chunk_bf16_state"] = time_chunk_bf16_state(torch, flashrwkv2_amd, pre.w,
                                                            max(5, args.steps // 2))
+    if args.only in (None, "prefill") and args.config == 1 and pre is not None:
+        result["other_paths"] = time_other_paths(torch, flashrwkv2_amd, pre.w, args.steps)
     if args.only in (None, "long") and args.config == 1:
         result["varlen_prefill"] = time_varlen(torch, flashrwkv2_amd, max(5, args.steps // 2))
         result["long_context"] = time_long_context(torch, flashrwkv2_amd, max(4, args.steps // 4))
