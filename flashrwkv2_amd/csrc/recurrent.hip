@@ -49,9 +49,11 @@ __device__ __forceinline__ bool check_status(const SegArgs& p, int seg,
 }
 
 // ---------------------------------------------------------------------------
-// Token-serial kernel.  One workgroup of 4*D threads per (segment, head).
+// Token-serial kernel.  One workgroup of KS*D threads per (segment, head).
 // Thread (q, v) = (tid / D, tid % D) owns state column v for the key rows
-// [q*R, q*R+R), R = D/4, in registers for the whole segment.  Inputs are
+// [q*R, q*R+R), R = D/KS, in registers for the whole segment.  KS = 4, or 8
+// when the launch has at most one workgroup per CU (half the serial work per
+// wave per token, two waves per SIMD; D = 64 and 128).  Inputs are
 // staged TT = 1024/D tokens at a time through LDS as fp32 (the retention is
 // computed once while staging).  The sa reduction over the 4 key quarters goes
 // through a double-buffered LDS array (one barrier per token); the y partials
@@ -62,11 +64,10 @@ __device__ __forceinline__ bool check_status(const SegArgs& p, int seg,
 // S + S*delta + b*sa + k*v evaluated in fp32 and rounded to fp16 after every
 // token (the state registers always hold fp16 values), and y is read from
 // the rounded state (csrc/sm120/tmix/wkv7/infer_recurrent_fp16_forward_varlen.cu:243-336).
-template <int D, class Io, class St>
-__global__ __launch_bounds__(4 * D) void serial_kernel(SegArgs p) {
+template <int D, class Io, class St, int KS = 4>
+__global__ __launch_bounds__(KS * D) void serial_kernel(SegArgs p) {
   constexpr bool kAlbatross = __is_same(St, StF16);
   using raw = typename Io::raw;
-  constexpr int KS = 4;
   constexpr int NT = KS * D;
   constexpr int R = D / KS;
   constexpr int TT = 1024 / D;
@@ -372,15 +373,27 @@ __global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
 // ---------------------------------------------------------------------------
 // Host-side launch helpers.
 // ---------------------------------------------------------------------------
+constexpr int64_t kSerialWideUnits = 256;
+
 template <class Io, class St>
 static int launch_serial_io(int D, const SegArgs& p, int nseg, hipStream_t s) {
   const dim3 grid(p.num_heads, nseg);
+  // at most one workgroup per CU: split the key rows 8 ways (config-1 batch
+  // at D = 64: 2.17 vs 2.61 ms); with more workgroups the 4-way split packs
+  // better (2 048 units of 100 tokens: 0.239 vs 0.292 ms)
+  const bool wide = static_cast<int64_t>(p.num_heads) * nseg <= kSerialWideUnits;
   switch (D) {
     case 64:
-      hipLaunchKernelGGL((serial_kernel<64, Io, St>), grid, dim3(256), 0, s, p);
+      if (wide)
+        hipLaunchKernelGGL((serial_kernel<64, Io, St, 8>), grid, dim3(512), 0, s, p);
+      else
+        hipLaunchKernelGGL((serial_kernel<64, Io, St>), grid, dim3(256), 0, s, p);
       break;
     case 128:
-      hipLaunchKernelGGL((serial_kernel<128, Io, St>), grid, dim3(512), 0, s, p);
+      if (wide)
+        hipLaunchKernelGGL((serial_kernel<128, Io, St, 8>), grid, dim3(1024), 0, s, p);
+      else
+        hipLaunchKernelGGL((serial_kernel<128, Io, St>), grid, dim3(512), 0, s, p);
       break;
     case 256:
       hipLaunchKernelGGL((serial_kernel<256, Io, St>), grid, dim3(1024), 0, s, p);
