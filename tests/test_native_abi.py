@@ -90,3 +90,50 @@ def test_null_pointers_and_bad_sizes_are_rejected_before_any_launch(lib):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="not built"):
         N.load(tmp_path / "libmissing.so")
+
+
+def _plan(lib, n, h, d, maxlen):
+    import ctypes
+    pc, pl, ll, wb = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    rc = lib.fr2_wkv7_recurrent_fp32_split_plan(n, h, d, maxlen, ctypes.byref(pc),
+                                                ctypes.byref(pl), ctypes.byref(ll),
+                                                ctypes.byref(wb))
+    assert rc == N.FR2_OK
+    return pc.value, pl.value, ll.value, wb.value
+
+
+def test_split_plan_config4_and_no_split_cases(lib):
+    """The pipelined split plan (host code, no GPU): BASELINE config 4 gets
+    5 pieces with a longer piece 0; config 1 (256 units), D != 64, short
+    sequences and more than 128 units are not split."""
+    assert _plan(lib, 1, 64, 64, 65536) == (5, 12608, 15104, (3 * 5 - 2) * 64 * 64 * 64 * 4)
+    for args in ((8, 32, 64, 4096), (1, 64, 128, 65536), (1, 32, 64, 1024), (1, 129, 64, 65536),
+                 (4, 32, 64, 127)):
+        assert _plan(lib, *args)[0] == 1, args
+
+
+@pytest.mark.parametrize("n,h,maxlen", [(1, 4, 8192), (2, 2, 4000), (2, 32, 4096), (1, 64, 2048),
+                                        (3, 32, 65536), (1, 8, 65536), (128, 1, 3000)])
+def test_split_plan_invariants(lib, n, h, maxlen):
+    """Every split plan covers max_seqlen exactly with its pieces, keeps
+    pieces of at least 384 tokens in multiples of 32, gives piece 0 at least
+    the others' length, fills at most one workgroup per CU in each phase, and
+    asks for the classic workspace bound."""
+    P, plen, lead, ws = _plan(lib, n, h, 64, maxlen)
+    assert P >= 3
+    assert plen >= 384 and plen % 32 == 0 and lead % 32 == 0 and lead >= plen
+    assert lead + (P - 2) * plen < maxlen <= lead + (P - 1) * plen
+    assert (P - 1) * n * h <= 256
+    assert ws == n * (3 * P - 2) * h * 64 * 64 * 4
+
+
+def test_split_plan_rejects_bad_arguments(lib):
+    import ctypes
+    one = ctypes.c_int32()
+    wb = ctypes.c_int64()
+    assert lib.fr2_wkv7_recurrent_fp32_split_plan(0, 4, 64, 8192, ctypes.byref(one),
+                                                  ctypes.byref(one), ctypes.byref(one),
+                                                  ctypes.byref(wb)) == N.FR2_ERR_INVALID_ARGUMENT
+    assert lib.fr2_wkv7_recurrent_fp32_split_plan(1, 4, 64, 8192, None, ctypes.byref(one),
+                                                  ctypes.byref(one),
+                                                  ctypes.byref(wb)) == N.FR2_ERR_INVALID_ARGUMENT
