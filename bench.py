@@ -866,6 +866,16 @@ def main() -> int:
                        "parallelism": "single GPU"},
             "roofline": roofline_obj(bytes1, kms, measured_traffic(pre.kernel_name(), w1.name)),
             "mfma": mfma_obj(w1, kms) if pre.kernel_name().startswith("chunk") else None,
+            # the token-serial form's own roofline: recurrence-form flops
+            # (5 x D x D FMA per token-head) over this kernel's time
+            "valu_equivalent": {
+                "achieved_tflops": round(w1.total_tokens * w1.num_heads * FLOPS_PER_TOKEN_HEAD
+                                         / (kms * 1e-3) / 1e12, 2),
+                "peak_tflops": VALU_FP32_PEAK_TFLOPS,
+                "frac": round(w1.total_tokens * w1.num_heads * FLOPS_PER_TOKEN_HEAD
+                              / (kms * 1e-3) / 1e12 / VALU_FP32_PEAK_TFLOPS, 4),
+                "flops_per_token_head": FLOPS_PER_TOKEN_HEAD,
+            },
             "kernel_ms": round(kms, 5),
             "algorithmic_bytes": bytes1,
         })
