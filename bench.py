@@ -129,7 +129,7 @@ class Runner:
             return "decode64_kernel<IoBF16,StF32>"
         if ms >= 128:
             return "chunk64_kernel<IoBF16,false>"
-        return "serial_kernel<64,IoBF16,StF32>"
+        return "serial64w_kernel<IoBF16,StF32>"
 
 
 def cpu_baseline(w, threads: int, sample_tokens: int | None, min_seconds: float = 12.0):
@@ -486,7 +486,7 @@ def time_other_paths(torch, flashrwkv2_amd, w, steps: int):
     out_obj = {
         "workload": w.name,
         "token_serial": {
-            "kernel": "serial_kernel<64,IoBF16,StF32>", "kernel_ms": round(s_ms, 4),
+            "kernel": "serial64w_kernel<IoBF16,StF32>", "kernel_ms": round(s_ms, 4),
             "tokens_per_s": round(T / (s_ms * 1e-3), 1),
             "roofline": roofline_obj(io + 2 * B * H * STATE_BYTES, s_ms),
             "valu": {"achieved_tflops": round(flops / (s_ms * 1e-3) / 1e12, 2),
@@ -501,7 +501,7 @@ def time_other_paths(torch, flashrwkv2_amd, w, steps: int):
             "roofline": roofline_obj(io + 2 * B * H * STATE_BYTES, f_ms),
         },
         "rl_infctx_replay": {
-            "kernel": "serial_kernel<64,IoBF16,StF32> per 16-token chunk (sa written)",
+            "kernel": "serial64w_kernel<IoBF16,StF32> per 16-token chunk (sa written)",
             "chunks": nchunks, "kernel_ms": round(r_ms, 4),
             "tokens_per_s": round(T / (r_ms * 1e-3), 1),
             "roofline": roofline_obj(replay_bytes, r_ms), "algorithmic_bytes": replay_bytes,
