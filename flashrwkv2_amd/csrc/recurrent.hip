@@ -281,34 +281,54 @@ __global__ __launch_bounds__(256) void serial64w_kernel(SegArgs p) {
   const raw* bias = static_cast<const raw*>(p.bias);
   raw* y = static_cast<raw*>(p.y);
 
-  for (int tile = t0; tile < t1; tile += TT) {
-    const int n = min(TT, t1 - tile);
-    __syncthreads();  // previous tile fully consumed
-    for (int idx = tid; idx < 6 * TT * V8; idx += NT) {
+  // the 6 x TT x 64 token values of a tile are 768 16-byte pieces, three per
+  // thread; the next tile's pieces are loaded into registers while the
+  // current tile computes
+  constexpr int PER = 6 * TT * V8 / NT;
+  static_assert(PER * NT == 6 * TT * V8, "tile pieces must divide evenly");
+  Raw8 pre[PER];
+  auto fetch = [&](int tile) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int idx = tid + u * NT;
       const int which = idx / (TT * V8);
       const int rem = idx - which * (TT * V8);
       const int tt = rem / V8;
       const int c8 = rem - tt * V8;
-      if (tt < n) {
-        const int64_t off = (static_cast<int64_t>(tile + tt) * H + h) * D + c8 * 8;
-        const Raw8 pk = *reinterpret_cast<const Raw8*>(src[which] + off);
-        float f[8];
+      // rows past the segment repeat its last row (in bounds; never consumed)
+      const int row = min(tile + tt, t1 - 1);
+      pre[u] = *reinterpret_cast<const Raw8*>(src[which] +
+                                              (static_cast<int64_t>(row) * H + h) * D + c8 * 8);
+    }
+  };
+  if (t0 < t1) fetch(t0);
+  for (int tile = t0; tile < t1; tile += TT) {
+    const int n = min(TT, t1 - tile);
+    __syncthreads();  // previous tile fully consumed
 #pragma unroll
-        for (int i = 0; i < 8; ++i) f[i] = raw8_get<Io>(pk, i);
-        if (which == 1) {
+    for (int u = 0; u < PER; ++u) {
+      const int idx = tid + u * NT;
+      const int which = idx / (TT * V8);
+      const int rem = idx - which * (TT * V8);
+      const int tt = rem / V8;
+      const int c8 = rem - tt * V8;
+      float f[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            float x = f[i];
-            if (bias != nullptr) x += Io::to_f32(bias[h * D + c8 * 8 + i]);
-            f[i] = retention_from_logit(x);
-          }
+      for (int i = 0; i < 8; ++i) f[i] = raw8_get<Io>(pre[u], i);
+      if (which == 1) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float x = f[i];
+          if (bias != nullptr) x += Io::to_f32(bias[h * D + c8 * 8 + i]);
+          f[i] = retention_from_logit(x);
         }
-        float4* dst = reinterpret_cast<float4*>(&s_in[which][tt][c8 * 8]);
-        dst[0] = make_float4(f[0], f[1], f[2], f[3]);
-        dst[1] = make_float4(f[4], f[5], f[6], f[7]);
       }
+      float4* dst = reinterpret_cast<float4*>(&s_in[which][tt][c8 * 8]);
+      dst[0] = make_float4(f[0], f[1], f[2], f[3]);
+      dst[1] = make_float4(f[4], f[5], f[6], f[7]);
     }
     __syncthreads();
+    if (tile + TT < t1) fetch(tile + TT);
 
     for (int tt = 0; tt < n; ++tt) {
       // the token's rows for this lane's 16 keys (broadcast reads within a
