@@ -76,6 +76,26 @@ def _dtype_code(t: torch.Tensor) -> int:
     return _TOKEN_DTYPES[t.dtype]
 
 
+def handoff_fault_count(device: torch.device | None = None, *, reset: bool = False) -> int:
+    """Blocks of the chunked MFMA kernels on ``device`` that failed closed
+    since the last reset: a bounded wave hand-off wait gave up, so the block
+    wrote NaN outputs and left its state slots untouched.  Synchronises the
+    current stream (call it after the work it should cover)."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    count = ctypes.c_int32(0)
+    with torch.cuda.device(device):
+        N.check(N.load().fr2_handoff_fault_count(ctypes.byref(count), int(reset),
+                                                 _stream(device)), "fr2_handoff_fault_count")
+    return int(count.value)
+
+
+def _set_handoff_spin_limit(polls: int) -> None:
+    """Test hook: polls a hand-off wait makes before it gives up, for later
+    launches in this process (negative restores the default)."""
+    N.check(N.load().fr2_debug_set_handoff_spin_limit(int(polls)),
+            "fr2_debug_set_handoff_spin_limit")
+
+
 # ---------------------------------------------------------------------------
 # Metadata tickets
 # ---------------------------------------------------------------------------

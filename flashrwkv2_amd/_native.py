@@ -37,6 +37,8 @@ SIGNATURES: dict[str, tuple] = {
     "fr2_abi_version": (c_int32, []),
     "fr2_status_string": (c_char_p, [c_int32]),
     "fr2_last_error": (c_char_p, []),
+    "fr2_handoff_fault_count": (c_int32, [_i32p, c_int32, c_void_p]),
+    "fr2_debug_set_handoff_spin_limit": (c_int32, [c_int32]),
     "fr2_wkv7_prepare_metadata": (
         c_int32,
         [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p,

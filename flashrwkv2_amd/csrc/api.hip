@@ -18,9 +18,14 @@ constexpr int kChunkMinSeqlen = 128;
 
 enum Family { kAuto = -1, kSerial = 0, kDecode = 1, kChunked = 2 };
 
+// Token tensors are read and written as 16-byte vectors: every token
+// pointer must be present and 16-byte aligned (a contiguous view with an odd
+// storage offset is rejected instead of faulting on a misaligned access).
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool tokens_ok(const void* r, const void* l, const void* k, const void* v,
                const void* a, const void* b, const void* y) {
-  return r && l && k && v && a && b && y;
+  return r && l && k && v && a && b && y && aligned16(r) && aligned16(l) && aligned16(k) &&
+         aligned16(v) && aligned16(a) && aligned16(b) && aligned16(y);
 }
 
 int run_family(int family, int D, int dtype, bool bf16_state, const SegArgs& p,
@@ -269,7 +274,7 @@ extern "C" int fr2_wkv7_pretrain_backward(
     const void* grad_output, const float* boundary, const float* state_dot_a,
     float* workspace, void* grad_r, void* grad_w, void* grad_k, void* grad_v,
     void* grad_a, void* grad_b, void* stream) {
-  if (!r || !w || !k || !v || !a || !b || !grad_output || !boundary || !state_dot_a ||
+  if (!tokens_ok(r, w, k, v, a, b, grad_output) || !boundary || !state_dot_a ||
       !workspace || !grad_r || !grad_w || !grad_k || !grad_v || !grad_a || !grad_b)
     return FR2_ERR_INVALID_ARGUMENT;
   if (batch <= 0 || tokens <= 0 || tokens % 16 != 0 || num_heads <= 0 ||
@@ -484,8 +489,9 @@ extern "C" int fr2_wkv7_statetune_backward(
     const float* boundary, float* workspace, void* grad_r, void* grad_decay_logits,
     void* grad_k, void* grad_v, void* grad_a, void* grad_b, float* grad_initial_state,
     float scale, void* stream) {
-  if (!sequence_chunk_offsets || !chunk_token_starts || !chunk_token_ends || !r ||
-      !decay_logits || !k || !v || !a || !b || !state_dot_a || !boundary || !workspace)
+  if (!sequence_chunk_offsets || !chunk_token_starts || !chunk_token_ends ||
+      !tokens_ok(r, decay_logits, k, v, a, b, r) || !state_dot_a || !boundary || !workspace ||
+      (grad_output != nullptr && !aligned16(grad_output)))
     return FR2_ERR_INVALID_ARGUMENT;
   if (!statetune_sizes_ok(num_sequences, num_chunks, total_tokens, num_heads))
     return FR2_ERR_INVALID_ARGUMENT;
@@ -559,7 +565,7 @@ extern "C" int fr2_wkv7_statetune_uniform_backward(
     const float* boundary, const float* snapshots, float* workspace, void* grad_r,
     void* grad_decay_logits, void* grad_k, void* grad_v, void* grad_a, void* grad_b,
     float* grad_initial_state, float scale, void* stream) {
-  if (!r || !decay_logits || !k || !v || !a || !b || !state_dot_a || !grad_output || !boundary ||
+  if (!tokens_ok(r, decay_logits, k, v, a, b, grad_output) || !state_dot_a || !boundary ||
       !snapshots || !workspace || !grad_r || !grad_decay_logits || !grad_k || !grad_v ||
       !grad_a || !grad_b || !grad_initial_state)
     return FR2_ERR_INVALID_ARGUMENT;
@@ -626,4 +632,33 @@ extern "C" int fr2_tmix_readout_prelinear_forward(int64_t tokens, int32_t num_he
   return fr2::launch_readout_prelinear(tokens, num_heads, head_size, wkv_output, r, k, v, r_k,
                                        ln_weight, ln_bias, gate, output,
                                        static_cast<hipStream_t>(stream));
+}
+
+// Blocks of the chunked kernels that failed closed because a wave hand-off
+// wait gave up (their outputs are NaN and their state untouched).  Waits for
+// `stream`, reads the current device's counter and, with reset != 0, clears
+// it.  No counterpart in the reference, whose kernels have no bounded waits.
+extern "C" int fr2_handoff_fault_count(int32_t* count, int32_t reset, void* stream) {
+  if (!count) return FR2_ERR_INVALID_ARGUMENT;
+  int* word = fr2::handoff_fault_word();
+  if (word == nullptr) return FR2_ERR_LAUNCH;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int32_t host = 0;
+  if (hipMemcpyAsync(&host, word, sizeof(host), hipMemcpyDeviceToHost, s) != hipSuccess ||
+      (reset != 0 && hipMemsetAsync(word, 0, sizeof(int32_t), s) != hipSuccess) ||
+      hipStreamSynchronize(s) != hipSuccess) {
+    (void)hipGetLastError();
+    return FR2_ERR_LAUNCH;
+  }
+  *count = host;
+  return FR2_OK;
+}
+
+// Polls a chunked-kernel hand-off wait makes before it gives up, for every
+// later launch in the process (negative: the default, 2^20).  A test hook:
+// with 0 the first wait that finds its counter short gives up, which lets a
+// test check the fail-closed path while every kernel still exits normally.
+extern "C" int fr2_debug_set_handoff_spin_limit(int32_t polls) {
+  fr2::set_handoff_spin_limit(polls);
+  return FR2_OK;
 }

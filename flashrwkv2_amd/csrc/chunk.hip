@@ -39,6 +39,7 @@
 #include "mfma.h"
 #include "recurrent.h"
 
+#include <atomic>
 #include <cstddef>
 #include <type_traits>
 
@@ -94,6 +95,7 @@ struct alignas(16) Smem {
   // groups state wave w has finished / whose output rows it has written back
   // (consumed has a slot for each of the summary pass's eight state waves)
   int ready[4], part1[4], drained[4], consumed[8];
+  int fault;                          // a bounded wait gave up
 };
 
 // Column position of key k in the A~ / R~ rows: for each half m = k/32 the 32
@@ -477,10 +479,10 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
 // polls the counter, and its later LDS reads issue after the poll returned.
 // Compiler fences keep the memory operations on their side of each step.
 // (Acquire/release atomics would also wait for outstanding global loads,
-// stalling the row prefetch.)  Every wait is bounded, so a counting mistake
-// can only produce wrong values, never a wave that does not finish.
-constexpr int kSpinLimit = 1 << 20;
-
+// stalling the row prefetch.)  Every wait is bounded by the launch's spin
+// limit so that every wave finishes; a wait that gives up raises the block's
+// fault flag, and the block then fails closed at its end (NaN outputs, state
+// untouched, the library's fault counter incremented).
 __device__ __forceinline__ void signal(int* c, int v) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): own LDS stores have landed
@@ -490,21 +492,28 @@ __device__ __forceinline__ void signal(int* c, int v) {
 __device__ __forceinline__ int peek(int* c) {
   return __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-__device__ __forceinline__ void wait_ge(int* c, int v) {
+__device__ __forceinline__ void raise_fault(int* fault) {
+  __hip_atomic_store(fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void wait_ge(int* c, int v, int limit, int* fault) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  for (int it = 0; it < kSpinLimit && peek(c) < v; ++it) __builtin_amdgcn_s_sleep(1);
+  int it = 0;
+  for (; it < limit && peek(c) < v; ++it) __builtin_amdgcn_s_sleep(1);
+  if (it == limit && peek(c) < v) raise_fault(fault);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 // wait until all four counters c[0..3] (kEight: c[0..7]) reach v
 template <bool kEight = false>
-__device__ __forceinline__ void wait_min_ge(int* c, int v) {
+__device__ __forceinline__ void wait_min_ge(int* c, int v, int limit, int* fault) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  for (int it = 0; it < kSpinLimit; ++it) {
+  auto low = [&]() {
     int m = min(min(peek(c), peek(c + 1)), min(peek(c + 2), peek(c + 3)));
     if constexpr (kEight) m = min(m, min(min(peek(c + 4), peek(c + 5)), min(peek(c + 6), peek(c + 7))));
-    if (m >= v) break;
-    __builtin_amdgcn_s_sleep(1);
-  }
+    return m;
+  };
+  int it = 0;
+  for (; it < limit && low() < v; ++it) __builtin_amdgcn_s_sleep(1);
+  if (it == limit && low() < v) raise_fault(fault);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
@@ -528,7 +537,10 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
   const int seg = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = tid >> 6;
+  // wave index as a scalar: the role branches below are uniform per wave, so
+  // each wave runs only its own role's code (no exec-masked pass through the
+  // other role, whose matrix instructions would run regardless of exec)
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 15;
   const int q = lane >> 4;
   const int H = p.num_heads;
@@ -582,22 +594,22 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
   const int ngroups = (t1 - t0 + GT - 1) / GT;
   raw* yout = static_cast<raw*>(p.y);
 
-  if (tid < 20) (&sm.ready[0])[tid] = 0;
+  if (tid < 21) (&sm.ready[0])[tid] = 0;
   __syncthreads();   // the only workgroup barrier: counters are zero
 
   constexpr int kStateWaves = kSum ? 8 : 4;
+  // state waves: columns [16wv, 16wv+16); in the summary pass waves 4-7
+  // repeat the columns for the transition (kind 1)
+  const int vcol = 16 * (wv & 3) + i;
+  const int kind = kSum ? (wv >> 2) : 0;
+  const int64_t sbase = (static_cast<int64_t>(slot) * H + h) * D * D;
+  const int64_t pbase = (static_cast<int64_t>(seq) * (npc > 0 ? npc : 1) + piece) * H + h;
+  f32x4 S[4];
   if (wv < kStateWaves) {
-    // ---------------- state waves: columns [16wv, 16wv+16); in the summary
-    // pass waves 4-7 repeat the columns for the transition (kind 1)
-    const int vcol = 16 * (wv & 3) + i;
-    const int kind = kSum ? (wv >> 2) : 0;
-    const int64_t sbase = (static_cast<int64_t>(slot) * H + h) * D * D;
-    f32x4 S[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) S[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     // state of a piece after the first (real split pass): the combined
     // start state; the summary pass starts from zero (F) or identity (Phi)
-    const int64_t pbase = (static_cast<int64_t>(seq) * (npc > 0 ? npc : 1) + piece) * H + h;
     if constexpr (kSum) {
       if (kind == 1) {
 #pragma unroll
@@ -630,7 +642,7 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
     const int seg_len = t1 - t0;
     auto write_out = [&](int gi) {
       if (gi < 0) return;
-      wait_min_ge(sm.consumed, gi + 1);       // every state wave staged its columns
+      wait_min_ge(sm.consumed, gi + 1, p.spin_limit, &sm.fault);   // every state wave staged its columns
       const int pos = gi * GT + o_tok;        // position in processing order
       if (pos < seg_len) {
         const int row = kRev ? t1 - 1 - pos : t0 + pos;
@@ -672,7 +684,7 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
     };
     auto group = [&](auto par_c, int gi) {
       constexpr int par = decltype(par_c)::value;
-      wait_min_ge(sm.ready, gi + 1);          // operators of group gi stored
+      wait_min_ge(sm.ready, gi + 1, p.spin_limit, &sm.fault);   // operators of group gi stored
       if constexpr (kSum) {
         // state update only: no outputs to stage or drain
         chunk_sum(state_load<kVExact, true>(sm.ops[par][0], vcol, i, q));
@@ -680,7 +692,7 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
         signal(&sm.consumed[wv], gi + 1);
         return;
       }
-      wait_min_ge(sm.drained, gi - 1);        // outputs of group gi-2 written back
+      wait_min_ge(sm.drained, gi - 1, p.spin_limit, &sm.fault);   // outputs of group gi-2 written back
       if (!kTrain && t0 + gi * GT + GT <= t1) {
         // both chunks: the second chunk's first-needed operand reads (the
         // S-side rows and V-side blocks) go out before the first chunk's chain
@@ -702,41 +714,7 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
       group(std::integral_constant<int, 0>{}, gi);
       if (gi + 1 < ngroups) group(std::integral_constant<int, 1>{}, gi + 1);
     }
-    if constexpr (kSum) {
-      float* sout = p.split_summary + ((static_cast<int64_t>(seg) * 2 + kind) * H + h) * D * D;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
-      return;
-    } else {
-      write_out(ngroups - 1);
-    }
-    if (!last_piece) {
-      // a piece before the last hands on nothing (its successor starts from
-      // the combined state), except the lead pass's piece 0, whose end state
-      // is piece 1's start
-      if (p.split_lead_pass && piece == 0) {
-        float* sout = p.split_state + (pbase + H) * D * D;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
-      }
-    } else if (p.state_out != nullptr) {
-      float* sout = static_cast<float*>(p.state_out);
-      uint16_t* soutb = static_cast<uint16_t*>(p.state_out);
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t at = sbase + (kb * 16 + 4 * q + e) * D + vcol;
-          if (p.state_bf16)
-            soutb[at] = IoBF16::from_f32(S[kb][e]);
-          else
-            sout[at] = S[kb][e];
-        }
-    }
+    if constexpr (!kSum) write_out(ngroups - 1);
   } else {
     // ---------------- key waves: chunk cc of each group, key half hh
     // The key waves are the pipeline's critical path and share each SIMD
@@ -803,7 +781,7 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
     auto iter = [&](auto par_c, u32x4 (&cur)[6], u32x4 (&nxt)[6], int gn) {
       constexpr int par = decltype(par_c)::value;   // parity of gn
       if (gn + 1 < ngroups) load_rows(nxt, gn + 1);
-      wait_min_ge<kSum>(sm.consumed, gn - 1);       // group gn-2 no longer read
+      wait_min_ge<kSum>(sm.consumed, gn - 1, p.spin_limit, &sm.fault);   // group gn-2 no longer read
       const bool active = t0 + gn * GT + cc * L < t1;
       if constexpr (kRev) {
         // position 0 of the segment: the shifted rows lie past its end
@@ -831,7 +809,7 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
                                                      tok0 + gn * GT < t1, par, cc, hh, i, q, kr);
       }
       signal(&sm.part1[kw], gn + 1);
-      wait_ge(&sm.part1[partner], gn + 1);
+      wait_ge(&sm.part1[partner], gn + 1, p.spin_limit, &sm.fault);
       if (active) key_part2<kVExact, kSum>(sm, sm.ops[par][cc], par, cc, hh, i, q, kr);
       signal(&sm.ready[kw], gn + 1);
     };
@@ -839,13 +817,104 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
       iter(std::integral_constant<int, 0>{}, rawA, rawB, gn);
       if (gn + 1 < ngroups) iter(std::integral_constant<int, 1>{}, rawB, rawA, gn + 1);
     }
+    __builtin_amdgcn_s_setprio(0);
+  }
+
+  // Every wave has left its loop; a raised fault flag means a hand-off wait
+  // gave up, so the values computed are not trustworthy: fail closed.
+  __syncthreads();
+  if (peek(&sm.fault) != 0) {
+    if (tid == 0 && p.handoff_fault != nullptr) atomicAdd(p.handoff_fault, 1);
+    const float qnan = quiet_nan();
+    if constexpr (kSum) {
+      // the pieces that start from this summary come out NaN as well
+      float* sout = p.split_summary + (static_cast<int64_t>(seg) * 2 * H + h) * D * D;
+      for (int e = tid; e < D * D; e += NT_SUM) {
+        sout[e] = qnan;
+        sout[static_cast<int64_t>(H) * D * D + e] = qnan;
+      }
+    } else {
+      const raw nanv = Io::from_f32(qnan);
+      for (int64_t e = tid; e < static_cast<int64_t>(t1 - t0) * D; e += NT)
+        yout[(t0 + e / D) * row_stride + head_off + e % D] = nanv;
+      if constexpr (kTrain) {
+        for (int64_t e = tid; e < static_cast<int64_t>(t1 - t0) * D; e += NT)
+          p.sa_out[(t0 + e / D) * row_stride + head_off + e % D] = qnan;
+      }
+      if (npc > 0 && p.split_lead_pass && piece == 0 && !last_piece) {
+        // the lead piece's successor starts from NaN
+        float* sout = p.split_state + (pbase + H) * D * D;
+        for (int e = tid; e < D * D; e += NT) sout[e] = qnan;
+      }
+    }
+    return;
+  }
+  if (wv >= kStateWaves) return;
+  if constexpr (kSum) {
+    float* sout = p.split_summary + ((static_cast<int64_t>(seg) * 2 + kind) * H + h) * D * D;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
+  } else if (!last_piece) {
+    // a piece before the last hands on nothing (its successor starts from
+    // the combined state), except the lead pass's piece 0, whose end state
+    // is piece 1's start
+    if (p.split_lead_pass && piece == 0) {
+      float* sout = p.split_state + (pbase + H) * D * D;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
+    }
+  } else if (p.state_out != nullptr) {
+    float* sout = static_cast<float*>(p.state_out);
+    uint16_t* soutb = static_cast<uint16_t*>(p.state_out);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t at = sbase + (kb * 16 + 4 * q + e) * D + vcol;
+        if (p.state_bf16)
+          soutb[at] = IoBF16::from_f32(S[kb][e]);
+        else
+          sout[at] = S[kb][e];
+      }
   }
 }
 
 }  // namespace
 
-int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen, hipStream_t s) {
+namespace {
+// Blocks of the chunked kernels whose wave hand-off gave up, per device (each
+// device holds its own copy; read through fr2_handoff_fault_count).
+__device__ int g_handoff_faults;
+std::atomic<int> g_spin_limit{1 << 20};
+std::atomic<int*> g_fault_ptr[64];
+}  // namespace
+
+int* handoff_fault_word() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  int* ptr = g_fault_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    if (hipGetSymbolAddress(reinterpret_cast<void**>(&ptr), HIP_SYMBOL(g_handoff_faults)) !=
+        hipSuccess)
+      return nullptr;
+    g_fault_ptr[dev].store(ptr, std::memory_order_release);
+  }
+  return ptr;
+}
+int handoff_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
+void set_handoff_spin_limit(int polls) {
+  g_spin_limit.store(polls < 0 ? (1 << 20) : polls, std::memory_order_relaxed);
+}
+
+int launch_chunked(int dtype, const SegArgs& args, int nseg, int max_seqlen, hipStream_t s) {
   (void)max_seqlen;
+  SegArgs p = args;
+  p.spin_limit = handoff_spin_limit();
+  p.handoff_fault = handoff_fault_word();
   const bool train = p.sa_out != nullptr || p.boundary != nullptr || p.reverse;
   const dim3 grid(p.num_heads, nseg);
   if (train) {
@@ -943,9 +1012,34 @@ int64_t split_workspace_floats(int nseg, int H, int pieces) {
 
 namespace {
 
+// Fork/join events of the pipelined split, created once per thread and
+// device (an event recorded by one thread is never re-recorded by another
+// while its wait is pending).
+struct SplitEvents {
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+thread_local SplitEvents t_split_events[64];
+
+bool split_events(SplitEvents*& ev) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  ev = &t_split_events[dev];
+  if (ev->fork == nullptr &&
+      hipEventCreateWithFlags(&ev->fork, hipEventDisableTiming) != hipSuccess) {
+    ev->fork = nullptr;
+    return false;
+  }
+  if (ev->join == nullptr &&
+      hipEventCreateWithFlags(&ev->join, hipEventDisableTiming) != hipSuccess) {
+    ev->join = nullptr;
+    return false;
+  }
+  return true;
+}
+
 template <class Io>
-void launch_split_kernels(const SegArgs& p, int nseg, int pieces, hipStream_t s,
-                          hipStream_t aux) {
+int launch_split_kernels(const SegArgs& p, int nseg, int pieces, hipStream_t s,
+                         hipStream_t aux) {
   const int H = p.num_heads;
   if (p.split_lead <= 0) {
     // classic: summaries of pieces 0..P-2, combine from the slot, every piece
@@ -953,17 +1047,19 @@ void launch_split_kernels(const SegArgs& p, int nseg, int pieces, hipStream_t s,
     hipLaunchKernelGGL((chunk64_kernel<Io, false, false, true>), gsum, dim3(NT_SUM), 0, s, p);
     hipLaunchKernelGGL(split_combine_kernel, gcomb, dim3(256), 0, s, p);
     hipLaunchKernelGGL((chunk64_kernel<Io, false>), greal, dim3(NT), 0, s, p);
-    return;
+    return FR2_OK;
   }
   // lead: piece 0 (from the slot) on the aux stream, concurrently with the
   // summaries of pieces 1..P-2; then the combine from piece 0's end state and
-  // pieces 1..P-1
-  hipEvent_t fork = nullptr, join = nullptr;
+  // pieces 1..P-1.  Without a usable second stream (or its events) the same
+  // passes run on one stream, with the same results.
+  SplitEvents* ev = nullptr;
   if (aux != nullptr) {
-    if (hipEventCreateWithFlags(&fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&join, hipEventDisableTiming) != hipSuccess ||
-        hipEventRecord(fork, s) != hipSuccess || hipStreamWaitEvent(aux, fork, 0) != hipSuccess)
-      aux = nullptr;   // fall back to one stream (same results, no overlap)
+    if (!split_events(ev) || hipEventRecord(ev->fork, s) != hipSuccess ||
+        hipStreamWaitEvent(aux, ev->fork, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      aux = nullptr;   // nothing is enqueued yet: one stream is still legal
+    }
   }
   const hipStream_t s_lead = aux != nullptr ? aux : s;
   SegArgs pl = p;
@@ -978,8 +1074,11 @@ void launch_split_kernels(const SegArgs& p, int nseg, int pieces, hipStream_t s,
     hipLaunchKernelGGL((chunk64_kernel<Io, false, false, true>), dim3(H, nseg * (pieces - 2)),
                        dim3(NT_SUM), 0, s, ps);
   if (aux != nullptr) {
-    if (hipEventRecord(join, aux) != hipSuccess || hipStreamWaitEvent(s, join, 0) != hipSuccess)
-      hipStreamSynchronize(aux);   // cannot order the streams: wait on the host
+    // the join cannot be replaced by a host wait: that is illegal while the
+    // streams are being captured into a graph
+    if (hipEventRecord(ev->join, aux) != hipSuccess ||
+        hipStreamWaitEvent(s, ev->join, 0) != hipSuccess)
+      return FR2_ERR_LAUNCH;
   }
   if (pieces > 2) hipLaunchKernelGGL(split_combine_kernel, dim3(H, nseg), dim3(256), 0, s, ps);
   SegArgs pr = p;
@@ -987,10 +1086,7 @@ void launch_split_kernels(const SegArgs& p, int nseg, int pieces, hipStream_t s,
   pr.split_count = pieces - 1;
   hipLaunchKernelGGL((chunk64_kernel<Io, false>), dim3(H, nseg * (pieces - 1)), dim3(NT), 0, s,
                      pr);
-  // destroying an event with pending waits is legal: the runtime keeps it
-  // until they complete
-  if (fork != nullptr) hipEventDestroy(fork);
-  if (join != nullptr) hipEventDestroy(join);
+  return FR2_OK;
 }
 
 }  // namespace
@@ -1005,16 +1101,17 @@ int launch_chunked_split(int dtype, SegArgs p, int nseg, int pieces, int piece_l
       p.state_out != p.state_in || static_cast<int64_t>(nseg) * pieces > 65535)
     return FR2_ERR_INVALID_ARGUMENT;
   if (dtype != FR2_DTYPE_BFLOAT16 && dtype != FR2_DTYPE_FLOAT16) return FR2_ERR_UNSUPPORTED;
+  p.spin_limit = handoff_spin_limit();
+  p.handoff_fault = handoff_fault_word();
   p.split_pieces = pieces;
   p.split_len = piece_len;
   p.split_lead = lead_len;
   p.split_summary = workspace;
   p.split_state = workspace + static_cast<int64_t>(nseg) * (pieces - 1) * 2 * p.num_heads * D * D;
-  if (dtype == FR2_DTYPE_BFLOAT16)
-    launch_split_kernels<IoBF16>(p, nseg, pieces, s, aux);
-  else
-    launch_split_kernels<IoF16>(p, nseg, pieces, s, aux);
-  return record_launch();
+  const int rc = dtype == FR2_DTYPE_BFLOAT16 ? launch_split_kernels<IoBF16>(p, nseg, pieces, s, aux)
+                                             : launch_split_kernels<IoF16>(p, nseg, pieces, s, aux);
+  const int lrc = record_launch();
+  return rc != FR2_OK ? rc : lrc;
 }
 
 }  // namespace fr2

@@ -79,6 +79,11 @@ struct SegArgs {
   int split_first = 0;
   int split_count = 0;
   bool split_lead_pass = false;
+  // Bounded waits of the chunked kernel's wave hand-off: polls before a wait
+  // gives up, and the device word that counts blocks that gave up (the block
+  // then fails closed: NaN outputs, state untouched)
+  int spin_limit = 1 << 20;
+  int* handoff_fault = nullptr;
 };
 
 // Token range [start, start + len) of piece j of a split sequence of n
@@ -108,6 +113,11 @@ int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen,
 // `aux` concurrently with the summary pass; aux null runs it on s).
 // workspace holds split_workspace_floats(nseg, H, pieces) floats.
 int64_t split_workspace_floats(int nseg, int H, int pieces);
+// Device address of the current device's hand-off fault counter (null if the
+// symbol lookup failed) and the spin limit every chunked launch uses.
+int* handoff_fault_word();
+int handoff_spin_limit();
+void set_handoff_spin_limit(int polls);   // negative: the default
 int launch_chunked_split(int dtype, SegArgs p, int nseg, int pieces, int piece_len,
                          int lead_len, float* workspace, hipStream_t s, hipStream_t aux);
 

@@ -66,6 +66,22 @@ const char* fr2_status_string(int status);
 const char* fr2_last_error(void);
 
 /*
+ * Count of chunked-kernel blocks that failed closed since the last reset on
+ * the current device: a wave hand-off wait inside the block gave up, so the
+ * block wrote NaN outputs and left its state untouched.  Waits for `stream`.
+ * No counterpart in the reference (its kernels have no bounded waits); the
+ * fail-closed result mirrors the metadata path
+ * (csrc/validation/recurrent_metadata.cu:24-132).
+ */
+int fr2_handoff_fault_count(int32_t* count, int32_t reset, void* stream);
+
+/*
+ * Test hook: polls a hand-off wait makes before giving up, for later launches
+ * (negative: the default 2^20).  No counterpart in the reference.
+ */
+int fr2_debug_set_handoff_spin_limit(int32_t polls);
+
+/*
  * Device-side validation of packed metadata, one 256-thread workgroup.
  * Writes status[3]; copies query_start_loc/state_indices into the snapshot
  * buffers when they are non-null (static tickets) and validates the copies.

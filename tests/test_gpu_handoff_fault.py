@@ -1,0 +1,71 @@
+"""The chunked kernels' bounded wave hand-off fails closed.
+
+Every wait between the key and state waves of the chunked MFMA kernel is
+bounded.  A wait that gives up must not pass wrong numbers off as results: the
+block writes NaN outputs, leaves its state slots untouched and counts itself
+in the library's fault counter.  The test forces the give-up from the host
+with a spin limit of zero polls (the state waves' first wait then always
+finds its counter short, since the key waves cannot have built any operator
+yet), so every kernel still runs to its normal end.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from wkv7_testlib import (
+    assert_output_close,
+    assert_state_close,
+    make_case,
+    oracle_expect,
+    require_gpu,
+    to_np,
+    tokens,
+)
+
+pytestmark = pytest.mark.gpu
+
+CHUNKED = 2
+
+
+def _forced_chunked(C, case, pool):
+    from flashrwkv2_amd.tmix.wkv7 import prepare_tmix_wkv7_recurrent_metadata
+
+    out = torch.empty_like(case["v"])
+    ticket = prepare_tmix_wkv7_recurrent_metadata(
+        case["cu_seqlens"], case["state_indices"], total_tokens=case["r"].shape[0],
+        state_pool_size=pool.shape[0])
+    C.tmix_wkv7_recurrent_fp32_kernel_forced(
+        CHUNKED, case["cu_seqlens"], case["state_indices"], pool, *tokens(case), out, 1.0,
+        case["decay_bias"], ticket)
+    torch.cuda.synchronize()
+    return out
+
+
+def test_handoff_give_up_fails_closed_and_is_counted():
+    C = require_gpu()
+    print("case handoff spin limit 0, lengths (200, 300), H=2", flush=True)
+    case = make_case(lengths=(200, 300), num_heads=2, seed=71)
+    C.handoff_fault_count(reset=True)
+    pool = case["state_pool"].clone()
+    before = pool.clone()
+    C._set_handoff_spin_limit(0)
+    try:
+        out = _forced_chunked(C, case, pool)
+    finally:
+        C._set_handoff_spin_limit(-1)
+    faults = C.handoff_fault_count(reset=True)
+    # one block per (sequence, head), each gives up at its first wait
+    assert faults == 4, faults
+    assert torch.isnan(out.float()).all()
+    assert torch.equal(pool, before), "a failed-closed block must leave its state untouched"
+
+    # default limit again: no fault, results match the oracle
+    pool = case["state_pool"].clone()
+    out = _forced_chunked(C, case, pool)
+    assert C.handoff_fault_count(reset=True) == 0
+    y_ref, pool_ref = oracle_expect(case)
+    assert_output_close(to_np(out), y_ref)
+    assert_state_close(to_np(pool), pool_ref)

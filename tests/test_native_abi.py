@@ -137,3 +137,24 @@ def test_split_plan_rejects_bad_arguments(lib):
     assert lib.fr2_wkv7_recurrent_fp32_split_plan(1, 4, 64, 8192, None, ctypes.byref(one),
                                                   ctypes.byref(one),
                                                   ctypes.byref(wb)) == N.FR2_ERR_INVALID_ARGUMENT
+
+
+def test_misaligned_token_pointers_are_rejected_before_any_launch(lib):
+    """Token rows are accessed as 16-byte vectors: a token pointer that is not
+    16-byte aligned (e.g. a contiguous view with an odd storage offset) is
+    an invalid argument, answered before any HIP call."""
+    fake, odd = 0x1000, 0x1002
+    for pos in range(7):   # r, decay_logits, k, v, a, b, output
+        toks = [fake] * 7
+        toks[pos] = odd
+        r, l, k, v, a, b, out = toks
+        assert lib.fr2_wkv7_recurrent_fp32_forward(
+            fake, fake, fake, 1, 1, 64, 1, 1, N.FR2_DTYPE_BFLOAT16, fake, r, l, None, k, v, a,
+            b, out, 1.0, None) == N.FR2_ERR_INVALID_ARGUMENT, pos
+    assert lib.fr2_wkv7_pretrain_forward(
+        1, 16, 1, 64, odd, *([fake] * 9), None) == N.FR2_ERR_INVALID_ARGUMENT
+
+
+def test_handoff_hooks_validate_their_arguments(lib):
+    assert lib.fr2_handoff_fault_count(None, 0, None) == N.FR2_ERR_INVALID_ARGUMENT
+    assert lib.fr2_debug_set_handoff_spin_limit(-1) == N.FR2_OK
