@@ -160,23 +160,45 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
   // c = -exp(-1/2) log2(e), evaluated as 1 / ((1 + 2^(-log2(e) x)) / c)
   constexpr float kC = kNegExpHalf * kLog2e;
   constexpr float kInvC = 1.0f / kC;
-  float at[8], rt[8], bh[8], kh[8];
+  // Stage by stage over the lane's eight keys: the eight chains are
+  // independent, so each stage's instructions (DPP steps included) issue
+  // back to back instead of waiting on one key's dependent chain.
+  float g2[8], gm[8], gp[8], at[8], rt[8], bh[8], kh[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    g2[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(xl[e], -kLog2e, nbias8[e]));
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float ex = __builtin_amdgcn_exp2f(__builtin_fmaf(xl[e], -kLog2e, nbias8[e]));
-    float lw2 = __builtin_amdgcn_rcpf(__builtin_fmaf(ex, kInvC, kInvC));
+    float lw2 = __builtin_amdgcn_rcpf(__builtin_fmaf(g2[e], kInvC, kInvC));
     if constexpr (!kFull) lw2 = valid ? lw2 : 0.0f;
     if constexpr (kUnitW) lw2 = unit_w ? 0.0f : lw2;
-    const float g2 = row_scan(lw2);
-    const float gm = __builtin_amdgcn_exp2f(g2);      // gamma_t
-    const float gp = row_prev(gm, 1.0f);              // gamma_{t-1}
-    const float ig = __builtin_amdgcn_exp2f(-g2);     // 1 / gamma_t
-    at[e] = xa[e] * gp;
-    if constexpr (!kSum) rt[e] = xr[e] * gm;
+    g2[e] = lw2;
+  }
+  // inclusive prefix sum over the 16 tokens (the lanes of a DPP row)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) g2[e] += row_shr<1>(g2[e]);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) g2[e] += row_shr<2>(g2[e]);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) g2[e] += row_shr<4>(g2[e]);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) g2[e] += row_shr<8>(g2[e]);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) gm[e] = __builtin_amdgcn_exp2f(g2[e]);      // gamma_t
+#pragma unroll
+  for (int e = 0; e < 8; ++e) gp[e] = row_prev(gm[e], 1.0f);              // gamma_{t-1}
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float ig = __builtin_amdgcn_exp2f(-g2[e]);                     // 1 / gamma_t
+    at[e] = xa[e] * gp[e];
+    if constexpr (!kSum) rt[e] = xr[e] * gm[e];
     bh[e] = xb[e] * ig;
     kh[e] = xk[e] * ig;
     if constexpr (kUnitW) kh[e] *= kscale;   // reverse mode: k is r_t, times scale
-    if (i == L - 1) op.gl[kbase + e] = gm;
+  }
+  if (i == L - 1) {
+    *reinterpret_cast<f32x4*>(&op.gl[kbase]) = f32x4{gm[0], gm[1], gm[2], gm[3]};
+    *reinterpret_cast<f32x4*>(&op.gl[kbase + 4]) = f32x4{gm[4], gm[5], gm[6], gm[7]};
   }
   kr.As = split8(at);
   if constexpr (!kSum) kr.Rs = split8(rt);
