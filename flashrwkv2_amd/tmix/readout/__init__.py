@@ -12,7 +12,41 @@ from __future__ import annotations
 
 import torch
 
+from .. import _checks as ck
 from ..wkv7 import _extension
+
+_FP16_CONTIGUOUS = "{name} must be contiguous CUDA float16"
+_PACKED = ("wkv_output", "receptance", "key", "value", "gate")
+_PER_CHANNEL = ("r_k", "ln_weight", "ln_bias")
+
+
+def _rows(packed, per_channel, output_weight, lora, head_size):
+    ref = packed[0]
+    rows = [("head_size", head_size, [ck.holds(lambda n: n in (64, 128, 256),
+                                               "head_size must be one of 64, 128, or 256")])]
+    rows += ck.each(_PACKED, packed, [
+        ck.is_tensor(),
+        ck.cuda_contiguous_of(torch.float16, _FP16_CONTIGUOUS),
+        ck.matches(ref, "{name} must match wkv_output's packed shape and device"),
+    ])
+    rows.append(("wkv_output", ref, [ck.holds(
+        lambda t: t.ndim == 2 and t.shape[0] > 0 and t.shape[1] % head_size == 0,
+        "wkv_output must have packed shape [total_tokens,H*head_size]")]))
+    channels = lambda: ref.shape[1]   # noqa: E731  (read after the layout rows)
+    rows += ck.each(_PER_CHANNEL, per_channel, [
+        ck.cuda_contiguous_of(torch.float16, _FP16_CONTIGUOUS),
+        ck.holds(lambda t: t.device == ref.device and tuple(t.shape) == (channels(),),
+                 "{name} must have shape [C] on wkv_output's device"),
+    ])
+    rows.append(("output_weight", output_weight, [
+        ck.cuda_contiguous_of(torch.float16, _FP16_CONTIGUOUS),
+        ck.holds(lambda w: w.device == ref.device and tuple(w.shape) == (channels(),) * 2,
+                 "{name} must have shape [C,C]"),
+    ]))
+    rows.append(("output", lora, [ck.holds(lambda p: (p[0] is None) == (p[1] is None),
+                                           "{name}_lora_a and {name}_lora_b must be provided "
+                                           "together")]))
+    return rows
 
 
 def infer_tmix_readout_forward_varlen(
@@ -34,31 +68,8 @@ def infer_tmix_readout_forward_varlen(
     max_seqlen: int | None = None,
 ) -> torch.Tensor:
     """Run head normalization, RKV residual, gate and output projection."""
-    if head_size not in {64, 128, 256}:
-        raise ValueError("head_size must be one of 64, 128, or 256")
-    for name, tensor in (("wkv_output", wkv_output), ("receptance", receptance), ("key", key),
-                         ("value", value), ("gate", gate)):
-        if not isinstance(tensor, torch.Tensor):
-            raise TypeError(f"{name} must be a torch.Tensor")
-        if tensor.dtype != torch.float16 or not tensor.is_cuda or not tensor.is_contiguous():
-            raise ValueError(f"{name} must be contiguous CUDA float16")
-        if tensor.device != wkv_output.device or tensor.shape != wkv_output.shape:
-            raise ValueError(f"{name} must match wkv_output's packed shape and device")
-    if wkv_output.ndim != 2 or wkv_output.shape[0] <= 0 or wkv_output.shape[1] % head_size:
-        raise ValueError("wkv_output must have packed shape [total_tokens,H*head_size]")
-    channels = wkv_output.shape[1]
-    for name, tensor in (("r_k", r_k), ("ln_weight", ln_weight), ("ln_bias", ln_bias)):
-        if tensor.dtype != torch.float16 or not tensor.is_cuda or not tensor.is_contiguous():
-            raise ValueError(f"{name} must be contiguous CUDA float16")
-        if tensor.device != wkv_output.device or tensor.shape != (channels,):
-            raise ValueError(f"{name} must have shape [C] on wkv_output's device")
-    if (output_weight.dtype != torch.float16 or not output_weight.is_cuda
-            or not output_weight.is_contiguous()):
-        raise ValueError("output_weight must be contiguous CUDA float16")
-    if output_weight.device != wkv_output.device or output_weight.shape != (channels, channels):
-        raise ValueError("output_weight must have shape [C,C]")
-    if (output_lora_a is None) != (output_lora_b is None):
-        raise ValueError("output_lora_a and output_lora_b must be provided together")
+    ck.verify(_rows((wkv_output, receptance, key, value, gate), (r_k, ln_weight, ln_bias),
+                    output_weight, (output_lora_a, output_lora_b), head_size))
     if max_seqlen is None:
         max_seqlen = wkv_output.shape[0]
     return _extension().tmix_readout_forward_varlen(

@@ -11,6 +11,8 @@ from __future__ import annotations
 
 import torch
 
+from .. import _checks as ck
+
 
 def _extension():
     """The native operator module (…/wkv7/__init__.py:8-17)."""
@@ -25,33 +27,39 @@ def _extension():
     return extension
 
 
+_TOKENS = ("r", "decay_logits", "k", "v", "a", "b")
+# rule tables (static: built once, applied per call)
+_PACKED_RULES = (
+    ck.is_tensor(),
+    ck.holds(lambda t: t.ndim == 3, "{name} must have packed shape [total_tokens,H,D]"),
+    ck.holds(lambda t: t.is_contiguous(), "{name} must be contiguous"),
+)
+_FP32_POOL_RULES = (
+    ck.is_tensor(),
+    ck.holds(lambda t: t.is_contiguous(), "{name} must be contiguous"),
+    ck.dtype_in((torch.float32,), "{name} must have dtype float32"),
+)
+_FP16_POOL_RULES = (
+    ck.is_tensor(),
+    ck.holds(lambda t: t.is_contiguous(), "{name} must be contiguous"),
+    ck.dtype_in((torch.float16,), "FP16-state {name} must have dtype float16"),
+)
+_CU_SEQLENS_RULES = (ck.is_tensor(),
+                     ck.holds(lambda t: t.ndim == 1, "{name} must be one-dimensional"))
+
+
 def _validate_packed_inputs(*tensors: torch.Tensor) -> tuple[torch.Tensor, ...]:
-    for name, tensor in zip(("r", "decay_logits", "k", "v", "a", "b"), tensors):
-        if not isinstance(tensor, torch.Tensor):
-            raise TypeError(f"{name} must be a torch.Tensor")
-        if tensor.ndim != 3:
-            raise ValueError(f"{name} must have packed shape [total_tokens,H,D]")
-        if not tensor.is_contiguous():
-            raise ValueError(f"{name} must be contiguous")
+    ck.verify(ck.each(_TOKENS, tensors, _PACKED_RULES))
     return tensors
 
 
 def _validate_state(state: torch.Tensor) -> None:
-    if not isinstance(state, torch.Tensor):
-        raise TypeError("state_pool must be a torch.Tensor")
-    if not state.is_contiguous():
-        raise ValueError("state_pool must be contiguous")
-    if state.dtype != torch.float32:
-        raise TypeError("state_pool must have dtype float32")
+    ck.verify((("state_pool", state, _FP32_POOL_RULES),))
 
 
 def _check_metadata_inputs(cu_seqlens: torch.Tensor, state_indices: torch.Tensor) -> None:
-    if not isinstance(cu_seqlens, torch.Tensor):
-        raise TypeError("cu_seqlens must be a torch.Tensor")
-    if cu_seqlens.ndim != 1:
-        raise ValueError("cu_seqlens must be one-dimensional")
-    if not isinstance(state_indices, torch.Tensor):
-        raise TypeError("state_indices must be a torch.Tensor")
+    ck.verify((("cu_seqlens", cu_seqlens, _CU_SEQLENS_RULES),
+               ("state_indices", state_indices, (ck.is_tensor(),))))
 
 
 def _resolve_max_seqlen(cu_seqlens: torch.Tensor, max_seqlen: int | None) -> int:
@@ -169,27 +177,20 @@ def infer_tmix_wkv7_recurrent_fp32io16_forward_varlen(
 
 def _validate_fp16_state(state: torch.Tensor) -> None:
     """…/wkv7/__init__.py:41-47."""
-    if not isinstance(state, torch.Tensor):
-        raise TypeError("state_pool must be a torch.Tensor")
-    if not state.is_contiguous():
-        raise ValueError("state_pool must be contiguous")
-    if state.dtype != torch.float16:
-        raise TypeError("FP16-state state_pool must have dtype float16")
+    ck.verify((("state_pool", state, _FP16_POOL_RULES),))
 
 
 def _validate_fp16_elapsed_state(elapsed_state_pool: torch.Tensor,
                                  state_pool: torch.Tensor) -> None:
     """…/wkv7/__init__.py:50-62."""
-    if not isinstance(elapsed_state_pool, torch.Tensor):
-        raise TypeError("elapsed_state_pool must be a torch.Tensor")
-    if elapsed_state_pool.dtype != torch.int32:
-        raise TypeError("elapsed_state_pool must have dtype torch.int32")
-    if not elapsed_state_pool.is_cuda or not elapsed_state_pool.is_contiguous():
-        raise ValueError("elapsed_state_pool must be contiguous CUDA int32")
-    if elapsed_state_pool.device != state_pool.device:
-        raise ValueError("elapsed_state_pool must share state_pool's device")
-    if elapsed_state_pool.ndim != 1 or elapsed_state_pool.shape[0] != state_pool.shape[0]:
-        raise ValueError("elapsed_state_pool must have shape [state_pool_slots]")
+    ck.verify((("elapsed_state_pool", elapsed_state_pool, (
+        ck.is_tensor(),
+        ck.dtype_in((torch.int32,), "{name} must have dtype torch.int32"),
+        ck.cuda_contiguous("{name} must be contiguous CUDA int32"),
+        ck.on_device_of(state_pool, "{name} must share state_pool's device"),
+        ck.holds(lambda t: t.ndim == 1 and t.shape[0] == state_pool.shape[0],
+                 "{name} must have shape [state_pool_slots]"),
+    )),))
 
 
 def infer_tmix_wkv7_recurrent_fp16_forward_varlen(

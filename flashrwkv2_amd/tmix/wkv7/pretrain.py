@@ -1,85 +1,91 @@
-"""``[B,T,C]`` bf16 training-layout WKV7 forward with zero initial state.
+"""``[B,T,C]`` bf16 training-layout WKV7 with zero initial state, with autograd.
 
-Mirrors ``flashrwkv2.tmix.wkv7.pretrain`` (flashrwkv2/tmix/wkv7/pretrain.py:14-130):
-same validation messages, the same ``boundary`` (post-chunk state every 16
-tokens, fp32 ``[B,H,T/16,N,N]``) and ``state_dot_a`` (fp32 ``[B,T,H,N]``)
-checkpoints, and the backward (pretrain.py:88-114 of the reference) that
-consumes them through ``pretrain_tmix_wkv7_recurrent_backward``.
+Public contract of ``flashrwkv2.tmix.wkv7.pretrain`` (flashrwkv2/tmix/wkv7/pretrain.py:14-130):
+the same function, keyword ``head_size`` and error messages.  The forward
+keeps two checkpoints for the backward: the post-chunk state every 16 tokens
+(``boundary``, fp32 ``[B,H,T/16,N,N]``) and every token's pre-update ``S^T a``
+(``state_dot_a``, fp32 ``[B,T,H,N]``); the backward consumes them through
+``pretrain_tmix_wkv7_recurrent_backward``.
 """
 
 from __future__ import annotations
 
 import torch
 
+from .. import _checks as ck
 from . import _extension
 
 CHUNK_LEN = 16
+_NAMES = ("r", "w", "k", "v", "a", "b")
 
 
-def _validate_inputs(tensors: tuple[torch.Tensor, ...], head_size: int) -> tuple[int, int, int]:
-    if head_size not in {64, 128, 256}:
-        raise ValueError("head_size must be one of 64, 128, or 256")
-    if len(tensors) != 6:
-        raise ValueError("clampw requires r, w, k, v, a, and b")
+def _rows(tensors):
     r = tensors[0]
-    if not isinstance(r, torch.Tensor):
-        raise TypeError("r must be a torch.Tensor")
-    if r.ndim != 3 or min(r.shape) <= 0:
-        raise ValueError("r must have shape [B,T,C] with nonzero dimensions")
-    if r.dtype != torch.bfloat16:
-        raise TypeError("r must be bfloat16")
-    if not r.is_cuda or not r.is_contiguous():
-        raise ValueError("r must be contiguous CUDA")
-    for name, tensor in zip(("w", "k", "v", "a", "b"), tensors[1:]):
-        if not isinstance(tensor, torch.Tensor):
-            raise TypeError(f"{name} must be a torch.Tensor")
-        if tensor.dtype != torch.bfloat16:
-            raise TypeError(f"{name} must be bfloat16")
-        if not tensor.is_cuda or not tensor.is_contiguous():
-            raise ValueError(f"{name} must be contiguous CUDA")
-        if tensor.shape != r.shape:
-            raise ValueError(f"{name} must match r shape")
-        if tensor.device != r.device:
-            raise ValueError(f"{name} must share the r device")
-    batch, tokens, channels = r.shape
-    if channels % head_size != 0:
-        raise ValueError("C must be divisible by head_size")
-    if tokens % CHUNK_LEN != 0:
-        raise ValueError("T must be divisible by the canonical chunk length 16")
+    first = [
+        ck.is_tensor(),
+        ck.holds(lambda t: t.ndim == 3 and min(t.shape) > 0,
+                 "r must have shape [B,T,C] with nonzero dimensions"),
+        ck.dtype_in((torch.bfloat16,), "{name} must be bfloat16"),
+        ck.cuda_contiguous(),
+    ]
+    rest = [
+        ck.is_tensor(),
+        ck.dtype_in((torch.bfloat16,), "{name} must be bfloat16"),
+        ck.cuda_contiguous(),
+        ck.matches(r, "{name} must match r shape", device=False),
+        ck.on_device_of(r, "{name} must share the r device"),
+    ]
+    return [("r", r, first), *ck.each(_NAMES[1:], tensors[1:], rest)]
+
+
+def _layout(tensors, head_size):
+    """(batch, tokens, channels) after every argument check."""
+    if head_size not in (64, 128, 256):
+        raise ValueError("head_size must be one of 64, 128, or 256")
+    if len(tensors) != len(_NAMES):
+        raise ValueError("clampw requires r, w, k, v, a, and b")
+    ck.verify(_rows(tensors))
+    batch, tokens, channels = tensors[0].shape
+    ck.verify([
+        ("C", channels, [ck.holds(lambda c: c % head_size == 0,
+                                  "C must be divisible by head_size")]),
+        ("T", tokens, [ck.holds(lambda t: t % CHUNK_LEN == 0,
+                                "T must be divisible by the canonical chunk length 16")]),
+    ])
     return batch, tokens, channels
 
 
-class _PretrainRecurrent(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, r, w, k, v, a, b, head_size):  # type: ignore[override]
-        batch, tokens, channels = _validate_inputs((r, w, k, v, a, b), head_size)
-        heads = channels // head_size
-        values = tuple(t.view(batch, tokens, heads, head_size) for t in (r, w, k, v, a, b))
-        output = torch.empty_like(values[3])
-        boundary = torch.empty((batch, heads, tokens // CHUNK_LEN, head_size, head_size),
-                               device=r.device, dtype=torch.float32)
-        state_dot_a = torch.empty((batch, tokens, heads, head_size), device=r.device,
-                                  dtype=torch.float32)
-        _extension().pretrain_tmix_wkv7_recurrent_forward(
-            *values, output, boundary, state_dot_a, head_size)
-        ctx.save_for_backward(*values, boundary, state_dot_a)
-        ctx.input_shape = (batch, tokens, channels)
-        ctx.head_size = head_size
-        return output.view(batch, tokens, channels)
+def _heads(t: torch.Tensor, head_size: int) -> torch.Tensor:
+    """[B,T,C] -> [B,T,H,N] view."""
+    b, n, c = t.shape
+    return t.view(b, n, c // head_size, head_size)
+
+
+class _PretrainWKV7(torch.autograd.Function):
+    """Forward on the chunked kernels with checkpoints; backward from them."""
 
     @staticmethod
-    def backward(ctx, grad_output):  # type: ignore[override]
-        r, w, k, v, a, b, boundary, state_dot_a = ctx.saved_tensors
-        batch, tokens, channels = ctx.input_shape
-        head_size = ctx.head_size
-        heads = channels // head_size
-        grad_output_4d = grad_output.contiguous().view(batch, tokens, heads, head_size)
-        if grad_output_4d.dtype != torch.bfloat16:
-            grad_output_4d = grad_output_4d.to(torch.bfloat16)
-        gradients = tuple(torch.empty_like(t) for t in (r, w, k, v, a, b))
-        _extension().pretrain_tmix_wkv7_recurrent_backward(
-            r, w, k, v, a, b, grad_output_4d, boundary, state_dot_a, *gradients, head_size)
-        return tuple(g.view(batch, tokens, channels) for g in gradients) + (None,)
+    def forward(ctx, head_size, *inputs):  # type: ignore[override]
+        x = [_heads(t, head_size) for t in inputs]
+        batch, tokens, heads, _ = x[0].shape
+        f32 = dict(device=inputs[0].device, dtype=torch.float32)
+        out = torch.empty_like(x[3])
+        boundary = torch.empty((batch, heads, tokens // CHUNK_LEN, head_size, head_size), **f32)
+        sa = torch.empty((batch, tokens, heads, head_size), **f32)
+        _extension().pretrain_tmix_wkv7_recurrent_forward(*x, out, boundary, sa, head_size)
+        ctx.head_size = head_size
+        ctx.save_for_backward(*x, boundary, sa)
+        return out.view_as(inputs[0])
+
+    @staticmethod
+    def backward(ctx, grad_out):  # type: ignore[override]
+        *x, boundary, sa = ctx.saved_tensors
+        dy = _heads(grad_out.to(torch.bfloat16).contiguous(), ctx.head_size)
+        grads = [torch.empty_like(t) for t in x]
+        _extension().pretrain_tmix_wkv7_recurrent_backward(*x, dy, boundary, sa, *grads,
+                                                           ctx.head_size)
+        flat = dy.shape[:2] + (dy.shape[2] * dy.shape[3],)
+        return (None, *(g.view(flat) for g in grads))
 
 
 def pretrain_tmix_wkv7_recurrent_bf16(
@@ -93,8 +99,8 @@ def pretrain_tmix_wkv7_recurrent_bf16(
     head_size: int = 64,
 ) -> torch.Tensor:
     """WKV7 over ``[B,T,C]`` bf16 inputs (``w`` holds decay logits), zero state."""
-    _validate_inputs((r, w, k, v, a, b), head_size)
-    return _PretrainRecurrent.apply(r, w, k, v, a, b, head_size)
+    _layout((r, w, k, v, a, b), head_size)
+    return _PretrainWKV7.apply(head_size, r, w, k, v, a, b)
 
 
 __all__ = ["pretrain_tmix_wkv7_recurrent_bf16"]
