@@ -66,6 +66,13 @@ SIGNATURES: dict[str, tuple] = {
          c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32,
          c_int32, c_void_p, c_int64, c_void_p, c_void_p],
     ),
+    "fr2_wkv7_recurrent_fp32_forward_split_noalloc": (
+        c_int32,
+        [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64,
+         c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32,
+         c_int32, c_void_p],
+    ),
     "fr2_wkv7_recurrent_fp16_forward": (
         c_int32,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64,

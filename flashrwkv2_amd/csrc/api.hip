@@ -2,8 +2,10 @@
 // include/flashrwkv2_amd.h).  Each validates pointers and sizes, fills a
 // segment descriptor and enqueues the chosen kernel family on `stream`.
 #include "recurrent.h"
+#include "../../include/flashrwkv2_amd.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace {
 
@@ -197,6 +199,67 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_split(
                                    static_cast<float*>(workspace),
                                    static_cast<hipStream_t>(stream),
                                    static_cast<hipStream_t>(aux_stream));
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation form of fr2_wkv7_recurrent_fp32_forward_split.  Its
+// workspace is `scratch`, a file-scope device array of kNoAllocScratchFloats
+// floats that every GPU the library runs on holds until the process ends.
+// The array's name is a host-side stand-in for the device symbol: host code
+// uses only the device address hipGetSymbolAddress returns, looked up once
+// per device with that device current and kept in g_scratch_ptr.
+// No clearing is needed: every float of the workspace a call reads was
+// written earlier in the same call (summaries, then chained start states).
+// Calls that overlap on one GPU share the array and race.
+// ---------------------------------------------------------------------------
+constexpr int64_t kNoAllocScratchFloats = int64_t{4} << 20;   // 16 MiB
+static_assert(kNoAllocScratchFloats * 4 == FR2_NOALLOC_SCRATCH_BYTES,
+              "header and library must agree on the scratch size");
+__device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+namespace {
+std::atomic<float*> g_scratch_ptr[64];
+
+float* scratch_address() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  float* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    if (hipGetSymbolAddress(reinterpret_cast<void**>(&ptr), HIP_SYMBOL(scratch)) != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+  }
+  return ptr;
+}
+}  // namespace
+
+extern "C" int fr2_wkv7_recurrent_fp32_forward_split_noalloc(
+    const int32_t* query_start_loc, const int32_t* state_indices, const int32_t* status,
+    int32_t num_sequences, int32_t num_heads, int32_t head_size, int64_t total_tokens,
+    int32_t max_seqlen, int32_t dtype, float* state, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a, const void* b,
+    void* output, float scale, int32_t pieces, int32_t piece_len, int32_t lead_len,
+    void* stream) {
+  if (num_sequences <= 0 || num_heads <= 0 || pieces < 2) return FR2_ERR_INVALID_ARGUMENT;
+  const int64_t need = fr2::split_workspace_floats(num_sequences, num_heads, pieces);
+  if (need > kNoAllocScratchFloats) {
+    fr2::set_last_error(
+        "fr2_wkv7_recurrent_fp32_forward_split_noalloc: the split's workspace exceeds the "
+        "16 MiB no-allocation scratch (num_sequences * (3 pieces - 2) * num_heads * 16 KiB)");
+    return FR2_ERR_INVALID_ARGUMENT;
+  }
+  float* ws = scratch_address();
+  if (ws == nullptr) {
+    fr2::set_last_error("fr2_wkv7_recurrent_fp32_forward_split_noalloc: scratch lookup failed");
+    return FR2_ERR_LAUNCH;
+  }
+  // one stream: the pipelined split's second stream would need events
+  return fr2_wkv7_recurrent_fp32_forward_split(
+      query_start_loc, state_indices, status, num_sequences, num_heads, head_size, total_tokens,
+      max_seqlen, dtype, state, r, decay_logits, decay_bias, k, v, a, b, output, scale, pieces,
+      piece_len, lead_len, ws, need * 4, stream, nullptr);
 }
 
 extern "C" int fr2_wkv7_recurrent_fp16_forward(

@@ -7,6 +7,8 @@ thread_local const char* g_last_error = "";
 }
 
 namespace fr2 {
+void set_last_error(const char* text) { g_last_error = text; }
+
 int record_launch() {
   const hipError_t e = hipGetLastError();
   if (e == hipSuccess) return FR2_OK;

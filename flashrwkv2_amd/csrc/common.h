@@ -113,4 +113,8 @@ __device__ void fill_output_nan(typename Io::raw* out, int64_t n,
 // fr2_last_error() in the calling thread.
 int record_launch();
 
+// Sets the text fr2_last_error() reports in the calling thread (static
+// storage only).
+void set_last_error(const char* text);
+
 }  // namespace fr2

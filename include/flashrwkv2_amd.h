@@ -186,6 +186,28 @@ int fr2_wkv7_recurrent_fp32_forward_split(
     void* aux_stream);
 
 /*
+ * fr2_wkv7_recurrent_fp32_forward_split without a workspace argument: the
+ * library's own device scratch array (FR2_NOALLOC_SCRATCH_BYTES per GPU, held
+ * until the process ends) replaces it, and the call allocates nothing (no
+ * hipMalloc/hipFree, no allocating library routine) and runs every pass on
+ * `stream`.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  A plan whose workspace exceeds the
+ * scratch (num_sequences * (3 pieces - 2) * num_heads * 16 KiB bytes) is
+ * rejected with FR2_ERR_INVALID_ARGUMENT and an fr2_last_error() text.
+ * Every call on one GPU shares that GPU's scratch: calls that overlap on one
+ * GPU (two streams, two threads) race.
+ */
+#define FR2_NOALLOC_SCRATCH_BYTES (16ll << 20)
+int fr2_wkv7_recurrent_fp32_forward_split_noalloc(
+    const int32_t* query_start_loc, const int32_t* state_indices, const int32_t* status,
+    int32_t num_sequences, int32_t num_heads, int32_t head_size, int64_t total_tokens,
+    int32_t max_seqlen, int32_t dtype, float* state, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a, const void* b,
+    void* output, float scale, int32_t pieces, int32_t piece_len, int32_t lead_len,
+    void* stream);
+
+/*
  * Packed varlen recurrence with an FP16 state pool [slots,H,D,D] updated in
  * place (the "Albatross" FP16-state contract, fp16 token tensors only):
  *   delta  = fp16(w - 1 + dither(phase)),
