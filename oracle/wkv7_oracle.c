@@ -101,6 +101,12 @@ void wkv7_oracle_f64(int n, int H, int D, const int32_t* cu, const int32_t* slot
                      const float* bias, const float* k, const float* v,
                      const float* a, const float* b, double scale, double* y,
                      double* sa, double* boundary, int blen, int per_seq) {
+  /* (sequence, head) pairs are independent (distinct state blocks and output
+   * rows), and each is evaluated in the same order whatever the thread
+   * count, so the result does not depend on the threading */
+#ifdef _OPENMP
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+#endif
   for (int s = 0; s < n; ++s)
     for (int h = 0; h < H; ++h) WKV7_BODY(double, ret_f64)
 }
