@@ -21,6 +21,7 @@ Reference bindings mirrored:
 from __future__ import annotations
 
 import ctypes
+import functools
 import math
 from typing import Sequence
 
@@ -53,8 +54,35 @@ def _tensor_version(t: torch.Tensor) -> int | None:
     return t._version
 
 
+_raw_stream = torch._C._cuda_getCurrentRawStream
+_get_device = torch._C._cuda_getDevice
+_set_device = torch._C._cuda_setDevice
+
+
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current HIP stream handle of `device` (raw getter: no Stream object)."""
+    idx = device.index
+    return _raw_stream(_get_device() if idx is None else idx)
+
+
+class _on_device:
+    """``torch.cuda.device`` without its bookkeeping: switches the current
+    device only when it differs, and switches back on exit."""
+
+    __slots__ = ("_idx", "_prev")
+
+    def __init__(self, device):
+        self._idx = device.index if isinstance(device, torch.device) else device
+
+    def __enter__(self):
+        self._prev = _get_device()
+        if self._idx is not None and self._idx != self._prev:
+            _set_device(self._idx)
+
+    def __exit__(self, *exc):
+        if self._idx is not None and self._idx != self._prev:
+            _set_device(self._prev)
+        return False
 
 
 _aux_streams: dict[int, torch.cuda.Stream] = {}
@@ -83,7 +111,7 @@ def handoff_fault_count(device: torch.device | None = None, *, reset: bool = Fal
     current stream (call it after the work it should cover)."""
     device = torch.device("cuda", torch.cuda.current_device()) if device is None else device
     count = ctypes.c_int32(0)
-    with torch.cuda.device(device):
+    with _on_device(device):
         N.check(N.load().fr2_handoff_fault_count(ctypes.byref(count), int(reset),
                                                  _stream(device)), "fr2_handoff_fault_count")
     return int(count.value)
@@ -135,6 +163,20 @@ class _RecurrentMetadataTicket:
 
     def _check_compatible(self, query_start_loc, state_indices, total_tokens,
                           state_pool_size, max_seqlen) -> None:
+        if (query_start_loc is self._qsl and state_indices is self._slots
+                and query_start_loc.data_ptr() == self._qsl_ptr
+                and state_indices.data_ptr() == self._slots_ptr
+                and (self._graph or self._qsl_version is None
+                     or _tensor_version(query_start_loc) == self._qsl_version)
+                and (self._graph or self._slots_version is None
+                     or _tensor_version(state_indices) == self._slots_version)
+                and int(total_tokens) == self._total_tokens
+                and int(state_pool_size) == self._pool_size
+                and (max_seqlen <= 0 or int(max_seqlen) == self._max_seqlen_v)
+                and _stream(self._device) == self._stream_handle
+                and (tuple(query_start_loc.shape), tuple(query_start_loc.stride())) == self._qsl_geom
+                and (tuple(state_indices.shape), tuple(state_indices.stride())) == self._slots_geom):
+            return   # same tensors, same storage, same device (the identity implies it)
         _check(query_start_loc is self._qsl,
                "validated_metadata query_start_loc identity mismatch")
         _check(state_indices is self._slots,
@@ -191,12 +233,12 @@ def _launch_validation(qsl, slots, live_tokens, live_seqs, total_tokens, num_seq
     """Device validation (recurrent_metadata.cu:134-194): status, workspace,
     and private snapshots for the static form."""
     dev = qsl.device
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         status = torch.empty(3, device=dev, dtype=torch.int32)
         seen = torch.empty(pool_size, device=dev, dtype=torch.int32)
         qsl_snap = torch.empty_like(qsl) if snapshot else qsl
         slots_snap = torch.empty_like(slots) if snapshot else slots
-        rc = N.load().fr2_wkv7_prepare_metadata(
+        rc = N.fast().prepare_metadata(
             qsl.data_ptr(), slots.data_ptr(), int(num_seqs), int(total_tokens),
             int(pool_size), int(max_seqlen),
             N.ptr(live_tokens), N.ptr(live_seqs), status.data_ptr(), seen.data_ptr(),
@@ -276,6 +318,43 @@ def prepare_tmix_wkv7_recurrent_graph_metadata(query_start_loc, state_indices,
                                                token_capacity, sequence_capacity,
                                                state_pool_size, max_seqlen_capacity):
     """Live capacity ticket for warmup / graph capture (…cpp:277-326)."""
+    if not _graph_metadata_ok(query_start_loc, state_indices, num_active_tokens,
+                              num_active_sequences, token_capacity, sequence_capacity,
+                              state_pool_size, max_seqlen_capacity):
+        _graph_metadata_error(query_start_loc, state_indices, num_active_tokens,
+                              num_active_sequences, token_capacity, sequence_capacity,
+                              state_pool_size, max_seqlen_capacity)
+    stream = _stream(query_start_loc.device)
+    snap_q, snap_s, status, seen = _launch_validation(
+        query_start_loc, state_indices, num_active_tokens, num_active_sequences,
+        token_capacity, sequence_capacity, state_pool_size, max_seqlen_capacity, False)
+    return _RecurrentMetadataTicket(query_start_loc, state_indices, snap_q, snap_s, status,
+                                    seen, num_active_tokens, num_active_sequences,
+                                    token_capacity, state_pool_size, max_seqlen_capacity,
+                                    True, stream)
+
+
+def _graph_metadata_ok(qsl, slots, live_tokens, live_seqs, token_capacity, sequence_capacity,
+                       state_pool_size, max_seqlen_capacity) -> bool:
+    """The valid case of prepare_tmix_wkv7_recurrent_graph_metadata in one expression."""
+    try:
+        dev = qsl.get_device()
+        return (all(t.is_cuda and t.is_contiguous() and t.get_device() == dev
+                    and t.dtype == torch.int32 for t in (qsl, slots, live_tokens, live_seqs))
+                and 0 < sequence_capacity <= 65535 and slots.dim() == 1
+                and slots.numel() == sequence_capacity and qsl.dim() == 1
+                and qsl.numel() == sequence_capacity + 1
+                and 0 < token_capacity <= INT32_MAX and 0 < state_pool_size <= INT32_MAX
+                and 0 < max_seqlen_capacity <= token_capacity
+                and live_tokens.numel() == 1 and live_seqs.numel() == 1)
+    except (AttributeError, TypeError):
+        return False
+
+
+def _graph_metadata_error(query_start_loc, state_indices, num_active_tokens,
+                          num_active_sequences, token_capacity, sequence_capacity,
+                          state_pool_size, max_seqlen_capacity):
+    """The checks of the graph-ticket entry in order: raises the first failure."""
     check_cuda_contiguous(query_start_loc, "query_start_loc")
     check_cuda_contiguous(state_indices, "state_indices")
     _check(state_indices.device == query_start_loc.device,
@@ -295,25 +374,44 @@ def prepare_tmix_wkv7_recurrent_graph_metadata(query_start_loc, state_indices,
            "max_seqlen_capacity must be positive and not exceed token_capacity")
     _check_graph_scalar(num_active_tokens, query_start_loc, "num_active_tokens")
     _check_graph_scalar(num_active_sequences, query_start_loc, "num_active_sequences")
-    stream = _stream(query_start_loc.device)
-    snap_q, snap_s, status, seen = _launch_validation(
-        query_start_loc, state_indices, num_active_tokens, num_active_sequences,
-        token_capacity, sequence_capacity, state_pool_size, max_seqlen_capacity, False)
-    return _RecurrentMetadataTicket(query_start_loc, state_indices, snap_q, snap_s, status,
-                                    seen, num_active_tokens, num_active_sequences,
-                                    token_capacity, state_pool_size, max_seqlen_capacity,
-                                    True, stream)
 
 
 # ---------------------------------------------------------------------------
 # fp32-state packed recurrence
 # ---------------------------------------------------------------------------
+_LAYOUT_NAMES = ("query_start_loc", "state_indices", "state", "r", "decay_logits", "k", "v",
+                 "a", "b", "output")
+
+
 def check_recurrent_layout(qsl, slots, state, r, decay_logits, k, v, a, b, output, scale):
-    """validation.cpp:27-129."""
-    for t, name in ((qsl, "query_start_loc"), (slots, "state_indices"), (state, "state"),
-                    (r, "r"), (decay_logits, "decay_logits"), (k, "k"), (v, "v"),
-                    (a, "a"), (b, "b"), (output, "output")):
-        check_cuda_contiguous(t, name)
+    """validation.cpp:27-129.  The common, valid case is decided by one
+    expression; only a failing call walks the checks in order for its message."""
+    tensors = (qsl, slots, state, r, decay_logits, k, v, a, b, output)
+    try:
+        n, h, d = slots.numel(), state.size(1), state.size(2)
+        dev, rs, rd = state.get_device(), r.shape, r.dtype
+        ok = (all(t.is_cuda and t.is_contiguous() and t.get_device() == dev for t in tensors)
+              and qsl.dtype == torch.int32 and slots.dtype == torch.int32
+              and state.dtype == torch.float32 and rd in _TOKEN_DTYPES
+              and math.isfinite(scale) and 0 < n <= 65535 and slots.dim() == 1
+              and qsl.dim() == 1 and qsl.size(0) == n + 1 and state.dim() == 4
+              and state.size(0) > 0 and 0 < h <= INT32_MAX and state.size(3) == d
+              and d in (64, 128, 256) and state.size(0) <= INT32_MAX and len(rs) == 3
+              and 0 < rs[0] <= INT32_MAX and rs[1] == h and rs[2] == d
+              and all(t.shape == rs and t.dtype == rd
+                      for t in (decay_logits, k, v, a, b, output)))
+    except (AttributeError, TypeError, IndexError, RuntimeError):
+        ok = False
+    if ok:
+        return n, h, d
+    return _recurrent_layout_error(tensors, scale)
+
+
+def _recurrent_layout_error(tensors, scale):
+    qsl, slots, state, r, decay_logits, k, v, a, b, output = tensors
+    if not all(isinstance(t, torch.Tensor) and t.is_cuda and t.is_contiguous() for t in tensors):
+        for t, name in zip(tensors, _LAYOUT_NAMES):   # the first offender's message
+            check_cuda_contiguous(t, name)
     _check(qsl.dtype == torch.int32, "query_start_loc must be int32")
     _check(slots.dtype == torch.int32, "state_indices must be int32")
     _check(math.isfinite(scale), "scale must be finite")
@@ -337,10 +435,11 @@ def check_recurrent_layout(qsl, slots, state, r, decay_logits, k, v, a, b, outpu
     _check(r.dtype in _TOKEN_DTYPES, "token tensors must be float16 or bfloat16")
     _check(all(t.dtype == r.dtype for t in (decay_logits, k, v, a, b, output)),
            "r,decay_logits,k,v,a,b,output dtype mismatch")
-    for t, name in ((qsl, "query_start_loc"), (slots, "state_indices"), (r, "r"),
-                    (decay_logits, "decay_logits"), (k, "k"), (v, "v"), (a, "a"),
-                    (b, "b"), (output, "output")):
-        check_same_device(state, t, name)
+    dev = state.get_device()
+    if not all(t.get_device() == dev for t in tensors):
+        for t, name in zip(tensors, _LAYOUT_NAMES):
+            if t is not state:
+                check_same_device(state, t, name)
     return n, h, d
 
 
@@ -386,7 +485,7 @@ def _recurrent_launch(kernel, qsl, slots, state, r, decay_logits, k, v, a, b, ou
         pieces, piece_len, lead_len, ws_bytes = split_plan(n, h, d, ms, split_pieces)
         if kernel == N.KERNEL_SPLIT and pieces < 2:
             raise RuntimeError("sequence split needs head size 64 and at least two pieces")
-    with torch.cuda.device(state.device):
+    with _on_device(state.device):
         stream = _stream(state.device)
         if pieces > 1:
             # workspace from the caching allocator on this stream: it is only
@@ -397,10 +496,23 @@ def _recurrent_launch(kernel, qsl, slots, state, r, decay_logits, k, v, a, b, ou
                                                            ws.data_ptr(), ws_bytes, stream, aux)
             del ws
         elif kernel is None:
-            rc = lib.fr2_wkv7_recurrent_fp32_forward(*common, stream)
+            rc = N.fast().recurrent_fp32_forward(*common, stream)
         else:
-            rc = lib.fr2_wkv7_recurrent_fp32_forward_kernel(int(kernel), *common, stream)
+            rc = N.fast().recurrent_fp32_forward_kernel(int(kernel), *common, stream)
     N.check(rc, "tmix_wkv7_recurrent_fp32_from_decay_logits")
+
+
+@functools.lru_cache(maxsize=256)
+def _library_split_plan(num_sequences: int, num_heads: int, head_size: int,
+                        max_seqlen: int) -> tuple[int, int, int, int]:
+    lib = N.load()
+    pc, pl, ll, wb = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    N.check(lib.fr2_wkv7_recurrent_fp32_split_plan(num_sequences, num_heads, head_size,
+                                                   max_seqlen, ctypes.byref(pc),
+                                                   ctypes.byref(pl), ctypes.byref(ll),
+                                                   ctypes.byref(wb)),
+            "fr2_wkv7_recurrent_fp32_split_plan")
+    return pc.value, pl.value, ll.value, wb.value
 
 
 def split_plan(num_sequences: int, num_heads: int, head_size: int, max_seqlen: int,
@@ -410,15 +522,9 @@ def split_plan(num_sequences: int, num_heads: int, head_size: int, max_seqlen: i
     `pieces` equal pieces of the classic split (lead_len 0) or, with
     `pieces=(P, lead_len)`, P pieces of the pipelined split whose piece 0 has
     lead_len tokens."""
-    lib = N.load()
     if pieces is None:
-        pc, pl, ll, wb = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
-        N.check(lib.fr2_wkv7_recurrent_fp32_split_plan(num_sequences, num_heads, head_size,
-                                                       max_seqlen, ctypes.byref(pc),
-                                                       ctypes.byref(pl), ctypes.byref(ll),
-                                                       ctypes.byref(wb)),
-                "fr2_wkv7_recurrent_fp32_split_plan")
-        return pc.value, pl.value, ll.value, wb.value
+        return _library_split_plan(int(num_sequences), int(num_heads), int(head_size),
+                                   int(max_seqlen))
     lead = 0
     if isinstance(pieces, tuple):
         pieces, lead = pieces
@@ -517,7 +623,7 @@ def tmix_wkv7_recurrent_fp16_from_decay_logits(query_start_loc, state_indices, e
     lq, ls, status, max_seqlen, keep = _resolve_launch_metadata(
         query_start_loc, state_indices, r.size(0), state.size(0), int(max_seqlen),
         validated_metadata)
-    with torch.cuda.device(state.device):
+    with _on_device(state.device):
         rc = N.load().fr2_wkv7_recurrent_fp16_forward(
             lq.data_ptr(), ls.data_ptr(), status.data_ptr(), elapsed_state.data_ptr(), n, h, d,
             r.size(0), int(max_seqlen), state.data_ptr(), r.data_ptr(), decay_logits.data_ptr(),
@@ -548,7 +654,7 @@ def pretrain_tmix_wkv7_recurrent_forward(r, w, k, v, a, b, output, boundary, sta
            and boundary.dtype == torch.float32, "boundary must be float32 [B,H,T/16,N,N]")
     _check(state_dot_a.shape == r.shape and state_dot_a.dtype == torch.float32,
            "state_dot_a must be float32 [B,T,H,N]")
-    with torch.cuda.device(r.device):
+    with _on_device(r.device):
         rc = N.load().fr2_wkv7_pretrain_forward(
             B, T, H, head_size, r.data_ptr(), w.data_ptr(), k.data_ptr(), v.data_ptr(),
             a.data_ptr(), b.data_ptr(), output.data_ptr(), boundary.data_ptr(),
@@ -589,7 +695,7 @@ def pretrain_tmix_wkv7_recurrent_backward(r, w, k, v, a, b, grad_output, boundar
     nws = N.load().fr2_wkv7_pretrain_backward_workspace_floats(B, T, H, head_size)
     _check(nws > 0, "pretrain backward: unsupported shape")
     workspace = torch.empty(nws, device=r.device, dtype=torch.float32)
-    with torch.cuda.device(r.device):
+    with _on_device(r.device):
         rc = N.load().fr2_wkv7_pretrain_backward(
             B, T, H, head_size, r.data_ptr(), w.data_ptr(), k.data_ptr(), v.data_ptr(),
             a.data_ptr(), b.data_ptr(), grad_output.data_ptr(), boundary.data_ptr(),
@@ -675,7 +781,7 @@ def statetune_tmix_wkv7_recurrent_fp32io16_forward(sequence_chunk_offsets, chunk
            "state_dot_a must be float32 [total_tokens,H,D]")
     length = _statetune_uniform_chunk_len(sequence_chunk_offsets, chunk_token_starts,
                                           chunk_token_ends, B, C, T, D, r.dtype)
-    with torch.cuda.device(state.device):
+    with _on_device(state.device):
         if length is not None:
             per_seq = T // B
             snapshots = torch.empty((B, H, per_seq // 16, D, D), device=state.device,
@@ -750,7 +856,7 @@ def statetune_tmix_wkv7_recurrent_fp32io16_backward(sequence_chunk_offsets, chun
         nws = N.load().fr2_wkv7_statetune_uniform_backward_workspace_floats(B, per_seq, H)
         _check(nws > 0, "statetune backward: unsupported shape")
         workspace = torch.empty(nws, device=r.device, dtype=torch.float32)
-        with torch.cuda.device(final_state.device):
+        with _on_device(final_state.device):
             rc = N.load().fr2_wkv7_statetune_uniform_backward(
                 B, per_seq, H, length, r.data_ptr(), decay_logits.data_ptr(), k.data_ptr(),
                 v.data_ptr(), a.data_ptr(), b.data_ptr(), state_dot_a.data_ptr(),
@@ -762,7 +868,7 @@ def statetune_tmix_wkv7_recurrent_fp32io16_backward(sequence_chunk_offsets, chun
     nws = N.load().fr2_wkv7_statetune_backward_workspace_floats(T, H, D)
     _check(nws > 0, "statetune backward: unsupported shape")
     workspace = torch.empty(nws, device=r.device, dtype=torch.float32)
-    with torch.cuda.device(final_state.device):
+    with _on_device(final_state.device):
         rc = N.load().fr2_wkv7_statetune_backward(
             sequence_chunk_offsets.data_ptr(), chunk_token_starts.data_ptr(),
             chunk_token_ends.data_ptr(), B, C, T, H, D, _dtype_code(r), r.data_ptr(),
@@ -832,7 +938,7 @@ def infer_tmix_wkv7_chunk_bf16_forward_varlen(r, decay_logits, k, v, a, b, state
             v.data_ptr(), a.data_ptr(), b.data_ptr(), output.data_ptr(), float(scale))
     pieces, piece_len, lead_len, ws_bytes = split_plan(state_indices.numel(), h, 64,
                                                        int(max_seqlen), _chunk_split_pieces)
-    with torch.cuda.device(r.device):
+    with _on_device(r.device):
         if pieces > 1:
             # few long sequences: the sequence split (workspace on this stream)
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=r.device)
@@ -913,7 +1019,7 @@ def rl_infctx_tmix_wkv7_chunk_fp32io16_forward(sequence_chunk_offsets, chunk_tok
     # metadata describes is the smallest of 16/32/64 holding every chunk.
     _check(longest_chunk <= 64, "chunk token ranges must not exceed 64 tokens")
     chunk_size = 16 if longest_chunk <= 16 else (32 if longest_chunk <= 32 else 64)
-    with torch.cuda.device(r.device):
+    with _on_device(r.device):
         rc = N.load().fr2_wkv7_rl_infctx_forward(
             sequence_chunk_offsets.data_ptr(), chunk_token_starts.data_ptr(),
             chunk_token_ends.data_ptr(), n, chunk_token_starts.numel(), h, d, r.size(0),
@@ -973,7 +1079,7 @@ def rl_infctx_tmix_wkv7_chunk_fp32io16_backward_replay(chunk_token_starts, chunk
     en = chunk_token_ends.to("cpu").tolist()
     _check(all(0 <= s < e <= r.size(0) for s, e in zip(st, en)),
            "chunk token ranges must be non-empty and within the packed tokens")
-    with torch.cuda.device(r.device):
+    with _on_device(r.device):
         rc = N.load().fr2_wkv7_rl_infctx_replay(
             chunk_token_starts.data_ptr(), chunk_token_ends.data_ptr(),
             chunk_token_starts.numel(), h, d, r.size(0), _dtype_code(r), boundary.data_ptr(),

@@ -177,6 +177,33 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
     return lib
 
 
+_FAST = None
+
+
+def fast():
+    """The CPython fast-call module over the same library (built next to it by
+    :mod:`flashrwkv2_amd.build`): the per-step entries without ctypes'
+    argument conversion.  Loaded once, after the library itself."""
+    global _FAST
+    if _FAST is None:
+        import importlib.machinery
+        import importlib.util
+
+        from .build import fastcall_name
+
+        load()
+        path = LIB_PATH.parent / fastcall_name()
+        if not path.exists():
+            raise RuntimeError(f"flashrwkv2_amd fast-call module not built: {path} is missing; "
+                               "run `python -m flashrwkv2_amd.build`")
+        loader = importlib.machinery.ExtensionFileLoader("_fastcall", str(path))
+        spec = importlib.util.spec_from_file_location("_fastcall", path, loader=loader)
+        module = importlib.util.module_from_spec(spec)
+        loader.exec_module(module)
+        _FAST = module
+    return _FAST
+
+
 def check(status: int, what: str) -> None:
     """Raise RuntimeError for a non-zero fr2_status_t."""
     if status == FR2_OK:

@@ -49,6 +49,33 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+FASTCALL_SRC = CSRC / "fastcall.c"
+
+
+def fastcall_name() -> str:
+    import sysconfig
+
+    return "_fastcall" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so")
+
+
+def _build_fastcall(lib: Path) -> Path:
+    """The CPython fast-call module over the library (plain C, linked to the
+    library with an $ORIGIN rpath, so both load from flashrwkv2_amd/lib)."""
+    import sysconfig
+
+    out = LIB_DIR / fastcall_name()
+    tmp = LIB_DIR / (out.name + ".tmp")
+    cc = shutil.which("gcc") or "cc"
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", f"-I{sysconfig.get_paths()['include']}",
+           str(FASTCALL_SRC), f"-L{LIB_DIR}", f"-l:{lib.name}", "-Wl,-rpath,$ORIGIN",
+           "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"fastcall build failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = True) -> Path:
     OBJ_DIR.mkdir(exist_ok=True)
     LIB_DIR.mkdir(exist_ok=True)
@@ -58,14 +85,16 @@ def build(verbose: bool = True) -> Path:
         objects = list(pool.map(_compile, sources))
     out = LIB_DIR / LIB_NAME
     tmp = LIB_DIR / (LIB_NAME + ".tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,-soname,{LIB_NAME}",
+           "-o", str(tmp),
            *map(str, objects)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, out)
+    fast = _build_fastcall(out)
     if verbose:
-        print(f"built {out}", file=sys.stderr)
+        print(f"built {out} and {fast.name}", file=sys.stderr)
     return out
 
 

@@ -48,18 +48,27 @@ _CU_SEQLENS_RULES = (ck.is_tensor(),
                      ck.holds(lambda t: t.ndim == 1, "{name} must be one-dimensional"))
 
 
+# Each validator first tests the common case in one expression and only walks
+# the rule table (for the first failing rule's message) when that fails: the
+# decode path calls these on every step.
 def _validate_packed_inputs(*tensors: torch.Tensor) -> tuple[torch.Tensor, ...]:
-    ck.verify(ck.each(_TOKENS, tensors, _PACKED_RULES))
+    if not all(isinstance(t, torch.Tensor) and t.ndim == 3 and t.is_contiguous()
+               for t in tensors):
+        ck.verify(ck.each(_TOKENS, tensors, _PACKED_RULES))
     return tensors
 
 
 def _validate_state(state: torch.Tensor) -> None:
-    ck.verify((("state_pool", state, _FP32_POOL_RULES),))
+    if not (isinstance(state, torch.Tensor) and state.is_contiguous()
+            and state.dtype == torch.float32):
+        ck.verify((("state_pool", state, _FP32_POOL_RULES),))
 
 
 def _check_metadata_inputs(cu_seqlens: torch.Tensor, state_indices: torch.Tensor) -> None:
-    ck.verify((("cu_seqlens", cu_seqlens, _CU_SEQLENS_RULES),
-               ("state_indices", state_indices, (ck.is_tensor(),))))
+    if not (isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.ndim == 1
+            and isinstance(state_indices, torch.Tensor)):
+        ck.verify((("cu_seqlens", cu_seqlens, _CU_SEQLENS_RULES),
+                   ("state_indices", state_indices, (ck.is_tensor(),))))
 
 
 def _resolve_max_seqlen(cu_seqlens: torch.Tensor, max_seqlen: int | None) -> int:
@@ -117,11 +126,12 @@ def prepare_tmix_wkv7_recurrent_metadata(
                             ("state_pool_size", state_pool_size),
                             ("max_seqlen_capacity", max_seqlen_capacity)):
             _positive_int(name, value)
+        dev = cu_seqlens.get_device()
         for name, value in (("num_active_tokens", num_active_tokens),
                             ("num_active_sequences", num_active_sequences)):
             ok = (isinstance(value, torch.Tensor) and value.dtype == torch.int32
                   and value.is_cuda and value.is_contiguous() and value.numel() == 1
-                  and value.device == cu_seqlens.device)
+                  and value.get_device() == dev)
             if not ok:
                 raise ValueError(f"{name} must be a one-element contiguous CUDA int32 tensor")
         return _extension().prepare_tmix_wkv7_recurrent_graph_metadata(
