@@ -127,7 +127,7 @@ class Runner:
         ms = self.ticket._max_seqlen()
         if ms <= 4:
             return "decode64_kernel<IoBF16,StF32>"
-        if ms >= 128:
+        if ms >= 40:   # the library's chunked threshold (csrc/api.hip kChunkMinSeqlen)
             return "chunk64_kernel<IoBF16,false>"
         return "serial64w_kernel<IoBF16,StF32>"
 
@@ -160,6 +160,56 @@ def cpu_baseline(w, threads: int, sample_tokens: int | None, min_seconds: float 
     return n_tok * reps / dt, dt, n_tok, reps
 
 
+def cpu_info() -> dict:
+    """Host CPU of this run: logical CPUs, the ones this process may use, and
+    the model name lscpu prints."""
+    import subprocess
+
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return {"nproc": os.cpu_count(), "usable": len(os.sched_getaffinity(0)), "model": model}
+
+
+def cpu_baseline_plan(threads: int, repeats: int = 20) -> dict:
+    """The CPU baseline BASELINE.md plans: the pure-torch per-token fp32 loop
+    (the form of the reference's test oracle, vectorised over heads) on config
+    0 and on one config-2 decode step, median of `repeats` timed runs after a
+    warm-up, with torch limited to `threads` threads."""
+    import statistics
+
+    import torch
+
+    from flashrwkv2_amd import workloads
+    from oracle.torch_loop import wkv7_torch_packed
+
+    torch.set_num_threads(threads)
+    legs = {}
+    for name, w in (("cfg0_B1_T64_H4", workloads.config(0, "cpu", dtype=torch.float32)),
+                    ("cfg2_decode_N256_H32_one_step", workloads.config(2, "cpu"))):
+        toks = [t.float() for t in w.tokens]
+        cu = w.cu_seqlens.tolist()
+        states = w.state_pool.float()
+        wkv7_torch_packed(*toks, cu, states)   # warm-up
+        times = []
+        for _ in range(repeats):
+            t0 = time.perf_counter()
+            wkv7_torch_packed(*toks, cu, states)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        legs[name] = {"tokens_per_s": round(w.total_tokens / med, 1),
+                      "median_ms": round(med * 1e3, 3), "tokens": w.total_tokens,
+                      "repeats": repeats}
+    return {"kind": "port", "code": "oracle/torch_loop.py (per-token fp32 loop, heads vectorised)",
+            "threads": threads, "legs": legs}
+
+
 def measured_traffic(kernel: str, workload: str):
     """HBM bytes per launch of `kernel` on `workload` from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE measurement (profiles/hbm_traffic.json),
@@ -174,10 +224,18 @@ def measured_traffic(kernel: str, workload: str):
     return int(k["fetch_kib"] * 1024 * data["fetch_scale"] + k["write_kib"] * 1024 * data["write_scale"])
 
 
+TRAFFIC_SOURCE = ("profiles/hbm_traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of the "
+                  "same kernel and workload, scaled by a copy kernel; committed, not measured "
+                  "in this run")
+
+
 def roofline_obj(bytes_per_launch: int, kernel_ms: float, traffic=None):
     achieved = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
-    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+    out = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+           "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+    if traffic is not None:
+        out["traffic_source"] = TRAFFIC_SOURCE
+    return out
 
 
 def time_fp16_state_decode(torch, flashrwkv2_amd, w, steps: int, warmup: int):
@@ -407,6 +465,41 @@ def time_varlen(torch, flashrwkv2_amd, steps: int):
     return out
 
 
+def time_mid_length(torch, flashrwkv2_amd, steps: int, n: int = 2048, length: int = 100,
+                    heads: int = 32):
+    """Serving-style batch of many mid-length sequences (2048 x 100 tokens,
+    H = 32, per-sequence fp32 states ~ N(0, 0.1)): the public call (which the
+    library dispatches by max_seqlen) and both candidate kernels forced, the
+    measurements behind the chunked-kernel threshold."""
+    from flashrwkv2_amd import workloads
+
+    toks = workloads.make_tokens(n * length, heads, u_range=(-6.0, -0.5), seed=1005,
+                                 device="cuda")
+    w = workloads._pack(f"mid_S{n}_T{length}_H{heads}", toks, [length] * n, heads, 0.1, 1005,
+                        "cuda", {"S": n, "T": length, "H": heads})
+    run = Runner(w, torch, flashrwkv2_amd)
+    ms = run.time_steps(steps, 5)
+    kms = run.time_kernel(steps)
+    nbytes = algorithmic_bytes(w.total_tokens, w.num_heads, w.state_indices.numel())
+    forced = {}
+    for kern, name in ((0, "serial64w_kernel<IoBF16,StF32>"), (2, "chunk64_kernel<IoBF16,false>")):
+        f = lambda k=kern: run.C.tmix_wkv7_recurrent_fp32_kernel_forced(
+            k, w.cu_seqlens, w.state_indices, run.state, *w.tokens, run.out, 1.0, None,
+            run.ticket)
+        fms = _events_ms(torch, f, steps)
+        forced[name] = {"kernel_ms": round(fms, 4), "roofline": roofline_obj(nbytes, fms)}
+    out = {
+        "workload": w.name, "total_tokens": w.total_tokens,
+        "ms_per_step": round(ms, 4), "tokens_per_s": round(w.total_tokens / (ms * 1e-3), 1),
+        "kernel_ms": round(kms, 4), "kernel": run.kernel_name(),
+        "roofline": roofline_obj(nbytes, kms), "algorithmic_bytes": nbytes,
+        "forced": forced,
+    }
+    del run, w, toks
+    torch.cuda.empty_cache()
+    return out
+
+
 def _events_ms(torch, fn, launches: int, warmup: int = 5) -> float:
     """Average duration (ms) of `fn` over `launches` back-to-back calls on the
     current stream, HIP events on both sides (and the wall clock, whichever
@@ -436,7 +529,7 @@ def time_other_paths(torch, flashrwkv2_amd, w, steps: int):
     16-token chunks, one block per sequence) and its backward replay (every
     chunk from its start-of-chunk state, sa written)."""
     from flashrwkv2_amd import _native as N
-    from flashrwkv2_amd.tmix.wkv7.rl_infctx import _make_chunk_metadata
+    from flashrwkv2_amd.tmix.wkv7.rl_infctx import _chunk_table
 
     lib = N.load()
     stream = torch.cuda.current_stream().cuda_stream
@@ -456,7 +549,7 @@ def time_other_paths(torch, flashrwkv2_amd, w, steps: int):
             "serial")
 
     offsets = w.cu_seqlens.cpu().tolist()
-    seq_chunks, starts, ends = _make_chunk_metadata(offsets, 16, w.r.device)
+    seq_chunks, starts, ends = _chunk_table(w.cu_seqlens.cpu().to(torch.int64), 16, w.r.device)
     nchunks = starts.numel()
 
     def rl_forward():
@@ -793,6 +886,9 @@ def mfma_obj(w, kernel_ms: float):
         if m is not None and m.get("workload") == w.name:
             out["measured_util"] = m["mfma_util"]
             out["measured_sclk_mhz"] = m["effective_sclk_mhz"]
+            out["measured_source"] = ("profiles/mfma_counters.json: rocprofv3 --pmc "
+                                      "SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE of the same "
+                                      "kernel and workload; committed, not measured in this run")
     return out
 
 
@@ -923,6 +1019,7 @@ def main() -> int:
         result["other_paths"] = time_other_paths(torch, flashrwkv2_amd, pre.w, args.steps)
     if args.only in (None, "long") and args.config == 1:
         result["varlen_prefill"] = time_varlen(torch, flashrwkv2_amd, max(5, args.steps // 2))
+        result["mid_length"] = time_mid_length(torch, flashrwkv2_amd, max(5, args.steps // 4))
         result["long_context"] = time_long_context(torch, flashrwkv2_amd, max(4, args.steps // 4))
     if args.only in (None, "train") and not args.no_train:
         wt = pre.w if (pre is not None and args.config == 1) else workloads.config(1, "cuda")
@@ -932,14 +1029,16 @@ def main() -> int:
         result["layer_stages"] = time_layer_stages(torch, 8 * 4096, 32)
     result["device"] = device_info(torch)
     if pre is not None and not args.no_cpu and args.config == 1:
-        threads = min(16, os.cpu_count() or 1)
+        threads = min(16, len(os.sched_getaffinity(0)) or 1)
         tps, dt, n_tok, reps = cpu_baseline(pre.w, threads, args.cpu_sample_tokens)
         result["cpu_baseline"] = {
             "value": round(tps, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"first {args.cpu_sample_tokens} tokens of each of the 8 config-1 "
                       f"sequences, all 32 heads ({n_tok} tokens x {reps} passes, {dt:.2f} s), fp32 C "
                       "recurrence (oracle/wkv7_oracle.c, OpenMP over sequence x head)",
+            "cpu": cpu_info(),
         }
+        result["cpu_baseline_plan"] = cpu_baseline_plan(threads)
     print(json.dumps(result), flush=True)
     return 0
 

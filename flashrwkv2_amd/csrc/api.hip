@@ -14,9 +14,13 @@ using fr2::SegArgs;
 // Kernel-family policy (replaces use_small_auto,
 // csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:378-391).
 // Short requests stream the state once with the decode kernel; long ones go
-// to the chunked MFMA kernel; everything else runs token-serial.
+// to the chunked MFMA kernel; everything else runs token-serial.  The
+// chunked threshold is the measured crossover at D = 64, H = 32, about 200 k
+// tokens per call of equal-length sequences (forced kernels, ms per call,
+// serial / chunked): L = 32: 5.93 / 6.54; L = 48: 5.75 / 5.36; L = 64:
+// 5.70 / 4.47; L = 128: 5.49 / 3.28.
 constexpr int kDecodeMaxSeqlen = 4;
-constexpr int kChunkMinSeqlen = 128;
+constexpr int kChunkMinSeqlen = 40;
 
 enum Family { kAuto = -1, kSerial = 0, kDecode = 1, kChunked = 2 };
 

@@ -240,3 +240,24 @@ def test_cpu_fp32_baseline_tracks_fp64():
                                    state_pool=c["pool"], threads=2)
     assert np.abs(y32 - y64).max() <= 1e-5 * max(1.0, np.abs(y64).max())
     assert np.abs(p32 - p64).max() <= 1e-5 * max(1.0, np.abs(p64).max())
+
+
+def test_torch_loop_baseline_matches_the_fp64_oracle():
+    """The pure-torch per-token loop bench.py times as the planned CPU
+    baseline computes the same recurrence as the fp64 C oracle (fp32
+    rounding only), on config-0 shapes with a nonzero state and scale."""
+    import torch
+
+    from oracle.torch_loop import wkv7_torch_packed
+    from flashrwkv2_amd import workloads
+
+    wl = workloads.config(0, "cpu", dtype=torch.float32)
+    g = torch.Generator().manual_seed(4)
+    states = torch.randn((1, 4, 64, 64), generator=g) * 0.1
+    toks = [t.float() for t in wl.tokens]
+    y, s = wkv7_torch_packed(*toks, wl.cu_seqlens.tolist(), states, scale=0.5)
+    y_ref, pool_ref, _, _ = oracle.wkv7_f64(*(t.numpy() for t in toks),
+                                            cu_seqlens=wl.cu_seqlens.numpy(),
+                                            state_pool=states.numpy(), scale=0.5)
+    np.testing.assert_allclose(y.numpy(), y_ref, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(s.numpy(), pool_ref, rtol=1e-4, atol=1e-4)
