@@ -278,11 +278,13 @@ def time_fp16_state_decode(torch, flashrwkv2_amd, w, steps: int, warmup: int):
             out.data_ptr(), 1.0, stream.cuda_stream)
     state.copy_(state0)
     torch.cuda.synchronize()
+    # the state-streaming kernel alone (the update half of the entry, without
+    # the separate elapsed-advance launch)
     start.record(stream)
     for _ in range(steps * 4):
-        rc = lib.fr2_wkv7_recurrent_fp16_forward(*args)
+        rc = lib.fr2_wkv7_recurrent_fp16_update(*args)
         if rc:
-            N.check(rc, "fr2_wkv7_recurrent_fp16_forward")
+            N.check(rc, "fr2_wkv7_recurrent_fp16_update")
     end.record(stream)
     torch.cuda.synchronize()
     return ms, start.elapsed_time(end) / (steps * 4)
@@ -998,7 +1000,9 @@ def main() -> int:
         result["decode_fp16_state"] = {
             "workload": w3.name + "_fp16_state", "tokens_per_s": round(w3.total_tokens / (f16_ms * 1e-3), 1),
             "ms_per_step": round(f16_ms, 5), "kernel_ms": round(f16_kms, 5),
-            "kernel": "decode64_kernel<IoF16,StF16>",
+            "kernel": "decode64_f16s_kernel<IoF16>",
+            "kernel_ms_note": "fr2_wkv7_recurrent_fp16_update alone; the public step also "
+                              "launches the elapsed-state advance",
             "roofline": roofline_obj(bytes3, f16_kms), "algorithmic_bytes": bytes3,
         }
         # the same decode shape, and a small serving batch, as a captured

@@ -266,13 +266,13 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_split_noalloc(
       piece_len, lead_len, ws, need * 4, stream, nullptr);
 }
 
-extern "C" int fr2_wkv7_recurrent_fp16_forward(
-    const int32_t* query_start_loc, const int32_t* state_indices,
-    const int32_t* status, int32_t* elapsed_state, int32_t num_sequences,
-    int32_t num_heads, int32_t head_size, int64_t total_tokens, int32_t max_seqlen,
-    void* state_f16, const void* r, const void* decay_logits, const void* decay_bias,
-    const void* k, const void* v, const void* a, const void* b, void* output, float scale,
-    void* stream) {
+namespace {
+int recurrent_fp16(bool advance, const int32_t* query_start_loc, const int32_t* state_indices,
+                   const int32_t* status, int32_t* elapsed_state, int32_t num_sequences,
+                   int32_t num_heads, int32_t head_size, int64_t total_tokens,
+                   int32_t max_seqlen, void* state_f16, const void* r, const void* decay_logits,
+                   const void* decay_bias, const void* k, const void* v, const void* a,
+                   const void* b, void* output, float scale, void* stream) {
   if (!query_start_loc || !state_indices || !status || !elapsed_state || !state_f16 ||
       !tokens_ok(r, decay_logits, k, v, a, b, output))
     return FR2_ERR_INVALID_ARGUMENT;
@@ -291,7 +291,49 @@ extern "C" int fr2_wkv7_recurrent_fp16_forward(
   p.y = output;
   p.scale = scale;
   return fr2::launch_fp16_state(head_size, p, num_sequences, max_seqlen, elapsed_state,
-                                static_cast<hipStream_t>(stream));
+                                static_cast<hipStream_t>(stream), advance);
+}
+}  // namespace
+
+extern "C" int fr2_wkv7_recurrent_fp16_forward(
+    const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, int32_t* elapsed_state, int32_t num_sequences,
+    int32_t num_heads, int32_t head_size, int64_t total_tokens, int32_t max_seqlen,
+    void* state_f16, const void* r, const void* decay_logits, const void* decay_bias,
+    const void* k, const void* v, const void* a, const void* b, void* output, float scale,
+    void* stream) {
+  return recurrent_fp16(true, query_start_loc, state_indices, status, elapsed_state,
+                        num_sequences, num_heads, head_size, total_tokens, max_seqlen, state_f16,
+                        r, decay_logits, decay_bias, k, v, a, b, output, scale, stream);
+}
+
+extern "C" int fr2_wkv7_recurrent_fp16_update(
+    const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, const int32_t* elapsed_state, int32_t num_sequences,
+    int32_t num_heads, int32_t head_size, int64_t total_tokens, int32_t max_seqlen,
+    void* state_f16, const void* r, const void* decay_logits, const void* decay_bias,
+    const void* k, const void* v, const void* a, const void* b, void* output, float scale,
+    void* stream) {
+  return recurrent_fp16(false, query_start_loc, state_indices, status,
+                        const_cast<int32_t*>(elapsed_state), num_sequences, num_heads, head_size,
+                        total_tokens, max_seqlen, state_f16, r, decay_logits, decay_bias, k, v, a,
+                        b, output, scale, stream);
+}
+
+extern "C" int fr2_wkv7_recurrent_fp16_advance_elapsed(const int32_t* query_start_loc,
+                                                       const int32_t* state_indices,
+                                                       const int32_t* status,
+                                                       int32_t* elapsed_state,
+                                                       int32_t num_sequences, void* stream) {
+  if (!query_start_loc || !state_indices || !status || !elapsed_state || num_sequences <= 0 ||
+      num_sequences > 65535)
+    return FR2_ERR_INVALID_ARGUMENT;
+  SegArgs p;
+  p.bounds = query_start_loc;
+  p.slots = state_indices;
+  p.status = status;
+  return fr2::launch_advance_elapsed(p, num_sequences, elapsed_state,
+                                     static_cast<hipStream_t>(stream));
 }
 
 extern "C" int fr2_wkv7_pretrain_forward(int32_t batch, int32_t tokens,

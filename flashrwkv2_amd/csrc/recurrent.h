@@ -102,7 +102,9 @@ int launch_decode(int D, int dtype, const SegArgs& p, int nseg, hipStream_t s);
 // FP16 state pool with the Albatross delta update (fp16 tokens), followed by
 // the elapsed-count advance of every active sequence's slot.
 int launch_fp16_state(int D, const SegArgs& p, int nseg, int max_seqlen, int32_t* elapsed,
-                      hipStream_t s);
+                      hipStream_t s, bool advance);
+// elapsed[slot] += length for every active sequence (after the update)
+int launch_advance_elapsed(const SegArgs& p, int nseg, int32_t* elapsed, hipStream_t s);
 // Chunked MFMA prefill (D = 64, fp32 state).  Returns FR2_ERR_UNSUPPORTED
 // for contracts it does not cover (sa output / boundaries / bf16 state).
 int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen,

@@ -11,6 +11,8 @@
 //  csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:90-192).
 #include "recurrent.h"
 
+#include <type_traits>
+
 namespace fr2 {
 
 __device__ __forceinline__ bool resolve_segment(const SegArgs& p, int seg,
@@ -413,7 +415,7 @@ __device__ __forceinline__ f4 shfl_xor4(f4 x, int m) {
 // serial_kernel); the staged retention becomes delta and each updated value
 // is rounded to fp16 before it feeds y and the store.
 template <class Io, class St>
-__global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
+__device__ __forceinline__ void decode64_body(const SegArgs& p) {
   constexpr bool kAlbatross = __is_same(St, StF16);
   typedef _Float16 h4 __attribute__((ext_vector_type(4)));
   using raw = typename Io::raw;
@@ -433,22 +435,26 @@ __global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
   const int c4 = lane & 15;
   const int rq = lane >> 4;
   const int64_t sbase = (static_cast<int64_t>(slot) * H + h) * D * D;
-  f4 S[16];
+  // The FP16 state stays packed in registers (two per 4-vector instead of
+  // four): every value is an fp16 number anyway, and the halved register
+  // count lets more waves stay resident.
+  using Reg = std::conditional_t<kAlbatross, h4, f4>;
+  Reg S[16];
+  auto get = [&](int j) -> f4 {
+    if constexpr (kAlbatross) return __builtin_convertvector(S[j], f4);
+    else return S[j];
+  };
   const int elapsed_base = (kAlbatross && p.elapsed != nullptr) ? p.elapsed[slot] : 0;
   if (p.state_in != nullptr) {
     const typename St::raw* sin =
         static_cast<const typename St::raw*>(p.state_in) + sbase + rq * D + 4 * c4;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      if constexpr (kAlbatross)
-        S[j] = __builtin_convertvector(
-            __builtin_nontemporal_load(reinterpret_cast<const h4*>(sin + 4 * j * D)), f4);
-      else
-        S[j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(sin + 4 * j * D));
+      S[j] = __builtin_nontemporal_load(reinterpret_cast<const Reg*>(sin + 4 * j * D));
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) S[j] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 16; ++j) S[j] = Reg{0, 0, 0, 0};
   }
 
   const raw* rp = static_cast<const raw*>(p.r);
@@ -481,10 +487,11 @@ __global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const float aj = Ar[j];
-      sa.x = fmaf(aj, S[j].x, sa.x);
-      sa.y = fmaf(aj, S[j].y, sa.y);
-      sa.z = fmaf(aj, S[j].z, sa.z);
-      sa.w = fmaf(aj, S[j].w, sa.w);
+      const f4 sj = get(j);
+      sa.x = fmaf(aj, sj.x, sa.x);
+      sa.y = fmaf(aj, sj.y, sa.y);
+      sa.z = fmaf(aj, sj.z, sa.z);
+      sa.w = fmaf(aj, sj.w, sa.w);
     }
     f4 o = shfl_xor4(sa, 16);
     sa.x += o.x; sa.y += o.y; sa.z += o.z; sa.w += o.w;
@@ -500,24 +507,27 @@ __global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const float wj = Wr[j], bj = Br[j], kj = Kr[j], rj = Rr[j];
+      f4 sj = get(j);
       if constexpr (kAlbatross) {
         // wj holds delta: fp16(S + S*delta + b*sa + k*v)
         f4 u;
-        u.x = fmaf(kj, vv.x, fmaf(bj, sa.x, fmaf(S[j].x, wj, S[j].x)));
-        u.y = fmaf(kj, vv.y, fmaf(bj, sa.y, fmaf(S[j].y, wj, S[j].y)));
-        u.z = fmaf(kj, vv.z, fmaf(bj, sa.z, fmaf(S[j].z, wj, S[j].z)));
-        u.w = fmaf(kj, vv.w, fmaf(bj, sa.w, fmaf(S[j].w, wj, S[j].w)));
-        S[j] = __builtin_convertvector(__builtin_convertvector(u, h4), f4);
+        u.x = fmaf(kj, vv.x, fmaf(bj, sa.x, fmaf(sj.x, wj, sj.x)));
+        u.y = fmaf(kj, vv.y, fmaf(bj, sa.y, fmaf(sj.y, wj, sj.y)));
+        u.z = fmaf(kj, vv.z, fmaf(bj, sa.z, fmaf(sj.z, wj, sj.z)));
+        u.w = fmaf(kj, vv.w, fmaf(bj, sa.w, fmaf(sj.w, wj, sj.w)));
+        S[j] = __builtin_convertvector(u, h4);
+        sj = __builtin_convertvector(S[j], f4);
       } else {
-        S[j].x = fmaf(wj, S[j].x, fmaf(bj, sa.x, kj * vv.x));
-        S[j].y = fmaf(wj, S[j].y, fmaf(bj, sa.y, kj * vv.y));
-        S[j].z = fmaf(wj, S[j].z, fmaf(bj, sa.z, kj * vv.z));
-        S[j].w = fmaf(wj, S[j].w, fmaf(bj, sa.w, kj * vv.w));
+        sj.x = fmaf(wj, sj.x, fmaf(bj, sa.x, kj * vv.x));
+        sj.y = fmaf(wj, sj.y, fmaf(bj, sa.y, kj * vv.y));
+        sj.z = fmaf(wj, sj.z, fmaf(bj, sa.z, kj * vv.z));
+        sj.w = fmaf(wj, sj.w, fmaf(bj, sa.w, kj * vv.w));
+        S[j] = sj;
       }
-      yy.x = fmaf(rj, S[j].x, yy.x);
-      yy.y = fmaf(rj, S[j].y, yy.y);
-      yy.z = fmaf(rj, S[j].z, yy.z);
-      yy.w = fmaf(rj, S[j].w, yy.w);
+      yy.x = fmaf(rj, sj.x, yy.x);
+      yy.y = fmaf(rj, sj.y, yy.y);
+      yy.z = fmaf(rj, sj.z, yy.z);
+      yy.w = fmaf(rj, sj.w, yy.w);
     }
     o = shfl_xor4(yy, 16);
     yy.x += o.x; yy.y += o.y; yy.z += o.z; yy.w += o.w;
@@ -538,12 +548,21 @@ __global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
         static_cast<typename St::raw*>(p.state_out) + sbase + rq * D + 4 * c4;
 #pragma unroll
     for (int j = 0; j < 16; ++j)
-      if constexpr (kAlbatross)
-        __builtin_nontemporal_store(__builtin_convertvector(S[j], h4),
-                                    reinterpret_cast<h4*>(sout + 4 * j * D));
-      else
-        __builtin_nontemporal_store(S[j], reinterpret_cast<f4*>(sout + 4 * j * D));
+      __builtin_nontemporal_store(S[j], reinterpret_cast<Reg*>(sout + 4 * j * D));
   }
+}
+
+template <class Io, class St>
+__global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
+  decode64_body<Io, St>(p);
+}
+// The FP16-state form holds its state packed (32 registers): capped at 96
+// registers it keeps five waves per SIMD resident instead of four, with no
+// spills.
+template <class Io>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void decode64_f16s_kernel(
+    SegArgs p) {
+  decode64_body<Io, StF16>(p);
 }
 
 // ---------------------------------------------------------------------------
@@ -605,20 +624,27 @@ __global__ __launch_bounds__(256) void advance_elapsed_kernel(SegArgs p, int nse
 constexpr int kFp16DecodeMaxSeqlen = 4;
 
 int launch_fp16_state(int D, const SegArgs& p, int nseg, int max_seqlen, int32_t* elapsed,
-                      hipStream_t s) {
+                      hipStream_t s, bool advance) {
   if (elapsed == nullptr || p.sa_out != nullptr || p.boundary != nullptr)
     return FR2_ERR_INVALID_ARGUMENT;
   SegArgs q = p;
   q.elapsed = elapsed;
   if (D == 64 && max_seqlen > 0 && max_seqlen <= kFp16DecodeMaxSeqlen) {
-    hipLaunchKernelGGL((decode64_kernel<IoF16, StF16>), dim3(p.num_heads, nseg), dim3(64), 0,
-                       s, q);
+    hipLaunchKernelGGL((decode64_f16s_kernel<IoF16>), dim3(p.num_heads, nseg), dim3(64), 0, s,
+                       q);
     const int rc = record_launch();
     if (rc != FR2_OK) return rc;
   } else {
     const int rc = launch_serial_io<IoF16, StF16>(D, q, nseg, s);
     if (rc != FR2_OK) return rc;
   }
+  return advance ? launch_advance_elapsed(p, nseg, elapsed, s) : FR2_OK;
+}
+
+int launch_advance_elapsed(const SegArgs& p, int nseg, int32_t* elapsed, hipStream_t s) {
+  if (elapsed == nullptr) return FR2_ERR_INVALID_ARGUMENT;
+  SegArgs q = p;
+  q.elapsed = elapsed;
   hipLaunchKernelGGL(advance_elapsed_kernel, dim3((nseg + 255) / 256), dim3(256), 0, s, q, nseg,
                      elapsed);
   return record_launch();

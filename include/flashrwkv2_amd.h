@@ -234,6 +234,28 @@ int fr2_wkv7_recurrent_fp16_forward(
     void* stream);
 
 /*
+ * The two halves of fr2_wkv7_recurrent_fp16_forward, as the reference splits
+ * them: the state update and outputs (reads elapsed_state for the dither
+ * phase, does not advance it) replaces tmix_wkv7_recurrent_fp16_from_decay_logits_cuda,
+ * and the elapsed advance (elapsed_state[slot] += sequence length for every
+ * active sequence) replaces recurrent_fp16_advance_i32_varlen_cuda
+ * (csrc/sm120/tmix/wkv7/infer_recurrent_fp16_forward_varlen.cpp:121-187).
+ * Calling the first, then the second, on one stream equals the combined entry.
+ */
+int fr2_wkv7_recurrent_fp16_update(
+    const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, const int32_t* elapsed_state, int32_t num_sequences,
+    int32_t num_heads, int32_t head_size, int64_t total_tokens,
+    int32_t max_seqlen, void* state_f16, const void* r,
+    const void* decay_logits, const void* decay_bias, const void* k,
+    const void* v, const void* a, const void* b, void* output, float scale,
+    void* stream);
+int fr2_wkv7_recurrent_fp16_advance_elapsed(const int32_t* query_start_loc,
+                                            const int32_t* state_indices,
+                                            const int32_t* status, int32_t* elapsed_state,
+                                            int32_t num_sequences, void* stream);
+
+/*
  * [B,T,H,D] bf16 training forward with zero initial state.  Writes y (bf16),
  * state_dot_a [B,T,H,D] fp32 (the pre-update sa of every token) and
  * boundary [B,H,T/16,D,D] fp32, the post-chunk state after every 16 tokens.

@@ -211,3 +211,47 @@ def test_fp16_state_decode_and_serial_paths_agree():
     assert relative_rmse(to_np(s1), to_np(s2)) <= 1e-3
     check_against_oracle(case, o1, s1, e1)
     check_against_oracle(case, o2, s2, e2)
+
+
+@pytest.mark.parametrize("lengths", ((1,) * 9, (3, 40, 7)))
+def test_fp16_state_update_then_advance_equals_the_combined_entry(lengths):
+    """fr2_wkv7_recurrent_fp16_update followed by
+    fr2_wkv7_recurrent_fp16_advance_elapsed (the reference's two native calls)
+    leave exactly what fr2_wkv7_recurrent_fp16_forward leaves; the update
+    alone leaves elapsed_state untouched."""
+    require_gpu()
+    from flashrwkv2_amd import _native as N
+    from flashrwkv2_amd.tmix.wkv7 import prepare_tmix_wkv7_recurrent_metadata
+
+    print(f"case fp16 update/advance split lengths={lengths}", flush=True)
+    case = make_case(lengths=lengths, seed=301)
+    lib = N.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    max_seqlen = max(lengths)
+    results = []
+    for split in (False, True):
+        state = case["state_pool"].clone()
+        elapsed = case["elapsed_state_pool"].clone()
+        out = torch.empty_like(case["v"])
+        t = prepare_tmix_wkv7_recurrent_metadata(
+            case["cu_seqlens"], case["state_indices"], total_tokens=case["r"].shape[0],
+            state_pool_size=state.shape[0])
+        meta = (t._query_start_loc_snapshot().data_ptr(), t._state_indices_snapshot().data_ptr(),
+                t._status().data_ptr(), elapsed.data_ptr())
+        rest = (len(lengths), case["r"].shape[1], 64, case["r"].shape[0], max_seqlen,
+                state.data_ptr(), case["r"].data_ptr(), case["decay_logits"].data_ptr(),
+                case["decay_bias"].data_ptr(), *(case[n].data_ptr() for n in NAMES[2:]),
+                out.data_ptr(), 0.5, stream)
+        if split:
+            N.check(lib.fr2_wkv7_recurrent_fp16_update(*meta, *rest), "update")
+            torch.cuda.synchronize()
+            assert torch.equal(elapsed, case["elapsed_state_pool"])
+            N.check(lib.fr2_wkv7_recurrent_fp16_advance_elapsed(*meta, len(lengths), stream),
+                    "advance")
+        else:
+            N.check(lib.fr2_wkv7_recurrent_fp16_forward(*meta, *rest), "forward")
+        torch.cuda.synchronize()
+        results.append((out, state, elapsed))
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
+    check_against_oracle(case, *results[1], scale=0.5)
