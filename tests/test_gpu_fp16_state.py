@@ -26,7 +26,7 @@ from flashrwkv2_amd.tmix.wkv7 import (  # noqa: E402
 import oracle  # noqa: E402
 
 NAMES = ("r", "decay_logits", "k", "v", "a", "b")
-GATE = 4.0e-3
+GATE = 3.0e-3   # the reference fixture's FP16 gate (tests/fixtures/tolerances-v1.json:24-38)
 
 
 def make_case(*, head_size=64, lengths=(1, 2, 4), num_heads=2, with_decay_bias=True,

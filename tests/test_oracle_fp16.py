@@ -57,11 +57,14 @@ def test_fp16_state_tracks_the_fp64_recurrence():
     y64, pool64, _, _ = oracle.wkv7_f64(*tok, cu_seqlens=cu, state_indices=slots,
                                         state_pool=pool.astype(np.float64), decay_bias=bias,
                                         scale=0.75)
+    # the reference fixture's FP16 gate (tests/fixtures/tolerances-v1.json:24-38,
+    # calibrated at 1.19e-3 / 1.51e-3 on its profile set); this case measures
+    # about 0.9e-3 on both
     rel = np.linalg.norm(y16.astype(np.float64) - y64) / np.linalg.norm(y64)
-    assert rel < 1e-2, rel
+    assert rel < 3e-3, rel
     act = slots.astype(np.int64)
     srel = np.linalg.norm(pool16[act].astype(np.float64) - pool64[act]) / np.linalg.norm(pool64[act])
-    assert srel < 1e-2, srel
+    assert srel < 3e-3, srel
     # with y taken from the pre-update state (a wrong contract) the error is far larger
     wrong = np.zeros_like(y64)
     for n in range(cu.size - 1):
@@ -110,3 +113,32 @@ def test_untouched_slots_and_counts():
     assert np.array_equal(p[untouched], pool[untouched])
     assert np.array_equal(e[untouched], elapsed[untouched])
     assert np.array_equal(e[slots], elapsed[slots] + np.diff(cu))
+
+
+def test_delta_is_rounded_to_fp16_before_the_update():
+    """Pure decay (k = v = a = b = 0) from a unit state: one token leaves
+    S' = fp16(1 + delta), so the rounding point of delta is observable.  Over a
+    sweep of logits, some deltas round differently as fp16 numbers than the
+    unrounded fp32 value would make 1 + delta round; the oracle must follow the
+    rounded delta at every point, and the sweep must contain such points."""
+    D, H = 64, 1
+    xs = np.linspace(-6.0, 6.0, 4096, dtype=np.float32).astype(np.float16)
+    n = xs.size // D
+    logits = xs[: n * D].reshape(n, H, D)
+    zeros = np.zeros_like(logits)
+    pool = np.ones((n, H, D, D), np.float16)
+    elapsed = np.zeros(n, np.int32)
+    cu = np.arange(n + 1, dtype=np.int32)
+    _, out, _ = oracle.wkv7_fp16_state(zeros, logits, zeros, zeros, zeros, zeros, cu_seqlens=cu,
+                                       state_indices=np.arange(n, dtype=np.int32),
+                                       state_pool=pool, elapsed_state_pool=elapsed)
+    x = logits.astype(np.float32)[:, 0, :]
+    w = np.exp(np.float32(-np.exp(-0.5)) / (1.0 + np.exp(-x))).astype(np.float32)
+    hk = np.arange(D)
+    dither = oracle.albatross_dither(hk)[None, :]          # phase = key index, elapsed 0
+    d32 = (w - np.float32(1.0) + dither).astype(np.float32)
+    rounded = (np.float32(1.0) + d32.astype(np.float16).astype(np.float32)).astype(np.float16)
+    unrounded = (np.float32(1.0) + d32).astype(np.float16)
+    got = out[:, 0, :, 0]                                   # every value column is the same
+    assert np.array_equal(got, rounded)
+    assert (rounded != unrounded).sum() > 0
