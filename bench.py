@@ -405,6 +405,78 @@ def time_layer_stages(torch, tokens: int, heads: int, steps: int = 20):
     return {"workload": f"cfg1_tokens{tokens}_C{C}_fp16", "kernels": out}
 
 
+def time_kk_fused(torch, flashrwkv2_amd, steps: int):
+    """wkv_prepare's kk / a-gate stage and the recurrence on BASELINE config
+    1's shape in fp16 (8 x 4096 tokens, H = 32): the reference's two kernels
+    (kk_a_gate_kernel writes key, a, b; the chunked recurrence reads them
+    back) against the chunked kernel that forms them in its load stage.  Both
+    read the projected key and a12 and write the gated key and y, so the
+    fused form moves 14 B per (token, channel) where the pair moves 24 B."""
+    from flashrwkv2_amd import _C as CC
+    from flashrwkv2_amd import _native as N
+    from flashrwkv2_amd import workloads
+
+    w = workloads.config(1, "cuda", dtype=torch.float16)
+    T, H, D = w.total_tokens, w.num_heads, 64
+    C = H * D
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3002)
+    r, logits, _, v, _, _ = w.tokens
+    k = (torch.randn((T, H, D), generator=g, device="cuda") * 0.7).half()
+    a12 = torch.randn((T, H, D), generator=g, device="cuda").half()
+    kk = (torch.randn(C, generator=g, device="cuda") * 0.2 + 0.85).half()
+    a0 = (torch.randn(C, generator=g, device="cuda") * 0.5).half()
+    ka = torch.rand(C, generator=g, device="cuda").half()
+    state = w.state_pool.clone()
+    new_k, a, b, out = (torch.empty_like(k) for _ in range(4))
+    ticket = flashrwkv2_amd.prepare_tmix_wkv7_recurrent_metadata(
+        w.cu_seqlens, w.state_indices, total_tokens=T, state_pool_size=state.shape[0])
+    lib = N.load()
+    sh = torch.cuda.current_stream().cuda_stream
+
+    def two_stage():
+        N.check(lib.fr2_tmix_kk_a_gate_forward(
+            T, H, D, k.data_ptr(), kk.data_ptr(), a0.data_ptr(), a12.data_ptr(), ka.data_ptr(),
+            new_k.data_ptr(), a.data_ptr(), b.data_ptr(), sh), "fr2_tmix_kk_a_gate_forward")
+        CC.tmix_wkv7_recurrent_fp32_from_decay_logits(
+            w.cu_seqlens, w.state_indices, state, r, logits, new_k, v, a, b, out, 1.0, None,
+            ticket)
+
+    def fused():
+        CC.tmix_wkv7_recurrent_fp32_from_kk_gate(
+            w.cu_seqlens, w.state_indices, state, r, logits, k, v, a12, kk, a0, ka, new_k, out,
+            1.0, None, ticket)
+
+    seqs = w.state_indices.numel()
+    state_bytes = 2 * seqs * H * D * D * 4
+    fused_bytes = 14 * T * C + state_bytes
+    pair_bytes = 24 * T * C + state_bytes
+    def recurrence():
+        CC.tmix_wkv7_recurrent_fp32_from_decay_logits(
+            w.cu_seqlens, w.state_indices, state, r, logits, new_k, v, a, b, out, 1.0, None,
+            ticket)
+
+    two_ms = _events_ms(torch, two_stage, steps)
+    fused_ms = _events_ms(torch, fused, steps)
+    rec_ms = _events_ms(torch, recurrence, steps)
+    out_obj = {
+        "workload": "cfg1_prefill_B8_T4096_H32_fp16_kk_gate", "total_tokens": T,
+        "two_stage": {"ms_per_step": round(two_ms, 4),
+                      "kernels": "kk_a_gate_kernel<64> + chunk64_kernel<IoF16,false>",
+                      "algorithmic_bytes": pair_bytes,
+                      "roofline": roofline_obj(pair_bytes, two_ms)},
+        "fused": {"ms_per_step": round(fused_ms, 4),
+                  "kernel": "chunk64_kernel<IoF16,false,false,false,true>",
+                  "algorithmic_bytes": fused_bytes,
+                  "roofline": roofline_obj(fused_bytes, fused_ms)},
+        "recurrence_alone_ms": round(rec_ms, 4),
+        "saved_ms": round(two_ms - fused_ms, 4),
+    }
+    del w, state, k, a12, new_k, a, b, out, ticket
+    torch.cuda.empty_cache()
+    return out_obj
+
+
 # Algorithmic HBM bytes of the training backward per (token, head) at D=64:
 # reads r, w, k, v, a, b, dy (7 x 2D bf16), sa (4D fp32) and the forward's
 # boundary snapshot amortised over its 16 tokens (4 D^2 / 16); writes the six
@@ -1031,6 +1103,7 @@ def main() -> int:
         result["statetune_training"] = time_statetune_training(torch, wt, max(3, args.steps // 4))
     if args.only in (None, "stages"):
         result["layer_stages"] = time_layer_stages(torch, 8 * 4096, 32)
+        result["kk_gate_fused"] = time_kk_fused(torch, flashrwkv2_amd, max(5, args.steps // 2))
     result["device"] = device_info(torch)
     if pre is not None and not args.no_cpu and args.config == 1:
         threads = min(16, len(os.sched_getaffinity(0)) or 1)

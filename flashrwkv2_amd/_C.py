@@ -502,6 +502,54 @@ def _recurrent_launch(kernel, qsl, slots, state, r, decay_logits, k, v, a, b, ou
     N.check(rc, "tmix_wkv7_recurrent_fp32_from_decay_logits")
 
 
+def tmix_wkv7_recurrent_fp32_from_kk_gate(query_start_loc, state_indices, state, r,
+                                          decay_logits, k, v, a12, k_k, a0, k_a, new_k, output,
+                                          scale, decay_bias=None, validated_metadata=None,
+                                          max_seqlen=-1):
+    """The recurrence with wkv_prepare's kk / a-gate stage in its load stage:
+    k is the projected key, a12 the a-gate logits, k_k / a0 / k_a the
+    per-channel parameters ([H*D] or [H,D], token dtype); the gated key is
+    written to new_k.  Outside the chunked family (head size 64, longest
+    sequence >= 40) the two stages run as separate kernels (fp16 tokens)."""
+    n, h, d = check_recurrent_layout(query_start_loc, state_indices, state, r, decay_logits, k,
+                                     v, a12, new_k, output, scale)
+    for t, name in ((k_k, "k_k"), (a0, "a0"), (k_a, "k_a")):
+        check_cuda_contiguous(t, name)
+        check_same_device(state, t, name)
+        _check(t.dtype == r.dtype, name, " must have the token dtype")
+        _check(t.numel() == h * d, name, " must have shape [H*D] or [H,D]")
+    if decay_bias is not None:
+        _check_decay_bias(decay_bias, state, r, h, d,
+                          "decay_bias must match the token tensor dtype")
+    lq, ls, status, ms, keep = _resolve_launch_metadata(
+        query_start_loc, state_indices, r.size(0), state.size(0), int(max_seqlen),
+        validated_metadata)
+    with _on_device(state.device):
+        stream = _stream(state.device)
+        rc = N.load().fr2_wkv7_recurrent_fp32_forward_kk_gate(
+            lq.data_ptr(), ls.data_ptr(), status.data_ptr(), n, h, d, r.size(0), int(ms),
+            _dtype_code(r), state.data_ptr(), r.data_ptr(), decay_logits.data_ptr(),
+            N.ptr(decay_bias), k.data_ptr(), v.data_ptr(), a12.data_ptr(), k_k.data_ptr(),
+            a0.data_ptr(), k_a.data_ptr(), new_k.data_ptr(), output.data_ptr(), float(scale),
+            stream)
+        if rc == N.FR2_ERR_UNSUPPORTED:
+            _check(r.dtype == torch.float16,
+                   "the kk / a-gate stage outside the chunked family needs float16 tokens")
+            a = torch.empty_like(k)
+            b = torch.empty_like(k)
+            N.check(N.load().fr2_tmix_kk_a_gate_forward(
+                r.size(0), h, d, k.data_ptr(), k_k.data_ptr(), a0.data_ptr(), a12.data_ptr(),
+                k_a.data_ptr(), new_k.data_ptr(), a.data_ptr(), b.data_ptr(), stream),
+                "fr2_tmix_kk_a_gate_forward")
+            rc = N.fast().recurrent_fp32_forward(
+                lq.data_ptr(), ls.data_ptr(), status.data_ptr(), n, h, d, r.size(0), int(ms),
+                _dtype_code(r), state.data_ptr(), r.data_ptr(), decay_logits.data_ptr(),
+                N.ptr(decay_bias), new_k.data_ptr(), v.data_ptr(), a.data_ptr(), b.data_ptr(),
+                output.data_ptr(), float(scale), stream)
+    N.check(rc, "tmix_wkv7_recurrent_fp32_from_kk_gate")
+    del keep
+
+
 @functools.lru_cache(maxsize=256)
 def _library_split_plan(num_sequences: int, num_heads: int, head_size: int,
                         max_seqlen: int) -> tuple[int, int, int, int]:
@@ -1300,6 +1348,7 @@ def exported_names() -> Sequence[str]:
         "prepare_tmix_wkv7_recurrent_graph_metadata",
         "tmix_wkv7_recurrent_fp32_from_decay_logits",
         "tmix_wkv7_recurrent_fp16_from_decay_logits",
+        "tmix_wkv7_recurrent_fp32_from_kk_gate",
         "pretrain_tmix_wkv7_recurrent_forward",
         "pretrain_tmix_wkv7_recurrent_backward",
         "statetune_tmix_wkv7_recurrent_fp32io16_forward",

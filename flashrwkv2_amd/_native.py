@@ -73,6 +73,11 @@ SIGNATURES: dict[str, tuple] = {
          c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int32, c_int32,
          c_int32, c_void_p],
     ),
+    "fr2_wkv7_recurrent_fp32_forward_kk_gate": (
+        c_int32,
+        [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64,
+         c_int32, c_int32] + [c_void_p] * 12 + [c_float, c_void_p],
+    ),
     "fr2_wkv7_recurrent_fp16_forward": (
         c_int32,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64,

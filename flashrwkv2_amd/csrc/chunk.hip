@@ -139,12 +139,20 @@ struct KeyRegs {
 // kUnitW: reverse mode, where unit_w marks a lane whose shifted retention
 // row lies past the segment (unit retention).
 // kSum: summary pass (no R~ operands, no R-side blocks).
-template <class Io, bool kVExact, bool kFull, bool kUnitW = false, bool kSum = false>
+// Per-lane channel parameters of the fused kk / a-gate stage: k_k for the
+// lane's keys of both key halves (own first), a0 and k_a for its own keys.
+struct KkParams {
+  float kk_own[8], kk_other[8], a0[8], ka[8];
+};
+
+template <class Io, bool kVExact, bool kFull, bool kUnitW = false, bool kSum = false,
+          bool kKK = false>
 __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& op,
                                           const u32x4 (&raw)[6], const float (&nbias8)[8],
                                           bool valid, int mp, int cc, int hh, int i, int q,
                                           KeyRegs& kr, bool unit_w = false,
-                                          float kscale = 1.0f) {
+                                          float kscale = 1.0f, const KkParams* kp = nullptr,
+                                          typename Io::raw* new_k_row = nullptr) {
   const int kbase = 32 * hh + 8 * q;
   // tokens past the sequence end (their rows repeat the last token) carry
   // zero operands and a unit retention
@@ -154,16 +162,79 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
   if constexpr (!kSum) unpack8<Io>(tok(0), xr);
   unpack8<Io>(raw[1], xl);
   unpack8<Io>(tok(2), xk);
-  unpack8<Io>(tok(4), xa);
-  unpack8<Io>(tok(5), xb);
+  if constexpr (kKK) {
+    // Fused producer stage (the kk / a gate of wkv_prepare): raw[4] holds
+    // the a-gate logits a12 and raw[5] the same 8 key positions of the other
+    // key half, for the kk norm over all 64 keys:
+    //   u = k k_k, kk = u / max(|u|, 1e-12), g = sigmoid(a0 + a12),
+    //   k' = k (1 + (g - 1) k_a), a = -kk, b = kk g.
+    float xo[8], x12[8];
+    unpack8<Io>(tok(5), xo);
+    unpack8<Io>(tok(4), x12);
+    float u[8], ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      u[e] = xk[e] * kp->kk_own[e];
+      const float w = xo[e] * kp->kk_other[e];
+      ss = __builtin_fmaf(u[e], u[e], __builtin_fmaf(w, w, ss));
+    }
+    // the four lanes of token i (groups q = 0..3) hold all 64 keys
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    const float inv = __builtin_amdgcn_rcpf(fmaxf(__builtin_sqrtf(ss), 1.0e-12f));
+    float nk[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float g = __builtin_amdgcn_rcpf(
+          1.0f + __builtin_amdgcn_exp2f(-kLog2e * (kp->a0[e] + x12[e])));
+      const float kk = u[e] * inv;
+      nk[e] = xk[e] * __builtin_fmaf(g - 1.0f, kp->ka[e], 1.0f);
+      xa[e] = -kk;
+      xb[e] = kk * g;
+    }
+    if (new_k_row != nullptr && (kFull || valid)) {
+      u32x4 packed;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = __builtin_bit_cast(uint16_t, Io::from_f32(nk[2 * j]));
+        const uint32_t hi = __builtin_bit_cast(uint16_t, Io::from_f32(nk[2 * j + 1]));
+        packed[j] = lo | (hi << 16);
+      }
+      *reinterpret_cast<u32x4*>(new_k_row) = packed;
+    }
+    // the recurrence uses the gated key (masked rows stay zero)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xk[e] = (kFull || valid) ? nk[e] : 0.0f;
+  } else {
+    unpack8<Io>(tok(4), xa);
+    unpack8<Io>(tok(5), xb);
+  }
   // base-2 log of the retention, log2(w) = c sigmoid(x) with
   // c = -exp(-1/2) log2(e), evaluated as 1 / ((1 + 2^(-log2(e) x)) / c)
   constexpr float kC = kNegExpHalf * kLog2e;
   constexpr float kInvC = 1.0f / kC;
+  float at[8], rt[8], bh[8], kh[8];
+  if constexpr (kSum) {
+    // key by key: the summary pass runs 12 waves (168 registers each), where
+    // the staged form below would spill
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float ex = __builtin_amdgcn_exp2f(__builtin_fmaf(xl[e], -kLog2e, nbias8[e]));
+      float lw2 = __builtin_amdgcn_rcpf(__builtin_fmaf(ex, kInvC, kInvC));
+      if constexpr (!kFull) lw2 = valid ? lw2 : 0.0f;
+      const float g2 = row_scan(lw2);
+      const float gm = __builtin_amdgcn_exp2f(g2);
+      const float ig = __builtin_amdgcn_exp2f(-g2);
+      at[e] = xa[e] * row_prev(gm, 1.0f);
+      bh[e] = xb[e] * ig;
+      kh[e] = xk[e] * ig;
+      if (i == L - 1) op.gl[kbase + e] = gm;
+    }
+  } else {
   // Stage by stage over the lane's eight keys: the eight chains are
   // independent, so each stage's instructions (DPP steps included) issue
   // back to back instead of waiting on one key's dependent chain.
-  float g2[8], gm[8], gp[8], at[8], rt[8], bh[8], kh[8];
+  float g2[8], gm[8], gp[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e)
     g2[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(xl[e], -kLog2e, nbias8[e]));
@@ -199,6 +270,7 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
   if (i == L - 1) {
     *reinterpret_cast<f32x4*>(&op.gl[kbase]) = f32x4{gm[0], gm[1], gm[2], gm[3]};
     *reinterpret_cast<f32x4*>(&op.gl[kbase + 4]) = f32x4{gm[4], gm[5], gm[6], gm[7]};
+  }
   }
   kr.As = split8(at);
   if constexpr (!kSum) kr.Rs = split8(rt);
@@ -549,7 +621,7 @@ __device__ __forceinline__ void wait_min_ge(int* c, int v, int limit, int* fault
 // an identity start with V = 0 (Phi), to split_summary[(n * (pieces - 1) +
 // j) * 2 + {0: F, 1: Phi}, H, D, D].  Nothing else is written.
 constexpr int NT_SUM = 768;
-template <class Io, bool kTrain, bool kRev = false, bool kSum = false>
+template <class Io, bool kTrain, bool kRev = false, bool kSum = false, bool kKK = false>
 __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) {
   using raw = typename Io::raw;
   constexpr bool kVExact = !__is_same(Io, IoF16);
@@ -626,8 +698,9 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
   const int kind = kSum ? (wv >> 2) : 0;
   const int64_t sbase = (static_cast<int64_t>(slot) * H + h) * D * D;
   const int64_t pbase = (static_cast<int64_t>(seq) * (npc > 0 ? npc : 1) + piece) * H + h;
-  f32x4 S[4];
+  constexpr int kStateThreads = 64 * kStateWaves;
   if (wv < kStateWaves) {
+    f32x4 S[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) S[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     // state of a piece after the first (real split pass): the combined
@@ -737,6 +810,67 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
       if (gi + 1 < ngroups) group(std::integral_constant<int, 1>{}, gi + 1);
     }
     if constexpr (!kSum) write_out(ngroups - 1);
+    // Every wave has left its loop (the key waves meet this barrier at the
+    // end of their branch); a raised fault flag means a hand-off wait gave
+    // up, so the values computed are not trustworthy: fail closed.
+    __syncthreads();
+    if (peek(&sm.fault) != 0) {
+      if (tid == 0 && p.handoff_fault != nullptr) atomicAdd(p.handoff_fault, 1);
+      const float qnan = quiet_nan();
+      if constexpr (kSum) {
+        // the pieces that start from this summary come out NaN as well
+        float* sout = p.split_summary + (static_cast<int64_t>(seg) * 2 * H + h) * D * D;
+        for (int e = tid; e < D * D; e += kStateThreads) {
+          sout[e] = qnan;
+          sout[static_cast<int64_t>(H) * D * D + e] = qnan;
+        }
+      } else {
+        const raw nanv = Io::from_f32(qnan);
+        for (int64_t e = tid; e < static_cast<int64_t>(t1 - t0) * D; e += kStateThreads)
+          yout[(t0 + e / D) * row_stride + head_off + e % D] = nanv;
+        if constexpr (kTrain) {
+          for (int64_t e = tid; e < static_cast<int64_t>(t1 - t0) * D; e += kStateThreads)
+            p.sa_out[(t0 + e / D) * row_stride + head_off + e % D] = qnan;
+        }
+        if (npc > 0 && p.split_lead_pass && piece == 0 && !last_piece) {
+          // the lead piece's successor starts from NaN
+          float* sout = p.split_state + (pbase + H) * D * D;
+          for (int e = tid; e < D * D; e += kStateThreads) sout[e] = qnan;
+        }
+      }
+      return;
+    }
+    if constexpr (kSum) {
+      float* sout = p.split_summary + ((static_cast<int64_t>(seg) * 2 + kind) * H + h) * D * D;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
+    } else if (!last_piece) {
+      // a piece before the last hands on nothing (its successor starts from
+      // the combined state), except the lead pass's piece 0, whose end state
+      // is piece 1's start
+      if (p.split_lead_pass && piece == 0) {
+        float* sout = p.split_state + (pbase + H) * D * D;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
+      }
+    } else if (p.state_out != nullptr) {
+      float* sout = static_cast<float*>(p.state_out);
+      uint16_t* soutb = static_cast<uint16_t*>(p.state_out);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t at = sbase + (kb * 16 + 4 * q + e) * D + vcol;
+          if (p.state_bf16)
+            soutb[at] = IoBF16::from_f32(S[kb][e]);
+          else
+            sout[at] = S[kb][e];
+        }
+    }
   } else {
     // ---------------- key waves: chunk cc of each group, key half hh
     // The key waves are the pipeline's critical path and share each SIMD
@@ -752,6 +886,20 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
     for (int e = 0; e < 8; ++e)
       nbias8[e] = p.bias ? -kLog2e * Io::to_f32(static_cast<const raw*>(p.bias)[head_off + kbase + e])
                          : 0.f;
+    const int kbase_other = 32 * (hh ^ 1) + 8 * q;
+    KkParams kp;
+    if constexpr (kKK) {
+      const raw* kks = static_cast<const raw*>(p.kk_scale) + head_off;
+      const raw* a0 = static_cast<const raw*>(p.a_bias) + head_off;
+      const raw* ka = static_cast<const raw*>(p.k_a) + head_off;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        kp.kk_own[e] = Io::to_f32(kks[kbase + e]);
+        kp.kk_other[e] = Io::to_f32(kks[kbase_other + e]);
+        kp.a0[e] = Io::to_f32(a0[kbase + e]);
+        kp.ka[e] = Io::to_f32(ka[kbase + e]);
+      }
+    }
     // token rows of this lane (token i of chunk cc, keys kbase..+7), as
     // running pointers; the group stride is GT rows
     const int tok0 = t0 + cc * L + i;
@@ -763,7 +911,9 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
       src[2] = static_cast<const raw*>(p.k) + off;
       src[3] = static_cast<const raw*>(p.v) + off;
       src[4] = static_cast<const raw*>(p.a) + off;
-      src[5] = static_cast<const raw*>(p.b) + off;
+      // fused kk / a gate: slot 5 reads the key's other half instead of b
+      src[5] = kKK ? static_cast<const raw*>(p.k) + off + (kbase_other - kbase)
+                   : static_cast<const raw*>(p.b) + off;
     }
     const int64_t gstride = static_cast<int64_t>(GT) * row_stride;
     // Rows past the sequence end are loaded from the last valid row (always
@@ -823,12 +973,18 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
                                               t0 + gn * GT + cc * L + i < t1, par, cc, hh, i, q,
                                               kr, unit_w, p.kv_scale);
       } else {
+        raw* nk_row = nullptr;
+        if constexpr (kKK)
+          nk_row = static_cast<raw*>(p.new_k) +
+                   static_cast<int64_t>(tok0 + gn * GT) * row_stride + head_off + kbase;
         if (t0 + gn * GT + cc * L + L <= t1)
-          key_part1<Io, kVExact, true, false, kSum>(sm, sm.ops[par][cc], cur, nbias8, true, par,
-                                                    cc, hh, i, q, kr);
+          key_part1<Io, kVExact, true, false, kSum, kKK>(sm, sm.ops[par][cc], cur, nbias8, true,
+                                                         par, cc, hh, i, q, kr, false, 1.0f, &kp,
+                                                         nk_row);
         else if (active)
-          key_part1<Io, kVExact, false, false, kSum>(sm, sm.ops[par][cc], cur, nbias8,
-                                                     tok0 + gn * GT < t1, par, cc, hh, i, q, kr);
+          key_part1<Io, kVExact, false, false, kSum, kKK>(sm, sm.ops[par][cc], cur, nbias8,
+                                                          tok0 + gn * GT < t1, par, cc, hh, i, q,
+                                                          kr, false, 1.0f, &kp, nk_row);
       }
       signal(&sm.part1[kw], gn + 1);
       wait_ge(&sm.part1[partner], gn + 1, p.spin_limit, &sm.fault);
@@ -840,69 +996,9 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
       if (gn + 1 < ngroups) iter(std::integral_constant<int, 1>{}, rawB, rawA, gn + 1);
     }
     __builtin_amdgcn_s_setprio(0);
+    __syncthreads();   // pairs with the state waves' final barrier
   }
 
-  // Every wave has left its loop; a raised fault flag means a hand-off wait
-  // gave up, so the values computed are not trustworthy: fail closed.
-  __syncthreads();
-  if (peek(&sm.fault) != 0) {
-    if (tid == 0 && p.handoff_fault != nullptr) atomicAdd(p.handoff_fault, 1);
-    const float qnan = quiet_nan();
-    if constexpr (kSum) {
-      // the pieces that start from this summary come out NaN as well
-      float* sout = p.split_summary + (static_cast<int64_t>(seg) * 2 * H + h) * D * D;
-      for (int e = tid; e < D * D; e += NT_SUM) {
-        sout[e] = qnan;
-        sout[static_cast<int64_t>(H) * D * D + e] = qnan;
-      }
-    } else {
-      const raw nanv = Io::from_f32(qnan);
-      for (int64_t e = tid; e < static_cast<int64_t>(t1 - t0) * D; e += NT)
-        yout[(t0 + e / D) * row_stride + head_off + e % D] = nanv;
-      if constexpr (kTrain) {
-        for (int64_t e = tid; e < static_cast<int64_t>(t1 - t0) * D; e += NT)
-          p.sa_out[(t0 + e / D) * row_stride + head_off + e % D] = qnan;
-      }
-      if (npc > 0 && p.split_lead_pass && piece == 0 && !last_piece) {
-        // the lead piece's successor starts from NaN
-        float* sout = p.split_state + (pbase + H) * D * D;
-        for (int e = tid; e < D * D; e += NT) sout[e] = qnan;
-      }
-    }
-    return;
-  }
-  if (wv >= kStateWaves) return;
-  if constexpr (kSum) {
-    float* sout = p.split_summary + ((static_cast<int64_t>(seg) * 2 + kind) * H + h) * D * D;
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
-  } else if (!last_piece) {
-    // a piece before the last hands on nothing (its successor starts from
-    // the combined state), except the lead pass's piece 0, whose end state
-    // is piece 1's start
-    if (p.split_lead_pass && piece == 0) {
-      float* sout = p.split_state + (pbase + H) * D * D;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
-    }
-  } else if (p.state_out != nullptr) {
-    float* sout = static_cast<float*>(p.state_out);
-    uint16_t* soutb = static_cast<uint16_t*>(p.state_out);
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t at = sbase + (kb * 16 + 4 * q + e) * D + vcol;
-        if (p.state_bf16)
-          soutb[at] = IoBF16::from_f32(S[kb][e]);
-        else
-          sout[at] = S[kb][e];
-      }
-  }
 }
 
 }  // namespace
@@ -957,6 +1053,26 @@ int launch_chunked(int dtype, const SegArgs& args, int nseg, int max_seqlen, hip
   } else {
     return FR2_ERR_UNSUPPORTED;
   }
+  return record_launch();
+}
+
+int launch_chunked_kk(int dtype, const SegArgs& args, int nseg, hipStream_t s) {
+  if (args.sa_out != nullptr || args.boundary != nullptr || args.reverse ||
+      args.split_pieces > 0 || args.state_bf16 || args.kk_scale == nullptr ||
+      args.a_bias == nullptr || args.k_a == nullptr || args.new_k == nullptr)
+    return FR2_ERR_INVALID_ARGUMENT;
+  SegArgs p = args;
+  p.spin_limit = handoff_spin_limit();
+  p.handoff_fault = handoff_fault_word();
+  const dim3 grid(p.num_heads, nseg);
+  if (dtype == FR2_DTYPE_BFLOAT16)
+    hipLaunchKernelGGL((chunk64_kernel<IoBF16, false, false, false, true>), grid, dim3(NT), 0, s,
+                       p);
+  else if (dtype == FR2_DTYPE_FLOAT16)
+    hipLaunchKernelGGL((chunk64_kernel<IoF16, false, false, false, true>), grid, dim3(NT), 0, s,
+                       p);
+  else
+    return FR2_ERR_UNSUPPORTED;
   return record_launch();
 }
 

@@ -84,6 +84,13 @@ struct SegArgs {
   // then fails closed: NaN outputs, state untouched)
   int spin_limit = 1 << 20;
   int* handoff_fault = nullptr;
+  // Fused kk / a-gate producer stage (chunked kernel only): `k` holds the
+  // projected key, `a` the low-rank a-gate logits a12, `b` is unused; per
+  // channel k_k, a0, k_a ([H, D]); the gated key is written to new_k.
+  const void* kk_scale = nullptr;
+  const void* a_bias = nullptr;
+  const void* k_a = nullptr;
+  void* new_k = nullptr;
 };
 
 // Token range [start, start + len) of piece j of a split sequence of n
@@ -107,6 +114,9 @@ int launch_fp16_state(int D, const SegArgs& p, int nseg, int max_seqlen, int32_t
 int launch_advance_elapsed(const SegArgs& p, int nseg, int32_t* elapsed, hipStream_t s);
 // Chunked MFMA prefill (D = 64, fp32 state).  Returns FR2_ERR_UNSUPPORTED
 // for contracts it does not cover (sa output / boundaries / bf16 state).
+// The chunked kernel with the kk / a-gate stage fused into its load stage
+// (p.kk_scale, p.a_bias, p.k_a, p.new_k set).
+int launch_chunked_kk(int dtype, const SegArgs& p, int nseg, hipStream_t s);
 int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen,
                    hipStream_t s);
 // Sequence-split chunked prefill (D = 64, fp32 state, plain contract):

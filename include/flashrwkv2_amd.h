@@ -186,6 +186,32 @@ int fr2_wkv7_recurrent_fp32_forward_split(
     void* aux_stream);
 
 /*
+ * The packed fp32-state recurrence with wkv_prepare's kk / a-gate stage
+ * fused into the chunked kernel's load stage (fp16 or bf16 tokens,
+ * head_size 64).  Inputs: r, decay_logits, v as for
+ * fr2_wkv7_recurrent_fp32_forward; k the projected key (before the gate);
+ * a12 the low-rank a-gate logits [total_tokens, H, 64]; k_k, a0, k_a the
+ * per-channel parameters [H * 64].  Per (token, head) the kernel forms
+ *   u = k k_k, kk = u / max(|u|, 1e-12), g = sigmoid(a0 + a12),
+ *   key = k (1 + (g - 1) k_a), a = -kk, b = kk g
+ * in fp32, runs the recurrence on (key, a, b) and writes key to new_k (the
+ * readout's input); a and b are never stored.  FR2_ERR_UNSUPPORTED outside
+ * the chunked family (head_size 64, max_seqlen >= 40): the caller then runs
+ * fr2_tmix_kk_a_gate_forward and fr2_wkv7_recurrent_fp32_forward.  Replaces
+ * the pair tmix_kk_a_gate_forward_varlen_cuda
+ * (csrc/sm120/tmix/wkv_prepare/internal/kk_a_gate/infer_fp16_forward_varlen.cu)
+ * + tmix_wkv7_recurrent_fp32_from_decay_logits_cuda
+ * (…/infer_recurrent_fp32io16_forward_varlen.cu:457-517), which the reference
+ * runs as two kernels with k, a, b round-tripping through HBM.
+ */
+int fr2_wkv7_recurrent_fp32_forward_kk_gate(
+    const int32_t* query_start_loc, const int32_t* state_indices, const int32_t* status,
+    int32_t num_sequences, int32_t num_heads, int32_t head_size, int64_t total_tokens,
+    int32_t max_seqlen, int32_t dtype, float* state, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a12, const void* k_k,
+    const void* a0, const void* k_a, void* new_k, void* output, float scale, void* stream);
+
+/*
  * fr2_wkv7_recurrent_fp32_forward_split without a workspace argument: the
  * library's own device scratch array (FR2_NOALLOC_SCRATCH_BYTES per GPU, held
  * until the process ends) replaces it, and the call allocates nothing (no

@@ -1,0 +1,139 @@
+"""The chunked recurrence with wkv_prepare's kk / a-gate stage in its load
+stage, against the fp64 oracle composed from its two stages:
+``oracle.prepare.kk_a_gate_f64`` (the gate: gated key, a = -kk, b = kk*g)
+followed by ``oracle.wkv7_f64`` on exactly those values.
+
+The fused kernel forms a and b in fp32 and never rounds them to the token
+dtype, so it is compared with the unrounded fp64 composition, under the same
+output/state gates as every recurrent test (tests/wkv7_testlib.py).  The
+gated key it writes is compared elementwise with the oracle's: one rounding
+of an fp32 value to the token dtype, so |dk| <= 2^-p |k| + 1e-6 with p = 10
+for fp16 and 7 for bf16 (one ulp; half an ulp plus the fp32 arithmetic).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from wkv7_testlib import assert_output_close, assert_state_close, require_gpu, to_np
+
+import oracle
+from oracle.prepare import kk_a_gate_f64
+
+pytestmark = pytest.mark.gpu
+
+_ULP_BITS = {torch.float16: 10, torch.bfloat16: 7}
+
+
+def _case(lengths, heads, dtype, seed, *, bias=False):
+    g = torch.Generator().manual_seed(seed)
+    total, d = sum(lengths), 64
+    shape = (total, heads, d)
+
+    def rnd(*s, scale=1.0, shift=0.0):
+        return (torch.randn(s, generator=g) * scale + shift).to(dtype)
+
+    c = {
+        "r": rnd(*shape, scale=0.3),
+        "w": (torch.rand(shape, generator=g) * 5.5 - 6.0).to(dtype),
+        "k": rnd(*shape, scale=0.7),
+        "v": rnd(*shape, scale=0.5),
+        "a12": rnd(*shape, scale=1.0),
+        "k_k": rnd(heads * d, scale=0.2, shift=0.85),
+        "a0": rnd(heads * d, scale=0.5),
+        "k_a": torch.rand(heads * d, generator=g).to(dtype),
+        "bias": rnd(heads, d, scale=0.2) if bias else None,
+    }
+    n = len(lengths)
+    c["cu"] = torch.tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int32)
+    c["slots"] = torch.randperm(n + 3, generator=g)[:n].to(torch.int32)
+    c["pool"] = torch.randn((n + 3, heads, d, d), generator=g) * 0.05
+    return c
+
+
+def _expected(c, scale):
+    total, heads, d = c["k"].shape
+    flat = lambda t: to_np(t).reshape(total, heads * d)   # noqa: E731
+    new_k, a, b = kk_a_gate_f64(flat(c["k"]), to_np(c["k_k"]), to_np(c["a0"]), flat(c["a12"]),
+                                to_np(c["k_a"]), d)
+    shaped = [x.reshape(total, heads, d) for x in (new_k, a, b)]
+    y, pool, _, _ = oracle.wkv7_f64(
+        to_np(c["r"]), to_np(c["w"]), shaped[0], to_np(c["v"]), shaped[1], shaped[2],
+        cu_seqlens=c["cu"].numpy(), state_indices=c["slots"].numpy(),
+        state_pool=c["pool"].numpy(),
+        decay_bias=None if c["bias"] is None else to_np(c["bias"]), scale=scale)
+    return y, pool, shaped[0]
+
+
+def _run(c, scale, max_seqlen=None):
+    from flashrwkv2_amd.tmix.wkv7 import infer_tmix_wkv7_kk_gate_recurrent_forward_varlen
+    dev = {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in c.items()}
+    pool = dev["pool"].clone()
+    y, new_k = infer_tmix_wkv7_kk_gate_recurrent_forward_varlen(
+        dev["r"], dev["w"], dev["k"], dev["v"], dev["a12"], k_k=dev["k_k"], a0=dev["a0"],
+        k_a=dev["k_a"], state_pool=pool, cu_seqlens=dev["cu"], state_indices=dev["slots"],
+        scale=scale, decay_bias=dev["bias"], max_seqlen=max_seqlen)
+    torch.cuda.synchronize()
+    return y, pool, new_k
+
+
+def _check_key(actual, expected, dtype):
+    a = to_np(actual).astype(np.float64)
+    bound = 2.0 ** -_ULP_BITS[dtype] * np.abs(expected) + 1.0e-6
+    worst = float(np.max(np.abs(a - expected) - bound))
+    assert worst <= 0.0, f"gated key off by {worst:.3e} beyond one ulp"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("lengths,heads,bias", [
+    ((40, 1, 63, 130, 17), 3, False),
+    ((300, 64, 96, 41), 4, True),
+], ids=["ragged", "bias"])
+def test_fused_kk_gate_matches_the_two_stage_oracle(dtype, lengths, heads, bias):
+    require_gpu()
+    print(f"case kk-gate fused {dtype} lengths {lengths} H {heads} bias {bias}", flush=True)
+    c = _case(lengths, heads, dtype, seed=sum(lengths) + heads, bias=bias)
+    y, pool, new_k = _run(c, 0.8)
+    ey, epool, ek = _expected(c, 0.8)
+    assert_output_close(y, ey)
+    touched = c["slots"].long()
+    assert_state_close(to_np(pool)[touched], epool[touched])
+    untouched = sorted(set(range(c["pool"].shape[0])) - set(touched.tolist()))
+    assert torch.equal(pool.cpu()[untouched], c["pool"][untouched])
+    _check_key(new_k, ek, dtype)
+
+
+def test_short_batches_run_the_two_kernel_form():
+    """Below the chunked threshold the gate runs as its own kernel (fp16)."""
+    require_gpu()
+    print("case kk-gate short fp16", flush=True)
+    c = _case((1, 7, 39), 2, torch.float16, seed=9)
+    y, pool, new_k = _run(c, 1.0)
+    ey, epool, ek = _expected(c, 1.0)
+    # a and b are rounded to fp16 between the two kernels here
+    assert_output_close(y, ey)
+    touched = c["slots"].long()
+    assert_state_close(to_np(pool)[touched], epool[touched])
+    _check_key(new_k, ek, torch.float16)
+
+
+def test_short_bf16_batches_are_rejected():
+    require_gpu()
+    c = _case((5, 9), 2, torch.bfloat16, seed=11)
+    with pytest.raises(Exception, match="float16 tokens"):
+        _run(c, 1.0)
+
+
+def test_config1_shape_fp16():
+    """BASELINE config 1 (8 x 4096 tokens, 32 heads) through the fused entry."""
+    require_gpu()
+    print("case kk-gate config-1 shape fp16", flush=True)
+    c = _case([4096] * 8, 32, torch.float16, seed=1001)
+    y, pool, new_k = _run(c, 1.0)
+    ey, epool, ek = _expected(c, 1.0)
+    assert_output_close(y, ey)
+    touched = c["slots"].long()
+    assert_state_close(to_np(pool)[touched], epool[touched])
+    _check_key(new_k, ek, torch.float16)
