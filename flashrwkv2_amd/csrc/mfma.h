@@ -18,12 +18,12 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x4 mma32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -32,11 +32,21 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16(float x0, float x1) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, bf16x2));
 }
-// hi/lo split of two values: hi = bf16(x), lo = bf16(x - hi), packed pairs
-// (three VALU instructions per value)
+// hi/lo split of two values: hi = bf16(x), lo = bf16(x - hi), packed pairs.
+// The residuals x - hi come from v_dot2c_f32_bf16 against the packed pairs
+// (-1, 0) and (0, -1): x + (-1) hi + 0 = x - hi, which is exact in fp32 (hi
+// is x rounded to 8 significant bits), so no intermediate rounding occurs.
+// Two VALU instructions per value (two conversions and two dot products per
+// pair) instead of three with an explicit widening of hi.
 __device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
-  hi = pack_bf16(x0, x1);
-  lo = pack_bf16(x0 - __uint_as_float(hi << 16), x1 - __uint_as_float(hi & 0xffff0000u));
+  // the selector pairs are passed in scalar registers
+  uint32_t m0 = 0x0000bf80u, m1 = 0xbf800000u;
+  asm("" : "+s"(m0), "+s"(m1));
+  const bf16x2 h = __builtin_bit_cast(bf16x2, pack_bf16(x0, x1));
+  const float r0 = __builtin_amdgcn_fdot2_f32_bf16(h, __builtin_bit_cast(bf16x2, m0), x0, false);
+  const float r1 = __builtin_amdgcn_fdot2_f32_bf16(h, __builtin_bit_cast(bf16x2, m1), x1, false);
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = pack_bf16(r0, r1);
 }
 
 struct Sp8 { bf16x8 hi, lo; };
