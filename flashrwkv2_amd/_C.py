@@ -160,6 +160,10 @@ class _RecurrentMetadataTicket:
         self._graph = bool(graph_mode)
         self._device = qsl.device
         self._stream_handle = stream
+        # the same facts for the native fast path (hostpath.cpp)
+        self._facts = N.hostpath().TicketFacts(qsl, slots, qsl_snap, slots_snap, status,
+                                                self._total_tokens, self._pool_size,
+                                                self._max_seqlen_v, self._graph, stream)
 
     def _check_compatible(self, query_start_loc, state_indices, total_tokens,
                           state_pool_size, max_seqlen) -> None:
@@ -303,6 +307,31 @@ def prepare_tmix_wkv7_recurrent_metadata(query_start_loc, state_indices, total_t
     return _RecurrentMetadataTicket(query_start_loc, state_indices, snap_q, snap_s, status,
                                     seen, None, None, total_tokens, state_pool_size,
                                     max_seqlen, False, stream)
+
+
+def _prepare_graph_fast(query_start_loc, state_indices, num_active_tokens,
+                        num_active_sequences, token_capacity, sequence_capacity,
+                        state_pool_size, max_seqlen_capacity):
+    """The graph ticket through the native fast path (hostpath.cpp), or None
+    when the call is not plainly valid there (the caller then runs
+    prepare_tmix_wkv7_recurrent_graph_metadata, which raises or prepares)."""
+    try:
+        stream = _raw_stream(query_start_loc.get_device())
+        res = N.hostpath().prepare_graph(query_start_loc, state_indices, num_active_tokens,
+                                         num_active_sequences, token_capacity,
+                                         sequence_capacity, state_pool_size,
+                                         max_seqlen_capacity, stream)
+    except (TypeError, RuntimeError, AttributeError):
+        return None
+    if res is None:
+        return None
+    if isinstance(res, int):
+        N.check(res, "prepare_tmix_wkv7_recurrent_metadata")
+    status, seen = res
+    return _RecurrentMetadataTicket(query_start_loc, state_indices, query_start_loc,
+                                    state_indices, status, seen, num_active_tokens,
+                                    num_active_sequences, token_capacity, state_pool_size,
+                                    max_seqlen_capacity, True, stream)
 
 
 def _check_graph_scalar(t, ref, name):
@@ -589,6 +618,26 @@ def split_plan(num_sequences: int, num_heads: int, head_size: int, max_seqlen: i
     # caching allocator only hands them out again to work queued later on this
     # same stream, which runs after the kernels that read them.
     del keep
+
+
+def _recurrent_fp32_fast(query_start_loc, state_indices, state, r, decay_logits, k, v, a, b,
+                         scale, ticket, max_seqlen):
+    """The ticketed recurrence without decay bias through the native fast path
+    (hostpath.cpp): the output, or None when the call is not plainly valid
+    there or needs the sequence split (the caller then runs the full path,
+    which raises or launches)."""
+    facts = getattr(ticket, "_facts", None)
+    if facts is None:
+        return None
+    try:
+        res = N.hostpath().recurrent_fp32(facts, query_start_loc, state_indices, state, r,
+                                          decay_logits, k, v, a, b, scale, max_seqlen,
+                                          _raw_stream(ticket._device.index))
+    except (TypeError, RuntimeError):
+        return None
+    if isinstance(res, int):
+        N.check(res, "tmix_wkv7_recurrent_fp32_from_decay_logits")
+    return res
 
 
 def tmix_wkv7_recurrent_fp32_from_decay_logits(query_start_loc, state_indices, state, r,

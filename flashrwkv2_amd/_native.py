@@ -218,6 +218,33 @@ def fast():
     return _FAST
 
 
+_HOST = None
+
+
+def hostpath():
+    """The torch C++ extension with the native fast path of the per-step
+    ticket and recurrence calls (built next to the library by
+    :mod:`flashrwkv2_amd.build`; it links the library).  Loaded once."""
+    global _HOST
+    if _HOST is None:
+        import importlib.machinery
+        import importlib.util
+
+        from .build import hostpath_name
+
+        load()
+        path = LIB_PATH.parent / hostpath_name()
+        if not path.exists():
+            raise RuntimeError(f"flashrwkv2_amd host-path module not built: {path} is missing; "
+                               "run `python -m flashrwkv2_amd.build`")
+        loader = importlib.machinery.ExtensionFileLoader("_hostpath", str(path))
+        spec = importlib.util.spec_from_file_location("_hostpath", path, loader=loader)
+        module = importlib.util.module_from_spec(spec)
+        loader.exec_module(module)
+        _HOST = module
+    return _HOST
+
+
 def check(status: int, what: str) -> None:
     """Raise RuntimeError for a non-zero fr2_status_t."""
     if status == FR2_OK:

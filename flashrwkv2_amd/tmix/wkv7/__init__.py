@@ -109,6 +109,15 @@ def prepare_tmix_wkv7_recurrent_metadata(
     needs; warm up with zero active counts, then prepare again inside capture
     and reuse that ticket for the graph's operators.
     """
+    if (num_active_tokens is not None and total_tokens is None and max_seqlen is None
+            and type(token_capacity) is int and type(sequence_capacity) is int
+            and type(state_pool_size) is int and type(max_seqlen_capacity) is int):
+        # the per-step serving case: decided natively when plainly valid
+        ticket = _extension()._prepare_graph_fast(
+            cu_seqlens, state_indices, num_active_tokens, num_active_sequences,
+            token_capacity, sequence_capacity, state_pool_size, max_seqlen_capacity)
+        if ticket is not None:
+            return ticket
     _check_metadata_inputs(cu_seqlens, state_indices)
     live = (token_capacity, sequence_capacity, max_seqlen_capacity,
             num_active_tokens, num_active_sequences)
@@ -168,6 +177,14 @@ def infer_tmix_wkv7_recurrent_fp32io16_forward_varlen(
     ``[slots,H,D,D]``; returns the output ``[total_tokens,H,D]`` in the token
     dtype.  (…/wkv7/__init__.py:179-256.)
     """
+    if (validated_metadata is not None and decay_bias is None
+            and type(scale) in (float, int) and (max_seqlen is None or type(max_seqlen) is int)):
+        # the per-step serving case: decided natively when plainly valid
+        output = _extension()._recurrent_fp32_fast(
+            cu_seqlens, state_indices, state_pool, r, decay_logits, k, v, a, b, float(scale),
+            validated_metadata, -1 if max_seqlen is None else max_seqlen)
+        if output is not None:
+            return output
     packed = _validate_packed_inputs(r, decay_logits, k, v, a, b)
     _validate_state(state_pool)
     _check_metadata_inputs(cu_seqlens, state_indices)

@@ -8,6 +8,8 @@ from pathlib import Path
 
 import pytest
 
+import torch
+
 from flashrwkv2_amd import _native as N
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -158,3 +160,19 @@ def test_misaligned_token_pointers_are_rejected_before_any_launch(lib):
 def test_handoff_hooks_validate_their_arguments(lib):
     assert lib.fr2_handoff_fault_count(None, 0, None) == N.FR2_ERR_INVALID_ARGUMENT
     assert lib.fr2_debug_set_handoff_spin_limit(-1) == N.FR2_OK
+
+
+def test_fast_call_and_host_path_modules_load(lib):
+    """Both per-step modules are built next to the library and load on a
+    machine without a GPU (no compute calls)."""
+    from flashrwkv2_amd import _native as N
+
+    fast = N.fast()
+    for name in ("prepare_metadata", "recurrent_fp32_forward", "recurrent_fp32_forward_kernel"):
+        assert callable(getattr(fast, name))
+    host = N.hostpath()
+    for name in ("TicketFacts", "recurrent_fp32", "prepare_graph"):
+        assert hasattr(host, name)
+    # a CPU tensor is never plainly valid for the fast path: it declines
+    t = torch.zeros(1, dtype=torch.int32)
+    assert host.prepare_graph(t, t, t, t, 1, 1, 1, 1, 0) is None
