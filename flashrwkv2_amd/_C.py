@@ -539,7 +539,9 @@ def tmix_wkv7_recurrent_fp32_from_kk_gate(query_start_loc, state_indices, state,
     k is the projected key, a12 the a-gate logits, k_k / a0 / k_a the
     per-channel parameters ([H*D] or [H,D], token dtype); the gated key is
     written to new_k.  Outside the chunked family (head size 64, longest
-    sequence >= 40) the two stages run as separate kernels (fp16 tokens)."""
+    sequence >= 40), and for fp16 batches that the library's plan splits by
+    sequence (few long sequences: the split outruns one block per unit), the
+    gate runs as its own kernel and the recurrence through the public path."""
     n, h, d = check_recurrent_layout(query_start_loc, state_indices, state, r, decay_logits, k,
                                      v, a12, new_k, output, scale)
     for t, name in ((k_k, "k_k"), (a0, "a0"), (k_a, "k_a")):
@@ -553,28 +555,29 @@ def tmix_wkv7_recurrent_fp32_from_kk_gate(query_start_loc, state_indices, state,
     lq, ls, status, ms, keep = _resolve_launch_metadata(
         query_start_loc, state_indices, r.size(0), state.size(0), int(max_seqlen),
         validated_metadata)
-    with _on_device(state.device):
-        stream = _stream(state.device)
-        rc = N.load().fr2_wkv7_recurrent_fp32_forward_kk_gate(
-            lq.data_ptr(), ls.data_ptr(), status.data_ptr(), n, h, d, r.size(0), int(ms),
-            _dtype_code(r), state.data_ptr(), r.data_ptr(), decay_logits.data_ptr(),
-            N.ptr(decay_bias), k.data_ptr(), v.data_ptr(), a12.data_ptr(), k_k.data_ptr(),
-            a0.data_ptr(), k_a.data_ptr(), new_k.data_ptr(), output.data_ptr(), float(scale),
-            stream)
-        if rc == N.FR2_ERR_UNSUPPORTED:
-            _check(r.dtype == torch.float16,
-                   "the kk / a-gate stage outside the chunked family needs float16 tokens")
-            a = torch.empty_like(k)
-            b = torch.empty_like(k)
-            N.check(N.load().fr2_tmix_kk_a_gate_forward(
-                r.size(0), h, d, k.data_ptr(), k_k.data_ptr(), a0.data_ptr(), a12.data_ptr(),
-                k_a.data_ptr(), new_k.data_ptr(), a.data_ptr(), b.data_ptr(), stream),
-                "fr2_tmix_kk_a_gate_forward")
-            rc = N.fast().recurrent_fp32_forward(
+    fp16 = r.dtype == torch.float16
+    rc = N.FR2_ERR_UNSUPPORTED
+    if not (fp16 and d == 64 and int(ms) > 0 and split_plan(n, h, d, int(ms))[0] > 1):
+        with _on_device(state.device):
+            rc = N.load().fr2_wkv7_recurrent_fp32_forward_kk_gate(
                 lq.data_ptr(), ls.data_ptr(), status.data_ptr(), n, h, d, r.size(0), int(ms),
                 _dtype_code(r), state.data_ptr(), r.data_ptr(), decay_logits.data_ptr(),
-                N.ptr(decay_bias), new_k.data_ptr(), v.data_ptr(), a.data_ptr(), b.data_ptr(),
-                output.data_ptr(), float(scale), stream)
+                N.ptr(decay_bias), k.data_ptr(), v.data_ptr(), a12.data_ptr(), k_k.data_ptr(),
+                a0.data_ptr(), k_a.data_ptr(), new_k.data_ptr(), output.data_ptr(),
+                float(scale), _stream(state.device))
+    if rc == N.FR2_ERR_UNSUPPORTED:
+        _check(fp16, "the kk / a-gate stage outside the chunked family needs float16 tokens")
+        a = torch.empty_like(k)
+        b = torch.empty_like(k)
+        with _on_device(state.device):
+            N.check(N.load().fr2_tmix_kk_a_gate_forward(
+                r.size(0), h, d, k.data_ptr(), k_k.data_ptr(), a0.data_ptr(), a12.data_ptr(),
+                k_a.data_ptr(), new_k.data_ptr(), a.data_ptr(), b.data_ptr(),
+                _stream(state.device)), "fr2_tmix_kk_a_gate_forward")
+        _recurrent_launch(None, query_start_loc, state_indices, state, r, decay_logits, new_k,
+                          v, a, b, output, scale, decay_bias, validated_metadata, max_seqlen)
+        del keep
+        return
     N.check(rc, "tmix_wkv7_recurrent_fp32_from_kk_gate")
     del keep
 

@@ -137,3 +137,20 @@ def test_config1_shape_fp16():
     touched = c["slots"].long()
     assert_state_close(to_np(pool)[touched], epool[touched])
     _check_key(new_k, ek, torch.float16)
+
+
+def test_few_long_fp16_sequences_take_the_split():
+    """Few long fp16 sequences: the library's plan splits them by sequence, so
+    the gate runs as its own kernel and the recurrence takes the split."""
+    require_gpu()
+    from flashrwkv2_amd import _C
+
+    print("case kk-gate long fp16 split", flush=True)
+    c = _case([3000], 8, torch.float16, seed=21)
+    assert _C.split_plan(1, 8, 64, 3000)[0] > 1
+    y, pool, new_k = _run(c, 1.0)
+    ey, epool, ek = _expected(c, 1.0)
+    assert_output_close(y, ey)
+    touched = c["slots"].long()
+    assert_state_close(to_np(pool)[touched], epool[touched])
+    _check_key(new_k, ek, torch.float16)
