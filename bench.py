@@ -411,7 +411,11 @@ def time_kk_fused(torch, flashrwkv2_amd, steps: int):
     (kk_a_gate_kernel writes key, a, b; the chunked recurrence reads them
     back) against the chunked kernel that forms them in its load stage.  Both
     read the projected key and a12 and write the gated key and y, so the
-    fused form moves 14 B per (token, channel) where the pair moves 24 B."""
+    fused form moves 14 B per (token, channel) where the pair moves 24 B.
+    With the readout's elementwise stage (GroupNorm, the r k' r_k residual,
+    the gate) also in the kernel's write-back: three kernels move 36 B per
+    (token, channel), the fused one 16 B (it reads the gate and writes the
+    readout instead of y)."""
     from flashrwkv2_amd import _C as CC
     from flashrwkv2_amd import _native as N
     from flashrwkv2_amd import workloads
@@ -456,9 +460,31 @@ def time_kk_fused(torch, flashrwkv2_amd, steps: int):
             w.cu_seqlens, w.state_indices, state, r, logits, new_k, v, a, b, out, 1.0, None,
             ticket)
 
+    gate = torch.sigmoid(torch.randn((T, H, D), generator=g, device="cuda")).half()
+    rk = (torch.randn(C, generator=g, device="cuda") * 0.3).half()
+    lnw = (1.0 + 0.1 * torch.randn(C, generator=g, device="cuda")).half()
+    lnb = (0.1 * torch.randn(C, generator=g, device="cuda")).half()
+    ro = torch.empty_like(k)
+
+    def three_stage():
+        two_stage()
+        N.check(lib.fr2_tmix_readout_prelinear_forward(
+            T, H, D, out.data_ptr(), r.data_ptr(), new_k.data_ptr(), v.data_ptr(), rk.data_ptr(),
+            lnw.data_ptr(), lnb.data_ptr(), gate.data_ptr(), ro.data_ptr(), sh),
+            "fr2_tmix_readout_prelinear_forward")
+
+    def fused_ro():
+        CC.tmix_wkv7_recurrent_fp32_from_kk_gate_readout(
+            w.cu_seqlens, w.state_indices, state, r, logits, k, v, a12, gate, kk, a0, ka, rk,
+            lnw, lnb, new_k, ro, None, 1.0, None, ticket)
+
     two_ms = _events_ms(torch, two_stage, steps)
     fused_ms = _events_ms(torch, fused, steps)
     rec_ms = _events_ms(torch, recurrence, steps)
+    three_ms = _events_ms(torch, three_stage, steps)
+    fused_ro_ms = _events_ms(torch, fused_ro, steps)
+    three_bytes = 36 * T * C + state_bytes
+    fused_ro_bytes = 16 * T * C + state_bytes
     out_obj = {
         "workload": "cfg1_prefill_B8_T4096_H32_fp16_kk_gate", "total_tokens": T,
         "two_stage": {"ms_per_step": round(two_ms, 4),
@@ -471,8 +497,20 @@ def time_kk_fused(torch, flashrwkv2_amd, steps: int):
                   "roofline": roofline_obj(fused_bytes, fused_ms)},
         "recurrence_alone_ms": round(rec_ms, 4),
         "saved_ms": round(two_ms - fused_ms, 4),
+        "with_readout": {
+            "three_stage": {"ms_per_step": round(three_ms, 4),
+                            "kernels": "kk_a_gate_kernel<64> + chunk64_kernel<IoF16,false> + "
+                                       "readout_prelinear_kernel<64>",
+                            "algorithmic_bytes": three_bytes,
+                            "roofline": roofline_obj(three_bytes, three_ms)},
+            "fused": {"ms_per_step": round(fused_ro_ms, 4),
+                      "kernel": "chunk64_kernel<IoF16,false,false,false,true,true>",
+                      "algorithmic_bytes": fused_ro_bytes,
+                      "roofline": roofline_obj(fused_ro_bytes, fused_ro_ms)},
+            "saved_ms": round(three_ms - fused_ro_ms, 4),
+        },
     }
-    del w, state, k, a12, new_k, a, b, out, ticket
+    del w, state, k, a12, new_k, a, b, out, ticket, gate, ro
     torch.cuda.empty_cache()
     return out_obj
 

@@ -582,6 +582,63 @@ def tmix_wkv7_recurrent_fp32_from_kk_gate(query_start_loc, state_indices, state,
     del keep
 
 
+def tmix_wkv7_recurrent_fp32_from_kk_gate_readout(query_start_loc, state_indices, state, r,
+                                                  decay_logits, k, v, a12, g, k_k, a0, k_a, r_k,
+                                                  ln_weight, ln_bias, new_k, readout, output,
+                                                  scale, decay_bias=None,
+                                                  validated_metadata=None, max_seqlen=-1):
+    """tmix_wkv7_recurrent_fp32_from_kk_gate with the readout's elementwise
+    stage in the output write-back: readout = (GroupNorm(y) ln_weight + ln_bias
+    + (sum r k' r_k) v) g per (token, head); `output` (y) may be None.  Where
+    the fused kernel does not apply (as for the kk-gate entry) the stages run
+    as separate kernels (fp16 tokens)."""
+    y = output if output is not None else torch.empty_like(v)
+    n, h, d = check_recurrent_layout(query_start_loc, state_indices, state, r, decay_logits, k,
+                                     v, a12, new_k, y, scale)
+    for t, name in ((g, "g"), (readout, "readout")):
+        check_cuda_contiguous(t, name)
+        check_same_device(state, t, name)
+        _check(t.dtype == r.dtype and t.shape == r.shape, name,
+               " must have the shape and dtype of the token tensors")
+    for t, name in ((k_k, "k_k"), (a0, "a0"), (k_a, "k_a"), (r_k, "r_k"),
+                    (ln_weight, "ln_weight"), (ln_bias, "ln_bias")):
+        check_cuda_contiguous(t, name)
+        check_same_device(state, t, name)
+        _check(t.dtype == r.dtype, name, " must have the token dtype")
+        _check(t.numel() == h * d, name, " must have shape [H*D] or [H,D]")
+    if decay_bias is not None:
+        _check_decay_bias(decay_bias, state, r, h, d,
+                          "decay_bias must match the token tensor dtype")
+    lq, ls, status, ms, keep = _resolve_launch_metadata(
+        query_start_loc, state_indices, r.size(0), state.size(0), int(max_seqlen),
+        validated_metadata)
+    fp16 = r.dtype == torch.float16
+    rc = N.FR2_ERR_UNSUPPORTED
+    if not (fp16 and d == 64 and int(ms) > 0 and split_plan(n, h, d, int(ms))[0] > 1):
+        with _on_device(state.device):
+            rc = N.load().fr2_wkv7_recurrent_fp32_forward_kk_gate_readout(
+                lq.data_ptr(), ls.data_ptr(), status.data_ptr(), n, h, d, r.size(0), int(ms),
+                _dtype_code(r), state.data_ptr(), r.data_ptr(), decay_logits.data_ptr(),
+                N.ptr(decay_bias), k.data_ptr(), v.data_ptr(), a12.data_ptr(), k_k.data_ptr(),
+                a0.data_ptr(), k_a.data_ptr(), g.data_ptr(), r_k.data_ptr(),
+                ln_weight.data_ptr(), ln_bias.data_ptr(), new_k.data_ptr(), readout.data_ptr(),
+                N.ptr(output), float(scale), _stream(state.device))
+    if rc == N.FR2_ERR_UNSUPPORTED:
+        _check(fp16, "the fused readout outside the chunked family needs float16 tokens")
+        tmix_wkv7_recurrent_fp32_from_kk_gate(
+            query_start_loc, state_indices, state, r, decay_logits, k, v, a12, k_k, a0, k_a,
+            new_k, y, scale, decay_bias, validated_metadata, max_seqlen)
+        with _on_device(state.device):
+            N.check(N.load().fr2_tmix_readout_prelinear_forward(
+                r.size(0), h, d, y.data_ptr(), r.data_ptr(), new_k.data_ptr(), v.data_ptr(),
+                r_k.data_ptr(), ln_weight.data_ptr(), ln_bias.data_ptr(), g.data_ptr(),
+                readout.data_ptr(), _stream(state.device)), "fr2_tmix_readout_prelinear_forward")
+        del keep
+        return
+    N.check(rc, "tmix_wkv7_recurrent_fp32_from_kk_gate_readout")
+    del keep
+
+
 @functools.lru_cache(maxsize=256)
 def _library_split_plan(num_sequences: int, num_heads: int, head_size: int,
                         max_seqlen: int) -> tuple[int, int, int, int]:
@@ -1401,6 +1458,7 @@ def exported_names() -> Sequence[str]:
         "tmix_wkv7_recurrent_fp32_from_decay_logits",
         "tmix_wkv7_recurrent_fp16_from_decay_logits",
         "tmix_wkv7_recurrent_fp32_from_kk_gate",
+        "tmix_wkv7_recurrent_fp32_from_kk_gate_readout",
         "pretrain_tmix_wkv7_recurrent_forward",
         "pretrain_tmix_wkv7_recurrent_backward",
         "statetune_tmix_wkv7_recurrent_fp32io16_forward",

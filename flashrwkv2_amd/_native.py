@@ -78,6 +78,11 @@ SIGNATURES: dict[str, tuple] = {
         [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64,
          c_int32, c_int32] + [c_void_p] * 12 + [c_float, c_void_p],
     ),
+    "fr2_wkv7_recurrent_fp32_forward_kk_gate_readout": (
+        c_int32,
+        [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64,
+         c_int32, c_int32] + [c_void_p] * 17 + [c_float, c_void_p],
+    ),
     "fr2_wkv7_recurrent_fp16_forward": (
         c_int32,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64,

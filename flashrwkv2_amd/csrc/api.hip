@@ -732,6 +732,38 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate(
   return fr2::launch_chunked_kk(dtype, p, num_sequences, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate_readout(
+    const int32_t* query_start_loc, const int32_t* state_indices, const int32_t* status,
+    int32_t num_sequences, int32_t num_heads, int32_t head_size, int64_t total_tokens,
+    int32_t max_seqlen, int32_t dtype, float* state, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a12, const void* k_k,
+    const void* a0, const void* k_a, const void* g, const void* r_k, const void* ln_weight,
+    const void* ln_bias, void* new_k, void* readout, void* output, float scale,
+    void* stream) {
+  if (!query_start_loc || !state_indices || !status || !state || !k_k || !a0 || !k_a ||
+      !r_k || !ln_weight || !ln_bias || !tokens_ok(r, decay_logits, k, v, a12, new_k, readout) ||
+      !aligned16(g) || !g || (output != nullptr && !aligned16(output)))
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 || total_tokens <= 0)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (head_size != 64 || max_seqlen < kChunkMinSeqlen) return FR2_ERR_UNSUPPORTED;
+  SegArgs p;
+  p.bounds = query_start_loc;
+  p.slots = state_indices;
+  p.status = status;
+  p.num_heads = num_heads;
+  p.out_elems = total_tokens * num_heads * head_size;
+  p.state_in = state;
+  p.state_out = state;
+  p.r = r; p.logits = decay_logits; p.bias = decay_bias; p.k = k; p.v = v; p.a = a12;
+  p.b = k;   // unused by the fused stage (slot 5 reads the key's other half)
+  p.kk_scale = k_k; p.a_bias = a0; p.k_a = k_a; p.new_k = new_k;
+  p.ro_g = g; p.ro_rk = r_k; p.ro_lnw = ln_weight; p.ro_lnb = ln_bias; p.ro_out = readout;
+  p.y = output;
+  p.scale = scale;
+  return fr2::launch_chunked_kk(dtype, p, num_sequences, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int fr2_tmix_kk_a_gate_forward(int64_t tokens, int32_t num_heads, int32_t head_size,
                                           const void* k, const void* k_k, const void* a0,
                                           const void* a12, const void* k_a, void* new_k,

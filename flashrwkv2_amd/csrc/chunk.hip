@@ -90,6 +90,11 @@ struct alignas(16) Smem {
   // strided column reads spread over the banks
   float mpart[2][G][2][4][L][MPP];    // [group parity][chunk][key half][block][s][t]
   uint16_t yb[2][GT][YP];             // outputs of a group, by parity (padded rows)
+  // fused readout: sum over a key half of r k' r_k per token of a group, by
+  // group index mod 4 (written by the key waves building group g after the
+  // state waves finished g - 2, read by the write-back of group g, which the
+  // state waves run after finishing g + 1)
+  float rkv[4][2][GT];
   // progress counters, each written by one wave only: groups whose operators
   // key wave w has stored, groups whose part-1 partials it has stored, and
   // groups state wave w has finished / whose output rows it has written back
@@ -146,13 +151,14 @@ struct KkParams {
 };
 
 template <class Io, bool kVExact, bool kFull, bool kUnitW = false, bool kSum = false,
-          bool kKK = false>
+          bool kKK = false, bool kRO = false>
 __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& op,
                                           const u32x4 (&raw)[6], const float (&nbias8)[8],
                                           bool valid, int mp, int cc, int hh, int i, int q,
                                           KeyRegs& kr, bool unit_w = false,
                                           float kscale = 1.0f, const KkParams* kp = nullptr,
-                                          typename Io::raw* new_k_row = nullptr) {
+                                          typename Io::raw* new_k_row = nullptr,
+                                          const float* rk8 = nullptr, float* rkv_row = nullptr) {
   const int kbase = 32 * hh + 8 * q;
   // tokens past the sequence end (their rows repeat the last token) carry
   // zero operands and a unit retention
@@ -208,6 +214,19 @@ __device__ __forceinline__ void key_part1(Smem<kVExact>& sm, ChunkOps<kVExact>& 
   } else {
     unpack8<Io>(tok(4), xa);
     unpack8<Io>(tok(5), xb);
+  }
+  if constexpr (kRO) {
+    // the readout's per-token residual weight over this lane's keys, summed
+    // over the four lanes of the token: sum r k' r_k with k' as stored
+    float part = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float kq = kKK ? Io::to_f32(Io::from_f32(xk[e])) : xk[e];
+      part = __builtin_fmaf(xr[e] * kq, rk8[e], part);
+    }
+    part += __shfl_xor(part, 16);
+    part += __shfl_xor(part, 32);
+    if (q == 0) rkv_row[i] = part;
   }
   // base-2 log of the retention, log2(w) = c sigmoid(x) with
   // c = -exp(-1/2) log2(e), evaluated as 1 / ((1 + 2^(-log2(e) x)) / c)
@@ -611,6 +630,69 @@ __device__ __forceinline__ void wait_min_ge(int* c, int v, int limit, int* fault
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Fused readout write-back of group gi (the state waves run it, one group
+// late, in place of the plain y write-back): thread (o_tok, o_c8) takes 8 channels of token o_tok of the group's
+// staged y rows.  GroupNorm over the head's 64 channels (the 8 consecutive
+// lanes of a token hold 8 channels each), the r k' r_k residual whose two
+// key-half sums the key waves left in sm.rkv, and the gate:
+//   out = (GroupNorm(y) * ln_w + ln_b + (sum r k' r_k) v) * g.
+template <class Io, bool kVExact>
+__device__ __forceinline__ void readout_write_back(const Smem<kVExact>& sm, const SegArgs& p,
+                                                   int gi, int o_tok, int o_c8, int t0,
+                                                   int seg_len, int64_t row_stride,
+                                                   int64_t head_off) {
+  using raw = typename Io::raw;
+  // this thread's 8 channels of ln_w / ln_b (read here rather than held in
+  // registers across the key waves' loop)
+  float ro_w[8], ro_b[8];
+  unpack8<Io>(*reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.ro_lnw) + head_off +
+                                              o_c8 * 8), ro_w);
+  unpack8<Io>(*reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.ro_lnb) + head_off +
+                                              o_c8 * 8), ro_b);
+  const int pos = gi * GT + o_tok;   // position in the segment
+  const bool in_seg = pos < seg_len;
+  const int64_t roff =
+      static_cast<int64_t>(t0 + min(pos, seg_len - 1)) * row_stride + head_off + o_c8 * 8;
+  const u32x4 ypiece = *reinterpret_cast<const u32x4*>(&sm.yb[gi & 1][o_tok][o_c8 * 8]);
+  const u32x4 vraw = *reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.v) + roff);
+  const u32x4 graw = *reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.ro_g) + roff);
+  float yv[8], vv[8], gv[8];
+  unpack8<Io>(ypiece, yv);
+  unpack8<Io>(vraw, vv);
+  unpack8<Io>(graw, gv);
+  float s1 = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s1 += yv[e];
+  s1 += __shfl_xor(s1, 1);
+  s1 += __shfl_xor(s1, 2);
+  s1 += __shfl_xor(s1, 4);
+  const float mean = s1 * (1.0f / D);
+  float s2 = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s2 = __builtin_fmaf(yv[e] - mean, yv[e] - mean, s2);
+  s2 += __shfl_xor(s2, 1);
+  s2 += __shfl_xor(s2, 2);
+  s2 += __shfl_xor(s2, 4);
+  const float inv = 1.0f / __builtin_sqrtf(s2 * (1.0f / D) + 64.0e-5f);
+  const float rkv = sm.rkv[gi & 3][0][o_tok] + sm.rkv[gi & 3][1][o_tok];
+  u32x4 packed;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float o2[2];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const int e = 2 * j + h2;
+      o2[h2] = (__builtin_fmaf((yv[e] - mean) * inv, ro_w[e], ro_b[e]) + rkv * vv[e]) * gv[e];
+    }
+    packed[j] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, Io::from_f32(o2[0]))) |
+                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, Io::from_f32(o2[1]))) << 16);
+  }
+  if (in_seg) {
+    *reinterpret_cast<u32x4*>(static_cast<raw*>(p.ro_out) + roff) = packed;
+    if (p.y != nullptr) *reinterpret_cast<u32x4*>(static_cast<raw*>(p.y) + roff) = ypiece;
+  }
+}
+
 // kTrain: the training-forward contract (pretrain path) also writes every
 // token's sa (p.sa_out) and the post-chunk state of every 16-token chunk
 // (p.boundary, [segment, H, boundary_per_seg, D, D]).
@@ -621,7 +703,8 @@ __device__ __forceinline__ void wait_min_ge(int* c, int v, int limit, int* fault
 // an identity start with V = 0 (Phi), to split_summary[(n * (pieces - 1) +
 // j) * 2 + {0: F, 1: Phi}, H, D, D].  Nothing else is written.
 constexpr int NT_SUM = 768;
-template <class Io, bool kTrain, bool kRev = false, bool kSum = false, bool kKK = false>
+template <class Io, bool kTrain, bool kRev = false, bool kSum = false, bool kKK = false,
+          bool kRO = false>
 __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) {
   using raw = typename Io::raw;
   constexpr bool kVExact = !__is_same(Io, IoF16);
@@ -649,10 +732,12 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
   }
   if (p.status != nullptr) {
     if (p.status[0] != 0) {
-      if constexpr (!kSum)
-        fill_output_nan<Io>(static_cast<raw*>(p.y), p.out_elems,
-                            static_cast<int64_t>(seg) * gridDim.x + h,
-                            static_cast<int64_t>(gridDim.x) * gridDim.y);
+      if constexpr (!kSum) {
+        const int64_t blk = static_cast<int64_t>(seg) * gridDim.x + h;
+        const int64_t nblk = static_cast<int64_t>(gridDim.x) * gridDim.y;
+        if (!kRO || p.y != nullptr) fill_output_nan<Io>(static_cast<raw*>(p.y), p.out_elems, blk, nblk);
+        if constexpr (kRO) fill_output_nan<Io>(static_cast<raw*>(p.ro_out), p.out_elems, blk, nblk);
+      }
       return;
     }
     if (seq >= p.status[2]) return;
@@ -739,7 +824,10 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
       if (gi < 0) return;
       wait_min_ge(sm.consumed, gi + 1, p.spin_limit, &sm.fault);   // every state wave staged its columns
       const int pos = gi * GT + o_tok;        // position in processing order
-      if (pos < seg_len) {
+      if constexpr (kRO) {
+        readout_write_back<Io, kVExact>(sm, p, gi, o_tok, o_c8, t0, seg_len, row_stride,
+                                        head_off);
+      } else if (pos < seg_len) {
         const int row = kRev ? t1 - 1 - pos : t0 + pos;
         *reinterpret_cast<u32x4*>(yout + static_cast<int64_t>(row) * row_stride + head_off +
                                   o_c8 * 8) =
@@ -826,8 +914,12 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
         }
       } else {
         const raw nanv = Io::from_f32(qnan);
-        for (int64_t e = tid; e < static_cast<int64_t>(t1 - t0) * D; e += kStateThreads)
-          yout[(t0 + e / D) * row_stride + head_off + e % D] = nanv;
+        if (yout != nullptr)
+          for (int64_t e = tid; e < static_cast<int64_t>(t1 - t0) * D; e += kStateThreads)
+            yout[(t0 + e / D) * row_stride + head_off + e % D] = nanv;
+        if constexpr (kRO)
+          for (int64_t e = tid; e < static_cast<int64_t>(t1 - t0) * D; e += kStateThreads)
+            static_cast<raw*>(p.ro_out)[(t0 + e / D) * row_stride + head_off + e % D] = nanv;
         if constexpr (kTrain) {
           for (int64_t e = tid; e < static_cast<int64_t>(t1 - t0) * D; e += kStateThreads)
             p.sa_out[(t0 + e / D) * row_stride + head_off + e % D] = qnan;
@@ -887,6 +979,12 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
       nbias8[e] = p.bias ? -kLog2e * Io::to_f32(static_cast<const raw*>(p.bias)[head_off + kbase + e])
                          : 0.f;
     const int kbase_other = 32 * (hh ^ 1) + 8 * q;
+    float rk8[8];
+    if constexpr (kRO) {
+      const raw* rk = static_cast<const raw*>(p.ro_rk) + head_off + kbase;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rk8[e] = Io::to_f32(rk[e]);
+    }
     KkParams kp;
     if constexpr (kKK) {
       const raw* kks = static_cast<const raw*>(p.kk_scale) + head_off;
@@ -978,13 +1076,13 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
           nk_row = static_cast<raw*>(p.new_k) +
                    static_cast<int64_t>(tok0 + gn * GT) * row_stride + head_off + kbase;
         if (t0 + gn * GT + cc * L + L <= t1)
-          key_part1<Io, kVExact, true, false, kSum, kKK>(sm, sm.ops[par][cc], cur, nbias8, true,
-                                                         par, cc, hh, i, q, kr, false, 1.0f, &kp,
-                                                         nk_row);
+          key_part1<Io, kVExact, true, false, kSum, kKK, kRO>(
+              sm, sm.ops[par][cc], cur, nbias8, true, par, cc, hh, i, q, kr, false, 1.0f, &kp,
+              nk_row, rk8, &sm.rkv[gn & 3][hh][cc * L]);
         else if (active)
-          key_part1<Io, kVExact, false, false, kSum, kKK>(sm, sm.ops[par][cc], cur, nbias8,
-                                                          tok0 + gn * GT < t1, par, cc, hh, i, q,
-                                                          kr, false, 1.0f, &kp, nk_row);
+          key_part1<Io, kVExact, false, false, kSum, kKK, kRO>(
+              sm, sm.ops[par][cc], cur, nbias8, tok0 + gn * GT < t1, par, cc, hh, i, q, kr, false,
+              1.0f, &kp, nk_row, rk8, &sm.rkv[gn & 3][hh][cc * L]);
       }
       signal(&sm.part1[kw], gn + 1);
       wait_ge(&sm.part1[partner], gn + 1, p.spin_limit, &sm.fault);
@@ -1065,14 +1163,27 @@ int launch_chunked_kk(int dtype, const SegArgs& args, int nseg, hipStream_t s) {
   p.spin_limit = handoff_spin_limit();
   p.handoff_fault = handoff_fault_word();
   const dim3 grid(p.num_heads, nseg);
-  if (dtype == FR2_DTYPE_BFLOAT16)
-    hipLaunchKernelGGL((chunk64_kernel<IoBF16, false, false, false, true>), grid, dim3(NT), 0, s,
-                       p);
-  else if (dtype == FR2_DTYPE_FLOAT16)
-    hipLaunchKernelGGL((chunk64_kernel<IoF16, false, false, false, true>), grid, dim3(NT), 0, s,
-                       p);
-  else
+  const bool ro = p.ro_out != nullptr;
+  if (ro && (p.ro_g == nullptr || p.ro_rk == nullptr || p.ro_lnw == nullptr ||
+             p.ro_lnb == nullptr))
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (dtype == FR2_DTYPE_BFLOAT16) {
+    if (ro)
+      hipLaunchKernelGGL((chunk64_kernel<IoBF16, false, false, false, true, true>), grid,
+                         dim3(NT), 0, s, p);
+    else
+      hipLaunchKernelGGL((chunk64_kernel<IoBF16, false, false, false, true>), grid, dim3(NT), 0,
+                         s, p);
+  } else if (dtype == FR2_DTYPE_FLOAT16) {
+    if (ro)
+      hipLaunchKernelGGL((chunk64_kernel<IoF16, false, false, false, true, true>), grid, dim3(NT),
+                         0, s, p);
+    else
+      hipLaunchKernelGGL((chunk64_kernel<IoF16, false, false, false, true>), grid, dim3(NT), 0,
+                         s, p);
+  } else {
     return FR2_ERR_UNSUPPORTED;
+  }
   return record_launch();
 }
 

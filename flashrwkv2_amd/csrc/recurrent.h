@@ -91,6 +91,16 @@ struct SegArgs {
   const void* a_bias = nullptr;
   const void* k_a = nullptr;
   void* new_k = nullptr;
+  // Fused readout prelinear stage (chunked kernel with the kk / a gate):
+  // per (token, head) out = (GroupNorm(y) * ln_w + ln_b + (sum r k' r_k) v) * g
+  // over the head's channels, written to ro_out ([T, H, D], token dtype);
+  // ro_g is the gate [T, H, D], r_k / ln_w / ln_b are [H, D].  y itself is
+  // written only when `y` is set.
+  const void* ro_g = nullptr;
+  const void* ro_rk = nullptr;
+  const void* ro_lnw = nullptr;
+  const void* ro_lnb = nullptr;
+  void* ro_out = nullptr;
 };
 
 // Token range [start, start + len) of piece j of a split sequence of n

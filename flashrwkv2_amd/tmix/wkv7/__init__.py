@@ -283,10 +283,14 @@ from .rl_infctx import (  # noqa: E402
     rl_infctx_tmix_wkv7_chunk_fp32io16_factor_recompute,
 )
 from .statetune import statetune_tmix_wkv7_recurrent_fp32io16  # noqa: E402
-from .fused import infer_tmix_wkv7_kk_gate_recurrent_forward_varlen  # noqa: E402
+from .fused import (  # noqa: E402
+    infer_tmix_wkv7_kk_gate_recurrent_forward_varlen,
+    infer_tmix_wkv7_kk_gate_recurrent_readout_forward_varlen,
+)
 
 __all__ += [
     "infer_tmix_wkv7_kk_gate_recurrent_forward_varlen",
+    "infer_tmix_wkv7_kk_gate_recurrent_readout_forward_varlen",
     "statetune_tmix_wkv7_recurrent_fp32io16",
     "pretrain_tmix_wkv7_recurrent_bf16",
     "infer_tmix_wkv7_chunk_bf16_forward_varlen",

@@ -212,6 +212,31 @@ int fr2_wkv7_recurrent_fp32_forward_kk_gate(
     const void* a0, const void* k_a, void* new_k, void* output, float scale, void* stream);
 
 /*
+ * fr2_wkv7_recurrent_fp32_forward_kk_gate with the readout's elementwise
+ * stage fused into the output write-back: per (token, head),
+ *   readout = (GroupNorm(y) * ln_weight + ln_bias + (sum_c r k' r_k) v) * g
+ * with GroupNorm over the head's channels of y as rounded to the token dtype
+ * (eps 64e-5), k' the gated key as stored, r_k / ln_weight / ln_bias of
+ * shape [H*D] and g [total_tokens, H, D] in the token dtype.  `readout`
+ * receives it; `output` (y) is written only when not null.  Replaces the
+ * triple tmix_kk_a_gate_forward_varlen_cuda
+ * (csrc/sm120/tmix/wkv_prepare/internal/kk_a_gate/infer_fp16_forward_varlen.cu),
+ * tmix_wkv7_recurrent_fp32_from_decay_logits_cuda
+ * (…/infer_recurrent_fp32io16_forward_varlen.cu:457-517) and
+ * tmix_lnx_rkvres_xg_forward_varlen_cuda
+ * (csrc/sm120/tmix/readout/infer_fp16_forward_varlen.cu), which the reference
+ * runs as three kernels with k, a, b and y round-tripping through HBM.
+ * Same FR2_ERR_UNSUPPORTED cases as the kk-gate entry.
+ */
+int fr2_wkv7_recurrent_fp32_forward_kk_gate_readout(
+    const int32_t* query_start_loc, const int32_t* state_indices, const int32_t* status,
+    int32_t num_sequences, int32_t num_heads, int32_t head_size, int64_t total_tokens,
+    int32_t max_seqlen, int32_t dtype, float* state, const void* r, const void* decay_logits,
+    const void* decay_bias, const void* k, const void* v, const void* a12, const void* k_k,
+    const void* a0, const void* k_a, const void* g, const void* r_k, const void* ln_weight,
+    const void* ln_bias, void* new_k, void* readout, void* output, float scale, void* stream);
+
+/*
  * fr2_wkv7_recurrent_fp32_forward_split without a workspace argument: the
  * library's own device scratch array (FR2_NOALLOC_SCRATCH_BYTES per GPU, held
  * until the process ends) replaces it, and the call allocates nothing (no

@@ -154,3 +154,90 @@ def test_few_long_fp16_sequences_take_the_split():
     touched = c["slots"].long()
     assert_state_close(to_np(pool)[touched], epool[touched])
     _check_key(new_k, ek, torch.float16)
+
+
+# ---------------------------------------------------------------------------
+# the readout's elementwise stage in the write-back
+# ---------------------------------------------------------------------------
+def _readout_params(c, seed):
+    g = torch.Generator().manual_seed(seed)
+    total, heads, d = c["k"].shape
+    dtype = c["k"].dtype
+    c["g"] = torch.sigmoid(torch.randn((total, heads, d), generator=g)).to(dtype)
+    c["r_k"] = (torch.randn(heads * d, generator=g) * 0.3).to(dtype)
+    c["ln_w"] = (1.0 + 0.1 * torch.randn(heads * d, generator=g)).to(dtype)
+    c["ln_b"] = (0.1 * torch.randn(heads * d, generator=g)).to(dtype)
+    return c
+
+
+def _expected_readout(c, scale):
+    """fp64 composition: gate -> recurrence -> readout prelinear, the readout
+    reading y and the gated key as rounded to the token dtype (what the
+    reference's three kernels pass through HBM)."""
+    from oracle.prepare import readout_prelinear_f64
+
+    y, pool, ek = _expected(c, scale)
+    total, heads, d = c["k"].shape
+    dtype = c["k"].dtype
+    rnd = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dtype).double().numpy()  # noqa: E731
+    flat = lambda a: np.asarray(a).reshape(total, heads * d)   # noqa: E731
+    out = readout_prelinear_f64(flat(rnd(y)), flat(to_np(c["r"])), flat(rnd(ek)),
+                                flat(to_np(c["v"])), to_np(c["r_k"]), to_np(c["ln_w"]),
+                                to_np(c["ln_b"]), flat(to_np(c["g"])), d)
+    return out.reshape(total, heads, d), y, pool, ek
+
+
+def _run_readout(c, scale, want_y=True):
+    from flashrwkv2_amd.tmix.wkv7 import infer_tmix_wkv7_kk_gate_recurrent_readout_forward_varlen
+    dev = {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in c.items()}
+    pool = dev["pool"].clone()
+    res = infer_tmix_wkv7_kk_gate_recurrent_readout_forward_varlen(
+        dev["r"], dev["w"], dev["k"], dev["v"], dev["a12"], dev["g"], k_k=dev["k_k"],
+        a0=dev["a0"], k_a=dev["k_a"], r_k=dev["r_k"], ln_weight=dev["ln_w"],
+        ln_bias=dev["ln_b"], state_pool=pool, cu_seqlens=dev["cu"], state_indices=dev["slots"],
+        scale=scale, decay_bias=dev["bias"], return_wkv_output=want_y)
+    torch.cuda.synchronize()
+    return (*res, pool)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("lengths,heads,bias", [
+    ((40, 1, 63, 130, 17), 3, True),
+    ((300, 64, 96, 41), 4, False),
+], ids=["ragged-bias", "long"])
+def test_fused_readout_matches_the_three_stage_oracle(dtype, lengths, heads, bias):
+    require_gpu()
+    print(f"case kk-gate+readout {dtype} lengths {lengths} H {heads} bias {bias}", flush=True)
+    c = _readout_params(_case(lengths, heads, dtype, seed=7 * sum(lengths) + heads, bias=bias), 3)
+    readout, new_k, y, pool = _run_readout(c, 0.9)
+    ero, ey, epool, ek = _expected_readout(c, 0.9)
+    assert_output_close(readout, ero)
+    assert_output_close(y, ey)
+    touched = c["slots"].long()
+    assert_state_close(to_np(pool)[touched], epool[touched])
+    _check_key(new_k, ek, dtype)
+
+
+def test_fused_readout_without_y_and_below_the_threshold():
+    """No y requested (the kernel then writes only the readout); and a short
+    fp16 batch, where the three stages run as separate kernels."""
+    require_gpu()
+    for lengths, seed in (((64, 50), 31), ((1, 7, 39), 32)):
+        print(f"case kk-gate+readout fp16 lengths {lengths}", flush=True)
+        c = _readout_params(_case(lengths, 2, torch.float16, seed=seed), seed)
+        readout, new_k, pool = _run_readout(c, 1.0, want_y=False)
+        ero, ey, epool, ek = _expected_readout(c, 1.0)
+        assert_output_close(readout, ero)
+        touched = c["slots"].long()
+        assert_state_close(to_np(pool)[touched], epool[touched])
+
+
+def test_fused_readout_config1_shape_fp16():
+    require_gpu()
+    print("case kk-gate+readout config-1 shape fp16", flush=True)
+    c = _readout_params(_case([4096] * 8, 32, torch.float16, seed=1001), 1001)
+    readout, new_k, pool = _run_readout(c, 1.0, want_y=False)
+    ero, ey, epool, ek = _expected_readout(c, 1.0)
+    assert_output_close(readout, ero)
+    touched = c["slots"].long()
+    assert_state_close(to_np(pool)[touched], epool[touched])
