@@ -57,12 +57,14 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegExpHalf = -0.6065306597126334f;   // -exp(-1/2)
 
 // Operators of one chunk consumed by the state path.  For bf16 tokens V is
-// exact in bf16 (no lo part) and the rows are padded for bank spread; fp16
-// tokens need V's lo part and use unpadded rows to fit the LDS budget.
+// exact in bf16 (no lo part); fp16 tokens need V's lo part, and their token
+// rows take a smaller pad so that the key rows keep theirs within the LDS
+// budget (unpadded 128-byte key rows put the eight lanes of each 16-byte
+// read on the same banks: 0.438 vs 0.344 ms on config 1 in fp16).
 template <bool kVExact>
 struct alignas(16) ChunkOps {
-  static constexpr int RP = kVExact ? D + 8 : D;    // key row length
-  static constexpr int TP = D + 16;                 // token row of B^, K^, V
+  static constexpr int RP = D + 8;                  // key row length
+  static constexpr int TP = kVExact ? D + 16 : D + 8;   // token row of B^, K^, V
   float gl[D];                        // gamma_L (read as 16-byte vectors)
   __bf16 at_h[L][RP], at_l[L][RP];    // A~ rows, keys at key_pos()
   __bf16 r_h[L][RP], r_l[L][RP];      // R~ rows, keys at key_pos()
