@@ -124,11 +124,15 @@ class Runner:
         return start.elapsed_time(end) / launches
 
     def kernel_name(self) -> str:
+        """The family the library's policy picks (csrc/api.hip run_family)."""
         ms = self.ticket._max_seqlen()
+        units = self.w.state_indices.numel() * self.w.num_heads
         if ms <= 4:
             return "decode64_kernel<IoBF16,StF32>"
-        if ms >= 40:   # the library's chunked threshold (csrc/api.hip kChunkMinSeqlen)
+        if ms >= (5 if units <= 256 else 24 if units <= 1024 else 48 if units <= 4096 else 56):
             return "chunk64_kernel<IoBF16,false>"
+        if ms <= 8 or units >= 4096:
+            return "decode64_kernel<IoBF16,StF32>"
         return "serial64w_kernel<IoBF16,StF32>"
 
 
@@ -608,6 +612,40 @@ def time_mid_length(torch, flashrwkv2_amd, steps: int, n: int = 2048, length: in
         "forced": forced,
     }
     del run, w, toks
+    torch.cuda.empty_cache()
+    return out
+
+
+def time_short_batches(torch, flashrwkv2_amd, steps: int, heads: int = 32):
+    """Short-sequence batches at both ends of the dispatch policy
+    (csrc/api.hip run_family), each through the public call and with every
+    kernel family forced: many 16-token sequences (65 536 (sequence, head)
+    units: the decode kernel, one wave per unit) and 8 sequences of 16 tokens
+    (256 units: the chunked kernel)."""
+    from flashrwkv2_amd import workloads
+
+    out = []
+    for n, length in ((2048, 16), (8, 16)):
+        toks = workloads.make_tokens(n * length, heads, u_range=(-6.0, -0.5), seed=1006,
+                                     device="cuda")
+        w = workloads._pack(f"short_S{n}_T{length}_H{heads}", toks, [length] * n, heads, 0.1,
+                            1006, "cuda", {"S": n, "T": length, "H": heads})
+        run = Runner(w, torch, flashrwkv2_amd)
+        ms = run.time_steps(steps, 5)
+        nbytes = algorithmic_bytes(w.total_tokens, w.num_heads, w.state_indices.numel())
+        forced = {}
+        for kern, name in ((0, "serial64w_kernel<IoBF16,StF32>"),
+                           (1, "decode64_kernel<IoBF16,StF32>"),
+                           (2, "chunk64_kernel<IoBF16,false>")):
+            f = lambda k=kern: run.C.tmix_wkv7_recurrent_fp32_kernel_forced(
+                k, w.cu_seqlens, w.state_indices, run.state, *w.tokens, run.out, 1.0, None,
+                run.ticket)
+            fms = _events_ms(torch, f, steps)
+            forced[name] = {"kernel_ms": round(fms, 5), "roofline": roofline_obj(nbytes, fms)}
+        out.append({"workload": w.name, "units": n * heads, "ms_per_step": round(ms, 5),
+                    "kernel": run.kernel_name(), "roofline": roofline_obj(nbytes, ms),
+                    "algorithmic_bytes": nbytes, "forced": forced})
+        del run, w, toks
     torch.cuda.empty_cache()
     return out
 
@@ -1134,6 +1172,7 @@ def main() -> int:
     if args.only in (None, "long") and args.config == 1:
         result["varlen_prefill"] = time_varlen(torch, flashrwkv2_amd, max(5, args.steps // 2))
         result["mid_length"] = time_mid_length(torch, flashrwkv2_amd, max(5, args.steps // 4))
+        result["short_batches"] = time_short_batches(torch, flashrwkv2_amd, max(5, args.steps // 2))
         result["long_context"] = time_long_context(torch, flashrwkv2_amd, max(4, args.steps // 4))
     if args.only in (None, "train") and not args.no_train:
         wt = pre.w if (pre is not None and args.config == 1) else workloads.config(1, "cuda")

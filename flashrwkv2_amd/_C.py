@@ -539,7 +539,8 @@ def tmix_wkv7_recurrent_fp32_from_kk_gate(query_start_loc, state_indices, state,
     k is the projected key, a12 the a-gate logits, k_k / a0 / k_a the
     per-channel parameters ([H*D] or [H,D], token dtype); the gated key is
     written to new_k.  Outside the chunked family (head size 64, longest
-    sequence >= 40), and for fp16 batches that the library's plan splits by
+    sequence at the library's chunked threshold for the launch's unit count),
+    and for fp16 batches that the library's plan splits by
     sequence (few long sequences: the split outruns one block per unit), the
     gate runs as its own kernel and the recurrence through the public path."""
     n, h, d = check_recurrent_layout(query_start_loc, state_indices, state, r, decay_logits, k,

@@ -11,16 +11,29 @@ namespace {
 
 using fr2::SegArgs;
 
-// Kernel-family policy (replaces use_small_auto,
-// csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:378-391).
-// Short requests stream the state once with the decode kernel; long ones go
-// to the chunked MFMA kernel; everything else runs token-serial.  The
-// chunked threshold is the measured crossover at D = 64, H = 32, about 200 k
-// tokens per call of equal-length sequences (forced kernels, ms per call,
-// serial / chunked): L = 32: 5.93 / 6.54; L = 48: 5.75 / 5.36; L = 64:
-// 5.70 / 4.47; L = 128: 5.49 / 3.28.
+// Kernel-family policy at D = 64 (replaces use_small_auto,
+// csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:378-391),
+// by the longest sequence L and the (sequence, head) unit count U of the
+// launch.  Measured with each family forced on equal-length batches, H = 32:
+//   U <= 256 (at most one chunked block per CU): the chunked kernel is the
+//     fastest from L = 5 on (L = 16: chunked 0.011, serial 0.013, decode
+//     0.024 ms);
+//   otherwise it wins from L = 24 (U <= 1024), 48 (U <= 4096), 56 (larger
+//     U; U = 65536, L = 48: decode 2.38, chunked 2.56, serial 2.86 ms;
+//     L = 64: chunked 2.86, decode 3.10 ms);
+//   below that the decode kernel (one wave per unit, the state in
+//     registers) beats the token-serial kernel except for U of 1024-4095 at
+//     L = 12-16 (U = 1024, L = 16: serial 0.025, decode 0.027 ms).
+// Longest sequence <= 4 always streams the state once with the decode kernel.
 constexpr int kDecodeMaxSeqlen = 4;
-constexpr int kChunkMinSeqlen = 40;
+constexpr int kChunkMinSeqlen = 5;   // the smallest chunked threshold (U <= 256)
+
+int chunk_min_seqlen(int64_t units) {
+  return units <= 256 ? kChunkMinSeqlen : units <= 1024 ? 24 : units <= 4096 ? 48 : 56;
+}
+bool decode_before_serial(int64_t units, int max_seqlen) {
+  return max_seqlen <= 8 || units >= 4096;
+}
 
 enum Family { kAuto = -1, kSerial = 0, kDecode = 1, kChunked = 2 };
 
@@ -38,14 +51,15 @@ int run_family(int family, int D, int dtype, bool bf16_state, const SegArgs& p,
                int nseg, int max_seqlen, hipStream_t s) {
   if (family == kAuto) {
     const bool plain = p.sa_out == nullptr && p.boundary == nullptr && !bf16_state;
+    const int64_t units = static_cast<int64_t>(nseg) * p.num_heads;
+    family = kSerial;
     if (D == 64 && plain && max_seqlen > 0 && max_seqlen <= kDecodeMaxSeqlen) {
       family = kDecode;
-    } else if (D == 64 && plain && max_seqlen >= kChunkMinSeqlen) {
+    } else if (D == 64 && plain && max_seqlen >= chunk_min_seqlen(units)) {
       const int rc = fr2::launch_chunked(dtype, p, nseg, max_seqlen, s);
       if (rc != FR2_ERR_UNSUPPORTED) return rc;
-      family = kSerial;
-    } else {
-      family = kSerial;
+    } else if (D == 64 && plain && max_seqlen > 0 && decode_before_serial(units, max_seqlen)) {
+      family = kDecode;
     }
   }
   switch (family) {
@@ -148,7 +162,8 @@ extern "C" int fr2_wkv7_recurrent_fp32_split_plan(int32_t num_sequences, int32_t
   *lead_len = 0;
   *workspace_bytes = 0;
   const int64_t units = static_cast<int64_t>(num_sequences) * num_heads;
-  if (head_size != 64 || max_seqlen < kChunkMinSeqlen || units > kSplitMaxUnits) return FR2_OK;
+  if (head_size != 64 || max_seqlen < chunk_min_seqlen(units) || units > kSplitMaxUnits)
+    return FR2_OK;
   // pieces after the lead piece: one block per CU in each phase, and pieces
   // of at least kSplitMinPiece tokens
   const int Q = static_cast<int>(std::min<int64_t>(
@@ -427,7 +442,7 @@ extern "C" int fr2_wkv7_chunk_bf16_forward(
   // bf16 once at the end (infer_chunk_bf16_forward_varlen.cu:195-270), so long
   // requests run on the chunked MFMA kernel with a bf16 state load / store;
   // chunk_size only shapes the reference's workspace, not the arithmetic.
-  if (max_seqlen >= kChunkMinSeqlen) {
+  if (max_seqlen >= chunk_min_seqlen(static_cast<int64_t>(num_sequences) * num_heads)) {
     p.state_bf16 = true;
     const int rc = fr2::launch_chunked(FR2_DTYPE_BFLOAT16, p, num_sequences, max_seqlen,
                                        static_cast<hipStream_t>(stream));
@@ -701,9 +716,10 @@ extern "C" int fr2_wkv7_statetune_uniform_backward(
 // wkv_prepare fused into the chunked kernel's load stage: the recurrence's
 // k, a, b come from the projected key, the low-rank a-gate logits a12 and the
 // per-channel k_k, a0, k_a (never stored), and the gated key the readout
-// needs is written to new_k.  Chunked family only: head_size 64 and
-// max_seqlen >= kChunkMinSeqlen, otherwise FR2_ERR_UNSUPPORTED (the caller
-// then runs fr2_tmix_kk_a_gate_forward and the plain entry).
+// needs is written to new_k.  Chunked family only: head_size 64 and a
+// longest sequence at the chunked threshold of the launch's unit count
+// (chunk_min_seqlen), otherwise FR2_ERR_UNSUPPORTED (the caller then runs
+// fr2_tmix_kk_a_gate_forward and the plain entry).
 extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate(
     const int32_t* query_start_loc, const int32_t* state_indices, const int32_t* status,
     int32_t num_sequences, int32_t num_heads, int32_t head_size, int64_t total_tokens,
@@ -715,7 +731,9 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate(
     return FR2_ERR_INVALID_ARGUMENT;
   if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 || total_tokens <= 0)
     return FR2_ERR_INVALID_ARGUMENT;
-  if (head_size != 64 || max_seqlen < kChunkMinSeqlen) return FR2_ERR_UNSUPPORTED;
+  if (head_size != 64 ||
+      max_seqlen < chunk_min_seqlen(static_cast<int64_t>(num_sequences) * num_heads))
+    return FR2_ERR_UNSUPPORTED;
   SegArgs p;
   p.bounds = query_start_loc;
   p.slots = state_indices;
@@ -746,7 +764,9 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate_readout(
     return FR2_ERR_INVALID_ARGUMENT;
   if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 || total_tokens <= 0)
     return FR2_ERR_INVALID_ARGUMENT;
-  if (head_size != 64 || max_seqlen < kChunkMinSeqlen) return FR2_ERR_UNSUPPORTED;
+  if (head_size != 64 ||
+      max_seqlen < chunk_min_seqlen(static_cast<int64_t>(num_sequences) * num_heads))
+    return FR2_ERR_UNSUPPORTED;
   SegArgs p;
   p.bounds = query_start_loc;
   p.slots = state_indices;

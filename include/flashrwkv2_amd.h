@@ -196,7 +196,8 @@ int fr2_wkv7_recurrent_fp32_forward_split(
  *   key = k (1 + (g - 1) k_a), a = -kk, b = kk g
  * in fp32, runs the recurrence on (key, a, b) and writes key to new_k (the
  * readout's input); a and b are never stored.  FR2_ERR_UNSUPPORTED outside
- * the chunked family (head_size 64, max_seqlen >= 40): the caller then runs
+ * the chunked family (head_size 64, max_seqlen at the chunked threshold of
+ * num_sequences * num_heads units: 5 for at most 256, up to 56): the caller then runs
  * fr2_tmix_kk_a_gate_forward and fr2_wkv7_recurrent_fp32_forward.  Replaces
  * the pair tmix_kk_a_gate_forward_varlen_cuda
  * (csrc/sm120/tmix/wkv_prepare/internal/kk_a_gate/infer_fp16_forward_varlen.cu)

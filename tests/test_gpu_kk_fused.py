@@ -106,10 +106,11 @@ def test_fused_kk_gate_matches_the_two_stage_oracle(dtype, lengths, heads, bias)
 
 
 def test_short_batches_run_the_two_kernel_form():
-    """Below the chunked threshold the gate runs as its own kernel (fp16)."""
+    """Below the chunked threshold (longest sequence <= 4 at this unit count)
+    the gate runs as its own kernel (fp16)."""
     require_gpu()
     print("case kk-gate short fp16", flush=True)
-    c = _case((1, 7, 39), 2, torch.float16, seed=9)
+    c = _case((1, 4, 3), 2, torch.float16, seed=9)
     y, pool, new_k = _run(c, 1.0)
     ey, epool, ek = _expected(c, 1.0)
     # a and b are rounded to fp16 between the two kernels here
@@ -121,7 +122,7 @@ def test_short_batches_run_the_two_kernel_form():
 
 def test_short_bf16_batches_are_rejected():
     require_gpu()
-    c = _case((5, 9), 2, torch.bfloat16, seed=11)
+    c = _case((2, 4), 2, torch.bfloat16, seed=11)
     with pytest.raises(Exception, match="float16 tokens"):
         _run(c, 1.0)
 
@@ -222,7 +223,7 @@ def test_fused_readout_without_y_and_below_the_threshold():
     """No y requested (the kernel then writes only the readout); and a short
     fp16 batch, where the three stages run as separate kernels."""
     require_gpu()
-    for lengths, seed in (((64, 50), 31), ((1, 7, 39), 32)):
+    for lengths, seed in (((64, 50), 31), ((1, 4, 3), 32)):
         print(f"case kk-gate+readout fp16 lengths {lengths}", flush=True)
         c = _readout_params(_case(lengths, 2, torch.float16, seed=seed), seed)
         readout, new_k, pool = _run_readout(c, 1.0, want_y=False)
