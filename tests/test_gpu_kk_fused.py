@@ -242,3 +242,26 @@ def test_fused_readout_config1_shape_fp16():
     assert_output_close(readout, ero)
     touched = c["slots"].long()
     assert_state_close(to_np(pool)[touched], epool[touched])
+
+
+def test_fused_readout_fails_closed_on_invalid_metadata():
+    """Device-detected metadata errors: the fused kernel writes NaN to the
+    readout (and y) and leaves the state pool untouched."""
+    C = require_gpu()
+    print("case kk-gate+readout fail-closed", flush=True)
+    c = _readout_params(_case((48,), 2, torch.float16, seed=41), 41)
+    dev = {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in c.items()}
+    bad_cu = torch.tensor([1, 48], device="cuda", dtype=torch.int32)   # must start at 0
+    pool = dev["pool"].clone()
+    before = pool.clone()
+    readout = torch.zeros_like(dev["v"])
+    y = torch.zeros_like(dev["v"])
+    new_k = torch.zeros_like(dev["k"])
+    C.tmix_wkv7_recurrent_fp32_from_kk_gate_readout(
+        bad_cu, dev["slots"], pool, dev["r"], dev["w"], dev["k"], dev["v"], dev["a12"], dev["g"],
+        dev["k_k"], dev["a0"], dev["k_a"], dev["r_k"], dev["ln_w"], dev["ln_b"], new_k, readout,
+        y, 1.0, None, None, 48)
+    torch.cuda.synchronize()
+    assert torch.isnan(readout).all()
+    assert torch.isnan(y).all()
+    assert torch.equal(pool, before)
