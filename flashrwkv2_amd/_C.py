@@ -593,9 +593,11 @@ def tmix_wkv7_recurrent_fp32_from_kk_gate_readout(query_start_loc, state_indices
     + (sum r k' r_k) v) g per (token, head); `output` (y) may be None.  Where
     the fused kernel does not apply (as for the kk-gate entry) the stages run
     as separate kernels (fp16 tokens)."""
-    y = output if output is not None else torch.empty_like(v)
+    # the layout check's output slot takes y when given, else the readout
+    # (same shape and dtype)
     n, h, d = check_recurrent_layout(query_start_loc, state_indices, state, r, decay_logits, k,
-                                     v, a12, new_k, y, scale)
+                                     v, a12, new_k, output if output is not None else readout,
+                                     scale)
     for t, name in ((g, "g"), (readout, "readout")):
         check_cuda_contiguous(t, name)
         check_same_device(state, t, name)
@@ -626,6 +628,7 @@ def tmix_wkv7_recurrent_fp32_from_kk_gate_readout(query_start_loc, state_indices
                 N.ptr(output), float(scale), _stream(state.device))
     if rc == N.FR2_ERR_UNSUPPORTED:
         _check(fp16, "the fused readout outside the chunked family needs float16 tokens")
+        y = output if output is not None else torch.empty_like(v)
         tmix_wkv7_recurrent_fp32_from_kk_gate(
             query_start_loc, state_indices, state, r, decay_logits, k, v, a12, k_k, a0, k_a,
             new_k, y, scale, decay_bias, validated_metadata, max_seqlen)
