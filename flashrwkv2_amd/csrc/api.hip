@@ -548,6 +548,12 @@ extern "C" int fr2_wkv7_rl_infctx_replay(
   p.y = output;
   p.sa_out = state_dot_a;
   p.scale = scale;
+  // chunks of at most 64 tokens: with many (chunk, head) units the decode
+  // kernel's one wave per unit beats the token-serial kernel at every such
+  // length (run_family's measured grid: 16 384 units, L = 16: 0.23 vs
+  // 0.29 ms; L = 64: 0.83 vs 0.94 ms)
+  if (head_size == 64 && static_cast<int64_t>(num_chunks) * num_heads >= 16384)
+    return fr2::launch_decode(64, dtype, p, num_chunks, static_cast<hipStream_t>(stream));
   return fr2::launch_serial(head_size, dtype, false, p, num_chunks,
                             static_cast<hipStream_t>(stream));
 }

@@ -497,6 +497,9 @@ __device__ __forceinline__ void decode64_body(const SegArgs& p) {
     sa.x += o.x; sa.y += o.y; sa.z += o.z; sa.w += o.w;
     o = shfl_xor4(sa, 32);
     sa.x += o.x; sa.y += o.y; sa.z += o.z; sa.w += o.w;
+    // the replay contract's per-token pre-update sa (fp32, [T, H, D])
+    if (p.sa_out != nullptr && rq == 0)
+      *reinterpret_cast<f4*>(p.sa_out + base + 4 * c4) = sa;
 
     const f4 vv = *reinterpret_cast<const f4*>(&s_in[3][4 * c4]);
     const float* Rr = &s_in[0][rq * 16];
@@ -662,7 +665,7 @@ int launch_serial(int D, int dtype, bool bf16_state, const SegArgs& p, int nseg,
 }
 
 int launch_decode(int D, int dtype, const SegArgs& p, int nseg, hipStream_t s) {
-  if (D != 64 || p.sa_out != nullptr || p.boundary != nullptr) return FR2_ERR_UNSUPPORTED;
+  if (D != 64 || p.boundary != nullptr) return FR2_ERR_UNSUPPORTED;
   const dim3 grid(p.num_heads, nseg);
   if (dtype == FR2_DTYPE_BFLOAT16)
     hipLaunchKernelGGL((decode64_kernel<IoBF16, StF32>), grid, dim3(64), 0, s, p);

@@ -425,3 +425,31 @@ def test_backend_is_the_in_tree_hip_library():
     with open("/proc/self/maps") as fh:
         maps = fh.read()
     assert str(_native.LIB_PATH) in maps or _native.LIB_PATH.name in maps
+
+
+def test_rl_infctx_replay_many_chunks_matches_recurrence():
+    """2 048 ragged chunks x 8 heads (16 384 (chunk, head) units, where the
+    replay runs on the one-wave-per-unit decode kernel), each from its own
+    start-of-chunk state, against the fp64 recurrence with per-token sa."""
+    C = require_gpu()
+    print("case rl_infctx replay 2048 chunks x 8 heads", flush=True)
+    g = torch.Generator().manual_seed(77)
+    heads, n = 8, 2048
+    lengths = torch.randint(1, 33, (n,), generator=g).numpy()
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    total = int(cu[-1])
+    inputs = [_randn((total, heads, 64), g, s, torch.bfloat16)
+              for s in (0.3, 2.0, 0.3, 0.3, 0.1, 0.1)]
+    boundary = _randn((n, heads, 64, 64), g, 0.05, torch.float32)
+    y_ref, _, sa_ref, _ = oracle.wkv7_f64(*(to_np(t) for t in inputs), cu_seqlens=cu,
+                                          state_indices=np.arange(n, dtype=np.int32),
+                                          state_pool=to_np(boundary), scale=0.5, want_sa=True)
+    out = torch.empty_like(inputs[3])
+    sa = torch.empty(inputs[0].shape, device="cuda", dtype=torch.float32)
+    C.rl_infctx_tmix_wkv7_chunk_fp32io16_backward_replay(
+        torch.tensor(cu[:-1], device="cuda", dtype=torch.int32),
+        torch.tensor(cu[1:], device="cuda", dtype=torch.int32), boundary.cuda(), *inputs, out,
+        sa, 0.5, None)
+    torch.cuda.synchronize()
+    assert_output_close(out, y_ref)
+    assert relative_rmse(to_np(sa), sa_ref) <= 1e-4
