@@ -632,11 +632,12 @@ __device__ __forceinline__ void wait_min_ge(int* c, int v, int limit, int* fault
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// Fused readout write-back of group gi (the state waves run it, one group
-// late, in place of the plain y write-back): thread (o_tok, o_c8) takes 8 channels of token o_tok of the group's
-// staged y rows.  GroupNorm over the head's 64 channels (the 8 consecutive
-// lanes of a token hold 8 channels each), the r k' r_k residual whose two
-// key-half sums the key waves left in sm.rkv, and the gate:
+// Fused readout write-back of group gi (the state waves run it one group
+// late, in place of the plain y write-back): thread (o_tok, o_c8) takes 8
+// channels of token o_tok of the group's staged y rows.  GroupNorm over the
+// head's 64 channels (the 8 consecutive lanes of a token hold 8 channels
+// each), the r k' r_k residual whose two key-half sums the key waves left in
+// sm.rkv, and the gate:
 //   out = (GroupNorm(y) * ln_w + ln_b + (sum r k' r_k) v) * g.
 template <class Io, bool kVExact>
 __device__ __forceinline__ void readout_write_back(const Smem<kVExact>& sm, const SegArgs& p,
@@ -737,8 +738,10 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
       if constexpr (!kSum) {
         const int64_t blk = static_cast<int64_t>(seg) * gridDim.x + h;
         const int64_t nblk = static_cast<int64_t>(gridDim.x) * gridDim.y;
-        if (!kRO || p.y != nullptr) fill_output_nan<Io>(static_cast<raw*>(p.y), p.out_elems, blk, nblk);
-        if constexpr (kRO) fill_output_nan<Io>(static_cast<raw*>(p.ro_out), p.out_elems, blk, nblk);
+        if (!kRO || p.y != nullptr)
+          fill_output_nan<Io>(static_cast<raw*>(p.y), p.out_elems, blk, nblk);
+        if constexpr (kRO)
+          fill_output_nan<Io>(static_cast<raw*>(p.ro_out), p.out_elems, blk, nblk);
       }
       return;
     }
