@@ -414,7 +414,8 @@ __device__ __forceinline__ f4 shfl_xor4(f4 x, int m) {
 // St = StF16: FP16 state pool with the Albatross delta update (see
 // serial_kernel); the staged retention becomes delta and each updated value
 // is rounded to fp16 before it feeds y and the store.
-template <class Io, class St>
+// kSa: also write every token's pre-update sa (the rl_infctx replay).
+template <class Io, class St, bool kSa = false>
 __device__ __forceinline__ void decode64_body(const SegArgs& p) {
   constexpr bool kAlbatross = __is_same(St, StF16);
   typedef _Float16 h4 __attribute__((ext_vector_type(4)));
@@ -498,8 +499,9 @@ __device__ __forceinline__ void decode64_body(const SegArgs& p) {
     o = shfl_xor4(sa, 32);
     sa.x += o.x; sa.y += o.y; sa.z += o.z; sa.w += o.w;
     // the replay contract's per-token pre-update sa (fp32, [T, H, D])
-    if (p.sa_out != nullptr && rq == 0)
-      *reinterpret_cast<f4*>(p.sa_out + base + 4 * c4) = sa;
+    if constexpr (kSa) {
+      if (rq == 0) *reinterpret_cast<f4*>(p.sa_out + base + 4 * c4) = sa;
+    }
 
     const f4 vv = *reinterpret_cast<const f4*>(&s_in[3][4 * c4]);
     const float* Rr = &s_in[0][rq * 16];
@@ -555,9 +557,9 @@ __device__ __forceinline__ void decode64_body(const SegArgs& p) {
   }
 }
 
-template <class Io, class St>
+template <class Io, class St, bool kSa = false>
 __global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
-  decode64_body<Io, St>(p);
+  decode64_body<Io, St, kSa>(p);
 }
 // The FP16-state form holds its state packed (32 registers): capped at 96
 // registers it keeps five waves per SIMD resident instead of four, with no
@@ -667,12 +669,20 @@ int launch_serial(int D, int dtype, bool bf16_state, const SegArgs& p, int nseg,
 int launch_decode(int D, int dtype, const SegArgs& p, int nseg, hipStream_t s) {
   if (D != 64 || p.boundary != nullptr) return FR2_ERR_UNSUPPORTED;
   const dim3 grid(p.num_heads, nseg);
-  if (dtype == FR2_DTYPE_BFLOAT16)
-    hipLaunchKernelGGL((decode64_kernel<IoBF16, StF32>), grid, dim3(64), 0, s, p);
-  else if (dtype == FR2_DTYPE_FLOAT16)
-    hipLaunchKernelGGL((decode64_kernel<IoF16, StF32>), grid, dim3(64), 0, s, p);
-  else
+  const bool sa = p.sa_out != nullptr;
+  if (dtype == FR2_DTYPE_BFLOAT16) {
+    if (sa)
+      hipLaunchKernelGGL((decode64_kernel<IoBF16, StF32, true>), grid, dim3(64), 0, s, p);
+    else
+      hipLaunchKernelGGL((decode64_kernel<IoBF16, StF32>), grid, dim3(64), 0, s, p);
+  } else if (dtype == FR2_DTYPE_FLOAT16) {
+    if (sa)
+      hipLaunchKernelGGL((decode64_kernel<IoF16, StF32, true>), grid, dim3(64), 0, s, p);
+    else
+      hipLaunchKernelGGL((decode64_kernel<IoF16, StF32>), grid, dim3(64), 0, s, p);
+  } else {
     return FR2_ERR_UNSUPPORTED;
+  }
   return record_launch();
 }
 
