@@ -124,16 +124,24 @@ class Runner:
         return start.elapsed_time(end) / launches
 
     def kernel_name(self) -> str:
-        """The family the library's policy picks (csrc/api.hip run_family)."""
+        """The kernel the library's policy picks (csrc/api.hip run_family,
+        decode_first / wave_per_unit)."""
         ms = self.ticket._max_seqlen()
-        units = self.w.state_indices.numel() * self.w.num_heads
-        if ms <= 4:
+        n = self.w.state_indices.numel()
+        units = n * self.w.num_heads
+        if ms <= 4 or (units >= 16384 and ms <= 6):
             return "decode64_kernel<IoBF16,StF32>"
-        if ms >= (5 if units <= 256 else 24 if units <= 1024 else 48 if units <= 4096 else 56):
-            return "chunk64_kernel<IoBF16,false>"
-        if ms <= 8 or units >= 4096:
-            return "decode64_kernel<IoBF16,StF32>"
-        return "serial64w_kernel<IoBF16,StF32>"
+        if units <= 256:
+            wave = False
+        elif units <= 512:
+            wave = ms <= 24
+        elif units <= 1024:
+            wave = ms <= 224
+        else:
+            wave = ms <= 512 or ms * n <= 2 * self.w.total_tokens
+        if wave:
+            return f"chunk64w_kernel<IoBF16,{'true' if n <= 256 else 'false'}>"
+        return "chunk64_kernel<IoBF16,false>"
 
 
 def cpu_baseline(w, threads: int, sample_tokens: int | None, min_seconds: float = 12.0):
@@ -585,8 +593,8 @@ def time_mid_length(torch, flashrwkv2_amd, steps: int, n: int = 2048, length: in
                     heads: int = 32):
     """Serving-style batch of many mid-length sequences (2048 x 100 tokens,
     H = 32, per-sequence fp32 states ~ N(0, 0.1)): the public call (which the
-    library dispatches by max_seqlen) and both candidate kernels forced, the
-    measurements behind the chunked-kernel threshold."""
+    library dispatches by max_seqlen and unit count) and the candidate
+    kernels forced, the measurements behind the policy."""
     from flashrwkv2_amd import workloads
 
     toks = workloads.make_tokens(n * length, heads, u_range=(-6.0, -0.5), seed=1005,
@@ -598,7 +606,8 @@ def time_mid_length(torch, flashrwkv2_amd, steps: int, n: int = 2048, length: in
     kms = run.time_kernel(steps)
     nbytes = algorithmic_bytes(w.total_tokens, w.num_heads, w.state_indices.numel())
     forced = {}
-    for kern, name in ((0, "serial64w_kernel<IoBF16,StF32>"), (2, "chunk64_kernel<IoBF16,false>")):
+    for kern, name in ((0, "serial64w_kernel<IoBF16,StF32>"), (2, "chunk64_kernel<IoBF16,false>"),
+                       (4, "chunk64w_kernel<IoBF16,false>")):
         f = lambda k=kern: run.C.tmix_wkv7_recurrent_fp32_kernel_forced(
             k, w.cu_seqlens, w.state_indices, run.state, *w.tokens, run.out, 1.0, None,
             run.ticket)
@@ -620,8 +629,8 @@ def time_short_batches(torch, flashrwkv2_amd, steps: int, heads: int = 32):
     """Short-sequence batches at both ends of the dispatch policy
     (csrc/api.hip run_family), each through the public call and with every
     kernel family forced: many 16-token sequences (65 536 (sequence, head)
-    units: the decode kernel, one wave per unit) and 8 sequences of 16 tokens
-    (256 units: the chunked kernel)."""
+    units: the chunked kernel with one wave per unit) and 8 sequences of 16
+    tokens (256 units: the chunked kernel with one workgroup per unit)."""
     from flashrwkv2_amd import workloads
 
     out = []
@@ -636,7 +645,8 @@ def time_short_batches(torch, flashrwkv2_amd, steps: int, heads: int = 32):
         forced = {}
         for kern, name in ((0, "serial64w_kernel<IoBF16,StF32>"),
                            (1, "decode64_kernel<IoBF16,StF32>"),
-                           (2, "chunk64_kernel<IoBF16,false>")):
+                           (2, "chunk64_kernel<IoBF16,false>"),
+                           (4, "chunk64w_kernel<IoBF16,false>")):
             f = lambda k=kern: run.C.tmix_wkv7_recurrent_fp32_kernel_forced(
                 k, w.cu_seqlens, w.state_indices, run.state, *w.tokens, run.out, 1.0, None,
                 run.ticket)

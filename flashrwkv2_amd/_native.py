@@ -29,6 +29,7 @@ KERNEL_SERIAL = 0
 KERNEL_DECODE = 1
 KERNEL_CHUNKED = 2
 KERNEL_SPLIT = 3   # chunked, long sequences cut into pieces (Python-side selector)
+KERNEL_CHUNKED_WAVE = 4   # chunked, one wavefront per (sequence, head)
 
 _i32p = POINTER(c_int32)
 

@@ -13,29 +13,52 @@ using fr2::SegArgs;
 
 // Kernel-family policy at D = 64 (replaces use_small_auto,
 // csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:378-391),
-// by the longest sequence L and the (sequence, head) unit count U of the
-// launch.  Measured with each family forced on equal-length batches, H = 32:
-//   U <= 256 (at most one chunked block per CU): the chunked kernel is the
-//     fastest from L = 5 on (L = 16: chunked 0.011, serial 0.013, decode
-//     0.024 ms);
-//   otherwise it wins from L = 24 (U <= 1024), 48 (U <= 4096), 56 (larger
-//     U; U = 65536, L = 48: decode 2.38, chunked 2.56, serial 2.86 ms;
-//     L = 64: chunked 2.86, decode 3.10 ms);
-//   below that the decode kernel (one wave per unit, the state in
-//     registers) beats the token-serial kernel except for U of 1024-4095 at
-//     L = 12-16 (U = 1024, L = 16: serial 0.025, decode 0.027 ms).
-// Longest sequence <= 4 always streams the state once with the decode kernel.
+// by the longest sequence L, the (sequence, head) unit count U and the mean
+// length of the launch.  Measured with each family forced on equal-length
+// batches, H = 32 (ms per call):
+//   L <= 4: the decode kernel (one wave per unit, tokens in order) streams
+//     the state once and is the fastest at every U; at U >= 16384 also up
+//     to L = 6 (U = 65536, L = 6: decode 0.472, chunked-wave 0.490);
+//   U <= 256 (at most one block per CU): the chunked kernel with one
+//     512-thread workgroup per unit from L = 5 on (L = 1024: 0.098 against
+//     0.399 with one wave per unit);
+//   larger U: the chunked kernel with one wave per unit (chunkw.hip), whose
+//     units hide each other's latency, up to L = 24 (U <= 512) or 224
+//     (U <= 1024) and at every L beyond that (U = 4096, L = 1024: 1.18
+//     against 1.42; U = 65536, L = 64: 1.48 against 2.86), except for
+//     skewed batches whose longest sequence exceeds twice the mean: a long
+//     sequence is one wave's serial chain there, and the workgroup-per-unit
+//     kernel finishes it sooner.
+// The token-serial kernel no longer wins anywhere on this grid; it remains
+// the kernel of the contracts the others do not cover (bf16 state, D != 64).
 constexpr int kDecodeMaxSeqlen = 4;
 constexpr int kChunkMinSeqlen = 5;   // the smallest chunked threshold (U <= 256)
 
-int chunk_min_seqlen(int64_t units) {
+bool decode_first(int64_t units, int max_seqlen) {
+  return max_seqlen <= kDecodeMaxSeqlen || (units >= 16384 && max_seqlen <= 6);
+}
+// one wave per unit (true) or one workgroup per unit, for a chunked launch
+bool wave_per_unit(int64_t units, int max_seqlen, int64_t total_tokens, int64_t nseg) {
+  if (units <= 256) return false;
+  if (units <= 512) return max_seqlen <= 24;
+  if (units <= 1024) return max_seqlen <= 224;
+  return max_seqlen <= 512 || static_cast<int64_t>(max_seqlen) * nseg <= 2 * total_tokens;
+}
+// the public policy's choice is the workgroup-per-unit chunked kernel (the
+// kernel the fused kk-gate / readout stages live in)
+bool workgroup_chunked(int64_t units, int max_seqlen, int64_t total_tokens, int64_t nseg) {
+  return max_seqlen > 0 && !decode_first(units, max_seqlen) &&
+         !wave_per_unit(units, max_seqlen, total_tokens, nseg);
+}
+// Contracts without a decode or wave form (the bf16-state entry) choose
+// between the workgroup-per-unit chunked kernel and the token-serial one:
+// chunked from L = 5 (U <= 256), 24 (U <= 1024), 48 (U <= 4096) or 56
+// (U = 65536, L = 48: serial 2.71, chunked 2.57 ms).
+int chunk_over_serial_min_seqlen(int64_t units) {
   return units <= 256 ? kChunkMinSeqlen : units <= 1024 ? 24 : units <= 4096 ? 48 : 56;
 }
-bool decode_before_serial(int64_t units, int max_seqlen) {
-  return max_seqlen <= 8 || units >= 4096;
-}
 
-enum Family { kAuto = -1, kSerial = 0, kDecode = 1, kChunked = 2 };
+enum Family { kAuto = -1, kSerial = 0, kDecode = 1, kChunked = 2, kChunkedWave = 4 };
 
 // Token tensors are read and written as 16-byte vectors: every token
 // pointer must be present and 16-byte aligned (a contiguous view with an odd
@@ -53,13 +76,16 @@ int run_family(int family, int D, int dtype, bool bf16_state, const SegArgs& p,
     const bool plain = p.sa_out == nullptr && p.boundary == nullptr && !bf16_state;
     const int64_t units = static_cast<int64_t>(nseg) * p.num_heads;
     family = kSerial;
-    if (D == 64 && plain && max_seqlen > 0 && max_seqlen <= kDecodeMaxSeqlen) {
-      family = kDecode;
-    } else if (D == 64 && plain && max_seqlen >= chunk_min_seqlen(units)) {
-      const int rc = fr2::launch_chunked(dtype, p, nseg, max_seqlen, s);
-      if (rc != FR2_ERR_UNSUPPORTED) return rc;
-    } else if (D == 64 && plain && max_seqlen > 0 && decode_before_serial(units, max_seqlen)) {
-      family = kDecode;
+    if (D == 64 && plain && max_seqlen > 0) {
+      if (decode_first(units, max_seqlen)) {
+        family = kDecode;
+      } else {
+        const int64_t total = p.out_elems / (static_cast<int64_t>(p.num_heads) * D);
+        const int rc = wave_per_unit(units, max_seqlen, total, nseg)
+                           ? fr2::launch_chunked_wave(dtype, p, nseg, s)
+                           : fr2::launch_chunked(dtype, p, nseg, max_seqlen, s);
+        if (rc != FR2_ERR_UNSUPPORTED) return rc;
+      }
     }
   }
   switch (family) {
@@ -70,6 +96,9 @@ int run_family(int family, int D, int dtype, bool bf16_state, const SegArgs& p,
     case kChunked:
       if (bf16_state || D != 64) return FR2_ERR_UNSUPPORTED;
       return fr2::launch_chunked(dtype, p, nseg, max_seqlen, s);
+    case kChunkedWave:
+      if (bf16_state || D != 64) return FR2_ERR_UNSUPPORTED;
+      return fr2::launch_chunked_wave(dtype, p, nseg, s);
     default: return FR2_ERR_INVALID_ARGUMENT;
   }
 }
@@ -123,7 +152,8 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kernel(
     const void* r, const void* decay_logits, const void* decay_bias,
     const void* k, const void* v, const void* a, const void* b, void* output,
     float scale, void* stream) {
-  if (kernel < kSerial || kernel > kChunked) return FR2_ERR_INVALID_ARGUMENT;
+  if (kernel != kSerial && kernel != kDecode && kernel != kChunked && kernel != kChunkedWave)
+    return FR2_ERR_INVALID_ARGUMENT;
   return recurrent_fp32(kernel, query_start_loc, state_indices, status,
                         num_sequences, num_heads, head_size, total_tokens,
                         max_seqlen, dtype, state, r, decay_logits, decay_bias, k,
@@ -162,7 +192,7 @@ extern "C" int fr2_wkv7_recurrent_fp32_split_plan(int32_t num_sequences, int32_t
   *lead_len = 0;
   *workspace_bytes = 0;
   const int64_t units = static_cast<int64_t>(num_sequences) * num_heads;
-  if (head_size != 64 || max_seqlen < chunk_min_seqlen(units) || units > kSplitMaxUnits)
+  if (head_size != 64 || max_seqlen < kChunkMinSeqlen || units > kSplitMaxUnits)
     return FR2_OK;
   // pieces after the lead piece: one block per CU in each phase, and pieces
   // of at least kSplitMinPiece tokens
@@ -442,7 +472,7 @@ extern "C" int fr2_wkv7_chunk_bf16_forward(
   // bf16 once at the end (infer_chunk_bf16_forward_varlen.cu:195-270), so long
   // requests run on the chunked MFMA kernel with a bf16 state load / store;
   // chunk_size only shapes the reference's workspace, not the arithmetic.
-  if (max_seqlen >= chunk_min_seqlen(static_cast<int64_t>(num_sequences) * num_heads)) {
+  if (max_seqlen >= chunk_over_serial_min_seqlen(static_cast<int64_t>(num_sequences) * num_heads)) {
     p.state_bf16 = true;
     const int rc = fr2::launch_chunked(FR2_DTYPE_BFLOAT16, p, num_sequences, max_seqlen,
                                        static_cast<hipStream_t>(stream));
@@ -722,10 +752,10 @@ extern "C" int fr2_wkv7_statetune_uniform_backward(
 // wkv_prepare fused into the chunked kernel's load stage: the recurrence's
 // k, a, b come from the projected key, the low-rank a-gate logits a12 and the
 // per-channel k_k, a0, k_a (never stored), and the gated key the readout
-// needs is written to new_k.  Chunked family only: head_size 64 and a
-// longest sequence at the chunked threshold of the launch's unit count
-// (chunk_min_seqlen), otherwise FR2_ERR_UNSUPPORTED (the caller then runs
-// fr2_tmix_kk_a_gate_forward and the plain entry).
+// needs is written to new_k.  Only where the public policy picks the
+// workgroup-per-unit chunked kernel (workgroup_chunked: head_size 64, no
+// decode or wave-per-unit form), otherwise FR2_ERR_UNSUPPORTED (the caller
+// then runs fr2_tmix_kk_a_gate_forward and the plain entry).
 extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate(
     const int32_t* query_start_loc, const int32_t* state_indices, const int32_t* status,
     int32_t num_sequences, int32_t num_heads, int32_t head_size, int64_t total_tokens,
@@ -737,8 +767,8 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate(
     return FR2_ERR_INVALID_ARGUMENT;
   if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 || total_tokens <= 0)
     return FR2_ERR_INVALID_ARGUMENT;
-  if (head_size != 64 ||
-      max_seqlen < chunk_min_seqlen(static_cast<int64_t>(num_sequences) * num_heads))
+  if (head_size != 64 || !workgroup_chunked(static_cast<int64_t>(num_sequences) * num_heads,
+                                            max_seqlen, total_tokens, num_sequences))
     return FR2_ERR_UNSUPPORTED;
   SegArgs p;
   p.bounds = query_start_loc;
@@ -770,8 +800,8 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate_readout(
     return FR2_ERR_INVALID_ARGUMENT;
   if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 || total_tokens <= 0)
     return FR2_ERR_INVALID_ARGUMENT;
-  if (head_size != 64 ||
-      max_seqlen < chunk_min_seqlen(static_cast<int64_t>(num_sequences) * num_heads))
+  if (head_size != 64 || !workgroup_chunked(static_cast<int64_t>(num_sequences) * num_heads,
+                                            max_seqlen, total_tokens, num_sequences))
     return FR2_ERR_UNSUPPORTED;
   SegArgs p;
   p.bounds = query_start_loc;

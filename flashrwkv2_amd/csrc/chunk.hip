@@ -351,36 +351,19 @@ __device__ __forceinline__ void key_part2(Smem<kVExact>& sm, ChunkOps<kVExact>& 
   // P[t][s] of block b, summed over the two key halves, is
   // mp0[0][b][s][t] + mp0[1][b][s][t]
   const float (*mp0)[4][L][MPP] = sm.mpart[mp][cc];
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   if (hh == mp) {
     // M[e] = Mab[4q+e][i] (accumulator layout), Mt[e] = Mab[i][4q+e]
     const f32x4 m4 = *reinterpret_cast<const f32x4*>(&mp0[0][0][i][4 * q]) +
                      *reinterpret_cast<const f32x4*>(&mp0[1][0][i][4 * q]);
-    f32x4 M, Mt, I4;
+    f32x4 M, Mt;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int r = 4 * q + e;
       const float mt = mp0[0][0][r][i] + mp0[1][0][r][i];
       M[e] = (r > i) ? m4[e] : 0.f;
       Mt[e] = (i > r) ? mt : 0.f;
-      I4[e] = (r == i) ? 1.0f : 0.0f;
     }
-    // T = (I - Mab)^-1 = (I+M)(I+M^2)(I+M^4)(I+M^8) (M strictly lower,
-    // 16x16), keeping both orientations of each factor in accumulator
-    // registers; X Y = mm_ab(A form of X^T's accumulator, B form of Y's).
-    const Split4 sM = split4(M), sMt = split4(Mt);
-    const f32x4 M2 = mm_ab(as_a(sMt), as_b(sM), zero);
-    const f32x4 M2t = mm_ab(as_a(sM), as_b(sMt), zero);
-    const Split4 sM2 = split4(M2), sM2t = split4(M2t);
-    const f32x4 T1t = I4 + Mt;
-    const f32x4 T2t = mm_ab(as_a(sM2), as_b(split4(T1t)), T1t);
-    const f32x4 M4 = mm_ab(as_a(sM2t), as_b(sM2), zero);
-    const f32x4 M4t = mm_ab(as_a(sM2), as_b(sM2t), zero);
-    const Split4 sM4 = split4(M4);
-    const f32x4 T4t = mm_ab(as_a(sM4), as_b(split4(T2t)), T2t);
-    const f32x4 M8 = mm_ab(as_a(split4(M4t)), as_b(sM4), zero);
-    const f32x4 Tt = mm_ab(as_a(split4(M8)), as_b(split4(T4t)), T4t);   // accumulator of T^T
-    store_aop(op.t, i, q, as_a(split4(Tt)));                            // = A operand of T
+    store_aop(op.t, i, q, t_inverse(M, Mt, i, q));
   } else {
     f32x4 mak, mrb, mrk;
 #pragma unroll

@@ -1,0 +1,382 @@
+// Chunked WKV7 prefill with one wavefront per (sequence, head) unit (D = 64,
+// fp32 state carry), for launches with many units.
+//
+// Same chunk algebra as chunk.hip (L = 16 tokens, S0 = start-of-chunk state,
+// gamma_t = cumulative retention inside the chunk):
+//   A~ = a*gamma_{t-1}, R~ = r*gamma_t, B^ = b/gamma_t, K^ = k/gamma_t
+//   T = (I - strict_tril(A~ B^T))^-1
+//   U = T (A~ S0 + Mak V),  Y = R~ S0 + Mrb U + Mrk V,
+//   S_L = diag(gamma_L) (S0 + B^^T U + K^^T V)
+// with every product on v_mfma_f32_16x16x32_bf16 over bf16 hi/lo split
+// operands (fp32-level accuracy).
+//
+// chunk64_kernel spreads one unit over a 512-thread workgroup whose waves
+// hand operators to each other through LDS; that is the fastest form when
+// there is at most one unit per CU.  With many units the per-unit pipeline's
+// hand-offs and shared operand reads cost more than they save: here one
+// wave does all of a unit's work, keeping the whole 64x64 state in 64
+// accumulator registers, and the SIMDs hide one wave's latency with another
+// unit's wave.  Nothing is exchanged between waves; LDS holds only each
+// wave's own transposes (B^, K^ and V rows read back as K = token operands)
+// and output staging.
+//
+// Register layout of lane (i, q) = (lane % 16, lane / 16):
+//   token operands (the A-operand layout): token i of the chunk, keys
+//     32m + 8q .. 32m + 8q + 7 for the two K steps m = 0, 1;
+//   state tile S[kb][vb] (accumulator layout): value column 16vb + i, keys
+//     32(kb/2) + 8q + 4(kb%2) + e, e = 0..3.  With this key order the tiles
+//     2m and 2m+1 of a column block are the B operand of K step m as they
+//     stand, and the transposed reads of B^ / K^ address the same keys.
+#include "mfma.h"
+#include "recurrent.h"
+
+namespace fr2 {
+namespace {
+
+constexpr int D = 64;
+constexpr int L = 16;
+constexpr int WPB = 4;          // waves (units) per workgroup
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegExpHalf = -0.6065306597126334f;   // -exp(-1/2)
+
+constexpr int kOrderMaxSeqs = 256;   // longest-first order up to this many sequences
+
+// One wave's LDS: its chunk's B^, K^ (hi and lo) and V rows, read back
+// transposed, gamma_L, and the staged output rows.
+template <bool kVExact>
+struct alignas(16) WaveLds {
+  static constexpr int TP = kVExact ? D + 16 : D + 8;   // token row pitch
+  float gl[D];
+  __bf16 b_h[L][TP], b_l[L][TP], k_h[L][TP], k_l[L][TP], v_h[L][TP];
+  __bf16 v_l[kVExact ? 1 : L][TP];                       // fp16 tokens only
+};
+static_assert(sizeof(WaveLds<true>::b_h) >= kOrderMaxSeqs * sizeof(int),
+              "the sequence lengths of the longest-first order fit in b_h");
+static_assert(sizeof(WaveLds<true>) % 16 == 0 && sizeof(WaveLds<false>) % 16 == 0,
+              "wave blocks must keep 16-byte alignment");
+static_assert(offsetof(WaveLds<true>, b_h) % 16 == 0 && offsetof(WaveLds<false>, v_l) % 16 == 0,
+              "row arrays must be 16-byte aligned");
+
+// Longest-first order of the sequences of a packed batch: with one wave per
+// unit, a long sequence is one long serial chain, so it has to start first
+// (the units of shorter sequences fill the SIMDs around it).  Returns the
+// index of the sequence of rank `rank` among sequences [0, n) by decreasing
+// length (ties by index), or -1 when rank >= n.  `len` is wave-private LDS
+// for n ints; the ranking is O(n^2 / 64) per wave, so it is used for small n
+// only (kOrderMaxSeqs).
+__device__ __attribute__((noinline)) int seq_of_rank(const int32_t* bounds, int n, int rank, int* len,
+                                           int lane) {
+  for (int k = lane; k < n; k += 64) len[k] = bounds[k + 1] - bounds[k];
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);   // one wave: its LDS accesses complete in order
+  for (int j0 = 0; j0 < n; j0 += 64) {
+    const int j = j0 + lane;
+    const int lj = j < n ? len[j] : -1;
+    int r = 0;
+    for (int k = 0; k < n; ++k) {
+      const int lk = len[k];
+      r += (lk > lj || (lk == lj && k < j)) ? 1 : 0;
+    }
+    const uint64_t hit = __ballot(j < n && r == rank);
+    if (hit != 0) return j0 + __builtin_ctzll(hit);
+  }
+  return -1;
+}
+
+// key held by item e of state tile kb in lane group q
+__device__ __forceinline__ int tile_key(int kb, int q, int e) {
+  return 32 * (kb >> 1) + 8 * q + 4 * (kb & 1) + e;
+}
+
+// kOrder: the units run in longest-first order of their sequences (packed
+// batches of at most kOrderMaxSeqs sequences)
+template <class Io, bool kOrder>
+__global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nunits) {
+  using raw = typename Io::raw;
+  constexpr bool kVExact = !__is_same(Io, IoF16);
+  __shared__ WaveLds<kVExact> lds[WPB];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 15;
+  const int q = lane >> 4;
+  const int H = p.num_heads;
+  raw* yout = static_cast<raw*>(p.y);
+  if (p.status != nullptr && p.status[0] != 0) {
+    fill_output_nan<Io>(yout, p.out_elems, blockIdx.x, gridDim.x);
+    return;
+  }
+  // the heads of a sequence are adjacent units (adjacent 128-byte pieces of
+  // every token row)
+  const int unit = blockIdx.x * WPB + wv;
+  if (unit >= nunits) return;
+  WaveLds<kVExact>& sm = lds[wv];
+  int seg = unit / H;
+  const int h = unit - seg * H;
+  const int nseq = nunits / H;
+  const int nactive = p.status != nullptr ? min(p.status[2], nseq) : nseq;
+  if (seg >= nactive) return;
+  if (kOrder && nactive > 1) {
+    // wave-uniform: keep the unit's indices in scalar registers
+    seg = __builtin_amdgcn_readfirstlane(
+        seq_of_rank(p.bounds, nactive, seg, reinterpret_cast<int*>(&sm.b_h[0][0]), lane));
+    if (seg < 0) return;
+  }
+  int t0, t1, slot;
+  resolve_segment(p, seg, t0, t1, slot);
+
+  const int64_t head_off = static_cast<int64_t>(h) * D;
+  const int64_t row_stride = static_cast<int64_t>(H) * D;
+  const int64_t sbase = (static_cast<int64_t>(slot) * H + h) * D * D;
+
+  f32x4 S[4][4];   // [kb][vb]
+  if (p.state_in != nullptr) {
+    const float* sin = static_cast<const float*>(p.state_in) + sbase + i;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[kb][vb][e] = sin[tile_key(kb, q, e) * D + 16 * vb];
+  } else {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb) S[kb][vb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // token rows of lane (i, q): row t of tensor j, keys 32m + 8q ..
+  const raw* src[6] = {static_cast<const raw*>(p.r), static_cast<const raw*>(p.logits),
+                       static_cast<const raw*>(p.k), static_cast<const raw*>(p.v),
+                       static_cast<const raw*>(p.a), static_cast<const raw*>(p.b)};
+  const int64_t lane_off = head_off + 8 * q;
+  const raw* bias = static_cast<const raw*>(p.bias);
+  // rows past the segment end are read from its last row (always in bounds)
+  // and zeroed when used
+  auto load_rows = [&](u32x4 (&dst)[6][2], int c) {
+    const int tok = min(t0 + c * L + i, t1 - 1);
+    const int64_t off = static_cast<int64_t>(tok) * row_stride + lane_off;
+#pragma unroll
+    for (int j = 0; j < 6; ++j)
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+        dst[j][m] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(src[j] + off + 32 * m));
+  };
+
+  constexpr float kC = kNegExpHalf * kLog2e;
+  constexpr float kInvC = 1.0f / kC;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  const int nchunks = (t1 - t0 + L - 1) / L;
+  u32x4 rows[6][2];
+  if (nchunks > 0) load_rows(rows, 0);
+  for (int c = 0; c < nchunks; ++c) {
+    const bool valid = t0 + c * L + i < t1;
+    const u32x4 zero4 = {0u, 0u, 0u, 0u};
+    // ---- operands of the chunk (keys of K step m in registers)
+    Sp8 As[2], Rs[2], Bs[2], Ks[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      __builtin_amdgcn_sched_barrier(0);
+      float xr[8], xl[8], xk[8], xa[8], xb[8];
+      unpack8<Io>(valid ? rows[0][m] : zero4, xr);
+      unpack8<Io>(rows[1][m], xl);
+      unpack8<Io>(valid ? rows[2][m] : zero4, xk);
+      unpack8<Io>(valid ? rows[4][m] : zero4, xa);
+      unpack8<Io>(valid ? rows[5][m] : zero4, xb);
+      float nb[8];
+      if (bias != nullptr) {
+        unpack8<Io>(*reinterpret_cast<const u32x4*>(bias + lane_off + 32 * m), nb);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) nb[e] *= -kLog2e;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) nb[e] = 0.f;
+      }
+      // log2 of the retention, log2(w) = c sigmoid(x) with c = -exp(-1/2)
+      // log2(e), as 1 / ((1 + 2^(-log2(e) x)) / c); then its prefix sum over
+      // the chunk's tokens (the 16 lanes of a DPP row)
+      float g2[8], gm[8], gp[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g2[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(xl[e], -kLog2e, nb[e]));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float lw2 = __builtin_amdgcn_rcpf(__builtin_fmaf(g2[e], kInvC, kInvC));
+        g2[e] = valid ? lw2 : 0.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g2[e] += row_shr<1>(g2[e]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g2[e] += row_shr<2>(g2[e]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g2[e] += row_shr<4>(g2[e]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g2[e] += row_shr<8>(g2[e]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) gm[e] = __builtin_amdgcn_exp2f(g2[e]);      // gamma_t
+#pragma unroll
+      for (int e = 0; e < 8; ++e) gp[e] = row_prev(gm[e], 1.0f);              // gamma_{t-1}
+      float at[8], rt[8], bh[8], kh[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float ig = __builtin_amdgcn_exp2f(-g2[e]);                     // 1 / gamma_t
+        at[e] = xa[e] * gp[e];
+        rt[e] = xr[e] * gm[e];
+        bh[e] = xb[e] * ig;
+        kh[e] = xk[e] * ig;
+      }
+      if (i == L - 1) {
+        *reinterpret_cast<f32x4*>(&sm.gl[32 * m + 8 * q]) = f32x4{gm[0], gm[1], gm[2], gm[3]};
+        *reinterpret_cast<f32x4*>(&sm.gl[32 * m + 8 * q + 4]) = f32x4{gm[4], gm[5], gm[6], gm[7]};
+      }
+      As[m] = split8(at);
+      Rs[m] = split8(rt);
+      Bs[m] = split8(bh);
+      Ks[m] = split8(kh);
+      const int col = 32 * m + 8 * q;
+      *reinterpret_cast<bf16x8*>(&sm.b_h[i][col]) = Bs[m].hi;
+      *reinterpret_cast<bf16x8*>(&sm.b_l[i][col]) = Bs[m].lo;
+      *reinterpret_cast<bf16x8*>(&sm.k_h[i][col]) = Ks[m].hi;
+      *reinterpret_cast<bf16x8*>(&sm.k_l[i][col]) = Ks[m].lo;
+      const u32x4 vraw = valid ? rows[3][m] : zero4;
+      if constexpr (kVExact) {
+        *reinterpret_cast<u32x4*>(&sm.v_h[i][col]) = vraw;      // bf16 values are exact
+      } else {
+        float xv[8];
+        unpack8<Io>(vraw, xv);
+        const Sp8 vs = split8(xv);
+        *reinterpret_cast<bf16x8*>(&sm.v_h[i][col]) = vs.hi;
+        *reinterpret_cast<bf16x8*>(&sm.v_l[i][col]) = vs.lo;
+      }
+    }
+
+    // ---- token-token blocks over the 64 keys.  mma32(X, Y) gives lane
+    // (i, q) item e = X_{4q+e} . Y_i, so each block is formed directly in
+    // the orientation its consumer needs.
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 mab = zero, mabt = zero, makt = zero, mrbt = zero, mrkt = zero;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      mab = mma32x3(As[m], Bs[m], mab);     // Mab[4q+e][i]
+      mabt = mma32x3(Bs[m], As[m], mabt);   // Mab[i][4q+e]
+      makt = mma32x3(Ks[m], As[m], makt);   // Mak[i][4q+e]  (A-operand form)
+      mrbt = mma32x3(Bs[m], Rs[m], mrbt);   // Mrb[i][4q+e]
+      mrkt = mma32x3(Ks[m], Rs[m], mrkt);   // Mrk[i][4q+e]
+    }
+    f32x4 M, Mt, mak, mrb, mrk;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int s = 4 * q + e;
+      M[e] = (s > i) ? mab[e] : 0.f;
+      Mt[e] = (i > s) ? mabt[e] : 0.f;
+      mak[e] = (i > s) ? makt[e] : 0.f;
+      mrb[e] = (i >= s) ? mrbt[e] : 0.f;
+      mrk[e] = (i >= s) ? mrkt[e] : 0.f;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const AOp Ta = t_inverse(M, Mt, i, q);
+    const AOp Mak = as_a(split4(mak));
+    const AOp Mrb = as_a(split4(mrb));
+    const AOp Mrk = as_a(split4(mrk));
+
+    // ---- state chain.  B^^T and K^^T as A operands (row = key of tile kb,
+    // K = token); gamma_L of the tile rows is read where it is applied.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const int trow = 4 * q + (i >> 2);
+#pragma unroll
+    for (int vb = 0; vb < 4; ++vb) {
+      // keep each column block's reads and products in its own region (a
+      // scheduler that hoists every block's LDS reads needs ~100 more registers)
+      __builtin_amdgcn_sched_barrier(0);
+      Sp8 Sb[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const Split4 x = split4(S[2 * m][vb]), y = split4(S[2 * m + 1][vb]);
+        Sb[m].hi = __builtin_bit_cast(bf16x8, u32x4{x.h0, x.h1, y.h0, y.h1});
+        Sb[m].lo = __builtin_bit_cast(bf16x8, u32x4{x.l0, x.l1, y.l0, y.l1});
+      }
+      // V[4q+e][16vb+i] as the K = token operand
+      const bf16x4 vh = tr_rows(&sm.v_h[4 * q + (i >> 2)][16 * vb + 4 * (i & 3)]);
+      auto times_v = [&](AOp a, f32x4 acc) {
+        if constexpr (kVExact) {
+          return mm_ax(a, as_bx(vh), acc);
+        } else {
+          const bf16x4 vl = tr_rows(&sm.v_l[4 * q + (i >> 2)][16 * vb + 4 * (i & 3)]);
+          return mm_ab(a, as_b(vh, vl), acc);
+        }
+      };
+      f32x4 X = times_v(Mak, zero);
+      f32x4 Y = times_v(Mrk, zero);
+      X = mma32x3(As[0], Sb[0], X);
+      X = mma32x3(As[1], Sb[1], X);
+      Y = mma32x3(Rs[0], Sb[0], Y);
+      Y = mma32x3(Rs[1], Sb[1], Y);
+      const f32x4 Uf = mm_ab(Ta, as_b(split4(X)), zero);
+      const BOp Us = as_b(split4(Uf));
+      Y = mm_ab(Mrb, Us, Y);
+      // y rows 4q + e, column 16vb + i
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (t0 + c * L + 4 * q + e < t1)
+          yout[static_cast<int64_t>(t0 + c * L + 4 * q + e) * row_stride + head_off + 16 * vb + i] =
+              Io::from_f32(p.scale * Y[e]);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        // B^^T and K^^T of tile kb as A operands (row = key, K = token)
+        const int col = 32 * (kb >> 1) + 8 * (i & 3) + 4 * (kb & 1);
+        const AOp Bt = __builtin_shufflevector(tr_rows(&sm.b_h[trow][col]),
+                                               tr_rows(&sm.b_l[trow][col]), 0, 1, 2, 3, 4, 5, 6, 7);
+        const AOp Kt = __builtin_shufflevector(tr_rows(&sm.k_h[trow][col]),
+                                               tr_rows(&sm.k_l[trow][col]), 0, 1, 2, 3, 4, 5, 6, 7);
+        f32x4 acc = mm_ab(Bt, Us, S[kb][vb]);
+        acc = times_v(Kt, acc);
+        S[kb][vb] = acc * *reinterpret_cast<const f32x4*>(&sm.gl[tile_key(kb, q, 0)]);
+      }
+    }
+    // the next chunk's rows are requested before this chunk's output stores
+    // (the other units' waves on the SIMD cover their latency)
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + 1 < nchunks) load_rows(rows, c + 1);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  }
+
+  if (p.state_out != nullptr) {
+    float* sout = static_cast<float*>(p.state_out) + sbase + i;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sout[tile_key(kb, q, e) * D + 16 * vb] = S[kb][vb][e];
+  }
+}
+
+}  // namespace
+
+int launch_chunked_wave(int dtype, const SegArgs& p, int nseg, hipStream_t s) {
+  if (p.sa_out != nullptr || p.boundary != nullptr || p.reverse || p.state_bf16 ||
+      p.split_pieces > 0 || p.kk_scale != nullptr || p.ro_out != nullptr)
+    return FR2_ERR_UNSUPPORTED;
+  const int64_t units = static_cast<int64_t>(nseg) * p.num_heads;
+  if (units <= 0 || units > (int64_t{1} << 30)) return FR2_ERR_INVALID_ARGUMENT;
+  const dim3 grid(static_cast<unsigned>((units + WPB - 1) / WPB));
+  const bool order = p.uniform_len <= 0 && p.chunk_offsets == nullptr && p.ends == nullptr &&
+                     nseg > 1 && nseg <= kOrderMaxSeqs;
+  const int n = static_cast<int>(units);
+  if (dtype == FR2_DTYPE_BFLOAT16) {
+    if (order)
+      hipLaunchKernelGGL((chunk64w_kernel<IoBF16, true>), grid, dim3(64 * WPB), 0, s, p, n);
+    else
+      hipLaunchKernelGGL((chunk64w_kernel<IoBF16, false>), grid, dim3(64 * WPB), 0, s, p, n);
+  } else if (dtype == FR2_DTYPE_FLOAT16) {
+    if (order)
+      hipLaunchKernelGGL((chunk64w_kernel<IoF16, true>), grid, dim3(64 * WPB), 0, s, p, n);
+    else
+      hipLaunchKernelGGL((chunk64w_kernel<IoF16, false>), grid, dim3(64 * WPB), 0, s, p, n);
+  } else {
+    return FR2_ERR_UNSUPPORTED;
+  }
+  return record_launch();
+}
+
+}  // namespace fr2

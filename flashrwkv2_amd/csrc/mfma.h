@@ -117,6 +117,31 @@ __device__ __forceinline__ BOp as_b(bf16x4 hi, bf16x4 lo) {
                                  3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
 }
 
+// T = (I - M)^-1 for a strictly lower triangular 16x16 M, given in both
+// accumulator orientations (lane (i, q): M[e] = M[4q+e][i], Mt[e] =
+// M[i][4q+e]), as (I+M)(I+M^2)(I+M^4)(I+M^8), keeping both orientations of
+// each factor in registers (X Y = mm_ab(A form of X^T's accumulator, B form
+// of Y's)).  Returns the A operand of T.
+__device__ __forceinline__ AOp t_inverse(f32x4 M, f32x4 Mt, int i, int q) {
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 I4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) I4[e] = (4 * q + e == i) ? 1.0f : 0.0f;
+  const Split4 sM = split4(M), sMt = split4(Mt);
+  const f32x4 M2 = mm_ab(as_a(sMt), as_b(sM), zero);
+  const f32x4 M2t = mm_ab(as_a(sM), as_b(sMt), zero);
+  const Split4 sM2 = split4(M2), sM2t = split4(M2t);
+  const f32x4 T1t = I4 + Mt;
+  const f32x4 T2t = mm_ab(as_a(sM2), as_b(split4(T1t)), T1t);
+  const f32x4 M4 = mm_ab(as_a(sM2t), as_b(sM2), zero);
+  const f32x4 M4t = mm_ab(as_a(sM2), as_b(sM2t), zero);
+  const Split4 sM4 = split4(M4);
+  const f32x4 T4t = mm_ab(as_a(sM4), as_b(split4(T2t)), T2t);
+  const f32x4 M8 = mm_ab(as_a(split4(M4t)), as_b(sM4), zero);
+  const f32x4 Tt = mm_ab(as_a(split4(M8)), as_b(split4(T4t)), T4t);   // accumulator of T^T
+  return as_a(split4(Tt));                                            // = A operand of T
+}
+
 // Inclusive prefix sum over the 16 lanes of a DPP row (the token axis).
 template <int N>
 __device__ __forceinline__ float row_shr(float x) {

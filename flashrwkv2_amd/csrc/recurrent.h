@@ -103,6 +103,28 @@ struct SegArgs {
   void* ro_out = nullptr;
 };
 
+// Token range [t0, t1) and state slot of segment `seg` (see SegArgs).
+__device__ __forceinline__ bool resolve_segment(const SegArgs& p, int seg,
+                                                int& t0, int& t1, int& slot) {
+  if (p.uniform_len > 0) {
+    t0 = seg * p.uniform_len;
+    t1 = t0 + p.uniform_len;
+  } else if (p.chunk_offsets != nullptr) {
+    const int c0 = p.chunk_offsets[seg];
+    const int c1 = p.chunk_offsets[seg + 1];
+    t0 = p.bounds[c0];
+    t1 = p.ends[c1 - 1];
+  } else if (p.ends != nullptr) {
+    t0 = p.bounds[seg];
+    t1 = p.ends[seg];
+  } else {
+    t0 = p.bounds[seg];
+    t1 = p.bounds[seg + 1];
+  }
+  slot = p.slots ? p.slots[seg] : seg;
+  return true;
+}
+
 // Token range [start, start + len) of piece j of a split sequence of n
 // tokens, and the index of the sequence's last piece.
 __host__ __device__ inline void split_piece(const SegArgs& p, int n, int j, int& start,
@@ -129,6 +151,10 @@ int launch_advance_elapsed(const SegArgs& p, int nseg, int32_t* elapsed, hipStre
 int launch_chunked_kk(int dtype, const SegArgs& p, int nseg, hipStream_t s);
 int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen,
                    hipStream_t s);
+// The chunked prefill with one wavefront per (sequence, head) unit (plain
+// contract: no sa / boundary outputs, fp32 state), for launches with many
+// units.
+int launch_chunked_wave(int dtype, const SegArgs& p, int nseg, hipStream_t s);
 // Sequence-split chunked prefill (D = 64, fp32 state, plain contract):
 // `pieces` pieces per sequence, of `piece_len` tokens except piece 0, which
 // has lead_len tokens when lead_len > 0 (the pipelined split: piece 0 runs on

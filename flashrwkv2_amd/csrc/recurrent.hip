@@ -15,27 +15,6 @@
 
 namespace fr2 {
 
-__device__ __forceinline__ bool resolve_segment(const SegArgs& p, int seg,
-                                                int& t0, int& t1, int& slot) {
-  if (p.uniform_len > 0) {
-    t0 = seg * p.uniform_len;
-    t1 = t0 + p.uniform_len;
-  } else if (p.chunk_offsets != nullptr) {
-    const int c0 = p.chunk_offsets[seg];
-    const int c1 = p.chunk_offsets[seg + 1];
-    t0 = p.bounds[c0];
-    t1 = p.ends[c1 - 1];
-  } else if (p.ends != nullptr) {
-    t0 = p.bounds[seg];
-    t1 = p.ends[seg];
-  } else {
-    t0 = p.bounds[seg];
-    t1 = p.bounds[seg + 1];
-  }
-  slot = p.slots ? p.slots[seg] : seg;
-  return true;
-}
-
 // Returns false when this workgroup has nothing to do (fail-closed status or
 // an inactive sequence).  On a bad status the whole grid writes NaN.
 template <class Io>

@@ -123,7 +123,9 @@ int fr2_wkv7_recurrent_fp32_forward(
 
 /*
  * Same contract, but the kernel family is forced: 0 = token-serial,
- * 1 = decode (state streaming), 2 = chunked MFMA (head_size 64 only).
+ * 1 = decode (state streaming), 2 = chunked MFMA, one workgroup per
+ * (sequence, head), 4 = chunked MFMA, one wavefront per (sequence, head)
+ * (2 and 4: head_size 64 only).
  * Used by tests and benchmarks to pin each kernel against the oracle.
  * Has no reference counterpart (the reference's dispatch is internal,
  * README.md:81-85); it exposes the same kernels as the entry above.
@@ -195,9 +197,11 @@ int fr2_wkv7_recurrent_fp32_forward_split(
  *   u = k k_k, kk = u / max(|u|, 1e-12), g = sigmoid(a0 + a12),
  *   key = k (1 + (g - 1) k_a), a = -kk, b = kk g
  * in fp32, runs the recurrence on (key, a, b) and writes key to new_k (the
- * readout's input); a and b are never stored.  FR2_ERR_UNSUPPORTED outside
- * the chunked family (head_size 64, max_seqlen at the chunked threshold of
- * num_sequences * num_heads units: 5 for at most 256, up to 56): the caller then runs
+ * readout's input); a and b are never stored.  FR2_ERR_UNSUPPORTED unless
+ * fr2_wkv7_recurrent_fp32_forward would run the workgroup-per-unit chunked
+ * kernel on this launch (head_size 64; max_seqlen >= 5 for at most 256
+ * (sequence, head) units, longer for more units, where the kernel with one
+ * wavefront per unit is faster): the caller then runs
  * fr2_tmix_kk_a_gate_forward and fr2_wkv7_recurrent_fp32_forward.  Replaces
  * the pair tmix_kk_a_gate_forward_varlen_cuda
  * (csrc/sm120/tmix/wkv_prepare/internal/kk_a_gate/infer_fp16_forward_varlen.cu)

@@ -31,7 +31,7 @@ from flashrwkv2_amd.tmix.wkv7 import (  # noqa: E402
     prepare_tmix_wkv7_recurrent_metadata,
 )
 
-SERIAL, DECODE, CHUNKED = 0, 1, 2
+SERIAL, DECODE, CHUNKED, CHUNKED_WAVE = 0, 1, 2, 4
 
 
 def _run(case, *, state_pool=None, **kw):
@@ -78,7 +78,7 @@ def test_packed_fp32_state_precision_and_state_safety(dtype, head_size, with_bia
     assert torch.equal(case["state_pool"], second)
 
 
-@pytest.mark.parametrize("kernel", [SERIAL, DECODE, CHUNKED])
+@pytest.mark.parametrize("kernel", [SERIAL, DECODE, CHUNKED, CHUNKED_WAVE])
 @pytest.mark.parametrize("lengths", [(1,), (1, 2, 4), (1, 15, 16, 17, 65), (3,) * 12,
                                      (200, 31, 48)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
