@@ -50,13 +50,6 @@ bool workgroup_chunked(int64_t units, int max_seqlen, int64_t total_tokens, int6
   return max_seqlen > 0 && !decode_first(units, max_seqlen) &&
          !wave_per_unit(units, max_seqlen, total_tokens, nseg);
 }
-// Contracts without a decode or wave form (the bf16-state entry) choose
-// between the workgroup-per-unit chunked kernel and the token-serial one:
-// chunked from L = 5 (U <= 256), 24 (U <= 1024), 48 (U <= 4096) or 56
-// (U = 65536, L = 48: serial 2.71, chunked 2.57 ms).
-int chunk_over_serial_min_seqlen(int64_t units) {
-  return units <= 256 ? kChunkMinSeqlen : units <= 1024 ? 24 : units <= 4096 ? 48 : 56;
-}
 
 enum Family { kAuto = -1, kSerial = 0, kDecode = 1, kChunked = 2, kChunkedWave = 4 };
 
@@ -469,16 +462,23 @@ extern "C" int fr2_wkv7_chunk_bf16_forward(
   p.y = output;
   p.scale = scale;
   // The contract keeps the state in fp32 inside the call and rounds it to
-  // bf16 once at the end (infer_chunk_bf16_forward_varlen.cu:195-270), so long
-  // requests run on the chunked MFMA kernel with a bf16 state load / store;
-  // chunk_size only shapes the reference's workspace, not the arithmetic.
-  if (max_seqlen >= chunk_over_serial_min_seqlen(static_cast<int64_t>(num_sequences) * num_heads)) {
-    p.state_bf16 = true;
-    const int rc = fr2::launch_chunked(FR2_DTYPE_BFLOAT16, p, num_sequences, max_seqlen,
-                                       static_cast<hipStream_t>(stream));
-    if (rc != FR2_ERR_UNSUPPORTED) return rc;
-    p.state_bf16 = false;
-  }
+  // bf16 once at the end (infer_chunk_bf16_forward_varlen.cu:195-270), so the
+  // request runs on a chunked MFMA kernel with a bf16 state load / store
+  // (chunk_size only shapes the reference's workspace, not the arithmetic):
+  // the wavefront-per-unit kernel where the fp32-state policy picks it, and
+  // also for sequences of at most 4 tokens (which have no decode form here;
+  // it beats the token-serial kernel there at every unit count measured),
+  // otherwise the workgroup-per-unit kernel.
+  const int64_t units = static_cast<int64_t>(num_sequences) * num_heads;
+  p.state_bf16 = true;
+  const int rc =
+      (max_seqlen < kChunkMinSeqlen || wave_per_unit(units, max_seqlen, total_tokens, num_sequences))
+          ? fr2::launch_chunked_wave(FR2_DTYPE_BFLOAT16, p, num_sequences,
+                                     static_cast<hipStream_t>(stream))
+          : fr2::launch_chunked(FR2_DTYPE_BFLOAT16, p, num_sequences, max_seqlen,
+                                static_cast<hipStream_t>(stream));
+  if (rc != FR2_ERR_UNSUPPORTED) return rc;
+  p.state_bf16 = false;
   return fr2::launch_serial(64, FR2_DTYPE_BFLOAT16, true, p, num_sequences,
                             static_cast<hipStream_t>(stream));
 }

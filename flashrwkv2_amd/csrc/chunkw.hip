@@ -131,13 +131,19 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
 
   f32x4 S[4][4];   // [kb][vb]
   if (p.state_in != nullptr) {
+    // fp32 state, or (bf16-state contract) bf16 widened once; the state
+    // stays fp32 for the whole call and is rounded back once at the end
     const float* sin = static_cast<const float*>(p.state_in) + sbase + i;
+    const uint16_t* sinb = static_cast<const uint16_t*>(p.state_in) + sbase + i;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int vb = 0; vb < 4; ++vb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) S[kb][vb][e] = sin[tile_key(kb, q, e) * D + 16 * vb];
+        for (int e = 0; e < 4; ++e) {
+          const int at = tile_key(kb, q, e) * D + 16 * vb;
+          S[kb][vb][e] = p.state_bf16 ? IoBF16::to_f32(sinb[at]) : sin[at];
+        }
   } else {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
@@ -342,20 +348,26 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
 
   if (p.state_out != nullptr) {
     float* sout = static_cast<float*>(p.state_out) + sbase + i;
+    uint16_t* soutb = static_cast<uint16_t*>(p.state_out) + sbase + i;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int vb = 0; vb < 4; ++vb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sout[tile_key(kb, q, e) * D + 16 * vb] = S[kb][vb][e];
+        for (int e = 0; e < 4; ++e) {
+          const int at = tile_key(kb, q, e) * D + 16 * vb;
+          if (p.state_bf16)
+            soutb[at] = IoBF16::from_f32(S[kb][vb][e]);
+          else
+            sout[at] = S[kb][vb][e];
+        }
   }
 }
 
 }  // namespace
 
 int launch_chunked_wave(int dtype, const SegArgs& p, int nseg, hipStream_t s) {
-  if (p.sa_out != nullptr || p.boundary != nullptr || p.reverse || p.state_bf16 ||
-      p.split_pieces > 0 || p.kk_scale != nullptr || p.ro_out != nullptr)
+  if (p.sa_out != nullptr || p.boundary != nullptr || p.reverse || p.split_pieces > 0 || p.kk_scale != nullptr || p.ro_out != nullptr)
     return FR2_ERR_UNSUPPORTED;
   const int64_t units = static_cast<int64_t>(nseg) * p.num_heads;
   if (units <= 0 || units > (int64_t{1} << 30)) return FR2_ERR_INVALID_ARGUMENT;

@@ -145,3 +145,34 @@ def test_wave_and_workgroup_kernels_agree_at_serving_size():
     assert dy <= 2 ** -7, dy
     ds = ((pools[0] - pools[1]).norm() / pools[0].norm()).item()
     assert ds <= 1e-5, ds
+
+
+def test_bf16_state_pool_on_many_units():
+    """The bf16-state chunk entry runs this kernel for many units (1 200 here)
+    with a bf16 state load and store (fp32 inside the call, one rounding at
+    the end): against the oracle from the same bf16 pool."""
+    require_gpu()
+    from flashrwkv2_amd.tmix.wkv7 import infer_tmix_wkv7_chunk_bf16_forward_varlen
+
+    import oracle
+    from wkv7_testlib import to_np
+
+    rng = np.random.default_rng(17)
+    lengths = tuple(int(x) for x in rng.integers(1, 120, size=300))
+    print(f"case wave bf16 state units=1200 max={max(lengths)}", flush=True)
+    case = make_case(dtype=torch.bfloat16, lengths=lengths, num_heads=4, seed=23)
+    pool = case["state_pool"].to(torch.bfloat16)
+    before = pool.clone()
+    y_ref, pool_ref, _, _ = oracle.wkv7_f64(
+        *(to_np(t) for t in tokens(case)), cu_seqlens=case["cu_seqlens"].cpu().numpy(),
+        state_indices=case["state_indices"].cpu().numpy(), state_pool=to_np(pool), scale=0.5)
+    out = infer_tmix_wkv7_chunk_bf16_forward_varlen(
+        *tokens(case), state_pool=pool, cu_seqlens=case["cu_seqlens"],
+        state_indices=case["state_indices"], max_seqlen=max(lengths), scale=0.5)
+    torch.cuda.synchronize()
+    assert_output_close(out, y_ref)
+    act = case["state_indices"].long()
+    # one bf16 rounding of the final fp32 state (2^-9 relative)
+    assert_state_close(pool[act], pool_ref[act.cpu().numpy()], rmse=4e-3, fro=4e-3)
+    idle = sorted(set(range(pool.shape[0])) - set(act.tolist()))
+    assert torch.equal(pool[idle], before[idle])

@@ -161,8 +161,9 @@ def test_chunk_bf16_long_requests_on_the_chunked_kernel():
     active = [4, 0, 2, 5]
     assert_state_close(pool[active], pool_ref[active], rmse=4e-3, fro=4e-3)
     assert torch.equal(pool[[1, 3]], before[[1, 3]])
-    # the same call forced token-serial (max_seqlen below the chunked threshold
-    # is only a dispatch hint here: it is resolved from the ticket otherwise)
+    # the same call on the wavefront-per-unit kernel: max_seqlen is only a
+    # dispatch hint to this entry (the kernels run every sequence to its end),
+    # and below 5 tokens it picks that kernel
     pool2 = before.clone()
     from flashrwkv2_amd import _native as N
     import flashrwkv2_amd
@@ -170,7 +171,7 @@ def test_chunk_bf16_long_requests_on_the_chunked_kernel():
     out2 = torch.empty_like(out)
     lq, ls, status, _, keep = C._resolve_launch_metadata(cu, slots, total, 6, 300, None)
     rc = N.load().fr2_wkv7_chunk_bf16_forward(
-        lq.data_ptr(), ls.data_ptr(), status.data_ptr(), 4, h, total, 16, 64,
+        lq.data_ptr(), ls.data_ptr(), status.data_ptr(), 4, h, total, 16, 4,
         pool2.data_ptr(), *(t.data_ptr() for t in inputs[:2]), None,
         *(t.data_ptr() for t in inputs[2:]), out2.data_ptr(), 1.0,
         torch.cuda.current_stream().cuda_stream)
