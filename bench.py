@@ -617,7 +617,8 @@ def time_mid_length(torch, flashrwkv2_amd, steps: int, n: int = 2048, length: in
         "workload": w.name, "total_tokens": w.total_tokens,
         "ms_per_step": round(ms, 4), "tokens_per_s": round(w.total_tokens / (ms * 1e-3), 1),
         "kernel_ms": round(kms, 4), "kernel": run.kernel_name(),
-        "roofline": roofline_obj(nbytes, kms), "algorithmic_bytes": nbytes,
+        "roofline": roofline_obj(nbytes, kms, measured_traffic(run.kernel_name(), w.name)),
+        "algorithmic_bytes": nbytes,
         "forced": forced,
     }
     del run, w, toks
@@ -1063,7 +1064,8 @@ def main() -> int:
                     help="tokens per sequence in the CPU baseline sample")
     ap.add_argument("--no-train", action="store_true",
                     help="skip the training (forward + backward) leg")
-    ap.add_argument("--only", choices=["prefill", "decode", "long", "train", "stages"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "long", "mid", "train", "stages"],
+                    default=None,
                     help="run one leg only (profiling)")
     ap.add_argument("--config", type=int, default=1, choices=[1, 3, 4],
                     help="prefill workload (BASELINE config; the metric is quoted on 1)")
@@ -1181,7 +1183,9 @@ def main() -> int:
         result["other_paths"] = time_other_paths(torch, flashrwkv2_amd, pre.w, args.steps)
     if args.only in (None, "long") and args.config == 1:
         result["varlen_prefill"] = time_varlen(torch, flashrwkv2_amd, max(5, args.steps // 2))
+    if args.only in (None, "long", "mid") and args.config == 1:
         result["mid_length"] = time_mid_length(torch, flashrwkv2_amd, max(5, args.steps // 4))
+    if args.only in (None, "long") and args.config == 1:
         result["short_batches"] = time_short_batches(torch, flashrwkv2_amd, max(5, args.steps // 2))
         result["long_context"] = time_long_context(torch, flashrwkv2_amd, max(4, args.steps // 4))
     if args.only in (None, "train") and not args.no_train:
