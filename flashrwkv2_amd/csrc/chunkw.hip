@@ -291,9 +291,9 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
     const int trow = 4 * q + (i >> 2);
 #pragma unroll
     for (int vb = 0; vb < 4; ++vb) {
-      // keep each column block's reads and products in its own region (a
-      // scheduler that hoists every block's LDS reads needs ~100 more registers)
-      __builtin_amdgcn_sched_barrier(0);
+      // the column blocks in two regions of two: a scheduler free to hoist
+      // every block's LDS reads to the top needs ~100 more registers
+      if (vb == 2) __builtin_amdgcn_sched_barrier(0);
       Sp8 Sb[2];
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
