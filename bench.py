@@ -755,7 +755,7 @@ def time_other_paths(torch, flashrwkv2_amd, w, steps: int):
             "roofline": roofline_obj(io + 2 * B * H * STATE_BYTES, f_ms),
         },
         "rl_infctx_replay": {
-            "kernel": "decode64_kernel<IoBF16,StF32> per 16-token chunk (sa written)",
+            "kernel": "chunk64w_kernel<IoBF16,false,true>: one wavefront per (16-token chunk, head), sa written",
             "chunks": nchunks, "kernel_ms": round(r_ms, 4),
             "tokens_per_s": round(T / (r_ms * 1e-3), 1),
             "roofline": roofline_obj(replay_bytes, r_ms), "algorithmic_bytes": replay_bytes,

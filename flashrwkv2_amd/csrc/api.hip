@@ -578,12 +578,13 @@ extern "C" int fr2_wkv7_rl_infctx_replay(
   p.y = output;
   p.sa_out = state_dot_a;
   p.scale = scale;
-  // chunks of at most 64 tokens: with many (chunk, head) units the decode
-  // kernel's one wave per unit beats the token-serial kernel at every such
-  // length (run_family's measured grid: 16 384 units, L = 16: 0.23 vs
-  // 0.29 ms; L = 64: 0.83 vs 0.94 ms)
-  if (head_size == 64 && static_cast<int64_t>(num_chunks) * num_heads >= 16384)
-    return fr2::launch_decode(64, dtype, p, num_chunks, static_cast<hipStream_t>(stream));
+  // chunks of at most 64 tokens from their boundary states: at D = 64 the
+  // chunked kernel with one wavefront per (chunk, head) unit, which also
+  // writes sa, beats the token-serial and decode kernels at every unit count
+  // and length of run_family's grid (256 units, L = 16: 0.011 vs 0.013 ms
+  // serial; 65 536 units, L = 16: 0.62 vs 0.90 ms decode)
+  if (head_size == 64)
+    return fr2::launch_chunked_wave(dtype, p, num_chunks, static_cast<hipStream_t>(stream));
   return fr2::launch_serial(head_size, dtype, false, p, num_chunks,
                             static_cast<hipStream_t>(stream));
 }

@@ -88,8 +88,10 @@ __device__ __forceinline__ int tile_key(int kb, int q, int e) {
 }
 
 // kOrder: the units run in longest-first order of their sequences (packed
-// batches of at most kOrderMaxSeqs sequences)
-template <class Io, bool kOrder>
+// batches of at most kOrderMaxSeqs sequences).  kSa: also write every
+// token's pre-update sa = S_{t-1}^T a_t (the rows of U) to p.sa_out (the
+// rl_infctx replay).
+template <class Io, bool kOrder, bool kSa = false>
 __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nunits) {
   using raw = typename Io::raw;
   constexpr bool kVExact = !__is_same(Io, IoF16);
@@ -318,6 +320,14 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
       Y = mma32x3(Rs[0], Sb[0], Y);
       Y = mma32x3(Rs[1], Sb[1], Y);
       const f32x4 Uf = mm_ab(Ta, as_b(split4(X)), zero);
+      if constexpr (kSa) {
+        // sa rows 4q + e, column 16vb + i
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (t0 + c * L + 4 * q + e < t1)
+            p.sa_out[static_cast<int64_t>(t0 + c * L + 4 * q + e) * row_stride + head_off +
+                     16 * vb + i] = Uf[e];
+      }
       const BOp Us = as_b(split4(Uf));
       Y = mm_ab(Mrb, Us, Y);
       // y rows 4q + e, column 16vb + i
@@ -367,24 +377,31 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
 }  // namespace
 
 int launch_chunked_wave(int dtype, const SegArgs& p, int nseg, hipStream_t s) {
-  if (p.sa_out != nullptr || p.boundary != nullptr || p.reverse || p.split_pieces > 0 || p.kk_scale != nullptr || p.ro_out != nullptr)
+  if (p.boundary != nullptr || p.reverse || p.split_pieces > 0 || p.kk_scale != nullptr ||
+      p.ro_out != nullptr)
     return FR2_ERR_UNSUPPORTED;
   const int64_t units = static_cast<int64_t>(nseg) * p.num_heads;
   if (units <= 0 || units > (int64_t{1} << 30)) return FR2_ERR_INVALID_ARGUMENT;
   const dim3 grid(static_cast<unsigned>((units + WPB - 1) / WPB));
   const bool order = p.uniform_len <= 0 && p.chunk_offsets == nullptr && p.ends == nullptr &&
                      nseg > 1 && nseg <= kOrderMaxSeqs;
+  const bool sa = p.sa_out != nullptr;
   const int n = static_cast<int>(units);
+  const dim3 block(64 * WPB);
   if (dtype == FR2_DTYPE_BFLOAT16) {
-    if (order)
-      hipLaunchKernelGGL((chunk64w_kernel<IoBF16, true>), grid, dim3(64 * WPB), 0, s, p, n);
+    if (sa)
+      hipLaunchKernelGGL((chunk64w_kernel<IoBF16, false, true>), grid, block, 0, s, p, n);
+    else if (order)
+      hipLaunchKernelGGL((chunk64w_kernel<IoBF16, true>), grid, block, 0, s, p, n);
     else
-      hipLaunchKernelGGL((chunk64w_kernel<IoBF16, false>), grid, dim3(64 * WPB), 0, s, p, n);
+      hipLaunchKernelGGL((chunk64w_kernel<IoBF16, false>), grid, block, 0, s, p, n);
   } else if (dtype == FR2_DTYPE_FLOAT16) {
-    if (order)
-      hipLaunchKernelGGL((chunk64w_kernel<IoF16, true>), grid, dim3(64 * WPB), 0, s, p, n);
+    if (sa)
+      hipLaunchKernelGGL((chunk64w_kernel<IoF16, false, true>), grid, block, 0, s, p, n);
+    else if (order)
+      hipLaunchKernelGGL((chunk64w_kernel<IoF16, true>), grid, block, 0, s, p, n);
     else
-      hipLaunchKernelGGL((chunk64w_kernel<IoF16, false>), grid, dim3(64 * WPB), 0, s, p, n);
+      hipLaunchKernelGGL((chunk64w_kernel<IoF16, false>), grid, block, 0, s, p, n);
   } else {
     return FR2_ERR_UNSUPPORTED;
   }

@@ -429,9 +429,10 @@ def test_backend_is_the_in_tree_hip_library():
 
 
 def test_rl_infctx_replay_many_chunks_matches_recurrence():
-    """2 048 ragged chunks x 8 heads (16 384 (chunk, head) units, where the
-    replay runs on the one-wave-per-unit decode kernel), each from its own
-    start-of-chunk state, against the fp64 recurrence with per-token sa."""
+    """2 048 ragged chunks x 8 heads (16 384 (chunk, head) units; at D = 64
+    the replay runs on the chunked kernel with one wavefront per unit, which
+    also writes sa), each from its own start-of-chunk state, against the fp64
+    recurrence with per-token sa."""
     C = require_gpu()
     print("case rl_infctx replay 2048 chunks x 8 heads", flush=True)
     g = torch.Generator().manual_seed(77)
