@@ -417,22 +417,39 @@ def time_layer_stages(torch, tokens: int, heads: int, steps: int = 20):
     return {"workload": f"cfg1_tokens{tokens}_C{C}_fp16", "kernels": out}
 
 
-def time_kk_fused(torch, flashrwkv2_amd, steps: int):
-    """wkv_prepare's kk / a-gate stage and the recurrence on BASELINE config
-    1's shape in fp16 (8 x 4096 tokens, H = 32): the reference's two kernels
-    (kk_a_gate_kernel writes key, a, b; the chunked recurrence reads them
-    back) against the chunked kernel that forms them in its load stage.  Both
-    read the projected key and a12 and write the gated key and y, so the
-    fused form moves 14 B per (token, channel) where the pair moves 24 B.
-    With the readout's elementwise stage (GroupNorm, the r k' r_k residual,
-    the gate) also in the kernel's write-back: three kernels move 36 B per
-    (token, channel), the fused one 16 B (it reads the gate and writes the
-    readout instead of y)."""
+def time_kk_fused(torch, flashrwkv2_amd, steps: int, serving: bool = False):
+    """wkv_prepare's kk / a-gate stage and the recurrence in fp16 on BASELINE
+    config 1's shape (8 x 4096 tokens, H = 32; the workgroup-per-unit
+    chunked kernel) or, with `serving`, on a serving batch of 2 048
+    sequences x 100 tokens (65 536 units; the wavefront-per-unit kernel): the
+    reference's two kernels (kk_a_gate_kernel writes key, a, b; the
+    recurrence reads them back) against the chunked kernel that forms them in
+    its load stage.  Both read the projected key and a12 and write the gated
+    key and y, so the fused form moves 14 B per (token, channel) where the
+    pair moves 24 B.  With the readout's elementwise stage (GroupNorm, the
+    r k' r_k residual, the gate) also in the kernel's write-back: three
+    kernels move 36 B per (token, channel), the fused one 16 B (it reads the
+    gate and writes the readout instead of y)."""
     from flashrwkv2_amd import _C as CC
     from flashrwkv2_amd import _native as N
     from flashrwkv2_amd import workloads
 
-    w = workloads.config(1, "cuda", dtype=torch.float16)
+    if serving:
+        n_seq, length, heads = 2048, 100, 32
+        toks = workloads.make_tokens(n_seq * length, heads, u_range=(-6.0, -0.5), seed=3003,
+                                     device="cuda", dtype=torch.float16)
+        w = workloads._pack(f"serving_S{n_seq}_T{length}_H{heads}_fp16_kk_gate", toks,
+                            [length] * n_seq, heads, 0.1, 3003, "cuda", {})
+        rec_kernel, kk_kernel, ro_kernel = (
+            "chunk64w_kernel<IoF16,false>", "chunk64w_kernel<IoF16,false,false,true>",
+            "chunk64w_kernel<IoF16,false,false,true,true>")
+        name = w.name
+    else:
+        w = workloads.config(1, "cuda", dtype=torch.float16)
+        rec_kernel, kk_kernel, ro_kernel = (
+            "chunk64_kernel<IoF16,false>", "chunk64_kernel<IoF16,false,false,false,true>",
+            "chunk64_kernel<IoF16,false,false,false,true,true>")
+        name = "cfg1_prefill_B8_T4096_H32_fp16_kk_gate"
     T, H, D = w.total_tokens, w.num_heads, 64
     C = H * D
     g = torch.Generator(device="cuda")
@@ -498,25 +515,25 @@ def time_kk_fused(torch, flashrwkv2_amd, steps: int):
     three_bytes = 36 * T * C + state_bytes
     fused_ro_bytes = 16 * T * C + state_bytes
     out_obj = {
-        "workload": "cfg1_prefill_B8_T4096_H32_fp16_kk_gate", "total_tokens": T,
+        "workload": name, "total_tokens": T,
         "two_stage": {"ms_per_step": round(two_ms, 4),
-                      "kernels": "kk_a_gate_kernel<64> + chunk64_kernel<IoF16,false>",
+                      "kernels": f"kk_a_gate_kernel<64> + {rec_kernel}",
                       "algorithmic_bytes": pair_bytes,
                       "roofline": roofline_obj(pair_bytes, two_ms)},
         "fused": {"ms_per_step": round(fused_ms, 4),
-                  "kernel": "chunk64_kernel<IoF16,false,false,false,true>",
+                  "kernel": kk_kernel,
                   "algorithmic_bytes": fused_bytes,
                   "roofline": roofline_obj(fused_bytes, fused_ms)},
         "recurrence_alone_ms": round(rec_ms, 4),
         "saved_ms": round(two_ms - fused_ms, 4),
         "with_readout": {
             "three_stage": {"ms_per_step": round(three_ms, 4),
-                            "kernels": "kk_a_gate_kernel<64> + chunk64_kernel<IoF16,false> + "
+                            "kernels": f"kk_a_gate_kernel<64> + {rec_kernel} + "
                                        "readout_prelinear_kernel<64>",
                             "algorithmic_bytes": three_bytes,
                             "roofline": roofline_obj(three_bytes, three_ms)},
             "fused": {"ms_per_step": round(fused_ro_ms, 4),
-                      "kernel": "chunk64_kernel<IoF16,false,false,false,true,true>",
+                      "kernel": ro_kernel,
                       "algorithmic_bytes": fused_ro_bytes,
                       "roofline": roofline_obj(fused_ro_bytes, fused_ro_ms)},
             "saved_ms": round(three_ms - fused_ro_ms, 4),
@@ -1195,6 +1212,8 @@ def main() -> int:
     if args.only in (None, "stages"):
         result["layer_stages"] = time_layer_stages(torch, 8 * 4096, 32)
         result["kk_gate_fused"] = time_kk_fused(torch, flashrwkv2_amd, max(5, args.steps // 2))
+        result["kk_gate_fused_serving"] = time_kk_fused(torch, flashrwkv2_amd,
+                                                        max(5, args.steps // 4), serving=True)
     result["device"] = device_info(torch)
     if pre is not None and not args.no_cpu and args.config == 1:
         threads = min(16, len(os.sched_getaffinity(0)) or 1)

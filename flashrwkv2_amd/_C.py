@@ -538,11 +538,12 @@ def tmix_wkv7_recurrent_fp32_from_kk_gate(query_start_loc, state_indices, state,
     """The recurrence with wkv_prepare's kk / a-gate stage in its load stage:
     k is the projected key, a12 the a-gate logits, k_k / a0 / k_a the
     per-channel parameters ([H*D] or [H,D], token dtype); the gated key is
-    written to new_k.  Outside the chunked family (head size 64, longest
-    sequence at the library's chunked threshold for the launch's unit count),
-    and for fp16 batches that the library's plan splits by
-    sequence (few long sequences: the split outruns one block per unit), the
-    gate runs as its own kernel and the recurrence through the public path."""
+    written to new_k.  Where the library's policy picks no chunked kernel
+    (head size other than 64, or the longest sequence at most 4 tokens, 6 with
+    many units: the decode kernel), and for fp16 batches that the library's
+    plan splits by sequence (few long sequences: the split outruns one block
+    per unit), the gate runs as its own kernel and the recurrence through the
+    public path."""
     n, h, d = check_recurrent_layout(query_start_loc, state_indices, state, r, decay_logits, k,
                                      v, a12, new_k, output, scale)
     for t, name in ((k_k, "k_k"), (a0, "a0"), (k_a, "k_a")):

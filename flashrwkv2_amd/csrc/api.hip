@@ -753,9 +753,10 @@ extern "C" int fr2_wkv7_statetune_uniform_backward(
 // wkv_prepare fused into the chunked kernel's load stage: the recurrence's
 // k, a, b come from the projected key, the low-rank a-gate logits a12 and the
 // per-channel k_k, a0, k_a (never stored), and the gated key the readout
-// needs is written to new_k.  Only where the public policy picks the
-// workgroup-per-unit chunked kernel (workgroup_chunked: head_size 64, no
-// decode or wave-per-unit form), otherwise FR2_ERR_UNSUPPORTED (the caller
+// needs is written to new_k.  On the chunked kernel the plain entry's
+// policy picks (one workgroup or one wavefront per unit); where that policy
+// picks the decode kernel (the longest sequence at most 4 tokens, 6 with
+// many units) or at head sizes other than 64, FR2_ERR_UNSUPPORTED (the caller
 // then runs fr2_tmix_kk_a_gate_forward and the plain entry).
 extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate(
     const int32_t* query_start_loc, const int32_t* state_indices, const int32_t* status,
@@ -768,8 +769,8 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate(
     return FR2_ERR_INVALID_ARGUMENT;
   if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 || total_tokens <= 0)
     return FR2_ERR_INVALID_ARGUMENT;
-  if (head_size != 64 || !workgroup_chunked(static_cast<int64_t>(num_sequences) * num_heads,
-                                            max_seqlen, total_tokens, num_sequences))
+  const int64_t units = static_cast<int64_t>(num_sequences) * num_heads;
+  if (head_size != 64 || max_seqlen <= 0 || decode_first(units, max_seqlen))
     return FR2_ERR_UNSUPPORTED;
   SegArgs p;
   p.bounds = query_start_loc;
@@ -784,7 +785,10 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate(
   p.kk_scale = k_k; p.a_bias = a0; p.k_a = k_a; p.new_k = new_k;
   p.y = output;
   p.scale = scale;
-  return fr2::launch_chunked_kk(dtype, p, num_sequences, static_cast<hipStream_t>(stream));
+  // the chunked kernel the plain entry's policy picks, with the stage fused
+  return workgroup_chunked(units, max_seqlen, total_tokens, num_sequences)
+             ? fr2::launch_chunked_kk(dtype, p, num_sequences, static_cast<hipStream_t>(stream))
+             : fr2::launch_chunked_wave(dtype, p, num_sequences, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate_readout(
@@ -801,8 +805,8 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate_readout(
     return FR2_ERR_INVALID_ARGUMENT;
   if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 || total_tokens <= 0)
     return FR2_ERR_INVALID_ARGUMENT;
-  if (head_size != 64 || !workgroup_chunked(static_cast<int64_t>(num_sequences) * num_heads,
-                                            max_seqlen, total_tokens, num_sequences))
+  const int64_t units = static_cast<int64_t>(num_sequences) * num_heads;
+  if (head_size != 64 || max_seqlen <= 0 || decode_first(units, max_seqlen))
     return FR2_ERR_UNSUPPORTED;
   SegArgs p;
   p.bounds = query_start_loc;
@@ -818,7 +822,10 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate_readout(
   p.ro_g = g; p.ro_rk = r_k; p.ro_lnw = ln_weight; p.ro_lnb = ln_bias; p.ro_out = readout;
   p.y = output;
   p.scale = scale;
-  return fr2::launch_chunked_kk(dtype, p, num_sequences, static_cast<hipStream_t>(stream));
+  // the chunked kernel the plain entry's policy picks, with the stage fused
+  return workgroup_chunked(units, max_seqlen, total_tokens, num_sequences)
+             ? fr2::launch_chunked_kk(dtype, p, num_sequences, static_cast<hipStream_t>(stream))
+             : fr2::launch_chunked_wave(dtype, p, num_sequences, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int fr2_tmix_kk_a_gate_forward(int64_t tokens, int32_t num_heads, int32_t head_size,

@@ -41,20 +41,31 @@ constexpr float kNegExpHalf = -0.6065306597126334f;   // -exp(-1/2)
 
 constexpr int kOrderMaxSeqs = 256;   // longest-first order up to this many sequences
 
+constexpr int YPW = D + 8;            // padded row of the staged outputs (fused readout)
+
 // One wave's LDS: its chunk's B^, K^ (hi and lo) and V rows, read back
-// transposed, gamma_L, and the staged output rows.
-template <bool kVExact>
+// transposed, and gamma_L; with the fused readout (kRO) also the chunk's y
+// rows, staged for the per-token GroupNorm, and each token's r k' r_k sum.
+template <bool kVExact, bool kRO>
 struct alignas(16) WaveLds {
   static constexpr int TP = kVExact ? D + 16 : D + 8;   // token row pitch
   float gl[D];
   __bf16 b_h[L][TP], b_l[L][TP], k_h[L][TP], k_l[L][TP], v_h[L][TP];
   __bf16 v_l[kVExact ? 1 : L][TP];                       // fp16 tokens only
+  uint16_t yb[kRO ? L : 1][YPW];
+  float rkv[kRO ? L : 4];
 };
-static_assert(sizeof(WaveLds<true>::b_h) >= kOrderMaxSeqs * sizeof(int),
+using WaveLdsB = WaveLds<true, false>;
+using WaveLdsH = WaveLds<false, false>;
+using WaveLdsBR = WaveLds<true, true>;
+using WaveLdsHR = WaveLds<false, true>;
+static_assert(sizeof(WaveLdsB::b_h) >= kOrderMaxSeqs * sizeof(int),
               "the sequence lengths of the longest-first order fit in b_h");
-static_assert(sizeof(WaveLds<true>) % 16 == 0 && sizeof(WaveLds<false>) % 16 == 0,
+static_assert(sizeof(WaveLdsB) % 16 == 0 && sizeof(WaveLdsH) % 16 == 0 &&
+                  sizeof(WaveLdsBR) % 16 == 0 && sizeof(WaveLdsHR) % 16 == 0,
               "wave blocks must keep 16-byte alignment");
-static_assert(offsetof(WaveLds<true>, b_h) % 16 == 0 && offsetof(WaveLds<false>, v_l) % 16 == 0,
+static_assert(offsetof(WaveLdsB, b_h) % 16 == 0 && offsetof(WaveLdsH, v_l) % 16 == 0 &&
+                  offsetof(WaveLdsBR, yb) % 16 == 0 && offsetof(WaveLdsHR, yb) % 16 == 0,
               "row arrays must be 16-byte aligned");
 
 // Longest-first order of the sequences of a packed batch: with one wave per
@@ -90,12 +101,15 @@ __device__ __forceinline__ int tile_key(int kb, int q, int e) {
 // kOrder: the units run in longest-first order of their sequences (packed
 // batches of at most kOrderMaxSeqs sequences).  kSa: also write every
 // token's pre-update sa = S_{t-1}^T a_t (the rows of U) to p.sa_out (the
-// rl_infctx replay).
-template <class Io, bool kOrder, bool kSa = false>
+// rl_infctx replay).  kKK: the kk / a-gate stage of wkv_prepare in the load
+// stage (k is the projected key, slot a the a-gate logits a12; the gated
+// key goes to p.new_k), and kRO with it the readout's elementwise stage in
+// the output write-back (p.ro_out; y itself only when p.y is set).
+template <class Io, bool kOrder, bool kSa = false, bool kKK = false, bool kRO = false>
 __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nunits) {
   using raw = typename Io::raw;
   constexpr bool kVExact = !__is_same(Io, IoF16);
-  __shared__ WaveLds<kVExact> lds[WPB];
+  __shared__ WaveLds<kVExact, kRO> lds[WPB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -105,14 +119,16 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
   const int H = p.num_heads;
   raw* yout = static_cast<raw*>(p.y);
   if (p.status != nullptr && p.status[0] != 0) {
-    fill_output_nan<Io>(yout, p.out_elems, blockIdx.x, gridDim.x);
+    if (!kRO || yout != nullptr) fill_output_nan<Io>(yout, p.out_elems, blockIdx.x, gridDim.x);
+    if constexpr (kRO)
+      fill_output_nan<Io>(static_cast<raw*>(p.ro_out), p.out_elems, blockIdx.x, gridDim.x);
     return;
   }
   // the heads of a sequence are adjacent units (adjacent 128-byte pieces of
   // every token row)
   const int unit = blockIdx.x * WPB + wv;
   if (unit >= nunits) return;
-  WaveLds<kVExact>& sm = lds[wv];
+  WaveLds<kVExact, kRO>& sm = lds[wv];
   int seg = unit / H;
   const int h = unit - seg * H;
   const int nseq = nunits / H;
@@ -168,8 +184,16 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
     for (int j = 0; j < 6; ++j)
 #pragma unroll
       for (int m = 0; m < 2; ++m)
-        dst[j][m] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(src[j] + off + 32 * m));
+        dst[j][m] = (kKK && j == 5)   // b is formed from the key with the gate stage
+                        ? u32x4{0u, 0u, 0u, 0u}
+                        : __builtin_nontemporal_load(
+                              reinterpret_cast<const u32x4*>(src[j] + off + 32 * m));
+  };
+  // per-channel parameters of the lane's 8 keys of K step m (read where used:
+  // they would otherwise hold 16-64 registers across the whole loop)
+  auto channel8 = [&](const void* base, int m, float* out) {
+    unpack8<Io>(*reinterpret_cast<const u32x4*>(static_cast<const raw*>(base) + lane_off + 32 * m),
+                out);
   };
 
   constexpr float kC = kNegExpHalf * kLog2e;
@@ -183,15 +207,74 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
     // ---- operands of the chunk (keys of K step m in registers)
     Sp8 As[2], Rs[2], Bs[2], Ks[2];
+    // fused kk stage: 1 / |k k_k| over the token's 64 keys (the four lanes of
+    // token i hold 16 each)
+    float kinv = 0.0f;
+    if constexpr (kKK) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        float xk[8], kks[8];
+        unpack8<Io>(rows[2][m], xk);
+        channel8(p.kk_scale, m, kks);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float u = xk[e] * kks[e];
+          ss = __builtin_fmaf(u, u, ss);
+        }
+      }
+      ss += __shfl_xor(ss, 16);
+      ss += __shfl_xor(ss, 32);
+      kinv = __builtin_amdgcn_rcpf(fmaxf(__builtin_sqrtf(ss), 1.0e-12f));
+    }
+    float rkv_part = 0.0f;   // fused readout: sum over the lane's keys of r k' r_k
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       __builtin_amdgcn_sched_barrier(0);
       float xr[8], xl[8], xk[8], xa[8], xb[8];
       unpack8<Io>(valid ? rows[0][m] : zero4, xr);
       unpack8<Io>(rows[1][m], xl);
-      unpack8<Io>(valid ? rows[2][m] : zero4, xk);
-      unpack8<Io>(valid ? rows[4][m] : zero4, xa);
-      unpack8<Io>(valid ? rows[5][m] : zero4, xb);
+      if constexpr (kKK) {
+        // u = k k_k, kk = u / |u|, g = sigmoid(a0 + a12), k' = k (1 + (g - 1) k_a),
+        // a = -kk, b = kk g (csrc/prepare.hip kk_a_gate_kernel, in fp32)
+        float kks[8], a0[8], ka[8], x12[8];
+        unpack8<Io>(rows[2][m], xk);
+        unpack8<Io>(rows[4][m], x12);
+        channel8(p.kk_scale, m, kks);
+        channel8(p.a_bias, m, a0);
+        channel8(p.k_a, m, ka);
+        u32x4 packed;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float kk = xk[e] * kks[e] * kinv;
+          const float g = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2e * (a0[e] + x12[e])));
+          const float nk = xk[e] * __builtin_fmaf(g - 1.0f, ka[e], 1.0f);
+          xa[e] = -kk;
+          xb[e] = valid ? kk * g : 0.0f;
+          xk[e] = valid ? nk : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          packed[j] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, Io::from_f32(xk[2 * j]))) |
+                      (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, Io::from_f32(xk[2 * j + 1])))
+                       << 16);
+        if (valid)
+          *reinterpret_cast<u32x4*>(static_cast<raw*>(p.new_k) +
+                                    static_cast<int64_t>(t0 + c * L + i) * row_stride + lane_off +
+                                    32 * m) = packed;
+        if constexpr (kRO) {
+          // the readout's residual weight uses the key as stored
+          float kq[8], rk[8];
+          unpack8<Io>(packed, kq);
+          channel8(p.ro_rk, m, rk);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) rkv_part = __builtin_fmaf(xr[e] * kq[e], rk[e], rkv_part);
+        }
+      } else {
+        unpack8<Io>(valid ? rows[2][m] : zero4, xk);
+        unpack8<Io>(valid ? rows[4][m] : zero4, xa);
+        unpack8<Io>(valid ? rows[5][m] : zero4, xb);
+      }
       float nb[8];
       if (bias != nullptr) {
         unpack8<Io>(*reinterpret_cast<const u32x4*>(bias + lane_off + 32 * m), nb);
@@ -256,6 +339,12 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
         *reinterpret_cast<bf16x8*>(&sm.v_h[i][col]) = vs.hi;
         *reinterpret_cast<bf16x8*>(&sm.v_l[i][col]) = vs.lo;
       }
+    }
+
+    if constexpr (kRO) {
+      rkv_part += __shfl_xor(rkv_part, 16);
+      rkv_part += __shfl_xor(rkv_part, 32);
+      if (q == 0) sm.rkv[i] = rkv_part;
     }
 
     // ---- token-token blocks over the 64 keys.  mma32(X, Y) gives lane
@@ -330,12 +419,16 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
       }
       const BOp Us = as_b(split4(Uf));
       Y = mm_ab(Mrb, Us, Y);
-      // y rows 4q + e, column 16vb + i
+      // y rows 4q + e, column 16vb + i (staged for the fused readout)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (t0 + c * L + 4 * q + e < t1)
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (kRO) {
+          sm.yb[4 * q + e][16 * vb + i] = __builtin_bit_cast(uint16_t, Io::from_f32(p.scale * Y[e]));
+        } else if (t0 + c * L + 4 * q + e < t1) {
           yout[static_cast<int64_t>(t0 + c * L + 4 * q + e) * row_stride + head_off + 16 * vb + i] =
               Io::from_f32(p.scale * Y[e]);
+        }
+      }
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
         // B^^T and K^^T of tile kb as A operands (row = key, K = token)
@@ -352,6 +445,65 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
     // the next chunk's rows are requested before this chunk's output stores
     // (the other units' waves on the SIMD cover their latency)
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kRO) {
+      // fused readout of the chunk's rows: lane l takes 16 channels of token
+      // l / 4; GroupNorm over the head's 64 channels (4 lanes per token),
+      // the r k' r_k residual and the gate:
+      //   out = (GroupNorm(y) ln_w + ln_b + (sum r k' r_k) v) g
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      const int orow = lane >> 2, oc = 16 * (lane & 3);
+      const int tok = t0 + c * L + orow;
+      const int64_t roff = static_cast<int64_t>(min(tok, t1 - 1)) * row_stride + head_off + oc;
+      const u32x4 yp[2] = {*reinterpret_cast<const u32x4*>(&sm.yb[orow][oc]),
+                           *reinterpret_cast<const u32x4*>(&sm.yb[orow][oc + 8])};
+      float yv[16];
+      unpack8<Io>(yp[0], yv);
+      unpack8<Io>(yp[1], yv + 8);
+      float s1 = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s1 += yv[e];
+      s1 += __shfl_xor(s1, 1);
+      s1 += __shfl_xor(s1, 2);
+      const float mean = s1 * (1.0f / D);
+      float s2 = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s2 = __builtin_fmaf(yv[e] - mean, yv[e] - mean, s2);
+      s2 += __shfl_xor(s2, 1);
+      s2 += __shfl_xor(s2, 2);
+      const float inv = 1.0f / __builtin_sqrtf(s2 * (1.0f / D) + 64.0e-5f);
+      const float rkv = sm.rkv[orow];
+#pragma unroll
+      for (int hp = 0; hp < 2; ++hp) {
+        float w8[8], b8[8], v8[8], g8[8];
+        unpack8<Io>(*reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.ro_lnw) + head_off +
+                                                    oc + 8 * hp), w8);
+        unpack8<Io>(*reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.ro_lnb) + head_off +
+                                                    oc + 8 * hp), b8);
+        unpack8<Io>(*reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.v) + roff + 8 * hp),
+                    v8);
+        unpack8<Io>(*reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.ro_g) + roff + 8 * hp),
+                    g8);
+        u32x4 packed;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float o2[2];
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const int e = 2 * j + h2;
+            o2[h2] = (__builtin_fmaf((yv[8 * hp + e] - mean) * inv, w8[e], b8[e]) + rkv * v8[e]) *
+                     g8[e];
+          }
+          packed[j] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, Io::from_f32(o2[0]))) |
+                      (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, Io::from_f32(o2[1])))
+                       << 16);
+        }
+        if (tok < t1) {
+          *reinterpret_cast<u32x4*>(static_cast<raw*>(p.ro_out) + roff + 8 * hp) = packed;
+          if (yout != nullptr) *reinterpret_cast<u32x4*>(yout + roff + 8 * hp) = yp[hp];
+        }
+      }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
     if (c + 1 < nchunks) load_rows(rows, c + 1);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
   }
@@ -376,35 +528,52 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
 
 }  // namespace
 
+namespace {
+
+template <class Io>
+void launch_wave_io(const SegArgs& p, int n, bool order, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((n + WPB - 1) / WPB)), block(64 * WPB);
+  const bool kk = p.kk_scale != nullptr, ro = p.ro_out != nullptr;
+  if (p.sa_out != nullptr)
+    hipLaunchKernelGGL((chunk64w_kernel<Io, false, true>), grid, block, 0, s, p, n);
+  else if (kk && ro && order)
+    hipLaunchKernelGGL((chunk64w_kernel<Io, true, false, true, true>), grid, block, 0, s, p, n);
+  else if (kk && ro)
+    hipLaunchKernelGGL((chunk64w_kernel<Io, false, false, true, true>), grid, block, 0, s, p, n);
+  else if (kk && order)
+    hipLaunchKernelGGL((chunk64w_kernel<Io, true, false, true>), grid, block, 0, s, p, n);
+  else if (kk)
+    hipLaunchKernelGGL((chunk64w_kernel<Io, false, false, true>), grid, block, 0, s, p, n);
+  else if (order)
+    hipLaunchKernelGGL((chunk64w_kernel<Io, true>), grid, block, 0, s, p, n);
+  else
+    hipLaunchKernelGGL((chunk64w_kernel<Io, false>), grid, block, 0, s, p, n);
+}
+
+}  // namespace
+
 int launch_chunked_wave(int dtype, const SegArgs& p, int nseg, hipStream_t s) {
-  if (p.boundary != nullptr || p.reverse || p.split_pieces > 0 || p.kk_scale != nullptr ||
-      p.ro_out != nullptr)
-    return FR2_ERR_UNSUPPORTED;
+  if (p.boundary != nullptr || p.reverse || p.split_pieces > 0) return FR2_ERR_UNSUPPORTED;
+  const bool kk = p.kk_scale != nullptr, ro = p.ro_out != nullptr;
+  // the fused stages: the gate needs all its inputs, the readout needs the
+  // gate, and neither combines with the replay's sa output or a bf16 state
+  if ((kk || ro) && (p.sa_out != nullptr || p.state_bf16 || p.a_bias == nullptr ||
+                     p.k_a == nullptr || p.new_k == nullptr || !kk))
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (ro && (p.ro_g == nullptr || p.ro_rk == nullptr || p.ro_lnw == nullptr ||
+             p.ro_lnb == nullptr))
+    return FR2_ERR_INVALID_ARGUMENT;
   const int64_t units = static_cast<int64_t>(nseg) * p.num_heads;
   if (units <= 0 || units > (int64_t{1} << 30)) return FR2_ERR_INVALID_ARGUMENT;
-  const dim3 grid(static_cast<unsigned>((units + WPB - 1) / WPB));
   const bool order = p.uniform_len <= 0 && p.chunk_offsets == nullptr && p.ends == nullptr &&
                      nseg > 1 && nseg <= kOrderMaxSeqs;
-  const bool sa = p.sa_out != nullptr;
   const int n = static_cast<int>(units);
-  const dim3 block(64 * WPB);
-  if (dtype == FR2_DTYPE_BFLOAT16) {
-    if (sa)
-      hipLaunchKernelGGL((chunk64w_kernel<IoBF16, false, true>), grid, block, 0, s, p, n);
-    else if (order)
-      hipLaunchKernelGGL((chunk64w_kernel<IoBF16, true>), grid, block, 0, s, p, n);
-    else
-      hipLaunchKernelGGL((chunk64w_kernel<IoBF16, false>), grid, block, 0, s, p, n);
-  } else if (dtype == FR2_DTYPE_FLOAT16) {
-    if (sa)
-      hipLaunchKernelGGL((chunk64w_kernel<IoF16, false, true>), grid, block, 0, s, p, n);
-    else if (order)
-      hipLaunchKernelGGL((chunk64w_kernel<IoF16, true>), grid, block, 0, s, p, n);
-    else
-      hipLaunchKernelGGL((chunk64w_kernel<IoF16, false>), grid, block, 0, s, p, n);
-  } else {
+  if (dtype == FR2_DTYPE_BFLOAT16)
+    launch_wave_io<IoBF16>(p, n, order, s);
+  else if (dtype == FR2_DTYPE_FLOAT16)
+    launch_wave_io<IoF16>(p, n, order, s);
+  else
     return FR2_ERR_UNSUPPORTED;
-  }
   return record_launch();
 }
 

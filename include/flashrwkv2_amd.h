@@ -197,11 +197,11 @@ int fr2_wkv7_recurrent_fp32_forward_split(
  *   u = k k_k, kk = u / max(|u|, 1e-12), g = sigmoid(a0 + a12),
  *   key = k (1 + (g - 1) k_a), a = -kk, b = kk g
  * in fp32, runs the recurrence on (key, a, b) and writes key to new_k (the
- * readout's input); a and b are never stored.  FR2_ERR_UNSUPPORTED unless
- * fr2_wkv7_recurrent_fp32_forward would run the workgroup-per-unit chunked
- * kernel on this launch (head_size 64; max_seqlen >= 5 for at most 256
- * (sequence, head) units, longer for more units, where the kernel with one
- * wavefront per unit is faster): the caller then runs
+ * readout's input); a and b are never stored.  Runs on the chunked kernel
+ * fr2_wkv7_recurrent_fp32_forward would pick for this launch (one workgroup
+ * or one wavefront per (sequence, head)); FR2_ERR_UNSUPPORTED where that
+ * entry would run the decode kernel (max_seqlen <= 4, or <= 6 with 16 384 or
+ * more units) or head_size != 64: the caller then runs
  * fr2_tmix_kk_a_gate_forward and fr2_wkv7_recurrent_fp32_forward.  Replaces
  * the pair tmix_kk_a_gate_forward_varlen_cuda
  * (csrc/sm120/tmix/wkv_prepare/internal/kk_a_gate/infer_fp16_forward_varlen.cu)

@@ -86,14 +86,20 @@ def _check_key(actual, expected, dtype):
     assert worst <= 0.0, f"gated key off by {worst:.3e} beyond one ulp"
 
 
+# 300 sequences x 4 heads = 1 200 units: the chunked kernel with one
+# wavefront per unit (the others run on the workgroup-per-unit kernel)
+_MANY = tuple((7 * i) % 97 + 5 for i in range(300))
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
 @pytest.mark.parametrize("lengths,heads,bias", [
     ((40, 1, 63, 130, 17), 3, False),
     ((300, 64, 96, 41), 4, True),
-], ids=["ragged", "bias"])
+    (_MANY, 4, True),
+], ids=["ragged", "bias", "many-units"])
 def test_fused_kk_gate_matches_the_two_stage_oracle(dtype, lengths, heads, bias):
     require_gpu()
-    print(f"case kk-gate fused {dtype} lengths {lengths} H {heads} bias {bias}", flush=True)
+    print(f"case kk-gate fused {dtype} {len(lengths)} sequences H {heads} bias {bias}", flush=True)
     c = _case(lengths, heads, dtype, seed=sum(lengths) + heads, bias=bias)
     y, pool, new_k = _run(c, 0.8)
     ey, epool, ek = _expected(c, 0.8)
@@ -205,10 +211,12 @@ def _run_readout(c, scale, want_y=True):
 @pytest.mark.parametrize("lengths,heads,bias", [
     ((40, 1, 63, 130, 17), 3, True),
     ((300, 64, 96, 41), 4, False),
-], ids=["ragged-bias", "long"])
+    (_MANY, 4, True),
+], ids=["ragged-bias", "long", "many-units"])
 def test_fused_readout_matches_the_three_stage_oracle(dtype, lengths, heads, bias):
     require_gpu()
-    print(f"case kk-gate+readout {dtype} lengths {lengths} H {heads} bias {bias}", flush=True)
+    print(f"case kk-gate+readout {dtype} {len(lengths)} sequences H {heads} bias {bias}",
+          flush=True)
     c = _readout_params(_case(lengths, heads, dtype, seed=7 * sum(lengths) + heads, bias=bias), 3)
     readout, new_k, y, pool = _run_readout(c, 0.9)
     ero, ey, epool, ek = _expected_readout(c, 0.9)
