@@ -54,6 +54,7 @@ struct alignas(16) WaveLds {
   __bf16 v_l[kVExact ? 1 : L][TP];                       // fp16 tokens only
   uint16_t yb[kRO ? L : 1][YPW];
   float rkv[kRO ? L : 4];
+  float lnw[kRO ? D : 4], lnb[kRO ? D : 4];   // the readout's GroupNorm weight and bias
 };
 using WaveLdsB = WaveLds<true, false>;
 using WaveLdsH = WaveLds<false, false>;
@@ -200,11 +201,27 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
   constexpr float kInvC = 1.0f / kC;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   const int nchunks = (t1 - t0 + L - 1) / L;
+  if constexpr (kRO) {
+    sm.lnw[lane] = Io::to_f32(static_cast<const raw*>(p.ro_lnw)[head_off + lane]);
+    sm.lnb[lane] = Io::to_f32(static_cast<const raw*>(p.ro_lnb)[head_off + lane]);
+  }
   u32x4 rows[6][2];
   if (nchunks > 0) load_rows(rows, 0);
   for (int c = 0; c < nchunks; ++c) {
     const bool valid = t0 + c * L + i < t1;
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
+    // fused readout: this lane's 16 gate values of the chunk's write-back
+    // (token lane / 4, channels 16 (lane % 4) ..), requested a whole chunk
+    // ahead of their use
+    u32x4 gpre[2];
+    if constexpr (kRO) {
+      const int64_t goff = static_cast<int64_t>(min(t0 + c * L + (lane >> 2), t1 - 1)) * row_stride +
+                           head_off + 16 * (lane & 3);
+      gpre[0] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.ro_g) + goff));
+      gpre[1] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.ro_g) + goff + 8));
+    }
     // ---- operands of the chunk (keys of K step m in registers)
     Sp8 As[2], Rs[2], Bs[2], Ks[2];
     // fused kk stage: 1 / |k k_k| over the token's 64 keys (the four lanes of
@@ -474,15 +491,24 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
       const float rkv = sm.rkv[orow];
 #pragma unroll
       for (int hp = 0; hp < 2; ++hp) {
+        // ln weight / bias from LDS, v from this chunk's V rows in LDS (for
+        // fp16 tokens hi + lo, which is exact), the gate from the prefetch
         float w8[8], b8[8], v8[8], g8[8];
-        unpack8<Io>(*reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.ro_lnw) + head_off +
-                                                    oc + 8 * hp), w8);
-        unpack8<Io>(*reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.ro_lnb) + head_off +
-                                                    oc + 8 * hp), b8);
-        unpack8<Io>(*reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.v) + roff + 8 * hp),
-                    v8);
-        unpack8<Io>(*reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.ro_g) + roff + 8 * hp),
-                    g8);
+        const int ch = oc + 8 * hp;
+        *reinterpret_cast<f32x4*>(w8) = *reinterpret_cast<const f32x4*>(&sm.lnw[ch]);
+        *reinterpret_cast<f32x4*>(w8 + 4) = *reinterpret_cast<const f32x4*>(&sm.lnw[ch + 4]);
+        *reinterpret_cast<f32x4*>(b8) = *reinterpret_cast<const f32x4*>(&sm.lnb[ch]);
+        *reinterpret_cast<f32x4*>(b8 + 4) = *reinterpret_cast<const f32x4*>(&sm.lnb[ch + 4]);
+        if constexpr (kVExact) {
+          unpack8<IoBF16>(*reinterpret_cast<const u32x4*>(&sm.v_h[orow][ch]), v8);
+        } else {
+          float vl8[8];
+          unpack8<IoBF16>(*reinterpret_cast<const u32x4*>(&sm.v_h[orow][ch]), v8);
+          unpack8<IoBF16>(*reinterpret_cast<const u32x4*>(&sm.v_l[orow][ch]), vl8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v8[e] += vl8[e];
+        }
+        unpack8<Io>(gpre[hp], g8);
         u32x4 packed;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
