@@ -84,9 +84,12 @@ def test_null_pointers_and_bad_sizes_are_rejected_before_any_launch(lib):
     assert lib.fr2_wkv7_rl_infctx_forward(
         fake, fake, fake, 1, 1, 1, 64, 1, 1, 8, 1, N.FR2_DTYPE_BFLOAT16, *([fake] * 9),
         1.0, nul) == N.FR2_ERR_UNSUPPORTED
-    assert lib.fr2_wkv7_recurrent_fp32_forward_kernel(
-        7, fake, fake, fake, 1, 1, 64, 1, 1, N.FR2_DTYPE_BFLOAT16, *([fake] * 9), 1.0,
-        nul) == N.FR2_ERR_INVALID_ARGUMENT
+    # kernel ids: 0 serial, 1 decode, 2 / 4 the two chunked forms; 3 is the
+    # Python layer's split selector, not a library kernel
+    for bad in (3, 5, 7, -2):
+        assert lib.fr2_wkv7_recurrent_fp32_forward_kernel(
+            bad, fake, fake, fake, 1, 1, 64, 1, 1, N.FR2_DTYPE_BFLOAT16, *([fake] * 9), 1.0,
+            nul) == N.FR2_ERR_INVALID_ARGUMENT
 
 
 def test_missing_library_fails_loudly(tmp_path):
