@@ -149,20 +149,26 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
   const int64_t sbase = (static_cast<int64_t>(slot) * H + h) * D * D;
 
   f32x4 S[4][4];   // [kb][vb]
-  if (p.state_in != nullptr) {
-    // fp32 state, or (bf16-state contract) bf16 widened once; the state
-    // stays fp32 for the whole call and is rounded back once at the end
-    const float* sin = static_cast<const float*>(p.state_in) + sbase + i;
+  // fp32 state, or (bf16-state contract) bf16 widened once; the state stays
+  // fp32 for the whole call and is rounded back once at the end (one branch
+  // around each loop: a per-element select compiles to a branch per load)
+  if (p.state_in != nullptr && p.state_bf16) {
     const uint16_t* sinb = static_cast<const uint16_t*>(p.state_in) + sbase + i;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int vb = 0; vb < 4; ++vb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int at = tile_key(kb, q, e) * D + 16 * vb;
-          S[kb][vb][e] = p.state_bf16 ? IoBF16::to_f32(sinb[at]) : sin[at];
-        }
+        for (int e = 0; e < 4; ++e)
+          S[kb][vb][e] = IoBF16::to_f32(sinb[tile_key(kb, q, e) * D + 16 * vb]);
+  } else if (p.state_in != nullptr) {
+    const float* sin = static_cast<const float*>(p.state_in) + sbase + i;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[kb][vb][e] = sin[tile_key(kb, q, e) * D + 16 * vb];
   } else {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
@@ -174,27 +180,39 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
   const raw* src[6] = {static_cast<const raw*>(p.r), static_cast<const raw*>(p.logits),
                        static_cast<const raw*>(p.k), static_cast<const raw*>(p.v),
                        static_cast<const raw*>(p.a), static_cast<const raw*>(p.b)};
-  const int64_t lane_off = head_off + 8 * q;
   const raw* bias = static_cast<const raw*>(p.bias);
-  // rows past the segment end are read from its last row (always in bounds)
-  // and zeroed when used
+  // Addresses: a wave-uniform 64-bit base per chunk (kept in scalar
+  // registers) plus a 32-bit per-lane byte offset within the chunk's 16 rows,
+  // so that no 64-bit per-lane pointer has to stay live (or spill) across
+  // the loop.  Rows past the segment end are read from its last row (always
+  // in bounds) and zeroed when used.
+  const int64_t rs_bytes = row_stride * static_cast<int64_t>(sizeof(raw));
+  // the fp32 row stride in bytes, 32 bits (a row is H * 64 elements)
+  const uint32_t rs4 = static_cast<uint32_t>(row_stride * static_cast<int64_t>(sizeof(float)));
+  auto chunk_base = [&](const void* ptr, int c) {
+    return static_cast<const char*>(ptr) + static_cast<int64_t>(t0 + c * L) * rs_bytes +
+           head_off * static_cast<int64_t>(sizeof(raw));
+  };
   auto load_rows = [&](u32x4 (&dst)[6][2], int c) {
-    const int tok = min(t0 + c * L + i, t1 - 1);
-    const int64_t off = static_cast<int64_t>(tok) * row_stride + lane_off;
+    const uint32_t lane_b = static_cast<uint32_t>(
+        static_cast<int64_t>(min(t0 + c * L + i, t1 - 1) - (t0 + c * L)) * rs_bytes +
+        16 * q);
 #pragma unroll
-    for (int j = 0; j < 6; ++j)
+    for (int j = 0; j < 6; ++j) {
+      const char* base = chunk_base(src[j], c);
 #pragma unroll
       for (int m = 0; m < 2; ++m)
         dst[j][m] = (kKK && j == 5)   // b is formed from the key with the gate stage
                         ? u32x4{0u, 0u, 0u, 0u}
                         : __builtin_nontemporal_load(
-                              reinterpret_cast<const u32x4*>(src[j] + off + 32 * m));
+                              reinterpret_cast<const u32x4*>(base + lane_b + 64 * m));
+    }
   };
   // per-channel parameters of the lane's 8 keys of K step m (read where used:
   // they would otherwise hold 16-64 registers across the whole loop)
   auto channel8 = [&](const void* base, int m, float* out) {
-    unpack8<Io>(*reinterpret_cast<const u32x4*>(static_cast<const raw*>(base) + lane_off + 32 * m),
-                out);
+    const char* hb = static_cast<const char*>(base) + head_off * static_cast<int64_t>(sizeof(raw));
+    unpack8<Io>(*reinterpret_cast<const u32x4*>(hb + static_cast<uint32_t>(16 * q + 64 * m)), out);
   };
 
   constexpr float kC = kNegExpHalf * kLog2e;
@@ -208,6 +226,11 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
   u32x4 rows[6][2];
   if (nchunks > 0) load_rows(rows, 0);
   for (int c = 0; c < nchunks; ++c) {
+    // the lane's (i, q), opaque once per chunk: the token masks and the
+    // identity derived from them are then formed where used instead of being
+    // hoisted out of the loop into registers (where they would spill)
+    int li = i, lq = q;
+    asm volatile("" : "+v"(li), "+v"(lq));
     const bool valid = t0 + c * L + i < t1;
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
     // fused readout: this lane's 16 gate values of the chunk's write-back
@@ -215,12 +238,12 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
     // ahead of their use
     u32x4 gpre[2];
     if constexpr (kRO) {
-      const int64_t goff = static_cast<int64_t>(min(t0 + c * L + (lane >> 2), t1 - 1)) * row_stride +
-                           head_off + 16 * (lane & 3);
-      gpre[0] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.ro_g) + goff));
-      gpre[1] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.ro_g) + goff + 8));
+      const char* gb = chunk_base(p.ro_g, c) +
+                       static_cast<uint32_t>((min(t0 + c * L + (lane >> 2), t1 - 1) - (t0 + c * L)) *
+                                                 rs_bytes +
+                                             32 * (lane & 3));
+      gpre[0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gb));
+      gpre[1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gb + 16));
     }
     // ---- operands of the chunk (keys of K step m in registers)
     Sp8 As[2], Rs[2], Bs[2], Ks[2];
@@ -276,9 +299,8 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, Io::from_f32(xk[2 * j + 1])))
                        << 16);
         if (valid)
-          *reinterpret_cast<u32x4*>(static_cast<raw*>(p.new_k) +
-                                    static_cast<int64_t>(t0 + c * L + i) * row_stride + lane_off +
-                                    32 * m) = packed;
+          *reinterpret_cast<u32x4*>(const_cast<char*>(chunk_base(p.new_k, c)) +
+                                    static_cast<uint32_t>(i * rs_bytes + 16 * q + 64 * m)) = packed;
         if constexpr (kRO) {
           // the readout's residual weight uses the key as stored
           float kq[8], rk[8];
@@ -294,7 +316,7 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
       }
       float nb[8];
       if (bias != nullptr) {
-        unpack8<Io>(*reinterpret_cast<const u32x4*>(bias + lane_off + 32 * m), nb);
+        channel8(bias, m, nb);
 #pragma unroll
         for (int e = 0; e < 8; ++e) nb[e] *= -kLog2e;
       } else {
@@ -380,15 +402,15 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
     f32x4 M, Mt, mak, mrb, mrk;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int s = 4 * q + e;
-      M[e] = (s > i) ? mab[e] : 0.f;
-      Mt[e] = (i > s) ? mabt[e] : 0.f;
-      mak[e] = (i > s) ? makt[e] : 0.f;
-      mrb[e] = (i >= s) ? mrbt[e] : 0.f;
-      mrk[e] = (i >= s) ? mrkt[e] : 0.f;
+      const int s = 4 * lq + e;
+      M[e] = (s > li) ? mab[e] : 0.f;
+      Mt[e] = (li > s) ? mabt[e] : 0.f;
+      mak[e] = (li > s) ? makt[e] : 0.f;
+      mrb[e] = (li >= s) ? mrbt[e] : 0.f;
+      mrk[e] = (li >= s) ? mrkt[e] : 0.f;
     }
     __builtin_amdgcn_sched_barrier(0);
-    const AOp Ta = t_inverse(M, Mt, i, q);
+    const AOp Ta = t_inverse(M, Mt, li, lq);
     const AOp Mak = as_a(split4(mak));
     const AOp Mrb = as_a(split4(mrb));
     const AOp Mrk = as_a(split4(mrk));
@@ -410,12 +432,12 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
         Sb[m].lo = __builtin_bit_cast(bf16x8, u32x4{x.l0, x.l1, y.l0, y.l1});
       }
       // V[4q+e][16vb+i] as the K = token operand
-      const bf16x4 vh = tr_rows(&sm.v_h[4 * q + (i >> 2)][16 * vb + 4 * (i & 3)]);
+      const bf16x4 vh = tr_rows(&sm.v_h[trow][16 * vb + 4 * (i & 3)]);
       auto times_v = [&](AOp a, f32x4 acc) {
         if constexpr (kVExact) {
           return mm_ax(a, as_bx(vh), acc);
         } else {
-          const bf16x4 vl = tr_rows(&sm.v_l[4 * q + (i >> 2)][16 * vb + 4 * (i & 3)]);
+          const bf16x4 vl = tr_rows(&sm.v_l[trow][16 * vb + 4 * (i & 3)]);
           return mm_ab(a, as_b(vh, vl), acc);
         }
       };
@@ -431,8 +453,10 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (t0 + c * L + 4 * q + e < t1)
-            p.sa_out[static_cast<int64_t>(t0 + c * L + 4 * q + e) * row_stride + head_off +
-                     16 * vb + i] = Uf[e];
+            *reinterpret_cast<float*>(
+                reinterpret_cast<char*>(p.sa_out + (static_cast<int64_t>(t0 + c * L) * row_stride +
+                                                    head_off)) +
+                (static_cast<uint32_t>(4 * q + e) * rs4 + (16 * vb + i) * 4u)) = Uf[e];
       }
       const BOp Us = as_b(split4(Uf));
       Y = mm_ab(Mrb, Us, Y);
@@ -442,7 +466,9 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
         if constexpr (kRO) {
           sm.yb[4 * q + e][16 * vb + i] = __builtin_bit_cast(uint16_t, Io::from_f32(p.scale * Y[e]));
         } else if (t0 + c * L + 4 * q + e < t1) {
-          yout[static_cast<int64_t>(t0 + c * L + 4 * q + e) * row_stride + head_off + 16 * vb + i] =
+          *reinterpret_cast<raw*>(const_cast<char*>(chunk_base(yout, c)) +
+                                  static_cast<uint32_t>((4 * q + e) * rs_bytes +
+                                                        (16 * vb + i) * sizeof(raw))) =
               Io::from_f32(p.scale * Y[e]);
         }
       }
@@ -470,7 +496,9 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       const int orow = lane >> 2, oc = 16 * (lane & 3);
       const int tok = t0 + c * L + orow;
-      const int64_t roff = static_cast<int64_t>(min(tok, t1 - 1)) * row_stride + head_off + oc;
+      // byte offset of this lane's 16 channels within the chunk's rows
+      const uint32_t rb = static_cast<uint32_t>((min(tok, t1 - 1) - (t0 + c * L)) * rs_bytes +
+                                                oc * sizeof(raw));
       const u32x4 yp[2] = {*reinterpret_cast<const u32x4*>(&sm.yb[orow][oc]),
                            *reinterpret_cast<const u32x4*>(&sm.yb[orow][oc + 8])};
       float yv[16];
@@ -524,8 +552,11 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
                        << 16);
         }
         if (tok < t1) {
-          *reinterpret_cast<u32x4*>(static_cast<raw*>(p.ro_out) + roff + 8 * hp) = packed;
-          if (yout != nullptr) *reinterpret_cast<u32x4*>(yout + roff + 8 * hp) = yp[hp];
+          *reinterpret_cast<u32x4*>(const_cast<char*>(chunk_base(p.ro_out, c)) + rb + 16 * hp) =
+              packed;
+          if (yout != nullptr)
+            *reinterpret_cast<u32x4*>(const_cast<char*>(chunk_base(yout, c)) + rb + 16 * hp) =
+                yp[hp];
         }
       }
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -534,21 +565,23 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
   }
 
-  if (p.state_out != nullptr) {
-    float* sout = static_cast<float*>(p.state_out) + sbase + i;
+  if (p.state_out != nullptr && p.state_bf16) {
     uint16_t* soutb = static_cast<uint16_t*>(p.state_out) + sbase + i;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int vb = 0; vb < 4; ++vb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int at = tile_key(kb, q, e) * D + 16 * vb;
-          if (p.state_bf16)
-            soutb[at] = IoBF16::from_f32(S[kb][vb][e]);
-          else
-            sout[at] = S[kb][vb][e];
-        }
+        for (int e = 0; e < 4; ++e)
+          soutb[tile_key(kb, q, e) * D + 16 * vb] = IoBF16::from_f32(S[kb][vb][e]);
+  } else if (p.state_out != nullptr) {
+    float* sout = static_cast<float*>(p.state_out) + sbase + i;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sout[tile_key(kb, q, e) * D + 16 * vb] = S[kb][vb][e];
   }
 }
 
