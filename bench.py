@@ -135,12 +135,11 @@ class Runner:
             wave = False
         elif units <= 512:
             wave = ms <= 24
-        elif units <= 1024:
-            wave = ms <= 224
         else:
             wave = ms <= 512 or ms * n <= 2 * self.w.total_tokens
         if wave:
-            return f"chunk64w_kernel<IoBF16,{'true' if n <= 256 else 'false'}>"
+            order = n <= 256 and ms >= 256 and 4 * ms * n > 5 * self.w.total_tokens
+            return f"chunk64w_kernel<IoBF16,{'true' if order else 'false'}>"
         return "chunk64_kernel<IoBF16,false>"
 
 

@@ -23,14 +23,13 @@ using fr2::SegArgs;
 //     512-thread workgroup per unit from L = 5 on (L = 1024: 0.098 against
 //     0.399 with one wave per unit);
 //   larger U: the chunked kernel with one wave per unit (chunkw.hip), whose
-//     units hide each other's latency, up to L = 24 (U <= 512) or 224
-//     (U <= 1024) and at every L beyond that (U = 4096, L = 1024: 1.18
-//     against 1.42; U = 65536, L = 64: 1.48 against 2.86), except for
-//     skewed batches whose longest sequence exceeds twice the mean: a long
-//     sequence is one wave's serial chain there, and the workgroup-per-unit
-//     kernel finishes it sooner.
-// The token-serial kernel no longer wins anywhere on this grid; it remains
-// the kernel of the contracts the others do not cover (bf16 state, D != 64).
+//     units hide each other's latency, up to L = 24 (U <= 512) and at every
+//     L beyond that (U = 1024, L = 1024: 0.351 against 0.395; U = 65536,
+//     L = 64: 1.41 against 2.85), except for skewed batches whose longest
+//     sequence exceeds twice the mean: a long sequence is one wave's serial
+//     chain there, and the workgroup-per-unit kernel finishes it sooner.
+// The token-serial kernel wins only within launch latency (U = 512, L = 5-8:
+// 0.0104 against 0.0114 ms); it remains the kernel of D != 64.
 constexpr int kDecodeMaxSeqlen = 4;
 constexpr int kChunkMinSeqlen = 5;   // the smallest chunked threshold (U <= 256)
 
@@ -41,7 +40,6 @@ bool decode_first(int64_t units, int max_seqlen) {
 bool wave_per_unit(int64_t units, int max_seqlen, int64_t total_tokens, int64_t nseg) {
   if (units <= 256) return false;
   if (units <= 512) return max_seqlen <= 24;
-  if (units <= 1024) return max_seqlen <= 224;
   return max_seqlen <= 512 || static_cast<int64_t>(max_seqlen) * nseg <= 2 * total_tokens;
 }
 // the public policy's choice is the workgroup-per-unit chunked kernel (the
@@ -75,7 +73,7 @@ int run_family(int family, int D, int dtype, bool bf16_state, const SegArgs& p,
       } else {
         const int64_t total = p.out_elems / (static_cast<int64_t>(p.num_heads) * D);
         const int rc = wave_per_unit(units, max_seqlen, total, nseg)
-                           ? fr2::launch_chunked_wave(dtype, p, nseg, s)
+                           ? fr2::launch_chunked_wave(dtype, p, nseg, max_seqlen, s)
                            : fr2::launch_chunked(dtype, p, nseg, max_seqlen, s);
         if (rc != FR2_ERR_UNSUPPORTED) return rc;
       }
@@ -91,7 +89,7 @@ int run_family(int family, int D, int dtype, bool bf16_state, const SegArgs& p,
       return fr2::launch_chunked(dtype, p, nseg, max_seqlen, s);
     case kChunkedWave:
       if (bf16_state || D != 64) return FR2_ERR_UNSUPPORTED;
-      return fr2::launch_chunked_wave(dtype, p, nseg, s);
+      return fr2::launch_chunked_wave(dtype, p, nseg, max_seqlen, s);
     default: return FR2_ERR_INVALID_ARGUMENT;
   }
 }
@@ -473,7 +471,7 @@ extern "C" int fr2_wkv7_chunk_bf16_forward(
   p.state_bf16 = true;
   const int rc =
       (max_seqlen < kChunkMinSeqlen || wave_per_unit(units, max_seqlen, total_tokens, num_sequences))
-          ? fr2::launch_chunked_wave(FR2_DTYPE_BFLOAT16, p, num_sequences,
+          ? fr2::launch_chunked_wave(FR2_DTYPE_BFLOAT16, p, num_sequences, max_seqlen,
                                      static_cast<hipStream_t>(stream))
           : fr2::launch_chunked(FR2_DTYPE_BFLOAT16, p, num_sequences, max_seqlen,
                                 static_cast<hipStream_t>(stream));
@@ -584,7 +582,7 @@ extern "C" int fr2_wkv7_rl_infctx_replay(
   // and length of run_family's grid (256 units, L = 16: 0.011 vs 0.013 ms
   // serial; 65 536 units, L = 16: 0.62 vs 0.90 ms decode)
   if (head_size == 64)
-    return fr2::launch_chunked_wave(dtype, p, num_chunks, static_cast<hipStream_t>(stream));
+    return fr2::launch_chunked_wave(dtype, p, num_chunks, 0, static_cast<hipStream_t>(stream));
   return fr2::launch_serial(head_size, dtype, false, p, num_chunks,
                             static_cast<hipStream_t>(stream));
 }
@@ -788,7 +786,8 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate(
   // the chunked kernel the plain entry's policy picks, with the stage fused
   return workgroup_chunked(units, max_seqlen, total_tokens, num_sequences)
              ? fr2::launch_chunked_kk(dtype, p, num_sequences, static_cast<hipStream_t>(stream))
-             : fr2::launch_chunked_wave(dtype, p, num_sequences, static_cast<hipStream_t>(stream));
+             : fr2::launch_chunked_wave(dtype, p, num_sequences, max_seqlen,
+                                        static_cast<hipStream_t>(stream));
 }
 
 extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate_readout(
@@ -825,7 +824,8 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate_readout(
   // the chunked kernel the plain entry's policy picks, with the stage fused
   return workgroup_chunked(units, max_seqlen, total_tokens, num_sequences)
              ? fr2::launch_chunked_kk(dtype, p, num_sequences, static_cast<hipStream_t>(stream))
-             : fr2::launch_chunked_wave(dtype, p, num_sequences, static_cast<hipStream_t>(stream));
+             : fr2::launch_chunked_wave(dtype, p, num_sequences, max_seqlen,
+                                        static_cast<hipStream_t>(stream));
 }
 
 extern "C" int fr2_tmix_kk_a_gate_forward(int64_t tokens, int32_t num_heads, int32_t head_size,

@@ -40,6 +40,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegExpHalf = -0.6065306597126334f;   // -exp(-1/2)
 
 constexpr int kOrderMaxSeqs = 256;   // longest-first order up to this many sequences
+constexpr int kOrderMinSeqlen = 256; // ... whose longest has at least this many tokens
 
 constexpr int YPW = D + 8;            // padded row of the staged outputs (fused readout)
 
@@ -77,16 +78,22 @@ static_assert(offsetof(WaveLdsB, b_h) % 16 == 0 && offsetof(WaveLdsH, v_l) % 16 
 // for n ints; the ranking is O(n^2 / 64) per wave, so it is used for small n
 // only (kOrderMaxSeqs).
 __device__ __attribute__((noinline)) int seq_of_rank(const int32_t* bounds, int n, int rank, int* len,
-                                           int lane) {
-  for (int k = lane; k < n; k += 64) len[k] = bounds[k + 1] - bounds[k];
+                                                     int lane) {
+  // lengths padded to a multiple of 4 with -1 (shorter than any sequence),
+  // compared four at a time from one 16-byte LDS read
+  const int n4 = (n + 3) & ~3;
+  for (int k = lane; k < n4; k += 64) len[k] = k < n ? bounds[k + 1] - bounds[k] : -1;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);   // one wave: its LDS accesses complete in order
   for (int j0 = 0; j0 < n; j0 += 64) {
     const int j = j0 + lane;
     const int lj = j < n ? len[j] : -1;
     int r = 0;
-    for (int k = 0; k < n; ++k) {
-      const int lk = len[k];
-      r += (lk > lj || (lk == lj && k < j)) ? 1 : 0;
+    for (int k = 0; k < n4; k += 4) {
+      const int4 l4 = *reinterpret_cast<const int4*>(&len[k]);
+      r += (l4.x > lj || (l4.x == lj && k < j)) ? 1 : 0;
+      r += (l4.y > lj || (l4.y == lj && k + 1 < j)) ? 1 : 0;
+      r += (l4.z > lj || (l4.z == lj && k + 2 < j)) ? 1 : 0;
+      r += (l4.w > lj || (l4.w == lj && k + 3 < j)) ? 1 : 0;
     }
     const uint64_t hit = __ballot(j < n && r == rank);
     if (hit != 0) return j0 + __builtin_ctzll(hit);
@@ -611,7 +618,7 @@ void launch_wave_io(const SegArgs& p, int n, bool order, hipStream_t s) {
 
 }  // namespace
 
-int launch_chunked_wave(int dtype, const SegArgs& p, int nseg, hipStream_t s) {
+int launch_chunked_wave(int dtype, const SegArgs& p, int nseg, int max_seqlen, hipStream_t s) {
   if (p.boundary != nullptr || p.reverse || p.split_pieces > 0) return FR2_ERR_UNSUPPORTED;
   const bool kk = p.kk_scale != nullptr, ro = p.ro_out != nullptr;
   // the fused stages: the gate needs all its inputs, the readout needs the
@@ -624,8 +631,14 @@ int launch_chunked_wave(int dtype, const SegArgs& p, int nseg, hipStream_t s) {
     return FR2_ERR_INVALID_ARGUMENT;
   const int64_t units = static_cast<int64_t>(nseg) * p.num_heads;
   if (units <= 0 || units > (int64_t{1} << 30)) return FR2_ERR_INVALID_ARGUMENT;
+  // the longest-first order pays when a long sequence would otherwise start
+  // late: packed batches of at most kOrderMaxSeqs sequences whose longest is
+  // at least kOrderMinSeqlen tokens and a quarter above the mean (the ranking
+  // costs each wave O(n^2 / 256) LDS steps)
+  const int64_t total = p.out_elems / (static_cast<int64_t>(p.num_heads) * D);
   const bool order = p.uniform_len <= 0 && p.chunk_offsets == nullptr && p.ends == nullptr &&
-                     nseg > 1 && nseg <= kOrderMaxSeqs;
+                     nseg > 1 && nseg <= kOrderMaxSeqs && max_seqlen >= kOrderMinSeqlen &&
+                     4 * static_cast<int64_t>(max_seqlen) * nseg > 5 * total;
   const int n = static_cast<int>(units);
   if (dtype == FR2_DTYPE_BFLOAT16)
     launch_wave_io<IoBF16>(p, n, order, s);

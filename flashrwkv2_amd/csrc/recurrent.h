@@ -154,7 +154,7 @@ int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen,
 // The chunked prefill with one wavefront per (sequence, head) unit (plain
 // contract: no sa / boundary outputs, fp32 state), for launches with many
 // units.
-int launch_chunked_wave(int dtype, const SegArgs& p, int nseg, hipStream_t s);
+int launch_chunked_wave(int dtype, const SegArgs& p, int nseg, int max_seqlen, hipStream_t s);
 // Sequence-split chunked prefill (D = 64, fp32 state, plain contract):
 // `pieces` pieces per sequence, of `piece_len` tokens except piece 0, which
 // has lead_len tokens when lead_len > 0 (the pipelined split: piece 0 runs on

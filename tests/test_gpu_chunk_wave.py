@@ -85,7 +85,8 @@ def test_longest_first_order_with_ties_permuted_slots_and_inactive_sequences():
     stay untouched."""
     C = require_gpu()
     rng = np.random.default_rng(5)
-    base = [97, 16, 16, 1, 33, 97, 64, 2, 200, 15, 17, 31]
+    # the order applies to batches whose longest sequence has >= 256 tokens
+    base = [97, 16, 16, 1, 33, 97, 64, 2, 300, 15, 17, 31]
     lengths = tuple(base[i % len(base)] if i % 3 else int(rng.integers(1, 260))
                     for i in range(40))
     print(f"case wave order lengths={lengths}", flush=True)
