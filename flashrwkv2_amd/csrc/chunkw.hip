@@ -45,15 +45,15 @@ constexpr int kOrderMinSeqlen = 256; // ... whose longest has at least this many
 constexpr int YPW = D + 8;            // padded row of the staged outputs (fused readout)
 
 // One wave's LDS: its chunk's B^, K^ (hi and lo) and V rows, read back
-// transposed, and gamma_L; with the fused readout (kRO) also the chunk's y
-// rows, staged for the per-token GroupNorm, and each token's r k' r_k sum.
+// transposed, gamma_L and the chunk's staged y rows; with the fused readout
+// (kRO) also each token's r k' r_k sum and the GroupNorm weight and bias.
 template <bool kVExact, bool kRO>
 struct alignas(16) WaveLds {
   static constexpr int TP = kVExact ? D + 16 : D + 8;   // token row pitch
   float gl[D];
   __bf16 b_h[L][TP], b_l[L][TP], k_h[L][TP], k_l[L][TP], v_h[L][TP];
   __bf16 v_l[kVExact ? 1 : L][TP];                       // fp16 tokens only
-  uint16_t yb[kRO ? L : 1][YPW];
+  uint16_t yb[L][YPW];                                   // the chunk's y rows
   float rkv[kRO ? L : 4];
   float lnw[kRO ? D : 4], lnb[kRO ? D : 4];   // the readout's GroupNorm weight and bias
 };
@@ -467,18 +467,12 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
       }
       const BOp Us = as_b(split4(Uf));
       Y = mm_ab(Mrb, Us, Y);
-      // y rows 4q + e, column 16vb + i (staged for the fused readout)
+      // y rows 4q + e, column 16vb + i, staged in LDS: the chunk's rows then
+      // leave as whole 32-byte pieces (2-byte stores straight from the
+      // accumulators cost a quarter of the kernel's time)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if constexpr (kRO) {
-          sm.yb[4 * q + e][16 * vb + i] = __builtin_bit_cast(uint16_t, Io::from_f32(p.scale * Y[e]));
-        } else if (t0 + c * L + 4 * q + e < t1) {
-          *reinterpret_cast<raw*>(const_cast<char*>(chunk_base(yout, c)) +
-                                  static_cast<uint32_t>((4 * q + e) * rs_bytes +
-                                                        (16 * vb + i) * sizeof(raw))) =
-              Io::from_f32(p.scale * Y[e]);
-        }
-      }
+      for (int e = 0; e < 4; ++e)
+        sm.yb[4 * q + e][16 * vb + i] = __builtin_bit_cast(uint16_t, Io::from_f32(p.scale * Y[e]));
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
         // B^^T and K^^T of tile kb as A operands (row = key, K = token)
@@ -569,6 +563,18 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
     if (c + 1 < nchunks) load_rows(rows, c + 1);
+    if constexpr (!kRO) {
+      // the staged y rows: lane l writes 16 channels of token l / 4 (issued
+      // after the next chunk's row loads, which then do not wait for them)
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      const int orow = lane >> 2, oc = 16 * (lane & 3);
+      if (t0 + c * L + orow < t1) {
+        char* dst = const_cast<char*>(chunk_base(yout, c)) +
+                    static_cast<uint32_t>(orow * rs_bytes + oc * sizeof(raw));
+        *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(&sm.yb[orow][oc]);
+        *reinterpret_cast<u32x4*>(dst + 16) = *reinterpret_cast<const u32x4*>(&sm.yb[orow][oc + 8]);
+      }
+    }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
   }
 
