@@ -42,7 +42,7 @@ constexpr float kNegExpHalf = -0.6065306597126334f;   // -exp(-1/2)
 constexpr int kOrderMaxSeqs = 256;   // longest-first order up to this many sequences
 constexpr int kOrderMinSeqlen = 256; // ... whose longest has at least this many tokens
 
-constexpr int YPW = D + 8;            // padded row of the staged outputs (fused readout)
+constexpr int YPW = D + 8;            // padded row of the staged outputs
 
 // One wave's LDS: its chunk's B^, K^ (hi and lo) and V rows, read back
 // transposed, gamma_L and the chunk's staged y rows; with the fused readout
@@ -75,8 +75,8 @@ static_assert(offsetof(WaveLdsB, b_h) % 16 == 0 && offsetof(WaveLdsH, v_l) % 16 
 // (the units of shorter sequences fill the SIMDs around it).  Returns the
 // index of the sequence of rank `rank` among sequences [0, n) by decreasing
 // length (ties by index), or -1 when rank >= n.  `len` is wave-private LDS
-// for n ints; the ranking is O(n^2 / 64) per wave, so it is used for small n
-// only (kOrderMaxSeqs).
+// for n ints (rounded up to 4); the ranking costs each wave O(n^2 / 64)
+// comparisons, so it is used for small n only (kOrderMaxSeqs).
 __device__ __attribute__((noinline)) int seq_of_rank(const int32_t* bounds, int n, int rank, int* len,
                                                      int lane) {
   // lengths padded to a multiple of 4 with -1 (shorter than any sequence),
