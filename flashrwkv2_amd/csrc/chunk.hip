@@ -791,18 +791,22 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) S[kb][e] = sin[(kb * 16 + 4 * q + e) * D + vcol];
-    } else if (p.state_in != nullptr) {
-      // fp32 state, or (bf16-state contract) bf16 widened once; the state
-      // stays fp32 for the whole call and is rounded back once at the end
-      const float* sin = static_cast<const float*>(p.state_in);
-      const uint16_t* sinb = static_cast<const uint16_t*>(p.state_in);
+    } else if (p.state_in != nullptr && p.state_bf16) {
+      // (bf16-state contract) bf16 widened once; the state stays fp32 for
+      // the whole call and is rounded back once at the end.  One branch
+      // around each loop: a per-element select compiles to a branch and a
+      // wait per load.
+      const uint16_t* sinb = static_cast<const uint16_t*>(p.state_in) + sbase + vcol;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t at = sbase + (kb * 16 + 4 * q + e) * D + vcol;
-          S[kb][e] = p.state_bf16 ? IoBF16::to_f32(sinb[at]) : sin[at];
-        }
+        for (int e = 0; e < 4; ++e) S[kb][e] = IoBF16::to_f32(sinb[(kb * 16 + 4 * q + e) * D]);
+    } else if (p.state_in != nullptr) {
+      const float* sin = static_cast<const float*>(p.state_in) + sbase + vcol;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[kb][e] = sin[(kb * 16 + 4 * q + e) * D];
     }
     // outputs of a finished group: 16-byte pieces of the staged rows, token
     // tid/8, elements 8*(tid%8).. (the four state waves cover the 32 rows)
@@ -937,19 +941,19 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
 #pragma unroll
           for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
       }
-    } else if (p.state_out != nullptr) {
-      float* sout = static_cast<float*>(p.state_out);
-      uint16_t* soutb = static_cast<uint16_t*>(p.state_out);
+    } else if (p.state_out != nullptr && p.state_bf16) {
+      uint16_t* soutb = static_cast<uint16_t*>(p.state_out) + sbase + vcol;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t at = sbase + (kb * 16 + 4 * q + e) * D + vcol;
-          if (p.state_bf16)
-            soutb[at] = IoBF16::from_f32(S[kb][e]);
-          else
-            sout[at] = S[kb][e];
-        }
+        for (int e = 0; e < 4; ++e)
+          soutb[(kb * 16 + 4 * q + e) * D] = IoBF16::from_f32(S[kb][e]);
+    } else if (p.state_out != nullptr) {
+      float* sout = static_cast<float*>(p.state_out) + sbase + vcol;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D] = S[kb][e];
     }
   } else {
     // ---------------- key waves: chunk cc of each group, key half hh
