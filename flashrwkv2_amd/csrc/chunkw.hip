@@ -200,6 +200,9 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
     return static_cast<const char*>(ptr) + static_cast<int64_t>(t0 + c * L) * rs_bytes +
            head_off * static_cast<int64_t>(sizeof(raw));
   };
+  // plain (cached) loads: a lane's two 16-byte pieces of a row are half
+  // cache lines whose other halves the neighbouring lanes load in the same
+  // instruction pair, and measured 2-5 % faster than non-temporal loads
   auto load_rows = [&](u32x4 (&dst)[6][2], int c) {
     const uint32_t lane_b = static_cast<uint32_t>(
         static_cast<int64_t>(min(t0 + c * L + i, t1 - 1) - (t0 + c * L)) * rs_bytes +
@@ -211,8 +214,7 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
       for (int m = 0; m < 2; ++m)
         dst[j][m] = (kKK && j == 5)   // b is formed from the key with the gate stage
                         ? u32x4{0u, 0u, 0u, 0u}
-                        : __builtin_nontemporal_load(
-                              reinterpret_cast<const u32x4*>(base + lane_b + 64 * m));
+                        : *reinterpret_cast<const u32x4*>(base + lane_b + 64 * m);
     }
   };
   // per-channel parameters of the lane's 8 keys of K step m (read where used:
