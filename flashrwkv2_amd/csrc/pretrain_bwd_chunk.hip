@@ -171,7 +171,7 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
   // global inputs of one chunk
   struct In {
     bf16x4 DYb[4], Vb[4];
-    f32x4 SA4[4], DS4[4], S04[4];
+    f32x4 SA4[4], DS4[4];
     u32x2 rw, rr, rk, ra, rb;
   };
   const int tp = tid & 15, kg = tid >> 4;   // prep role: token tp, keys 4kg..4kg+3
@@ -184,14 +184,6 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
       in.Vb[vb] = ld_bf4(p.v + tok(t0 + n) + j0);
       in.SA4[vb] = ld_f4(p.sa + tok(t0 + n) + j0);
       in.DS4[vb] = ld_f4(p.dsa + tok(t0 + n) + j0);
-      // chunk 0 starts from state0, or from the zero state (then row 0 of
-      // the snapshot of chunk 0 is loaded and discarded: always in bounds)
-      const float* s0 =
-          (m == 0 && p.state0 != nullptr)
-              ? p.state0 + static_cast<int64_t>(bidx) * p.state0_stride +
-                    static_cast<int64_t>(h) * kD * kD
-              : p.bnd + (static_cast<int64_t>(bh) * nchunk + max(m - 1, 0)) * kD * kD;
-      in.S04[vb] = ld_f4(s0 + static_cast<int64_t>(row) * kD + j0);
     }
     const int64_t pbase = tok(t0 + tp) + 4 * kg;
     in.rw = *reinterpret_cast<const u32x2*>(p.w + pbase);
@@ -200,6 +192,20 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
     in.ra = *reinterpret_cast<const u32x2*>(p.a + pbase);
     in.rb = *reinterpret_cast<const u32x2*>(p.b + pbase);
   };
+  auto load_s0 = [&](f32x4 (&S04)[4], int m) {
+    // chunk 0 starts from state0, or from the zero state (then row 0 of
+    // the snapshot of chunk 0 is loaded and discarded: always in bounds)
+    const float* s0 =
+        (m == 0 && p.state0 != nullptr)
+            ? p.state0 + static_cast<int64_t>(bidx) * p.state0_stride +
+                  static_cast<int64_t>(h) * kD * kD
+            : p.bnd + (static_cast<int64_t>(bh) * nchunk + max(m - 1, 0)) * kD * kD;
+#pragma unroll
+    for (int vb = 0; vb < 4; ++vb)
+      S04[vb] = ld_f4(s0 + static_cast<int64_t>(row) * kD + 16 * vb + 4 * q);
+  };
+  f32x4 S04[4];
+  load_s0(S04, m_hi);
   auto body = [&](int m) {
     const int t0 = kL * m;
     In in;
@@ -214,7 +220,7 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
       for (int e = 0; e < 4; ++e) {
         SAf[4 * vb + e] = in.SA4[vb][e];
         DSf[4 * vb + e] = in.DS4[vb][e];
-        S0f[4 * vb + e] = (m > 0 || p.state0 != nullptr) ? in.S04[vb][e] : 0.0f;
+        S0f[4 * vb + e] = (m > 0 || p.state0 != nullptr) ? S04[vb][e] : 0.0f;
       }
     }
     const u32x2 rw = in.rw, rr = in.rr, rk = in.rk, ra = in.ra, rb = in.rb;
@@ -326,6 +332,8 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
       for (int e = 0; e < 4; ++e) pcs0 = fmaf(PcT[vb][e], S0f[4 * vb + e], pcs0);
     pcs0 += __shfl_xor(pcs0, 16);
     pcs0 += __shfl_xor(pcs0, 32);
+    // the next (earlier) chunk's start state is requested here, a chunk ahead
+    if (m > m_lo) load_s0(S04, m - 1);
 
     __syncthreads();
 
