@@ -540,11 +540,12 @@ template <class Io, class St, bool kSa = false>
 __global__ __launch_bounds__(64) void decode64_kernel(SegArgs p) {
   decode64_body<Io, St, kSa>(p);
 }
-// The FP16-state form holds its state packed (32 registers): capped at 96
-// registers it keeps five waves per SIMD resident instead of four, with no
-// spills.
+// The FP16-state form holds its state packed (32 registers).  Capped at 96
+// registers (five waves per SIMD) it spills 26 values and runs no faster
+// than at 128 (config-2 shape: 0.0238 ms both; 80 registers, six waves:
+// 0.0359 ms), so it keeps 128 (2 spilled values).
 template <class Io>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void decode64_f16s_kernel(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void decode64_f16s_kernel(
     SegArgs p) {
   decode64_body<Io, StF16>(p);
 }
