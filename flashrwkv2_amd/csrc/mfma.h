@@ -119,27 +119,45 @@ __device__ __forceinline__ BOp as_b(bf16x4 hi, bf16x4 lo) {
 
 // T = (I - M)^-1 for a strictly lower triangular 16x16 M, given in both
 // accumulator orientations (lane (i, q): M[e] = M[4q+e][i], Mt[e] =
-// M[i][4q+e]), as (I+M)(I+M^2)(I+M^4)(I+M^8), keeping both orientations of
-// each factor in registers (X Y = mm_ab(A form of X^T's accumulator, B form
-// of Y's)).  Returns the A operand of T.
+// M[i][4q+e]).  Returns the A operand of T.
+//
+// Blocked over the four 4x4 diagonal blocks: with MD the block-diagonal part
+// of M and MO the rest (strictly block-lower),
+//   D = (I - MD)^-1 = (I + MD)(I + MD^2)             (4x4 blocks: MD^4 = 0)
+//   I - M = (I - MD)(I - N),  N = D MO               (strictly block-lower)
+//   T = (I - N)^-1 D = (I + N)(I + N^2) D            (N^4 = 0)
+// Every intermediate is a product of at most three factors of bounded size,
+// so the sums stay of the order of T itself.  The doubling form
+// (I+M)(I+M^2)(I+M^4)(I+M^8) over the whole block builds M^8, whose entries
+// are sums over up to C(15, 8) paths: with strongly correlated keys and an
+// in-context rate near 1 (Mab close to a constant below the diagonal) they
+// reach 10^3 while T stays of order 1, and the cancellation lost the output
+// gate even with split operands.
+// Products X Y are mm_ab(A form of X = split of acc(X^T), B form of Y = split
+// of acc(Y)); each needed orientation is formed as its own product.
 __device__ __forceinline__ AOp t_inverse(f32x4 M, f32x4 Mt, int i, int q) {
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   f32x4 I4;
 #pragma unroll
   for (int e = 0; e < 4; ++e) I4[e] = (4 * q + e == i) ? 1.0f : 0.0f;
-  const Split4 sM = split4(M), sMt = split4(Mt);
-  const f32x4 M2 = mm_ab(as_a(sMt), as_b(sM), zero);
-  const f32x4 M2t = mm_ab(as_a(sM), as_b(sMt), zero);
-  const Split4 sM2 = split4(M2), sM2t = split4(M2t);
-  const f32x4 T1t = I4 + Mt;
-  const f32x4 T2t = mm_ab(as_a(sM2), as_b(split4(T1t)), T1t);
-  const f32x4 M4 = mm_ab(as_a(sM2t), as_b(sM2), zero);
-  const f32x4 M4t = mm_ab(as_a(sM2), as_b(sM2t), zero);
-  const Split4 sM4 = split4(M4);
-  const f32x4 T4t = mm_ab(as_a(sM4), as_b(split4(T2t)), T2t);
-  const f32x4 M8 = mm_ab(as_a(split4(M4t)), as_b(sM4), zero);
-  const f32x4 Tt = mm_ab(as_a(split4(M8)), as_b(split4(T4t)), T4t);   // accumulator of T^T
-  return as_a(split4(Tt));                                            // = A operand of T
+  // rows 4q..4q+3 and column i (or the transpose) lie in one diagonal block
+  // exactly when q == i / 4, for all four items of the lane
+  const bool diag = q == (i >> 2);
+  const f32x4 MD = diag ? M : zero, MDt = diag ? Mt : zero, MO = diag ? zero : M;
+  const f32x4 MD2 = mm_ab(as_a(split4(MDt)), as_b(split4(MD)), zero);   // MD^2
+  const f32x4 E = I4 + MD, Et = I4 + MDt;                               // I + MD, (I + MD)^T
+  const Split4 sMD2 = split4(MD2), sEt = split4(Et);
+  const f32x4 Dm = mm_ab(as_a(sEt), as_b(sMD2), E);     // D = (I + MD) + (I + MD) MD^2
+  const f32x4 Dt = mm_ab(as_a(sMD2), as_b(sEt), Et);    // D^T
+  const Split4 sD = split4(Dm), sDt = split4(Dt), sMO = split4(MO);
+  const f32x4 N = mm_ab(as_a(sDt), as_b(sMO), zero);    // N = D MO
+  const f32x4 Nt = mm_ab(as_a(sMO), as_b(sDt), zero);   // N^T = MO^T D^T
+  const f32x4 N2 = mm_ab(as_a(split4(Nt)), as_b(split4(N)), zero);     // N^2
+  const f32x4 Ft = I4 + Nt;                                             // (I + N)^T
+  // (I + N)(I + N^2) = (I + N) + (I + N) N^2, transposed
+  const f32x4 Tpt = mm_ab(as_a(split4(N2)), as_b(split4(Ft)), Ft);
+  const f32x4 Tt = mm_ab(as_a(sD), as_b(split4(Tpt)), zero);            // T^T = D^T Tp^T
+  return as_a(split4(Tt));                                              // = A operand of T
 }
 
 // Inclusive prefix sum over the 16 lanes of a DPP row (the token axis).
