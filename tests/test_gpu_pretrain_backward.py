@@ -29,18 +29,24 @@ GRAD_REL_RMSE = 1.0e-2
 
 
 def _case(batch, tokens, heads, head_size, *, seed, scale=0.05, logit_shift=0.0,
-          logit_scale=None, rwkv=False):
+          logit_scale=None, rwkv=False, corr=None):
     """``rwkv=False``: every input 0.05 * randn, as the reference's test.
     ``rwkv=True``: the model's own operand structure (r, k, v ~ N(0,1),
     kk = L2-normalised N(0,1) per head, a = -kk, b = kk * sigmoid(N(0,1))),
-    which keeps the state bounded at O(1) inputs."""
+    which keeps the state bounded at O(1) inputs.  ``corr=(rho, rate)``: the
+    same with correlated keys, kk_t = normalise(base + rho * noise_t) per
+    head, and the gate fixed at ``rate``."""
     g = torch.Generator().manual_seed(seed)
     shape = (batch, tokens, heads * head_size)
     vals = [torch.randn(shape, generator=g) * scale for _ in range(6)]
-    if rwkv:
+    if rwkv or corr is not None:
         kk = torch.randn((batch, tokens, heads, head_size), generator=g)
-        kk = kk / kk.norm(dim=-1, keepdim=True)
         gate = torch.sigmoid(torch.randn((batch, tokens, heads, head_size), generator=g))
+        if corr is not None:
+            base = torch.randn((1, 1, heads, head_size), generator=g)
+            kk = base + corr[0] * kk
+            gate = torch.full_like(gate, corr[1])
+        kk = kk / kk.norm(dim=-1, keepdim=True)
         vals = [torch.randn(shape, generator=g) for _ in range(6)]
         vals[4] = (-kk).reshape(shape)
         vals[5] = (kk * gate).reshape(shape)
@@ -121,6 +127,17 @@ def test_backward_extreme_decay(shift):
     require_gpu()
     vals, dy = _case(1, 64, 2, 64, seed=int(50 + shift), rwkv=True, logit_shift=shift,
                      logit_scale=0.5)
+    _check(_run(vals, dy, 64), _expected(vals, dy, 64))
+
+
+@pytest.mark.parametrize("rho,rate", [(0.1, 1.0), (0.3, 0.98)])
+def test_backward_correlated_keys(rho, rate):
+    """Strongly correlated keys with the in-context rate near 1: the chunk
+    inverse T = (I - Mab)^-1 of the forward and of the reverse pass is formed
+    with no large intermediate sums (the doubling form lost accuracy here)."""
+    require_gpu()
+    print(f"case pretrain bwd correlated rho={rho} rate={rate}", flush=True)
+    vals, dy = _case(2, 512, 4, 64, seed=17, corr=(rho, rate), logit_shift=-2.0)
     _check(_run(vals, dy, 64), _expected(vals, dy, 64))
 
 
