@@ -158,10 +158,10 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kernel(
 // summary pass over pieces 1..P-2 (one block per unit and piece), then a
 // combine kernel chains the start states and pieces 1..P-1 run.  With
 // Q = 256/units and P = Q + 1 pieces, both phases hold one block per CU.  A
-// summary block costs ~1.3x a real block per token when the two run side by
-// side (config 4: 96 vs 73 ns per token), but the lead piece's block also
-// slows down next to it; piece 0 gets 1.2x the tokens of the others (the
-// best of 1.15x-1.33x measured at config 4).  Q is also capped so that
+// summary block and a real block next to it run at about the same rate per
+// token (config 4: 85 and 86 ns per token), so piece 0 gets 1.05x the
+// tokens of the others (config 4, lead lengths 13 120-15 104 tokens: 2.14-
+// 2.16 ms at 13 440-13 760, 2.25 ms at 15 104).  Q is also capped so that
 // pieces keep at least 384 tokens: shorter pieces lose to the fixed cost of
 // the extra passes (1024 tokens on 32 units: 3 pieces 0.095 ms, unsplit
 // 0.083 ms; 2048 tokens: 5 pieces 0.120 ms, unsplit 0.164 ms).  Split only
@@ -169,7 +169,7 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kernel(
 constexpr int kSplitMaxUnits = 128;
 constexpr int kSplitMinPiece = 384;
 constexpr int kSplitAlign = 32;
-constexpr float kSplitLeadRatio = 1.2f;
+constexpr float kSplitLeadRatio = 1.05f;
 
 extern "C" int fr2_wkv7_recurrent_fp32_split_plan(int32_t num_sequences, int32_t num_heads,
                                                   int32_t head_size, int32_t max_seqlen,

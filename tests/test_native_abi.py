@@ -111,7 +111,7 @@ def test_split_plan_config4_and_no_split_cases(lib):
     """The pipelined split plan (host code, no GPU): BASELINE config 4 gets
     5 pieces with a longer piece 0; config 1 (256 units), D != 64, short
     sequences and more than 128 units are not split."""
-    assert _plan(lib, 1, 64, 64, 65536) == (5, 12608, 15104, (3 * 5 - 2) * 64 * 64 * 64 * 4)
+    assert _plan(lib, 1, 64, 64, 65536) == (5, 12992, 13568, (3 * 5 - 2) * 64 * 64 * 64 * 4)
     for args in ((8, 32, 64, 4096), (1, 64, 128, 65536), (1, 32, 64, 1024), (1, 129, 64, 65536),
                  (4, 32, 64, 127)):
         assert _plan(lib, *args)[0] == 1, args
