@@ -1,4 +1,5 @@
-"""GPU parity of the chunked kernels on strongly correlated keys.
+"""GPU parity of the chunked kernels on strongly correlated keys and other
+input regimes that stress the chunk form.
 
 RWKV-7's wkv_prepare gives a = -kk and b = kk * g with kk the L2-normalised
 key and g the in-context rate in (0, 1).  When consecutive tokens' kk point
@@ -8,7 +9,10 @@ formed without large intermediate sums: powers of the whole 16x16 block
 (M^8) then reach ~10^3 while T stays of order 1.  These cases check both
 chunked kernels (forced), and the public entry with its policy (which splits
 a single long sequence), against the fp64 oracle with the suite's gates, for
-short- and long-memory decay.
+short- and long-memory decay.  The stress cases add the widest spread of
+1/gamma inside a chunk (half the channels at the retention floor, half near
+1), keys of five times the usual scale with long memory, and the retention
+floor with correlated keys.
 """
 
 from __future__ import annotations
@@ -31,10 +35,13 @@ pytestmark = pytest.mark.gpu
 CHUNKED, CHUNKED_WAVE = 2, 4
 
 
-def _correlated_case(lengths, *, heads, rho, rate, u_range, dtype, seed):
+def _correlated_case(lengths, *, heads, rho, rate, u_range, dtype, seed, k_scale=1.0,
+                     mixed_decay=False):
     """kk_t = normalise(base_head + rho * noise_t): cosine between tokens of
-    about 1 / (1 + rho^2) in 64 dimensions; b = kk * rate (rate None: the
-    usual sigmoid(N(0, 1)))."""
+    about 1 / (1 + rho^2) in 64 dimensions (rho None: independent kk);
+    b = kk * rate (rate None: the usual sigmoid(N(0, 1))).  ``mixed_decay``:
+    keys 0..31 decay at the retention floor (u ~ U(-0.6, -0.5)), keys 32..63
+    barely (u ~ U(-9, -8)), the widest spread of 1/gamma inside a chunk."""
     g = torch.Generator().manual_seed(seed)
     total, D = sum(lengths), 64
     shape = (total, heads, D)
@@ -42,11 +49,15 @@ def _correlated_case(lengths, *, heads, rho, rate, u_range, dtype, seed):
     def normal():
         return torch.randn(shape, generator=g, dtype=torch.float64)
 
-    r, k, v = normal(), normal(), normal()
+    r, k, v = normal(), normal() * k_scale, normal()
     lo, hi = u_range
     u = torch.rand(shape, generator=g, dtype=torch.float64) * (hi - lo) + lo
+    if mixed_decay:
+        fast = torch.rand(shape, generator=g, dtype=torch.float64) * 0.1 - 0.6
+        slow = torch.rand(shape, generator=g, dtype=torch.float64) - 9.0
+        u = torch.where(torch.arange(D) < D // 2, fast, slow)
     base = torch.randn((1, heads, D), generator=g, dtype=torch.float64)
-    kk = base + rho * normal()
+    kk = normal() if rho is None else base + rho * normal()
     kk = kk / kk.norm(dim=-1, keepdim=True)
     gate = torch.sigmoid(normal()) if rate is None else torch.full(shape, rate, dtype=torch.float64)
     case = {
@@ -116,5 +127,32 @@ def test_correlated_keys_public_entry_long_sequence_matches_oracle(dtype):
     out = wkv7(*tokens(case), state_pool=pool, cu_seqlens=case["cu_seqlens"],
                state_indices=case["state_indices"])
     torch.cuda.synchronize()
+    assert_output_close(out, y_ref)
+    assert_state_close(pool, pool_ref)
+
+
+STRESS = [
+    # (rho, rate, u_range, k_scale, mixed_decay)
+    (0.3, 1.0, (-6.0, -0.5), 1.0, True),
+    (None, None, (-6.0, -0.5), 1.0, True),
+    (None, None, (-9.0, -4.0), 5.0, False),
+    (0.3, 1.0, (-0.6, -0.5), 1.0, False),
+]
+
+
+@pytest.mark.parametrize("kernel", [CHUNKED, CHUNKED_WAVE])
+@pytest.mark.parametrize("rho,rate,u_range,k_scale,mixed", STRESS)
+def test_decay_spread_and_large_keys_match_oracle(kernel, rho, rate, u_range, k_scale, mixed):
+    """Half the channels at the retention floor and half near 1 (1/gamma spans
+    ~10^4 within a chunk), keys of five times the usual scale with long
+    memory, and the retention floor with correlated keys."""
+    C = require_gpu()
+    print(f"case stress kernel={kernel} rho={rho} rate={rate} u={u_range} k={k_scale} "
+          f"mixed={mixed}", flush=True)
+    case = _correlated_case((1200, 33, 400), heads=4, rho=rho, rate=rate, u_range=u_range,
+                            dtype=torch.bfloat16, seed=71, k_scale=k_scale, mixed_decay=mixed)
+    y_ref, pool_ref = oracle_expect(case)
+    pool = case["state_pool"].clone()
+    out = _forced(C, kernel, case, pool)
     assert_output_close(out, y_ref)
     assert_state_close(pool, pool_ref)
