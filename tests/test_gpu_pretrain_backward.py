@@ -141,6 +141,17 @@ def test_backward_correlated_keys(rho, rate):
     _check(_run(vals, dy, 64), _expected(vals, dy, 64))
 
 
+def test_backward_decay_spread_across_channels():
+    """Half of each head's channels at the retention floor and half near 1:
+    the key pass's rho = gamma_15 / gamma spans ~10^4 inside a chunk."""
+    require_gpu()
+    print("case pretrain bwd decay spread", flush=True)
+    heads, D = 4, 64
+    shift = torch.where(torch.arange(D) < D // 2, 6.0, -9.0).repeat(heads)
+    vals, dy = _case(2, 512, heads, D, seed=23, rwkv=True, logit_scale=0.5, logit_shift=shift)
+    _check(_run(vals, dy, 64), _expected(vals, dy, 64))
+
+
 def test_backward_is_deterministic():
     require_gpu()
     vals, dy = _case(2, 32, 2, 64, seed=3, rwkv=True, logit_scale=1.0)
