@@ -87,23 +87,43 @@ class Runner:
     def reset(self):
         self.state.copy_(self.state0)
 
-    def time_steps(self, steps: int, warmup: int) -> float:
+    def time_steps(self, steps: int, warmup: int, settle_s: float = 0.0) -> float:
+        """ms per public step over exactly `steps` timed steps, after `warmup`
+        untimed steps and, with settle_s > 0, further untimed steps until
+        settle_s seconds have passed since the warm-up began (the shader clock
+        ramps up over the first tens of milliseconds of sustained work).  Each
+        timed step is also bracketed by its own event pair (self.step_stats)."""
         torch = self.torch
+        t_begin = time.perf_counter()
         for _ in range(warmup):
             self.step()
         torch.cuda.synchronize()
+        extra = 0
+        while time.perf_counter() - t_begin < settle_s:
+            for _ in range(16):
+                self.step()
+            extra += 16
+            torch.cuda.synchronize()
+        self.settle = {"seconds": round(time.perf_counter() - t_begin, 3),
+                       "extra_steps": extra, "target_s": settle_s}
         self.reset()
         torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
         t0 = time.perf_counter()
-        start.record()
-        for _ in range(steps):
+        ev[0].record()
+        for j in range(steps):
             self.step()
-        end.record()
+            ev[j + 1].record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        return max(start.elapsed_time(end), wall * 1e3) / steps
+        per = sorted(ev[j].elapsed_time(ev[j + 1]) for j in range(steps))
+        event_ms = ev[0].elapsed_time(ev[steps])
+        self.step_stats = {"event_ms_min": round(per[0], 5),
+                           "event_ms_median": round(per[len(per) // 2], 5),
+                           "event_ms_max": round(per[-1], 5),
+                           "event_ms_mean": round(event_ms / steps, 5),
+                           "wall_ms_mean": round(wall * 1e3 / steps, 5)}
+        return max(event_ms, wall * 1e3) / steps
 
     def time_kernel(self, launches: int) -> float:
         """Average device duration of one launch (ms), direct C-ABI launches."""
@@ -124,23 +144,11 @@ class Runner:
         return start.elapsed_time(end) / launches
 
     def kernel_name(self) -> str:
-        """The kernel the library's policy picks (csrc/api.hip run_family,
-        decode_first / wave_per_unit)."""
-        ms = self.ticket._max_seqlen()
-        n = self.w.state_indices.numel()
-        units = n * self.w.num_heads
-        if ms <= 4 or (units >= 16384 and ms <= 6):
-            return "decode64_kernel<IoBF16,StF32>"
-        if units <= 256:
-            wave = False
-        elif units <= 512:
-            wave = ms <= 24
-        else:
-            wave = ms <= 512 or ms * n <= 2 * self.w.total_tokens
-        if wave:
-            order = n <= 256 and ms >= 256 and 4 * ms * n > 5 * self.w.total_tokens
-            return f"chunk64w_kernel<IoBF16,{'true' if order else 'false'}>"
-        return "chunk64_kernel<IoBF16,false>"
+        """The kernel the library's policy picks for this launch, as the
+        library reports it (fr2_wkv7_recurrent_fp32_dispatch)."""
+        w = self.w
+        return self.C.dispatch_kernel_name(w.state_indices.numel(), w.num_heads, 64,
+                                           w.total_tokens, self.ticket._max_seqlen())
 
 
 def cpu_baseline(w, threads: int, sample_tokens: int | None, min_seconds: float = 12.0):
@@ -1019,6 +1027,26 @@ def time_statetune_training(torch, w, steps: int, chunk_len: int = 1024):
     }
 
 
+def sclk_levels() -> list | None:
+    """Current shader-clock level (MHz) of every card whose sysfs
+    pp_dpm_sclk is readable (the line marked '*'), or None."""
+    import glob
+    import re
+
+    out = []
+    for path in sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk")):
+        try:
+            text = Path(path).read_text()
+        except OSError:
+            continue
+        for line in text.splitlines():
+            if line.rstrip().endswith("*"):
+                m = re.search(r"(\d+)\s*Mhz", line, re.I)
+                if m:
+                    out.append(int(m.group(1)))
+    return out or None
+
+
 def device_info(torch) -> dict:
     """Name and CU count of device 0, plus rocm-smi's current clock levels
     when the tool is present (the effective shader clock under the prefill
@@ -1069,11 +1097,106 @@ def mfma_obj(w, kernel_ms: float):
     return out
 
 
+def _frac(obj):
+    return None if not obj else obj.get("frac")
+
+
+def compact_line(result: dict) -> dict:
+    """The printed JSON line: the headline fields, the headline kernel's
+    roofline, timing, MFMA use and CPU baseline, then one short entry per
+    further leg (ms, roofline fraction, kernel) so that the whole line stays
+    a few KB.  The full tables go to --detail."""
+    keep = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+            "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config",
+            "roofline", "kernel_ms", "algorithmic_bytes", "timing")
+    line = {k: result[k] for k in keep if k in result}
+    if line.get("roofline") and line["roofline"].get("traffic_source"):
+        line["roofline"] = dict(line["roofline"])
+        line["roofline"]["traffic_source"] = "profiles/hbm_traffic.json (rocprofv3 PMC)"
+    m = result.get("mfma")
+    if m:
+        line["mfma"] = {k: m[k] for k in ("issued_tflops", "peak_tflops", "frac",
+                                          "measured_util") if k in m}
+    cb = result.get("cpu_baseline")
+    if cb:
+        line["cpu_baseline"] = {k: cb[k] for k in ("value", "unit", "cores", "kind", "sample")}
+    legs = {}
+    d = result.get("decode")
+    if d:
+        legs["decode_cfg2"] = {"ms": d["kernel_ms"], "public_ms": d["ms_per_step"],
+                               "frac": _frac(d["roofline"]), "kernel": d["kernel"]}
+    d = result.get("decode_fp16_state")
+    if d:
+        legs["decode_fp16_state"] = {"ms": d["kernel_ms"], "frac": _frac(d["roofline"])}
+    d = result.get("fp16_state_prefill")
+    if d:
+        legs["fp16_state_prefill_cfg1"] = {"ms": d["kernel_ms"], "frac": _frac(d["roofline"]),
+                                           "kernel": d["kernel"]}
+    d = result.get("decode_graph")
+    if d:
+        legs["decode_graph"] = [{"workload": g["workload"], "graph_ms": g["graph_ms_per_step"],
+                                 "eager_ms": g["eager_ms_per_step"]} for g in d]
+    d = result.get("chunk_bf16_state")
+    if d:
+        legs["chunk_bf16_state_cfg1"] = {"ms": d.get("ms_per_step"),
+                                         "frac": _frac(d.get("roofline"))}
+    d = result.get("varlen_prefill")
+    if d:
+        legs["varlen_cfg3"] = {"ms": d["kernel_ms"], "public_ms": d["ms_per_step"],
+                               "frac": _frac(d["roofline"]), "kernel": d["kernel"]}
+    d = result.get("mid_length")
+    if d:
+        legs["mid_length_2048x100"] = {"ms": d["kernel_ms"], "frac": _frac(d["roofline"]),
+                                       "kernel": d["kernel"]}
+    d = result.get("long_context")
+    if d:
+        r = d["roofline"]
+        legs["long_context_cfg4"] = {"ms": d["ms_per_step"], "frac": _frac(r),
+                                     "traffic_over_algorithmic":
+                                         round(r["traffic"] / d["algorithmic_bytes"], 3)
+                                         if r.get("traffic") else None,
+                                     "unsplit_ms": d["unsplit"]["ms_per_step"],
+                                     "pieces": d["pieces"]}
+    d = result.get("other_paths")
+    if d:
+        legs["other_paths_cfg1"] = {k: (v.get("kernel_ms") if isinstance(v, dict) else v)
+                                    for k, v in d.items()
+                                    if isinstance(v, dict) and "kernel_ms" in v}
+    for key in ("pretrain_training", "statetune_training"):
+        d = result.get(key)
+        if d:
+            legs[key] = {k: v for k, v in d.items()
+                         if k.endswith("_ms") or k in ("forward_ms", "backward_ms")}
+            for sub in ("chunked", "token_serial"):
+                if isinstance(d.get(sub), dict):
+                    legs[key][sub] = {k: v for k, v in d[sub].items() if k.endswith("_ms")}
+            if isinstance(d.get("backward_roofline"), dict):
+                legs[key]["backward_frac"] = d["backward_roofline"].get("frac")
+    d = result.get("kk_gate_fused")
+    if d:
+        legs["kk_gate_fused_cfg1_fp16"] = {"two_stage_ms": d["two_stage"]["ms_per_step"],
+                                           "fused_ms": d["fused"]["ms_per_step"],
+                                           "readout_fused_ms":
+                                               d["with_readout"]["fused"]["ms_per_step"]}
+    d = result.get("layer_stages")
+    if d:
+        legs["layer_stages"] = {k: _frac(v["roofline"]) for k, v in d["kernels"].items()}
+    line["device"] = {k: v for k, v in result.get("device", {}).items() if k != "rocm_smi_clocks"}
+    line["legs"] = legs
+    return line
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--settle", type=float, default=1.0,
+                    help="after the warm-up steps, keep issuing untimed steps until this many "
+                         "seconds have passed (clock ramp); reported in the line")
+    ap.add_argument("--detail", default=None,
+                    help="write the full result (every leg's tables) to this JSON file; the "
+                         "printed line carries a compact summary")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode (config 2) leg")
     ap.add_argument("--cpu-sample-tokens", type=int, default=4096,
@@ -1117,8 +1240,10 @@ def main() -> int:
     if args.only in (None, "prefill"):
         w1 = workloads.config(args.config, "cuda")
         pre = Runner(w1, torch, flashrwkv2_amd)
-        ms = pre.time_steps(args.steps, args.warmup)
+        sclk_before = sclk_levels()
+        ms = pre.time_steps(args.steps, args.warmup, args.settle)
         kms = pre.time_kernel(args.steps)
+        sclk_after = sclk_levels()
         bytes1 = algorithmic_bytes(w1.total_tokens, w1.num_heads, w1.state_indices.numel())
         result.update({
             "metric": METRIC,
@@ -1152,11 +1277,16 @@ def main() -> int:
             },
             "kernel_ms": round(kms, 5),
             "algorithmic_bytes": bytes1,
+            "timing": {"settle": pre.settle, "steps": pre.step_stats,
+                       "public_over_kernel": round(ms / kms, 4),
+                       "sclk_mhz_before_after": [sclk_before, sclk_after],
+                       "public_path": "_C.tmix_wkv7_recurrent_fp32_from_decay_logits with a "
+                                      "reused ticket (Python checks, METH_FASTCALL launch)"},
         })
     if args.only in (None, "decode") and not args.no_decode:
         w2 = workloads.config(2, "cuda")
         dec = Runner(w2, torch, flashrwkv2_amd)
-        dms = dec.time_steps(max(args.steps, 50), args.warmup)
+        dms = dec.time_steps(max(args.steps, 50), args.warmup, min(args.settle, 0.3))
         dkms = dec.time_kernel(max(args.steps, 200))
         bytes2 = algorithmic_bytes(w2.total_tokens, w2.num_heads, w2.state_indices.numel())
         result["decode"] = {
@@ -1225,7 +1355,9 @@ def main() -> int:
             "cpu": cpu_info(),
         }
         result["cpu_baseline_plan"] = cpu_baseline_plan(threads)
-    print(json.dumps(result), flush=True)
+    if args.detail:
+        Path(args.detail).write_text(json.dumps(result, indent=1))
+    print(json.dumps(compact_line(result)), flush=True)
     return 0
 
 

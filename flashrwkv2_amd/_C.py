@@ -28,6 +28,7 @@ from typing import Sequence
 import torch
 
 from . import _native as N
+from ._align import aligned_io
 
 INT32_MAX = 2**31 - 1
 _TOKEN_DTYPES = {torch.float16: N.FR2_DTYPE_FLOAT16, torch.bfloat16: N.FR2_DTYPE_BFLOAT16}
@@ -122,6 +123,13 @@ def _set_handoff_spin_limit(polls: int) -> None:
     launches in this process (negative restores the default)."""
     N.check(N.load().fr2_debug_set_handoff_spin_limit(int(polls)),
             "fr2_debug_set_handoff_spin_limit")
+
+
+def _set_handoff_stall(on: bool) -> None:
+    """Test hook: while on, the chunked kernel's key waves never publish their
+    operators, so every block stalls at its first operator wait and fails
+    closed after the spin limit."""
+    N.check(N.load().fr2_debug_set_handoff_stall(int(bool(on))), "fr2_debug_set_handoff_stall")
 
 
 # ---------------------------------------------------------------------------
@@ -538,12 +546,13 @@ def tmix_wkv7_recurrent_fp32_from_kk_gate(query_start_loc, state_indices, state,
     """The recurrence with wkv_prepare's kk / a-gate stage in its load stage:
     k is the projected key, a12 the a-gate logits, k_k / a0 / k_a the
     per-channel parameters ([H*D] or [H,D], token dtype); the gated key is
-    written to new_k.  Where the library's policy picks no chunked kernel
-    (head size other than 64, or the longest sequence at most 4 tokens, 6 with
-    many units: the decode kernel), and for fp16 batches that the library's
-    plan splits by sequence (few long sequences: the split outruns one block
-    per unit), the gate runs as its own kernel and the recurrence through the
-    public path."""
+    written to new_k.  For fp16 tokens where the library's policy picks no
+    chunked kernel (head size other than 64, or the longest sequence at most 4
+    tokens, 6 with many units: the decode kernel), and for fp16 batches that
+    the library's plan splits by sequence (few long sequences: the split
+    outruns one block per unit), the gate runs as its own kernel and the
+    recurrence through the public path.  bf16 batches at head size 64 always
+    run fused (short batches on the wavefront chunked kernel)."""
     n, h, d = check_recurrent_layout(query_start_loc, state_indices, state, r, decay_logits, k,
                                      v, a12, new_k, output, scale)
     for t, name in ((k_k, "k_k"), (a0, "a0"), (k_a, "k_a")):
@@ -655,6 +664,36 @@ def _library_split_plan(num_sequences: int, num_heads: int, head_size: int,
                                                    ctypes.byref(wb)),
             "fr2_wkv7_recurrent_fp32_split_plan")
     return pc.value, pl.value, ll.value, wb.value
+
+
+_FAMILY_KERNELS = {
+    N.KERNEL_SERIAL: "serial64w_kernel<{io},StF32>",
+    N.KERNEL_DECODE: "decode64_kernel<{io},StF32>",
+    N.KERNEL_CHUNKED: "chunk64_kernel<{io},false>",
+    N.KERNEL_CHUNKED_WAVE: "chunk64w_kernel<{io},false>",
+    5: "chunk64w_kernel<{io},true>",
+}
+
+
+def dispatch_kernel_name(num_sequences: int, num_heads: int, head_size: int,
+                         total_tokens: int, max_seqlen: int, dtype=torch.bfloat16) -> str:
+    """Name of the kernel the public fp32-state call runs for this shape: the
+    sequence split when the library's plan cuts the sequences, otherwise the
+    family fr2_wkv7_recurrent_fp32_dispatch reports (the library's own
+    policy, not a restatement of it)."""
+    if split_plan(num_sequences, num_heads, head_size, max_seqlen)[0] > 1:
+        return "split:lead+summary+combine+pieces"
+    lib = N.load()
+    fam = ctypes.c_int32()
+    N.check(lib.fr2_wkv7_recurrent_fp32_dispatch(int(num_sequences), int(num_heads),
+                                                 int(head_size), int(total_tokens),
+                                                 int(max_seqlen), ctypes.byref(fam)),
+            "fr2_wkv7_recurrent_fp32_dispatch")
+    io = "IoBF16" if dtype == torch.bfloat16 else "IoF16"
+    name = _FAMILY_KERNELS[fam.value].format(io=io)
+    if fam.value == N.KERNEL_SERIAL and head_size != 64:
+        name = f"serial_kernel<{head_size},{io},StF32>"
+    return name
 
 
 def split_plan(num_sequences: int, num_heads: int, head_size: int, max_seqlen: int,
@@ -1474,3 +1513,13 @@ def exported_names() -> Sequence[str]:
         "tmix_wkv_prepare_forward_varlen",
         "tmix_readout_forward_varlen",
     )
+
+
+# ---------------------------------------------------------------------------
+# Misaligned views: every entry below runs them on aligned copies
+# ---------------------------------------------------------------------------
+for _name in (*exported_names(), "tmix_wkv7_recurrent_fp32_kernel_forced"):
+    if _name.startswith("prepare_"):
+        continue
+    globals()[_name] = aligned_io(globals()[_name])
+del _name

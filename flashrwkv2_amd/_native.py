@@ -40,6 +40,7 @@ SIGNATURES: dict[str, tuple] = {
     "fr2_last_error": (c_char_p, []),
     "fr2_handoff_fault_count": (c_int32, [_i32p, c_int32, c_void_p]),
     "fr2_debug_set_handoff_spin_limit": (c_int32, [c_int32]),
+    "fr2_debug_set_handoff_stall": (c_int32, [c_int32]),
     "fr2_wkv7_prepare_metadata": (
         c_int32,
         [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p,
@@ -56,6 +57,9 @@ SIGNATURES: dict[str, tuple] = {
         [c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32,
          c_int64, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_void_p],
+    ),
+    "fr2_wkv7_recurrent_fp32_dispatch": (
+        c_int32, [c_int32, c_int32, c_int32, c_int64, c_int32, _i32p],
     ),
     "fr2_wkv7_recurrent_fp32_split_plan": (
         c_int32, [c_int32, c_int32, c_int32, c_int32, _i32p, _i32p, _i32p, POINTER(c_int64)],
@@ -257,7 +261,7 @@ def check(status: int, what: str) -> None:
         return
     lib = load()
     text = lib.fr2_status_string(status).decode()
-    detail = lib.fr2_last_error().decode() if status == FR2_ERR_LAUNCH else ""
+    detail = lib.fr2_last_error().decode()
     raise RuntimeError(f"{what} failed: {text}{(': ' + detail) if detail else ''}")
 
 

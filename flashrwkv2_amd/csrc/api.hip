@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <initializer_list>
 
 namespace {
 
@@ -51,14 +52,40 @@ bool workgroup_chunked(int64_t units, int max_seqlen, int64_t total_tokens, int6
 
 enum Family { kAuto = -1, kSerial = 0, kDecode = 1, kChunked = 2, kChunkedWave = 4 };
 
+// The family the public fp32-state policy picks for a plain launch (no sa /
+// boundary outputs, fp32 state); the one source of the choice that
+// run_family applies and fr2_wkv7_recurrent_fp32_dispatch reports.
+int plain_family(int D, int64_t units, int max_seqlen, int64_t total_tokens, int64_t nseg) {
+  if (D != 64 || max_seqlen <= 0) return kSerial;
+  if (decode_first(units, max_seqlen)) return kDecode;
+  return wave_per_unit(units, max_seqlen, total_tokens, nseg) ? kChunkedWave : kChunked;
+}
+
 // Token tensors are read and written as 16-byte vectors: every token
 // pointer must be present and 16-byte aligned (a contiguous view with an odd
 // storage offset is rejected instead of faulting on a misaligned access).
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool tokens_ok(const void* r, const void* l, const void* k, const void* v,
                const void* a, const void* b, const void* y) {
-  return r && l && k && v && a && b && y && aligned16(r) && aligned16(l) && aligned16(k) &&
-         aligned16(v) && aligned16(a) && aligned16(b) && aligned16(y);
+  if (!(r && l && k && v && a && b && y)) return false;
+  if (aligned16(r) && aligned16(l) && aligned16(k) && aligned16(v) && aligned16(a) &&
+      aligned16(b) && aligned16(y))
+    return true;
+  fr2::set_last_error("token tensors must be 16-byte aligned (a view with an odd storage "
+                      "offset needs an aligned copy)");
+  return false;
+}
+// Per-channel parameters ([H, D] vectors: decay bias, kk / a-gate and
+// readout parameters) are read as 16-byte vectors too; null means absent.
+bool params_aligned(std::initializer_list<const void*> ptrs) {
+  for (const void* q : ptrs) {
+    if (q != nullptr && !aligned16(q)) {
+      fr2::set_last_error("per-channel parameter tensors must be 16-byte aligned (a view "
+                          "with an odd storage offset needs an aligned copy)");
+      return false;
+    }
+  }
+  return true;
 }
 
 int run_family(int family, int D, int dtype, bool bf16_state, const SegArgs& p,
@@ -67,12 +94,13 @@ int run_family(int family, int D, int dtype, bool bf16_state, const SegArgs& p,
     const bool plain = p.sa_out == nullptr && p.boundary == nullptr && !bf16_state;
     const int64_t units = static_cast<int64_t>(nseg) * p.num_heads;
     family = kSerial;
-    if (D == 64 && plain && max_seqlen > 0) {
-      if (decode_first(units, max_seqlen)) {
+    if (plain) {
+      const int64_t total = p.out_elems / (static_cast<int64_t>(p.num_heads) * D);
+      const int f = plain_family(D, units, max_seqlen, total, nseg);
+      if (f == kDecode) {
         family = kDecode;
-      } else {
-        const int64_t total = p.out_elems / (static_cast<int64_t>(p.num_heads) * D);
-        const int rc = wave_per_unit(units, max_seqlen, total, nseg)
+      } else if (f != kSerial) {
+        const int rc = f == kChunkedWave
                            ? fr2::launch_chunked_wave(dtype, p, nseg, max_seqlen, s)
                            : fr2::launch_chunked(dtype, p, nseg, max_seqlen, s);
         if (rc != FR2_ERR_UNSUPPORTED) return rc;
@@ -129,10 +157,26 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward(
     float* state, const void* r, const void* decay_logits,
     const void* decay_bias, const void* k, const void* v, const void* a,
     const void* b, void* output, float scale, void* stream) {
+  if (!params_aligned({decay_bias})) return FR2_ERR_INVALID_ARGUMENT;
   return recurrent_fp32(kAuto, query_start_loc, state_indices, status,
                         num_sequences, num_heads, head_size, total_tokens,
                         max_seqlen, dtype, state, r, decay_logits, decay_bias, k,
                         v, a, b, output, scale, stream);
+}
+
+extern "C" int fr2_wkv7_recurrent_fp32_dispatch(int32_t num_sequences, int32_t num_heads,
+                                                int32_t head_size, int64_t total_tokens,
+                                                int32_t max_seqlen, int32_t* kernel) {
+  if (kernel == nullptr || num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 ||
+      total_tokens <= 0)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return FR2_ERR_UNSUPPORTED;
+  const int64_t units = static_cast<int64_t>(num_sequences) * num_heads;
+  int f = plain_family(head_size, units, max_seqlen, total_tokens, num_sequences);
+  if (f == kChunkedWave && fr2::wave_longest_first(num_sequences, max_seqlen, total_tokens))
+    f = 5;
+  *kernel = f;
+  return FR2_OK;
 }
 
 extern "C" int fr2_wkv7_recurrent_fp32_forward_kernel(
@@ -143,6 +187,7 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kernel(
     const void* r, const void* decay_logits, const void* decay_bias,
     const void* k, const void* v, const void* a, const void* b, void* output,
     float scale, void* stream) {
+  if (!params_aligned({decay_bias})) return FR2_ERR_INVALID_ARGUMENT;
   if (kernel != kSerial && kernel != kDecode && kernel != kChunked && kernel != kChunkedWave)
     return FR2_ERR_INVALID_ARGUMENT;
   return recurrent_fp32(kernel, query_start_loc, state_indices, status,
@@ -214,6 +259,7 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_split(
     const void* decay_bias, const void* k, const void* v, const void* a, const void* b,
     void* output, float scale, int32_t pieces, int32_t piece_len, int32_t lead_len,
     void* workspace, int64_t workspace_bytes, void* stream, void* aux_stream) {
+  if (!params_aligned({decay_bias})) return FR2_ERR_INVALID_ARGUMENT;
   (void)max_seqlen;
   if (!query_start_loc || !state_indices || !status || !state || !workspace ||
       !tokens_ok(r, decay_logits, k, v, a, b, output))
@@ -282,7 +328,12 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_split_noalloc(
     const void* decay_bias, const void* k, const void* v, const void* a, const void* b,
     void* output, float scale, int32_t pieces, int32_t piece_len, int32_t lead_len,
     void* stream) {
-  if (num_sequences <= 0 || num_heads <= 0 || pieces < 2) return FR2_ERR_INVALID_ARGUMENT;
+  if (!params_aligned({decay_bias})) return FR2_ERR_INVALID_ARGUMENT;
+  // the bounds the split itself enforces, checked before the workspace size
+  // is formed from them (so that the product cannot overflow)
+  if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 || pieces < 2 ||
+      pieces > 65535 || static_cast<int64_t>(num_sequences) * pieces > 65535)
+    return FR2_ERR_INVALID_ARGUMENT;
   const int64_t need = fr2::split_workspace_floats(num_sequences, num_heads, pieces);
   if (need > kNoAllocScratchFloats) {
     fr2::set_last_error(
@@ -338,6 +389,7 @@ extern "C" int fr2_wkv7_recurrent_fp16_forward(
     void* state_f16, const void* r, const void* decay_logits, const void* decay_bias,
     const void* k, const void* v, const void* a, const void* b, void* output, float scale,
     void* stream) {
+  if (!params_aligned({decay_bias})) return FR2_ERR_INVALID_ARGUMENT;
   return recurrent_fp16(true, query_start_loc, state_indices, status, elapsed_state,
                         num_sequences, num_heads, head_size, total_tokens, max_seqlen, state_f16,
                         r, decay_logits, decay_bias, k, v, a, b, output, scale, stream);
@@ -350,6 +402,7 @@ extern "C" int fr2_wkv7_recurrent_fp16_update(
     void* state_f16, const void* r, const void* decay_logits, const void* decay_bias,
     const void* k, const void* v, const void* a, const void* b, void* output, float scale,
     void* stream) {
+  if (!params_aligned({decay_bias})) return FR2_ERR_INVALID_ARGUMENT;
   return recurrent_fp16(false, query_start_loc, state_indices, status,
                         const_cast<int32_t*>(elapsed_state), num_sequences, num_heads, head_size,
                         total_tokens, max_seqlen, state_f16, r, decay_logits, decay_bias, k, v, a,
@@ -441,6 +494,7 @@ extern "C" int fr2_wkv7_chunk_bf16_forward(
     uint16_t* state_bf16, const void* r, const void* decay_logits,
     const void* decay_bias, const void* k, const void* v, const void* a,
     const void* b, void* output, float scale, void* stream) {
+  if (!params_aligned({decay_bias})) return FR2_ERR_INVALID_ARGUMENT;
   if (!query_start_loc || !state_indices || !status || !state_bf16 ||
       !tokens_ok(r, decay_logits, k, v, a, b, output))
     return FR2_ERR_INVALID_ARGUMENT;
@@ -490,6 +544,7 @@ extern "C" int fr2_wkv7_chunk_bf16_forward_split(
     const void* b, void* output, float scale, int32_t pieces, int32_t piece_len,
     int32_t lead_len, void* workspace, int64_t workspace_bytes, void* stream,
     void* aux_stream) {
+  if (!params_aligned({decay_bias})) return FR2_ERR_INVALID_ARGUMENT;
   (void)max_seqlen;
   if (!query_start_loc || !state_indices || !status || !state_bf16 || !workspace ||
       !tokens_ok(r, decay_logits, k, v, a, b, output))
@@ -527,6 +582,7 @@ extern "C" int fr2_wkv7_rl_infctx_forward(
     float* state, const void* r, const void* decay_logits,
     const void* decay_bias, const void* k, const void* v, const void* a,
     const void* b, void* output, float scale, void* stream) {
+  if (!params_aligned({decay_bias})) return FR2_ERR_INVALID_ARGUMENT;
   if (!sequence_chunk_offsets || !chunk_token_starts || !chunk_token_ends ||
       !state || !tokens_ok(r, decay_logits, k, v, a, b, output))
     return FR2_ERR_INVALID_ARGUMENT;
@@ -559,6 +615,7 @@ extern "C" int fr2_wkv7_rl_infctx_replay(
     const void* decay_logits, const void* decay_bias, const void* k,
     const void* v, const void* a, const void* b, void* output,
     float* state_dot_a, float scale, void* stream) {
+  if (!params_aligned({decay_bias})) return FR2_ERR_INVALID_ARGUMENT;
   if (!chunk_token_starts || !chunk_token_ends || !boundary || !state_dot_a ||
       !tokens_ok(r, decay_logits, k, v, a, b, output))
     return FR2_ERR_INVALID_ARGUMENT;
@@ -762,13 +819,19 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate(
     int32_t max_seqlen, int32_t dtype, float* state, const void* r, const void* decay_logits,
     const void* decay_bias, const void* k, const void* v, const void* a12, const void* k_k,
     const void* a0, const void* k_a, void* new_k, void* output, float scale, void* stream) {
+  if (!params_aligned({decay_bias, k_k, a0, k_a})) return FR2_ERR_INVALID_ARGUMENT;
   if (!query_start_loc || !state_indices || !status || !state || !k_k || !a0 || !k_a ||
       !tokens_ok(r, decay_logits, k, v, a12, new_k, output))
     return FR2_ERR_INVALID_ARGUMENT;
   if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 || total_tokens <= 0)
     return FR2_ERR_INVALID_ARGUMENT;
   const int64_t units = static_cast<int64_t>(num_sequences) * num_heads;
-  if (head_size != 64 || max_seqlen <= 0 || decode_first(units, max_seqlen))
+  // where the plain policy picks the decode kernel (or the longest sequence
+  // is unknown), fp16 batches take the two-kernel form (the separate gate
+  // kernel is fp16); bf16 batches run on the wavefront chunked kernel, which
+  // handles sequences of any length
+  const bool short_batch = max_seqlen <= 0 || decode_first(units, max_seqlen);
+  if (head_size != 64 || (short_batch && dtype != FR2_DTYPE_BFLOAT16))
     return FR2_ERR_UNSUPPORTED;
   SegArgs p;
   p.bounds = query_start_loc;
@@ -784,7 +847,7 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate(
   p.y = output;
   p.scale = scale;
   // the chunked kernel the plain entry's policy picks, with the stage fused
-  return workgroup_chunked(units, max_seqlen, total_tokens, num_sequences)
+  return !short_batch && workgroup_chunked(units, max_seqlen, total_tokens, num_sequences)
              ? fr2::launch_chunked_kk(dtype, p, num_sequences, static_cast<hipStream_t>(stream))
              : fr2::launch_chunked_wave(dtype, p, num_sequences, max_seqlen,
                                         static_cast<hipStream_t>(stream));
@@ -798,6 +861,8 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate_readout(
     const void* a0, const void* k_a, const void* g, const void* r_k, const void* ln_weight,
     const void* ln_bias, void* new_k, void* readout, void* output, float scale,
     void* stream) {
+  if (!params_aligned({decay_bias, k_k, a0, k_a, r_k, ln_weight, ln_bias}))
+    return FR2_ERR_INVALID_ARGUMENT;
   if (!query_start_loc || !state_indices || !status || !state || !k_k || !a0 || !k_a ||
       !r_k || !ln_weight || !ln_bias || !tokens_ok(r, decay_logits, k, v, a12, new_k, readout) ||
       !aligned16(g) || !g || (output != nullptr && !aligned16(output)))
@@ -805,7 +870,12 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate_readout(
   if (num_sequences <= 0 || num_sequences > 65535 || num_heads <= 0 || total_tokens <= 0)
     return FR2_ERR_INVALID_ARGUMENT;
   const int64_t units = static_cast<int64_t>(num_sequences) * num_heads;
-  if (head_size != 64 || max_seqlen <= 0 || decode_first(units, max_seqlen))
+  // where the plain policy picks the decode kernel (or the longest sequence
+  // is unknown), fp16 batches take the two-kernel form (the separate gate
+  // kernel is fp16); bf16 batches run on the wavefront chunked kernel, which
+  // handles sequences of any length
+  const bool short_batch = max_seqlen <= 0 || decode_first(units, max_seqlen);
+  if (head_size != 64 || (short_batch && dtype != FR2_DTYPE_BFLOAT16))
     return FR2_ERR_UNSUPPORTED;
   SegArgs p;
   p.bounds = query_start_loc;
@@ -822,7 +892,7 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_kk_gate_readout(
   p.y = output;
   p.scale = scale;
   // the chunked kernel the plain entry's policy picks, with the stage fused
-  return workgroup_chunked(units, max_seqlen, total_tokens, num_sequences)
+  return !short_batch && workgroup_chunked(units, max_seqlen, total_tokens, num_sequences)
              ? fr2::launch_chunked_kk(dtype, p, num_sequences, static_cast<hipStream_t>(stream))
              : fr2::launch_chunked_wave(dtype, p, num_sequences, max_seqlen,
                                         static_cast<hipStream_t>(stream));
@@ -832,6 +902,8 @@ extern "C" int fr2_tmix_kk_a_gate_forward(int64_t tokens, int32_t num_heads, int
                                           const void* k, const void* k_k, const void* a0,
                                           const void* a12, const void* k_a, void* new_k,
                                           void* neg_kk, void* kka, void* stream) {
+  if (!params_aligned({k_k, a0, k_a, k, a12, new_k, neg_kk, kka}))
+    return FR2_ERR_INVALID_ARGUMENT;
   if (!k || !k_k || !a0 || !a12 || !k_a || !new_k || !neg_kk || !kka)
     return FR2_ERR_INVALID_ARGUMENT;
   if (tokens <= 0 || num_heads <= 0) return FR2_ERR_INVALID_ARGUMENT;
@@ -843,6 +915,8 @@ extern "C" int fr2_tmix_kk_a_gate_forward(int64_t tokens, int32_t num_heads, int
 extern "C" int fr2_tmix_lowrank_activate(int64_t n_tanh, const void* tanh_in, void* tanh_out,
                                          int64_t n_sigmoid, const void* sigmoid_in,
                                          void* sigmoid_out, void* stream) {
+  if (!params_aligned({tanh_in, tanh_out, sigmoid_in, sigmoid_out}))
+    return FR2_ERR_INVALID_ARGUMENT;
   if (n_tanh < 0 || n_sigmoid < 0) return FR2_ERR_INVALID_ARGUMENT;
   if ((n_tanh > 0 && (!tanh_in || !tanh_out)) || (n_sigmoid > 0 && (!sigmoid_in || !sigmoid_out)))
     return FR2_ERR_INVALID_ARGUMENT;
@@ -853,6 +927,7 @@ extern "C" int fr2_tmix_lowrank_activate(int64_t n_tanh, const void* tanh_in, vo
 extern "C" int fr2_tmix_vres_forward(int64_t tokens, int32_t channels, const void* value,
                                      const void* v_first, const void* v0, const void* v12,
                                      void* output, void* stream) {
+  if (!params_aligned({value, v_first, v0, v12, output})) return FR2_ERR_INVALID_ARGUMENT;
   if (!value || !v_first || !v0 || !v12 || !output) return FR2_ERR_INVALID_ARGUMENT;
   if (tokens <= 0 || channels <= 0 || channels % 8 != 0) return FR2_ERR_INVALID_ARGUMENT;
   return fr2::launch_vres(tokens, channels, value, v_first, v0, v12, output,
@@ -865,6 +940,8 @@ extern "C" int fr2_tmix_readout_prelinear_forward(int64_t tokens, int32_t num_he
                                                   const void* r_k, const void* ln_weight,
                                                   const void* ln_bias, const void* gate,
                                                   void* output, void* stream) {
+  if (!params_aligned({r_k, ln_weight, ln_bias, wkv_output, r, k, v, gate, output}))
+    return FR2_ERR_INVALID_ARGUMENT;
   if (!wkv_output || !r || !k || !v || !r_k || !ln_weight || !ln_bias || !gate || !output)
     return FR2_ERR_INVALID_ARGUMENT;
   if (tokens <= 0 || num_heads <= 0) return FR2_ERR_INVALID_ARGUMENT;
@@ -900,5 +977,14 @@ extern "C" int fr2_handoff_fault_count(int32_t* count, int32_t reset, void* stre
 // test check the fail-closed path while every kernel still exits normally.
 extern "C" int fr2_debug_set_handoff_spin_limit(int32_t polls) {
   fr2::set_handoff_spin_limit(polls);
+  return FR2_OK;
+}
+
+// Test hook: while on, the chunked kernel's key waves never publish their
+// operators to the state waves, so every block stalls at its first
+// operator wait and, after the spin limit, fails closed; every kernel still
+// runs to its end.
+extern "C" int fr2_debug_set_handoff_stall(int32_t on) {
+  fr2::set_handoff_stall(on != 0);
   return FR2_OK;
 }

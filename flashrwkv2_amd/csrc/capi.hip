@@ -29,4 +29,10 @@ extern "C" const char* fr2_status_string(int status) {
   }
 }
 
-extern "C" const char* fr2_last_error(void) { return g_last_error; }
+// read and clear: a text reported once cannot be mistaken later for the
+// cause of another failure
+extern "C" const char* fr2_last_error(void) {
+  const char* text = g_last_error;
+  g_last_error = "";
+  return text;
+}

@@ -593,10 +593,13 @@ __device__ __forceinline__ int peek(int* c) {
 __device__ __forceinline__ void raise_fault(int* fault) {
   __hip_atomic_store(fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
+// Once the block's fault flag is up its results are NaN whatever happens, so
+// every later wait returns at once instead of polling to its limit (a real
+// stall then costs one wait's limit, not one per hand-off of the sequence).
 __device__ __forceinline__ void wait_ge(int* c, int v, int limit, int* fault) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   int it = 0;
-  for (; it < limit && peek(c) < v; ++it) __builtin_amdgcn_s_sleep(1);
+  for (; it < limit && peek(c) < v && peek(fault) == 0; ++it) __builtin_amdgcn_s_sleep(1);
   if (it == limit && peek(c) < v) raise_fault(fault);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
@@ -610,7 +613,7 @@ __device__ __forceinline__ void wait_min_ge(int* c, int v, int limit, int* fault
     return m;
   };
   int it = 0;
-  for (; it < limit && low() < v; ++it) __builtin_amdgcn_s_sleep(1);
+  for (; it < limit && low() < v && peek(fault) == 0; ++it) __builtin_amdgcn_s_sleep(1);
   if (it == limit && low() < v) raise_fault(fault);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
@@ -1079,7 +1082,7 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
       signal(&sm.part1[kw], gn + 1);
       wait_ge(&sm.part1[partner], gn + 1, p.spin_limit, &sm.fault);
       if (active) key_part2<kVExact, kSum>(sm, sm.ops[par][cc], par, cc, hh, i, q, kr);
-      signal(&sm.ready[kw], gn + 1);
+      if (!p.handoff_stall) signal(&sm.ready[kw], gn + 1);
     };
     for (int gn = 0; gn < ngroups; gn += 2) {
       iter(std::integral_constant<int, 0>{}, rawA, rawB, gn);
@@ -1098,6 +1101,7 @@ namespace {
 // device holds its own copy; read through fr2_handoff_fault_count).
 __device__ int g_handoff_faults;
 std::atomic<int> g_spin_limit{1 << 20};
+std::atomic<bool> g_handoff_stall{false};
 std::atomic<int*> g_fault_ptr[64];
 }  // namespace
 
@@ -1114,6 +1118,8 @@ int* handoff_fault_word() {
   return ptr;
 }
 int handoff_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
+bool handoff_stall() { return g_handoff_stall.load(std::memory_order_relaxed); }
+void set_handoff_stall(bool on) { g_handoff_stall.store(on, std::memory_order_relaxed); }
 void set_handoff_spin_limit(int polls) {
   g_spin_limit.store(polls < 0 ? (1 << 20) : polls, std::memory_order_relaxed);
 }
@@ -1122,6 +1128,7 @@ int launch_chunked(int dtype, const SegArgs& args, int nseg, int max_seqlen, hip
   (void)max_seqlen;
   SegArgs p = args;
   p.spin_limit = handoff_spin_limit();
+  p.handoff_stall = handoff_stall();
   p.handoff_fault = handoff_fault_word();
   const bool train = p.sa_out != nullptr || p.boundary != nullptr || p.reverse;
   const dim3 grid(p.num_heads, nseg);
@@ -1153,6 +1160,7 @@ int launch_chunked_kk(int dtype, const SegArgs& args, int nseg, hipStream_t s) {
     return FR2_ERR_INVALID_ARGUMENT;
   SegArgs p = args;
   p.spin_limit = handoff_spin_limit();
+  p.handoff_stall = handoff_stall();
   p.handoff_fault = handoff_fault_word();
   const dim3 grid(p.num_heads, nseg);
   const bool ro = p.ro_out != nullptr;
@@ -1343,6 +1351,7 @@ int launch_chunked_split(int dtype, SegArgs p, int nseg, int pieces, int piece_l
     return FR2_ERR_INVALID_ARGUMENT;
   if (dtype != FR2_DTYPE_BFLOAT16 && dtype != FR2_DTYPE_FLOAT16) return FR2_ERR_UNSUPPORTED;
   p.spin_limit = handoff_spin_limit();
+  p.handoff_stall = handoff_stall();
   p.handoff_fault = handoff_fault_word();
   p.split_pieces = pieces;
   p.split_len = piece_len;

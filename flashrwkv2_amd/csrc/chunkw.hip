@@ -637,6 +637,11 @@ void launch_wave_io(const SegArgs& p, int n, bool order, hipStream_t s) {
 
 }  // namespace
 
+bool wave_longest_first(int nseg, int max_seqlen, int64_t total_tokens) {
+  return nseg > 1 && nseg <= kOrderMaxSeqs && max_seqlen >= kOrderMinSeqlen &&
+         4 * static_cast<int64_t>(max_seqlen) * nseg > 5 * total_tokens;
+}
+
 int launch_chunked_wave(int dtype, const SegArgs& p, int nseg, int max_seqlen, hipStream_t s) {
   if (p.boundary != nullptr || p.reverse || p.split_pieces > 0) return FR2_ERR_UNSUPPORTED;
   const bool kk = p.kk_scale != nullptr, ro = p.ro_out != nullptr;
@@ -656,8 +661,7 @@ int launch_chunked_wave(int dtype, const SegArgs& p, int nseg, int max_seqlen, h
   // costs each wave O(n^2 / 256) LDS steps)
   const int64_t total = p.out_elems / (static_cast<int64_t>(p.num_heads) * D);
   const bool order = p.uniform_len <= 0 && p.chunk_offsets == nullptr && p.ends == nullptr &&
-                     nseg > 1 && nseg <= kOrderMaxSeqs && max_seqlen >= kOrderMinSeqlen &&
-                     4 * static_cast<int64_t>(max_seqlen) * nseg > 5 * total;
+                     wave_longest_first(nseg, max_seqlen, total);
   const int n = static_cast<int>(units);
   if (dtype == FR2_DTYPE_BFLOAT16)
     launch_wave_io<IoBF16>(p, n, order, s);

@@ -128,6 +128,10 @@ py::object recurrent_fp32(const TicketFacts& f, const at::Tensor& qsl, const at:
   for (const at::Tensor* t : {&w, &k, &v, &a, &b})
     if (t->scalar_type() != r.scalar_type() || t->sizes() != r.sizes() || !cuda_contig_on(*t, dev))
       return py::none();
+  // misaligned views (an odd storage offset) take the Python path, which
+  // runs them on aligned copies
+  for (const at::Tensor* t : {&r, &w, &k, &v, &a, &b})
+    if (reinterpret_cast<uintptr_t>(t->data_ptr()) & 15u) return py::none();
   if (!std::isfinite(scale)) return py::none();
   if (!f.matches(qsl, slots, r.size(0), state.size(0), max_seqlen, stream)) return py::none();
   if (!current_device_is(dev)) return py::none();

@@ -84,6 +84,9 @@ struct SegArgs {
   // then fails closed: NaN outputs, state untouched)
   int spin_limit = 1 << 20;
   int* handoff_fault = nullptr;
+  // test hook: the key waves never publish their operators, so the state
+  // waves' waits give up (forces a real stall from the host)
+  bool handoff_stall = false;
   // Fused kk / a-gate producer stage (chunked kernel only): `k` holds the
   // projected key, `a` the low-rank a-gate logits a12, `b` is unused; per
   // channel k_k, a0, k_a ([H, D]); the gated key is written to new_k.
@@ -155,6 +158,9 @@ int launch_chunked(int dtype, const SegArgs& p, int nseg, int max_seqlen,
 // contract: no sa / boundary outputs, fp32 state), for launches with many
 // units.
 int launch_chunked_wave(int dtype, const SegArgs& p, int nseg, int max_seqlen, hipStream_t s);
+// Whether that kernel runs its units in longest-first order of their
+// sequences (packed plain batches: few sequences, one long one).
+bool wave_longest_first(int nseg, int max_seqlen, int64_t total_tokens);
 // Sequence-split chunked prefill (D = 64, fp32 state, plain contract):
 // `pieces` pieces per sequence, of `piece_len` tokens except piece 0, which
 // has lead_len tokens when lead_len > 0 (the pipelined split: piece 0 runs on
@@ -166,6 +172,8 @@ int64_t split_workspace_floats(int nseg, int H, int pieces);
 int* handoff_fault_word();
 int handoff_spin_limit();
 void set_handoff_spin_limit(int polls);   // negative: the default
+bool handoff_stall();
+void set_handoff_stall(bool on);
 int launch_chunked_split(int dtype, SegArgs p, int nseg, int pieces, int piece_len,
                          int lead_len, float* workspace, hipStream_t s, hipStream_t aux);
 

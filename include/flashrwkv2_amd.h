@@ -62,7 +62,11 @@ int fr2_abi_version(void);
 /* Static text for an fr2_status_t value. */
 const char* fr2_status_string(int status);
 
-/* HIP error text of the last failing launch in this thread ("" if none). */
+/*
+ * Text of the last failure in this thread: the HIP error of a failing
+ * launch, or the reason an entry rejected its arguments where it gives one
+ * ("" if none).  Reading it clears it.
+ */
 const char* fr2_last_error(void);
 
 /*
@@ -80,6 +84,15 @@ int fr2_handoff_fault_count(int32_t* count, int32_t reset, void* stream);
  * (negative: the default 2^20).  No counterpart in the reference.
  */
 int fr2_debug_set_handoff_spin_limit(int32_t polls);
+
+/*
+ * Test hook: while on (non-zero), the chunked kernel's key waves never
+ * publish their operators, so each block's state waves stall at their first
+ * operator wait and, after the spin limit, the block fails closed.  Forces a
+ * real stall from the host while every kernel still runs to its end.  No
+ * counterpart in the reference.
+ */
+int fr2_debug_set_handoff_stall(int32_t on);
 
 /*
  * Device-side validation of packed metadata, one 256-thread workgroup.
@@ -138,6 +151,20 @@ int fr2_wkv7_recurrent_fp32_forward_kernel(
     const void* r, const void* decay_logits, const void* decay_bias,
     const void* k, const void* v, const void* a, const void* b, void* output,
     float scale, void* stream);
+
+/*
+ * The kernel family fr2_wkv7_recurrent_fp32_forward picks for a launch of
+ * this shape, written to *kernel: 0 = token-serial, 1 = decode, 2 = chunked
+ * MFMA with one workgroup per (sequence, head), 4 = chunked MFMA with one
+ * wavefront per (sequence, head), 5 = the same in longest-first order of the
+ * sequences.  Pure host computation (no device access, no state), so
+ * benchmarks and tests name the kernel that ran without restating the
+ * policy.  No reference counterpart: it reports the choice that replaces
+ * use_small_auto (csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:378-391).
+ */
+int fr2_wkv7_recurrent_fp32_dispatch(int32_t num_sequences, int32_t num_heads,
+                                     int32_t head_size, int64_t total_tokens,
+                                     int32_t max_seqlen, int32_t* kernel);
 
 /*
  * Sequence-split plan for the chunked prefill (head_size 64).  With few
@@ -199,10 +226,12 @@ int fr2_wkv7_recurrent_fp32_forward_split(
  * in fp32, runs the recurrence on (key, a, b) and writes key to new_k (the
  * readout's input); a and b are never stored.  Runs on the chunked kernel
  * fr2_wkv7_recurrent_fp32_forward would pick for this launch (one workgroup
- * or one wavefront per (sequence, head)); FR2_ERR_UNSUPPORTED where that
- * entry would run the decode kernel (max_seqlen <= 4, or <= 6 with 16 384 or
- * more units) or head_size != 64: the caller then runs
- * fr2_tmix_kk_a_gate_forward and fr2_wkv7_recurrent_fp32_forward.  Replaces
+ * or one wavefront per (sequence, head)).  Where that entry would run the
+ * decode kernel (max_seqlen <= 4, or <= 6 with 16 384 or more units; or
+ * max_seqlen <= 0, unknown), bf16 tokens run on the wavefront chunked kernel
+ * and fp16 tokens return FR2_ERR_UNSUPPORTED, as does head_size != 64: the
+ * caller then runs fr2_tmix_kk_a_gate_forward (fp16) and
+ * fr2_wkv7_recurrent_fp32_forward.  Replaces
  * the pair tmix_kk_a_gate_forward_varlen_cuda
  * (csrc/sm120/tmix/wkv_prepare/internal/kk_a_gate/infer_fp16_forward_varlen.cu)
  * + tmix_wkv7_recurrent_fp32_from_decay_logits_cuda

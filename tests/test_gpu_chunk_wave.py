@@ -78,7 +78,8 @@ def test_many_units_ragged_batch_matches_oracle(dtype):
     assert torch.equal(out, out2) and torch.equal(pool, pool2)
 
 
-def test_longest_first_order_with_ties_permuted_slots_and_inactive_sequences():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_longest_first_order_with_ties_permuted_slots_and_inactive_sequences(dtype):
     """40 sequences (the longest-first order applies) with repeated lengths,
     permuted slots and a graph ticket that leaves the last 7 inactive: the
     active ones match the oracle, the inactive ones' slots and output rows
@@ -89,8 +90,8 @@ def test_longest_first_order_with_ties_permuted_slots_and_inactive_sequences():
     base = [97, 16, 16, 1, 33, 97, 64, 2, 300, 15, 17, 31]
     lengths = tuple(base[i % len(base)] if i % 3 else int(rng.integers(1, 260))
                     for i in range(40))
-    print(f"case wave order lengths={lengths}", flush=True)
-    case = make_case(dtype=torch.bfloat16, lengths=lengths, num_heads=8, seed=9,
+    print(f"case wave order {dtype} lengths={lengths}", flush=True)
+    case = make_case(dtype=dtype, lengths=lengths, num_heads=8, seed=9,
                      state_pool_slots=48)
     perm = torch.from_numpy(rng.permutation(48)[:40].astype(np.int32))
     case["state_indices"] = perm.cuda()

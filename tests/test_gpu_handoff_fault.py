@@ -69,3 +69,35 @@ def test_handoff_give_up_fails_closed_and_is_counted():
     y_ref, pool_ref = oracle_expect(case)
     assert_output_close(to_np(out), y_ref)
     assert_state_close(to_np(pool), pool_ref)
+
+
+def test_real_stall_fails_closed_after_one_wait():
+    """A producer that never publishes (forced from the host: the key waves
+    skip their operator signal) makes the first operator wait give up; every
+    later wait of that block must then return at once instead of polling to
+    its limit, so a long sequence still ends in about one wait's limit."""
+    import time
+
+    C = require_gpu()
+    print("case handoff stall, spin limit 20000, length 16384, H=1", flush=True)
+    case = make_case(lengths=(16384,), num_heads=1, seed=72)
+    C.handoff_fault_count(reset=True)
+    pool = case["state_pool"].clone()
+    before = pool.clone()
+    _forced_chunked(C, make_case(lengths=(64,), num_heads=1, seed=73),
+                    make_case(lengths=(64,), num_heads=1, seed=73)["state_pool"].clone())
+    C._set_handoff_spin_limit(20000)
+    C._set_handoff_stall(True)
+    try:
+        t0 = time.perf_counter()
+        out = _forced_chunked(C, case, pool)
+        dt = time.perf_counter() - t0
+    finally:
+        C._set_handoff_stall(False)
+        C._set_handoff_spin_limit(-1)
+    print(f"stalled call took {dt * 1e3:.1f} ms", flush=True)
+    assert C.handoff_fault_count(reset=True) == 1
+    assert torch.isnan(out.float()).all()
+    assert torch.equal(pool, before)
+    # 512 groups; polling every hand-off to the limit takes seconds
+    assert dt < 0.5, dt

@@ -89,6 +89,9 @@ def _check_key(actual, expected, dtype):
 # 300 sequences x 4 heads = 1 200 units: the chunked kernel with one
 # wavefront per unit (the others run on the workgroup-per-unit kernel)
 _MANY = tuple((7 * i) % 97 + 5 for i in range(300))
+# 100 sequences x 8 heads = 800 units, one of 400 tokens and the rest 50:
+# the wavefront kernel in longest-first order of the sequences
+_SKEWED = (50,) * 37 + (400,) + (50,) * 62
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
@@ -96,7 +99,8 @@ _MANY = tuple((7 * i) % 97 + 5 for i in range(300))
     ((40, 1, 63, 130, 17), 3, False),
     ((300, 64, 96, 41), 4, True),
     (_MANY, 4, True),
-], ids=["ragged", "bias", "many-units"])
+    (_SKEWED, 8, True),
+], ids=["ragged", "bias", "many-units", "skewed-order-bias"])
 def test_fused_kk_gate_matches_the_two_stage_oracle(dtype, lengths, heads, bias):
     require_gpu()
     print(f"case kk-gate fused {dtype} {len(lengths)} sequences H {heads} bias {bias}", flush=True)
@@ -126,11 +130,26 @@ def test_short_batches_run_the_two_kernel_form():
     _check_key(new_k, ek, torch.float16)
 
 
-def test_short_bf16_batches_are_rejected():
+def test_short_bf16_batches_run_the_wavefront_kernel():
+    """Below the chunked threshold bf16 batches (whose gate has no separate
+    kernel) run the fused stage on the wavefront chunked kernel, which takes
+    sequences of any length; with and without the readout stage."""
     require_gpu()
-    c = _case((2, 4), 2, torch.bfloat16, seed=11)
-    with pytest.raises(Exception, match="float16 tokens"):
-        _run(c, 1.0)
+    for lengths, heads, seed in (((2, 4), 2, 11), ((1, 3, 4, 1), 3, 12)):
+        print(f"case kk-gate short bf16 lengths {lengths} H {heads}", flush=True)
+        c = _case(lengths, heads, torch.bfloat16, seed=seed, bias=seed == 12)
+        y, pool, new_k = _run(c, 1.0)
+        ey, epool, ek = _expected(c, 1.0)
+        assert_output_close(y, ey)
+        touched = c["slots"].long()
+        assert_state_close(to_np(pool)[touched], epool[touched])
+        _check_key(new_k, ek, torch.bfloat16)
+        c = _readout_params(c, seed)
+        readout, new_k, y, pool = _run_readout(c, 0.7)
+        ero, ey, epool, ek = _expected_readout(c, 0.7)
+        assert_output_close(readout, ero)
+        assert_output_close(y, ey)
+        assert_state_close(to_np(pool)[touched], epool[touched])
 
 
 def test_config1_shape_fp16():
@@ -212,7 +231,8 @@ def _run_readout(c, scale, want_y=True):
     ((40, 1, 63, 130, 17), 3, True),
     ((300, 64, 96, 41), 4, False),
     (_MANY, 4, True),
-], ids=["ragged-bias", "long", "many-units"])
+    (_SKEWED, 8, False),
+], ids=["ragged-bias", "long", "many-units", "skewed-order"])
 def test_fused_readout_matches_the_three_stage_oracle(dtype, lengths, heads, bias):
     require_gpu()
     print(f"case kk-gate+readout {dtype} {len(lengths)} sequences H {heads} bias {bias}",

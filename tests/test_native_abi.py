@@ -179,3 +179,31 @@ def test_fast_call_and_host_path_modules_load(lib):
     # a CPU tensor is never plainly valid for the fast path: it declines
     t = torch.zeros(1, dtype=torch.int32)
     assert host.prepare_graph(t, t, t, t, 1, 1, 1, 1, 0) is None
+
+
+@pytest.mark.parametrize("n,h,d,total,maxlen,want", [
+    (8, 32, 64, 8 * 4096, 4096, 2),        # config 1: one workgroup per unit
+    (256, 32, 64, 256, 1, 1),              # config 2: decode
+    (2048, 32, 64, 2048 * 100, 100, 4),    # many mid-length units: one wave per unit
+    (64, 64, 64, 68041, 2048, 5),          # config 3: longest-first order
+    (64, 64, 64, 60000, 2048, 2),          # longest above twice the mean: workgroup kernel
+    (64, 64, 64, 64 * 2048, 2048, 4),      # equal lengths: no order
+    (8, 32, 128, 8 * 4096, 4096, 0),       # head size 128: token-serial
+    (8, 32, 64, 8 * 4096, 0, 0),           # unknown max_seqlen: token-serial
+])
+def test_dispatch_query_reports_the_policy(lib, n, h, d, total, maxlen, want):
+    import ctypes
+    fam = ctypes.c_int32(-1)
+    assert lib.fr2_wkv7_recurrent_fp32_dispatch(n, h, d, total, maxlen, ctypes.byref(fam)) == 0
+    assert fam.value == want
+
+
+def test_dispatch_query_rejects_bad_arguments(lib):
+    import ctypes
+    fam = ctypes.c_int32(-1)
+    assert lib.fr2_wkv7_recurrent_fp32_dispatch(0, 4, 64, 10, 10, ctypes.byref(fam)) == \
+        N.FR2_ERR_INVALID_ARGUMENT
+    assert lib.fr2_wkv7_recurrent_fp32_dispatch(4, 4, 64, 10, 10, None) == \
+        N.FR2_ERR_INVALID_ARGUMENT
+    assert lib.fr2_wkv7_recurrent_fp32_dispatch(4, 4, 96, 10, 10, ctypes.byref(fam)) == \
+        N.FR2_ERR_UNSUPPORTED
