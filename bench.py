@@ -309,6 +309,62 @@ def time_fp16_state_decode(torch, flashrwkv2_amd, w, steps: int, warmup: int):
     return ms, start.elapsed_time(end) / (steps * 4)
 
 
+def time_fp16_state_prefill(torch, flashrwkv2_amd, steps: int):
+    """The FP16-state ("Albatross") recurrence on BASELINE config 1's shape
+    (8 x 4096 tokens, H = 32, fp16 tokens and an fp16 state pool): the public
+    entry (update + elapsed advance) with a reused ticket, and the token-serial
+    kernels forced through the C ABI: the barrier-free one (the policy's) and
+    the workgroup kernel with a barrier per token.  Per-token fp16 rounding of
+    the state makes this contract serial by construction."""
+    from flashrwkv2_amd import _native as N
+    from flashrwkv2_amd import workloads
+
+    w = workloads.config(1, "cuda", dtype=torch.float16)
+    state = w.state_pool.half().contiguous()
+    state0 = state.clone()
+    elapsed = torch.zeros(state.shape[0], dtype=torch.int32, device=state.device)
+    out = torch.empty_like(w.v)
+    ticket = flashrwkv2_amd.prepare_tmix_wkv7_recurrent_metadata(
+        w.cu_seqlens, w.state_indices, total_tokens=w.total_tokens,
+        state_pool_size=state.shape[0])
+    C = flashrwkv2_amd._C
+
+    def public():
+        C.tmix_wkv7_recurrent_fp16_from_decay_logits(
+            w.cu_seqlens, w.state_indices, elapsed, state, *w.tokens, out, 1.0, None, ticket)
+
+    ms = _events_ms(torch, public, steps)
+    lib = N.load()
+    sh = torch.cuda.current_stream().cuda_stream
+    args = (ticket._query_start_loc_snapshot().data_ptr(),
+            ticket._state_indices_snapshot().data_ptr(), ticket._status().data_ptr(),
+            elapsed.data_ptr(), w.state_indices.numel(), w.num_heads, 64, w.total_tokens,
+            ticket._max_seqlen(), state.data_ptr(), *(t.data_ptr() for t in w.tokens[:2]), None,
+            *(t.data_ptr() for t in w.tokens[2:]), out.data_ptr(), 1.0, sh)
+    forced = {}
+    for kern, name in ((6, "serial64h_kernel<IoF16>"),
+                       (0, "serial_kernel<64,IoF16,StF16,8>")):
+        state.copy_(state0)
+        fms = _events_ms(torch, lambda k=kern: N.check(
+            lib.fr2_wkv7_recurrent_fp16_update_kernel(k, *args),
+            "fr2_wkv7_recurrent_fp16_update_kernel"), max(3, steps // 2), warmup=2)
+        forced[name] = fms
+    nbytes = (w.total_tokens * w.num_heads * BYTES_PER_TOKEN_HEAD
+              + 2 * w.state_indices.numel() * w.num_heads * 64 * 64 * 2)
+    kms = forced["serial64h_kernel<IoF16>"]
+    out_obj = {
+        "workload": w.name + "_fp16_state", "ms_per_step": round(ms, 4),
+        "tokens_per_s": round(w.total_tokens / (ms * 1e-3), 1),
+        "kernel": "serial64h_kernel<IoF16>", "kernel_ms": round(kms, 4),
+        "roofline": roofline_obj(nbytes, kms), "algorithmic_bytes": nbytes,
+        "forced_ms": {k: round(v, 4) for k, v in forced.items()},
+        "speedup_over_workgroup_kernel": round(forced["serial_kernel<64,IoF16,StF16,8>"] / kms, 3),
+    }
+    del w, state, state0, out, ticket
+    torch.cuda.empty_cache()
+    return out_obj
+
+
 def time_graph_decode(torch, flashrwkv2_amd, w, steps: int = 16, reps: int = 20):
     """Serving-style decode loop on the graph-ticket path: `steps` consecutive
     T=1 steps (device-side metadata validation + recurrence each) captured in
@@ -1130,8 +1186,10 @@ def compact_line(result: dict) -> dict:
         legs["decode_fp16_state"] = {"ms": d["kernel_ms"], "frac": _frac(d["roofline"])}
     d = result.get("fp16_state_prefill")
     if d:
-        legs["fp16_state_prefill_cfg1"] = {"ms": d["kernel_ms"], "frac": _frac(d["roofline"]),
-                                           "kernel": d["kernel"]}
+        legs["fp16_state_prefill_cfg1"] = {"ms": d["kernel_ms"], "public_ms": d["ms_per_step"],
+                                           "frac": _frac(d["roofline"]), "kernel": d["kernel"],
+                                           "workgroup_kernel_ms":
+                                               d["forced_ms"]["serial_kernel<64,IoF16,StF16,8>"]}
     d = result.get("decode_graph")
     if d:
         legs["decode_graph"] = [{"workload": g["workload"], "graph_ms": g["graph_ms_per_step"],
@@ -1203,7 +1261,8 @@ def main() -> int:
                     help="tokens per sequence in the CPU baseline sample")
     ap.add_argument("--no-train", action="store_true",
                     help="skip the training (forward + backward) leg")
-    ap.add_argument("--only", choices=["prefill", "decode", "long", "mid", "train", "stages"],
+    ap.add_argument("--only", choices=["prefill", "decode", "long", "mid", "train", "stages",
+                                       "fp16"],
                     default=None,
                     help="run one leg only (profiling)")
     ap.add_argument("--config", type=int, default=1, choices=[1, 3, 4],
@@ -1322,6 +1381,9 @@ def main() -> int:
             result.update({"metric": METRIC, "value": result["decode"]["tokens_per_s"],
                            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
                            "warmup": args.warmup, "ms_per_step": round(dms, 5)})
+    if args.only in (None, "prefill", "fp16") and args.config == 1:
+        result["fp16_state_prefill"] = time_fp16_state_prefill(torch, flashrwkv2_amd,
+                                                               max(4, args.steps // 4))
     if args.only in (None, "prefill") and args.config == 1 and pre is not None:
         result["chunk_bf16_state"] = time_chunk_bf16_state(torch, flashrwkv2_amd, pre.w,
                                                            max(5, args.steps // 2))

@@ -100,6 +100,12 @@ SIGNATURES: dict[str, tuple] = {
          c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
          c_void_p, c_void_p, c_void_p, c_float, c_void_p],
     ),
+    "fr2_wkv7_recurrent_fp16_update_kernel": (
+        c_int32,
+        [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64,
+         c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_float, c_void_p],
+    ),
     "fr2_wkv7_recurrent_fp16_advance_elapsed": (
         c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_void_p],
     ),

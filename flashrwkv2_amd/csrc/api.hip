@@ -354,7 +354,8 @@ extern "C" int fr2_wkv7_recurrent_fp32_forward_split_noalloc(
 }
 
 namespace {
-int recurrent_fp16(bool advance, const int32_t* query_start_loc, const int32_t* state_indices,
+int recurrent_fp16(int family, bool advance, const int32_t* query_start_loc,
+                   const int32_t* state_indices,
                    const int32_t* status, int32_t* elapsed_state, int32_t num_sequences,
                    int32_t num_heads, int32_t head_size, int64_t total_tokens,
                    int32_t max_seqlen, void* state_f16, const void* r, const void* decay_logits,
@@ -378,7 +379,7 @@ int recurrent_fp16(bool advance, const int32_t* query_start_loc, const int32_t* 
   p.y = output;
   p.scale = scale;
   return fr2::launch_fp16_state(head_size, p, num_sequences, max_seqlen, elapsed_state,
-                                static_cast<hipStream_t>(stream), advance);
+                                static_cast<hipStream_t>(stream), advance, family);
 }
 }  // namespace
 
@@ -390,7 +391,7 @@ extern "C" int fr2_wkv7_recurrent_fp16_forward(
     const void* k, const void* v, const void* a, const void* b, void* output, float scale,
     void* stream) {
   if (!params_aligned({decay_bias})) return FR2_ERR_INVALID_ARGUMENT;
-  return recurrent_fp16(true, query_start_loc, state_indices, status, elapsed_state,
+  return recurrent_fp16(-1, true, query_start_loc, state_indices, status, elapsed_state,
                         num_sequences, num_heads, head_size, total_tokens, max_seqlen, state_f16,
                         r, decay_logits, decay_bias, k, v, a, b, output, scale, stream);
 }
@@ -403,7 +404,24 @@ extern "C" int fr2_wkv7_recurrent_fp16_update(
     const void* k, const void* v, const void* a, const void* b, void* output, float scale,
     void* stream) {
   if (!params_aligned({decay_bias})) return FR2_ERR_INVALID_ARGUMENT;
-  return recurrent_fp16(false, query_start_loc, state_indices, status,
+  return recurrent_fp16(-1, false, query_start_loc, state_indices, status,
+                        const_cast<int32_t*>(elapsed_state), num_sequences, num_heads, head_size,
+                        total_tokens, max_seqlen, state_f16, r, decay_logits, decay_bias, k, v, a,
+                        b, output, scale, stream);
+}
+
+extern "C" int fr2_wkv7_recurrent_fp16_update_kernel(
+    int32_t kernel, const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, const int32_t* elapsed_state, int32_t num_sequences,
+    int32_t num_heads, int32_t head_size, int64_t total_tokens, int32_t max_seqlen,
+    void* state_f16, const void* r, const void* decay_logits, const void* decay_bias,
+    const void* k, const void* v, const void* a, const void* b, void* output, float scale,
+    void* stream) {
+  if (!params_aligned({decay_bias})) return FR2_ERR_INVALID_ARGUMENT;
+  if (kernel != fr2::kFp16Serial && kernel != fr2::kFp16Decode &&
+      kernel != fr2::kFp16SerialWave)
+    return FR2_ERR_INVALID_ARGUMENT;
+  return recurrent_fp16(kernel, false, query_start_loc, state_indices, status,
                         const_cast<int32_t*>(elapsed_state), num_sequences, num_heads, head_size,
                         total_tokens, max_seqlen, state_f16, r, decay_logits, decay_bias, k, v, a,
                         b, output, scale, stream);

@@ -143,8 +143,11 @@ int launch_serial(int D, int dtype, bool bf16_state, const SegArgs& p, int nseg,
 int launch_decode(int D, int dtype, const SegArgs& p, int nseg, hipStream_t s);
 // FP16 state pool with the Albatross delta update (fp16 tokens), followed by
 // the elapsed-count advance of every active sequence's slot.
+// family: -1 the policy; kFp16Serial (serial_kernel), kFp16Decode (D = 64),
+// kFp16SerialWave (D = 64, barrier-free)
+constexpr int kFp16Serial = 0, kFp16Decode = 1, kFp16SerialWave = 6;
 int launch_fp16_state(int D, const SegArgs& p, int nseg, int max_seqlen, int32_t* elapsed,
-                      hipStream_t s, bool advance);
+                      hipStream_t s, bool advance, int family = -1);
 // elapsed[slot] += length for every active sequence (after the update)
 int launch_advance_elapsed(const SegArgs& p, int nseg, int32_t* elapsed, hipStream_t s);
 // Chunked MFMA prefill (D = 64, fp32 state).  Returns FR2_ERR_UNSUPPORTED

@@ -11,6 +11,7 @@
 //  csrc/sm120/tmix/wkv7/infer_recurrent_fp32io16_forward_varlen.cu:90-192).
 #include "recurrent.h"
 
+#include <array>
 #include <type_traits>
 
 namespace fr2 {
@@ -377,6 +378,310 @@ __global__ __launch_bounds__(256) void serial64w_kernel(SegArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// FP16-state (Albatross) token-serial kernel at D = 64 without a per-token
+// workgroup barrier.  Per token the state update is elementwise on the VALU
+// and the two dot products over the 64 keys (sa = a^T S before the update,
+// y = r^T S after it) run on the matrix cores: the state is fp16 by contract
+// and the token values a, r are fp16, so every product is exact and the
+// fp32 accumulation rounds only the sums.
+//
+// Four waves per (segment, head); wave w owns value columns [16w, 16w+16).
+// Lane (j, q) = (lane % 16, lane / 16) holds column 16w + j for keys
+// 32m + 8q + e (m = 0, 1; e = 0..7) twice: as fp32 (the update's operand)
+// and as packed fp16 pairs, which are as they stand the B operand of
+// v_mfma_f32_16x16x32_f16 for the two K steps m.  The A operand is the
+// token's a (or r) row replicated over the 16 rows, so every lane of a
+// column receives the dot product of its column.
+// The update S = fp16(S + S delta + b sa + k v) needs per key delta, b, k:
+// lane j of row q loads those of key 32(j / 8) + 8q + j % 8, which are
+// exactly the row's 16 state keys, and the DPP row broadcast
+// (row_newbcast) hands key j's values to the whole row inside the FMAs
+// (v_fmac_f32_dpp).  The fp32 result is rounded to fp16 two keys at a time
+// (v_cvt_pk_f16_f32), which forms the packed B operand, and widened back
+// for the next token's update: fp32 arithmetic, then the fp16 rounding, as
+// the reference's test contract states it (tests/tmix/wkv7/test.py:88-149).
+// Token values are staged per 16-token tile through LDS.
+// ---------------------------------------------------------------------------
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+// S32[8m + e] = fma(k_j, v, fma(b_j, sa, fma(d_j, S, S))) in fp32 for the
+// eight keys j = 8m + e of block m, stage by stage (no instruction waits on
+// the one before it), each key's d, b, k broadcast from lane j of the row.
+// The leading s_nop covers the wait states before the DPP reads (the
+// compiler does not see inside an asm block; sa arrives through a DPP move
+// the compiler emits, so its matrix-core wait is the compiler's).
+#define FR2_H_BLOCK0 \
+  "v_fmac_f32_dpp %0, %8, %0 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %1, %8, %1 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %2, %8, %2 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %3, %8, %3 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %4, %8, %4 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %5, %8, %5 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %6, %8, %6 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %7, %8, %7 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %0, %9, %11 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %1, %9, %11 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %2, %9, %11 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %3, %9, %11 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %4, %9, %11 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %5, %9, %11 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %6, %9, %11 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %7, %9, %11 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %0, %10, %12 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %1, %10, %12 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %2, %10, %12 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %3, %10, %12 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %4, %10, %12 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %5, %10, %12 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %6, %10, %12 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %7, %10, %12 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+#define FR2_H_BLOCK8 \
+  "v_fmac_f32_dpp %0, %8, %0 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %1, %8, %1 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %2, %8, %2 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %3, %8, %3 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %4, %8, %4 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %5, %8, %5 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %6, %8, %6 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %7, %8, %7 row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %0, %9, %11 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %1, %9, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %2, %9, %11 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %3, %9, %11 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %4, %9, %11 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %5, %9, %11 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %6, %9, %11 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %7, %9, %11 row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %0, %10, %12 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %1, %10, %12 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %2, %10, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %3, %10, %12 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %4, %10, %12 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %5, %10, %12 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %6, %10, %12 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_fmac_f32_dpp %7, %10, %12 row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+__device__ __forceinline__ void albatross_update_block(float (&S32)[16], float d, float b,
+                                                       float k, float sa, float v, int m) {
+  float* s = &S32[8 * m];
+  if (m == 0) {
+    asm volatile("s_nop 1\n\t" FR2_H_BLOCK0
+                 : "+v"(s[0]), "+v"(s[1]), "+v"(s[2]), "+v"(s[3]), "+v"(s[4]), "+v"(s[5]),
+                   "+v"(s[6]), "+v"(s[7])
+                 : "v"(d), "v"(b), "v"(k), "v"(sa), "v"(v));
+  } else {
+    asm volatile("s_nop 1\n\t" FR2_H_BLOCK8
+                 : "+v"(s[0]), "+v"(s[1]), "+v"(s[2]), "+v"(s[3]), "+v"(s[4]), "+v"(s[5]),
+                   "+v"(s[6]), "+v"(s[7])
+                 : "v"(d), "v"(b), "v"(k), "v"(sa), "v"(v));
+  }
+}
+#undef FR2_H_BLOCK0
+#undef FR2_H_BLOCK8
+
+// x^T S for the lane's column: x's 64 fp16 values as the A operand (every
+// row the same), the packed state as the B operand of the two K steps
+__device__ __forceinline__ float state_dot_f16(h8 x0, h8 x1, const uint32_t (&S16)[8]) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const h8 b0 = __builtin_bit_cast(h8, u32x4{S16[0], S16[1], S16[2], S16[3]});
+  const h8 b1 = __builtin_bit_cast(h8, u32x4{S16[4], S16[5], S16[6], S16[7]});
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, b0, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, b1, acc, 0, 0, 0);
+  return acc[0];
+}
+
+template <class Io>
+__global__ __launch_bounds__(256) void serial64h_kernel(SegArgs p) {
+  using raw = typename Io::raw;
+  constexpr int D = 64;
+  constexpr int NT = 256;
+  constexpr int TT = 16;
+  constexpr int TP = TT + 4;   // token pitch of the transposed rows (16-byte reads)
+  constexpr int V8 = D / 8;
+
+  // per-key values, transposed ([tensor][key][token], fp32): delta, k, b;
+  // v by value column
+  __shared__ __attribute__((aligned(16))) float s_t[4][D][TP];
+  // the a and r rows as they arrive (fp16), the matrix cores' A operands
+  __shared__ __attribute__((aligned(16))) _Float16 s_ar[2][TT][D];
+  __shared__ float s_y[TT][D];
+
+  const int h = blockIdx.x;
+  const int seg = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int j = lane & 15;
+  const int q = lane >> 4;
+  const int col = 16 * (tid >> 6) + j;                 // value column
+  const int kown = 32 * (j >> 3) + 8 * q + (j & 7);    // key whose values this lane loads
+  const int H = p.num_heads;
+  if (!check_status<Io>(p, seg, static_cast<int64_t>(seg) * gridDim.x + h,
+                        static_cast<int64_t>(gridDim.x) * gridDim.y))
+    return;
+  int t0, t1, slot;
+  resolve_segment(p, seg, t0, t1, slot);
+
+  const int64_t sbase = (static_cast<int64_t>(slot) * H + h) * D * D;
+  const int elapsed_base = p.elapsed != nullptr ? p.elapsed[slot] : 0;
+  float S32[16];
+  uint32_t S16[8];
+  {
+    const uint16_t* sin = static_cast<const uint16_t*>(p.state_in);
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const uint16_t lo = sin[sbase + (32 * m + 8 * q + e) * D + col];
+        const uint16_t hi = sin[sbase + (32 * m + 8 * q + e + 1) * D + col];
+        S16[4 * m + e / 2] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+        S32[8 * m + e] = static_cast<float>(__builtin_bit_cast(_Float16, lo));
+        S32[8 * m + e + 1] = static_cast<float>(__builtin_bit_cast(_Float16, hi));
+      }
+    }
+  }
+
+  const raw* src[6] = {
+      static_cast<const raw*>(p.r), static_cast<const raw*>(p.logits),
+      static_cast<const raw*>(p.k), static_cast<const raw*>(p.v),
+      static_cast<const raw*>(p.a), static_cast<const raw*>(p.b)};
+  const raw* bias = static_cast<const raw*>(p.bias);
+  raw* y = static_cast<raw*>(p.y);
+
+  constexpr int PER = 6 * TT * V8 / NT;
+  static_assert(PER * NT == 6 * TT * V8, "tile pieces must divide evenly");
+  Raw8 pre[PER];
+  auto fetch = [&](int tile) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int idx = tid + u * NT;
+      const int which = idx / (TT * V8);
+      const int rem = idx - which * (TT * V8);
+      const int tt = rem / V8;
+      const int c8 = rem - tt * V8;
+      // rows past the segment repeat its last row (in bounds; never consumed)
+      const int row = min(tile + tt, t1 - 1);
+      pre[u] = *reinterpret_cast<const Raw8*>(src[which] +
+                                              (static_cast<int64_t>(row) * H + h) * D + c8 * 8);
+    }
+  };
+  auto a_row = [&](int which, int tt, int m) {
+    return *reinterpret_cast<const h8*>(&s_ar[which][tt][32 * m + 8 * q]);
+  };
+  if (t0 < t1) fetch(t0);
+  for (int tile = t0; tile < t1; tile += TT) {
+    const int n = min(TT, t1 - tile);
+    __syncthreads();  // previous tile fully consumed
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int idx = tid + u * NT;
+      const int which = idx / (TT * V8);
+      const int rem = idx - which * (TT * V8);
+      const int tt = rem / V8;
+      const int c8 = rem - tt * V8;
+      if (which == 0 || which == 4) {
+        // r, a: fp16 rows as loaded
+        *reinterpret_cast<Raw8*>(&s_ar[which == 4 ? 0 : 1][tt][c8 * 8]) = pre[u];
+        continue;
+      }
+      float f[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = raw8_get<Io>(pre[u], i);
+      if (which == 1) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float x = f[i];
+          if (bias != nullptr) x += Io::to_f32(bias[h * D + c8 * 8 + i]);
+          f[i] = albatross_delta(x, elapsed_base + h * D + c8 * 8 + i + (tile + tt - t0));
+        }
+      }
+      // delta, k, v, b -> rows 0, 1, 2, 3 of s_t
+      const int slot_t = which == 1 ? 0 : which == 2 ? 1 : which == 3 ? 2 : 3;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s_t[slot_t][c8 * 8 + i][tt] = f[i];
+    }
+    __syncthreads();
+    if (tile + TT < t1) fetch(tile + TT);
+
+    // sa of the tile's first token; every later one comes with the y pass
+    float sa = state_dot_f16(a_row(0, 0, 0), a_row(0, 0, 1), S16);
+    // one token: the update, the state rounded to fp16 (packed pairs: the
+    // matrix cores' B operand), the next token's sa (the critical path) and
+    // y, and the state widened back for the next update
+    auto step = [&](int tt, bool has_next, float d, float b, float k, float v) {
+      // A operands of this token's y and the next token's sa, requested
+      // before the update so that their LDS latency hides behind it
+      const int tn = has_next ? tt + 1 : tt;
+      const h8 an0 = a_row(0, tn, 0), an1 = a_row(0, tn, 1);
+      const h8 r0 = a_row(1, tt, 0), r1 = a_row(1, tt, 1);
+      // sa passes through a DPP move the compiler emits, so the compiler
+      // places the matrix-core result wait before it
+      const float sa_v =
+          __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sa), 0xe4, 0xf, 0xf, false));
+      albatross_update_block(S32, d, b, k, sa_v, v, 0);
+      albatross_update_block(S32, d, b, k, sa_v, v, 1);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        S16[e] = __builtin_bit_cast(
+            uint32_t, __builtin_convertvector(f32x2{S32[2 * e], S32[2 * e + 1]}, f16x2));
+      }
+      if (has_next) sa = state_dot_f16(an0, an1, S16);
+      s_y[tt][col] = state_dot_f16(r0, r1, S16);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t w = S16[e];
+        S32[2 * e] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w)));
+        S32[2 * e + 1] =
+            static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+      }
+    };
+    auto group = [&](int t4) {
+      return std::array<f4, 4>{*reinterpret_cast<const f4*>(&s_t[0][kown][t4]),
+                               *reinterpret_cast<const f4*>(&s_t[3][kown][t4]),
+                               *reinterpret_cast<const f4*>(&s_t[1][kown][t4]),
+                               *reinterpret_cast<const f4*>(&s_t[2][col][t4])};
+    };
+    if (n == TT) {
+      // full tile: straight-line code, no per-token conditions
+#pragma unroll
+      for (int t4 = 0; t4 < TT; t4 += 4) {
+        const auto gv = group(t4);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          step(t4 + u, t4 + u + 1 < TT, gv[0][u], gv[1][u], gv[2][u], gv[3][u]);
+      }
+    } else {
+      for (int t4 = 0; t4 < n; t4 += 4) {
+        const auto gv = group(t4);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (t4 + u >= n) break;
+          step(t4 + u, t4 + u + 1 < n, gv[0][u], gv[1][u], gv[2][u], gv[3][u]);
+        }
+      }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < n * D; idx += NT) {
+      const int tt = idx / D;
+      const int vc = idx - tt * D;
+      y[(static_cast<int64_t>(tile + tt) * H + h) * D + vc] = Io::from_f32(p.scale * s_y[tt][vc]);
+    }
+  }
+
+  uint16_t* sout = static_cast<uint16_t*>(p.state_out);
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      sout[sbase + (32 * m + 8 * q + e) * D + col] = static_cast<uint16_t>(S16[4 * m + e / 2]);
+      sout[sbase + (32 * m + 8 * q + e + 1) * D + col] =
+          static_cast<uint16_t>(S16[4 * m + e / 2] >> 16);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Decode kernel (D = 64, fp32 state).  One wavefront per (segment, head).
 // Lane l owns columns 4*(l%16)..+3 of key rows {l/16 + 4j : j < 16}: the 16 KiB
 // state moves as 16 dwordx4 loads per lane, each wave instruction covering 4
@@ -609,20 +914,32 @@ __global__ __launch_bounds__(256) void advance_elapsed_kernel(SegArgs p, int nse
 constexpr int kFp16DecodeMaxSeqlen = 4;
 
 int launch_fp16_state(int D, const SegArgs& p, int nseg, int max_seqlen, int32_t* elapsed,
-                      hipStream_t s, bool advance) {
+                      hipStream_t s, bool advance, int family) {
   if (elapsed == nullptr || p.sa_out != nullptr || p.boundary != nullptr)
     return FR2_ERR_INVALID_ARGUMENT;
   SegArgs q = p;
   q.elapsed = elapsed;
-  if (D == 64 && max_seqlen > 0 && max_seqlen <= kFp16DecodeMaxSeqlen) {
+  if (family < 0) {
+    // D = 64: short requests stream the state once; longer ones run the
+    // barrier-free token-serial kernel
+    family = D != 64 ? kFp16Serial
+             : (max_seqlen > 0 && max_seqlen <= kFp16DecodeMaxSeqlen) ? kFp16Decode
+                                                                       : kFp16SerialWave;
+  }
+  if ((family == kFp16Decode || family == kFp16SerialWave) && D != 64) return FR2_ERR_UNSUPPORTED;
+  if (family == kFp16Decode) {
     hipLaunchKernelGGL((decode64_f16s_kernel<IoF16>), dim3(p.num_heads, nseg), dim3(64), 0, s,
                        q);
-    const int rc = record_launch();
-    if (rc != FR2_OK) return rc;
-  } else {
+  } else if (family == kFp16SerialWave) {
+    hipLaunchKernelGGL((serial64h_kernel<IoF16>), dim3(p.num_heads, nseg), dim3(256), 0, s, q);
+  } else if (family == kFp16Serial) {
     const int rc = launch_serial_io<IoF16, StF16>(D, q, nseg, s);
     if (rc != FR2_OK) return rc;
+  } else {
+    return FR2_ERR_INVALID_ARGUMENT;
   }
+  const int rc = record_launch();
+  if (rc != FR2_OK) return rc;
   return advance ? launch_advance_elapsed(p, nseg, elapsed, s) : FR2_OK;
 }
 

@@ -335,6 +335,22 @@ int fr2_wkv7_recurrent_fp16_update(
     const void* decay_logits, const void* decay_bias, const void* k,
     const void* v, const void* a, const void* b, void* output, float scale,
     void* stream);
+/*
+ * fr2_wkv7_recurrent_fp16_update with the kernel forced: 0 = the token-serial
+ * workgroup kernel (a barrier per token; every head size), 1 = the decode
+ * kernel (head_size 64), 6 = the barrier-free token-serial kernel (head_size
+ * 64; bit-identical to 0 at 256 or fewer (sequence, head) units).  Used by
+ * tests and benchmarks to pin each kernel; no reference counterpart (the
+ * reference's family selection is internal).
+ */
+int fr2_wkv7_recurrent_fp16_update_kernel(
+    int32_t kernel, const int32_t* query_start_loc, const int32_t* state_indices,
+    const int32_t* status, const int32_t* elapsed_state, int32_t num_sequences,
+    int32_t num_heads, int32_t head_size, int64_t total_tokens,
+    int32_t max_seqlen, void* state_f16, const void* r,
+    const void* decay_logits, const void* decay_bias, const void* k,
+    const void* v, const void* a, const void* b, void* output, float scale,
+    void* stream);
 int fr2_wkv7_recurrent_fp16_advance_elapsed(const int32_t* query_start_loc,
                                             const int32_t* state_indices,
                                             const int32_t* status, int32_t* elapsed_state,

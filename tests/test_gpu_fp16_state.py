@@ -255,3 +255,73 @@ def test_fp16_state_update_then_advance_equals_the_combined_entry(lengths):
     for a, b in zip(*results):
         assert torch.equal(a, b)
     check_against_oracle(case, *results[1], scale=0.5)
+
+
+def _forced_update(case, kernel, max_seqlen):
+    """fr2_wkv7_recurrent_fp16_update_kernel with the kernel forced; returns
+    (y, state) and leaves the case untouched."""
+    from flashrwkv2_amd import _native as N
+
+    lib = N.load()
+    state = case["state_pool"].clone()
+    out = torch.empty_like(case["v"])
+    t = prepare_tmix_wkv7_recurrent_metadata(
+        case["cu_seqlens"], case["state_indices"], total_tokens=case["r"].shape[0],
+        state_pool_size=state.shape[0])
+    bias = case["decay_bias"]
+    rc = lib.fr2_wkv7_recurrent_fp16_update_kernel(
+        kernel, t._query_start_loc_snapshot().data_ptr(), t._state_indices_snapshot().data_ptr(),
+        t._status().data_ptr(), case["elapsed_state_pool"].data_ptr(),
+        case["state_indices"].numel(), case["r"].shape[1], case["r"].shape[2], out.shape[0],
+        max_seqlen, state.data_ptr(), *(x.data_ptr() for x in tokens(case)[:2]),
+        None if bias is None else bias.data_ptr(), *(x.data_ptr() for x in tokens(case)[2:]),
+        out.data_ptr(), 0.75, torch.cuda.current_stream().cuda_stream)
+    N.check(rc, "fr2_wkv7_recurrent_fp16_update_kernel")
+    torch.cuda.synchronize()
+    return out, state
+
+
+@pytest.mark.parametrize("lengths,heads,bias", [
+    ((1, 2, 4), 2, True),
+    ((17, 33, 5, 64), 3, False),
+    ((300, 129), 4, True),
+    ((4096,) * 8, 32, False),          # BASELINE config 1's shape in fp16 (256 units)
+], ids=["short", "ragged", "long-bias", "config1-shape"])
+def test_barrier_free_fp16_kernel_matches_the_workgroup_kernel(lengths, heads, bias):
+    """The barrier-free D = 64 kernel (6) updates the state with the same
+    fp32 FMAs and the same fp16 rounding as the workgroup kernel (0); its two
+    dot products per token run on the matrix cores (exact fp16 products, fp32
+    sums in the hardware's order), so an fp16 rounding can land one unit
+    apart now and then.  The two agree far inside the oracle gate, and the
+    small cases meet the oracle."""
+    require_gpu()
+    print(f"case fp16 barrier-free vs workgroup lengths={lengths[:4]} H={heads} bias={bias}",
+          flush=True)
+    case = make_case(lengths=lengths, num_heads=heads, with_decay_bias=bias, seed=401)
+    y0, s0 = _forced_update(case, 0, max(lengths))
+    y6, s6 = _forced_update(case, 6, max(lengths))
+    assert torch.isfinite(y6).all() and torch.isfinite(s6).all()
+    act = case["state_indices"].long()
+    assert relative_rmse(to_np(y6), to_np(y0).astype(np.float64)) <= 2e-4
+    assert relative_rmse(to_np(s6[act]), to_np(s0[act]).astype(np.float64)) <= 2e-4
+    untouched = np.setdiff1d(np.arange(s6.shape[0]), act.cpu().numpy())
+    assert np.array_equal(to_np(s6)[untouched], to_np(case["state_pool"])[untouched])
+    if sum(lengths) * heads <= 4096:
+        el = case["elapsed_state_pool"].clone()
+        lens = (case["cu_seqlens"][1:] - case["cu_seqlens"][:-1]).to(torch.int32)
+        el.index_add_(0, act, lens)
+        check_against_oracle(case, y6, s6, el, scale=0.75)
+
+
+def test_barrier_free_fp16_kernel_many_units_meets_the_oracle():
+    """Above 256 units the workgroup kernel splits keys 4 ways (another sum
+    order); the barrier-free kernel keeps its order and meets the oracle."""
+    require_gpu()
+    lengths = tuple(5 + (7 * i) % 23 for i in range(100))
+    print("case fp16 barrier-free 100 sequences x 4 heads", flush=True)
+    case = make_case(lengths=lengths, num_heads=4, with_decay_bias=True, seed=402)
+    y6, s6 = _forced_update(case, 6, max(lengths))
+    el = case["elapsed_state_pool"].clone()
+    lens = (case["cu_seqlens"][1:] - case["cu_seqlens"][:-1]).to(torch.int32)
+    el.index_add_(0, case["state_indices"].long(), lens)
+    check_against_oracle(case, y6, s6, el, scale=0.75)
