@@ -495,7 +495,7 @@ __global__ __launch_bounds__(256) void serial64h_kernel(SegArgs p) {
   using raw = typename Io::raw;
   constexpr int D = 64;
   constexpr int NT = 256;
-  constexpr int TT = 16;
+  constexpr int TT = 32;
   constexpr int TP = TT + 4;   // token pitch of the transposed rows (16-byte reads)
   constexpr int V8 = D / 8;
 
@@ -607,7 +607,11 @@ __global__ __launch_bounds__(256) void serial64h_kernel(SegArgs p) {
     // one token: the update, the state rounded to fp16 (packed pairs: the
     // matrix cores' B operand), the next token's sa (the critical path) and
     // y, and the state widened back for the next update
+    float y_prev = 0.f;   // the previous token's y, stored one token late
     auto step = [&](int tt, bool has_next, float d, float b, float k, float v) {
+      // (storing y right after its matrix-core pass would stall the wave
+      // until that pass completes, in front of the next token's work)
+      if (tt > 0) s_y[tt - 1][col] = y_prev;
       // A operands of this token's y and the next token's sa, requested
       // before the update so that their LDS latency hides behind it
       const int tn = has_next ? tt + 1 : tt;
@@ -627,7 +631,7 @@ __global__ __launch_bounds__(256) void serial64h_kernel(SegArgs p) {
             uint32_t, __builtin_convertvector(f32x2{S32[2 * e], S32[2 * e + 1]}, f16x2));
       }
       if (has_next) sa = state_dot_f16(an0, an1, S16);
-      s_y[tt][col] = state_dot_f16(r0, r1, S16);
+      y_prev = state_dot_f16(r0, r1, S16);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t w = S16[e];
@@ -643,8 +647,8 @@ __global__ __launch_bounds__(256) void serial64h_kernel(SegArgs p) {
                                *reinterpret_cast<const f4*>(&s_t[2][col][t4])};
     };
     if (n == TT) {
-      // full tile: straight-line code, no per-token conditions
-#pragma unroll
+      // full tile: straight-line code within each group of four tokens
+#pragma unroll 2
       for (int t4 = 0; t4 < TT; t4 += 4) {
         const auto gv = group(t4);
 #pragma unroll
@@ -661,6 +665,7 @@ __global__ __launch_bounds__(256) void serial64h_kernel(SegArgs p) {
         }
       }
     }
+    s_y[n - 1][col] = y_prev;
     __syncthreads();
     for (int idx = tid; idx < n * D; idx += NT) {
       const int tt = idx / D;
