@@ -967,6 +967,75 @@ ST_FWD_BYTES_PER_TOKEN_HEAD = 6 * 128 + 128 + 256
 ST_BWD_BYTES_PER_TOKEN_HEAD = 768 + 768 + 128 + 256 + 256 + 512 + 640 + 640
 
 
+def time_statetune_ragged(torch, w, steps: int):
+    """StateTune on the config-1 shape (8 x 4096 tokens, H = 32) over a
+    ragged chunk list: chunks of seeded random lengths 1..700 (most not a
+    multiple of 16), a few empty, and 40 tokens of each sequence in no chunk.
+    Through the public `_C` entries (the forward builds the padded grid on
+    the host from the chunk metadata, then runs the chunked MFMA kernels;
+    the backward reuses the grid), per call, HIP events and wall clock; the
+    token-serial kernels on the same list for comparison."""
+    import numpy as np
+
+    import flashrwkv2_amd._C as CC
+
+    B, T, H = w.info["B"], w.info["T"], w.info["H"]
+    D = 64
+    dev = w.tokens[0].device
+    toks = list(w.tokens)
+    rng = np.random.default_rng(2003)
+    offsets, starts, ends = [0], [], []
+    for b in range(B):
+        t, end = b * T, (b + 1) * T - 40
+        while t < end:
+            n = min(int(rng.integers(0, 701)), end - t)
+            starts.append(t)
+            ends.append(t + n)
+            t += n
+        offsets.append(len(starts))
+    meta = [torch.tensor(x, dtype=torch.int32, device=dev) for x in (offsets, starts, ends)]
+    C = len(starts)
+    g = torch.Generator(device=dev)
+    g.manual_seed(2004)
+    state0 = torch.randn((B, H, D, D), generator=g, device=dev) * 0.1
+    state = state0.clone()
+    dy = torch.randn((B * T, H, D), generator=g, device=dev).to(torch.bfloat16)
+    dfin = torch.randn((B, H, D, D), generator=g, device=dev)
+    y = torch.empty_like(toks[3])
+    boundary = torch.empty((C, H, D, D), device=dev, dtype=torch.float32)
+    sa = torch.empty((B * T, H, D), device=dev, dtype=torch.float32)
+    grads = [torch.empty_like(t) for t in toks]
+    g0 = torch.empty_like(state)
+    res = {}
+
+    def fwd():
+        state.copy_(state0)
+        res["snap"] = CC.statetune_tmix_wkv7_recurrent_fp32io16_forward(
+            *meta, state, *toks, y, boundary, sa, 1.0)
+
+    def bwd():
+        CC.statetune_tmix_wkv7_recurrent_fp32io16_backward(
+            *meta, state, *toks, sa, dy, dfin, boundary, *grads, g0, 1.0,
+            snapshots=res["snap"])
+
+    out = {"workload": f"cfg1_shape_statetune_ragged_B{B}_T{T}_H{H}", "chunks": C,
+           "tokens_in_chunks": int(sum(e - s for s, e in zip(starts, ends)))}
+    for name, serial in (("chunked", False), ("token_serial", True)):
+        CC._statetune_force_serial = serial
+        try:
+            n = steps if not serial else max(2, steps // 3)
+            f_ms = _events_ms(torch, fwd, n, warmup=2)
+            b_ms = _events_ms(torch, bwd, n, warmup=2)
+        finally:
+            CC._statetune_force_serial = False
+        out[name] = {"forward_ms": round(f_ms, 4), "backward_ms": round(b_ms, 4),
+                     "path": type(res["snap"]).__name__}
+    out["gradients_finite"] = all(bool(torch.isfinite(t).all()) for t in (*grads, g0))
+    del state, dy, y, boundary, sa, grads, res
+    torch.cuda.empty_cache()
+    return out
+
+
 def time_statetune_training(torch, w, steps: int, chunk_len: int = 1024):
     """StateTune on the config-1 shape: B sequences of T tokens, each run as
     T/chunk_len chunks from a trainable fp32 initial state ~ N(0, 0.1);
@@ -1230,6 +1299,9 @@ def compact_line(result: dict) -> dict:
                     legs[key][sub] = {k: v for k, v in d[sub].items() if k.endswith("_ms")}
             if isinstance(d.get("backward_roofline"), dict):
                 legs[key]["backward_frac"] = d["backward_roofline"].get("frac")
+    d = result.get("statetune_ragged")
+    if d:
+        legs["statetune_ragged_cfg1"] = {k: d[k] for k in ("chunked", "token_serial")}
     d = result.get("kk_gate_fused")
     if d:
         legs["kk_gate_fused_cfg1_fp16"] = {"two_stage_ms": d["two_stage"]["ms_per_step"],
@@ -1400,6 +1472,7 @@ def main() -> int:
         wt = pre.w if (pre is not None and args.config == 1) else workloads.config(1, "cuda")
         result["pretrain_training"] = time_pretrain_training(torch, wt, max(3, args.steps // 4))
         result["statetune_training"] = time_statetune_training(torch, wt, max(3, args.steps // 4))
+        result["statetune_ragged"] = time_statetune_ragged(torch, wt, max(3, args.steps // 4))
     if args.only in (None, "stages"):
         result["layer_stages"] = time_layer_stages(torch, 8 * 4096, 32)
         result["kk_gate_fused"] = time_kk_fused(torch, flashrwkv2_amd, max(5, args.steps // 2))

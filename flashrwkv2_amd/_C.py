@@ -29,6 +29,7 @@ import torch
 
 from . import _native as N
 from ._align import aligned_io
+from ._statetune_plan import statetune_padded_plan as _statetune_padded_plan
 
 INT32_MAX = 2**31 - 1
 _TOKEN_DTYPES = {torch.float16: N.FR2_DTYPE_FLOAT16, torch.bfloat16: N.FR2_DTYPE_BFLOAT16}
@@ -957,6 +958,10 @@ def _statetune_uniform_chunk_len(offsets, starts, ends, B, C, T, D, dtype):
     return length if ok else None
 
 
+# tests set this to run every non-uniform chunk list token-serial
+_statetune_force_serial = False
+
+
 def statetune_tmix_wkv7_recurrent_fp32io16_forward(sequence_chunk_offsets, chunk_token_starts,
                                                    chunk_token_ends, state, r, decay_logits,
                                                    k, v, a, b, output, boundary, state_dot_a,
@@ -968,8 +973,12 @@ def statetune_tmix_wkv7_recurrent_fp32io16_forward(sequence_chunk_offsets, chunk
     When the chunk list is the uniform layout (D = 64, bf16, equal sequences
     packed back to back, equal chunks of a multiple of 16 tokens) it runs on
     the chunked MFMA kernels and returns the fp32 post-16-token state
-    snapshots ``[B,H,T/16,64,64]`` that the fast backward takes; otherwise it
-    runs token-serial and returns None (the reference returns None)."""
+    snapshots ``[B,H,T/16,64,64]`` that the fast backward takes.  Any other
+    chunk list at D = 64 in bf16 runs on the same kernels over a padded grid
+    (_statetune_padded_plan) and returns (snapshots, row_source,
+    seq_first_chunk) for the backward.  Otherwise (fp16, D = 128 / 256, or a
+    list the grid does not suit) it runs token-serial and returns None (the
+    reference returns None)."""
     B, C, T, H, D = _statetune_check(
         sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, state,
         ((r, "r"), (decay_logits, "decay_logits"), (k, "k"), (v, "v"), (a, "a"), (b, "b"),
@@ -982,6 +991,28 @@ def statetune_tmix_wkv7_recurrent_fp32io16_forward(sequence_chunk_offsets, chunk
            "state_dot_a must be float32 [total_tokens,H,D]")
     length = _statetune_uniform_chunk_len(sequence_chunk_offsets, chunk_token_starts,
                                           chunk_token_ends, B, C, T, D, r.dtype)
+    plan = None if (length is not None or _statetune_force_serial) else _statetune_padded_plan(
+        sequence_chunk_offsets, chunk_token_starts, chunk_token_ends, B, C, T, D, r.dtype)
+    if plan is not None:
+        Tp, row_source, chunk_seq, pstart, first = plan
+        dev = state.device
+        tables = [torch.from_numpy(x).to(dev) for x in (row_source, chunk_seq, pstart, first)]
+        snapshots = torch.empty((B, H, Tp // 16, D, D), device=dev, dtype=torch.float32)
+        lib = N.load()
+        nbytes = lib.fr2_wkv7_statetune_padded_workspace_bytes(B, Tp, H, 0)
+        _check(nbytes > 0, "statetune forward: unsupported shape")
+        ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+        with _on_device(dev):
+            rc = lib.fr2_wkv7_statetune_padded_forward(
+                B, Tp, H, C, tables[0].data_ptr(), tables[1].data_ptr(), tables[2].data_ptr(),
+                state.data_ptr(), r.data_ptr(), decay_logits.data_ptr(), k.data_ptr(),
+                v.data_ptr(), a.data_ptr(), b.data_ptr(), output.data_ptr(), boundary.data_ptr(),
+                state_dot_a.data_ptr(), snapshots.data_ptr(), ws.data_ptr(), float(scale),
+                _stream(dev))
+        N.check(rc, "statetune_tmix_wkv7_recurrent_fp32io16_forward")
+        del ws
+        # what the backward needs: the snapshots and the grid tables
+        return snapshots, tables[0], tables[3]
     with _on_device(state.device):
         if length is not None:
             per_seq = T // B
@@ -1044,6 +1075,29 @@ def statetune_tmix_wkv7_recurrent_fp32io16_backward(sequence_chunk_offsets, chun
                and grad_final_state.shape == final_state.shape,
                "grad_final_state must be float32 [B,H,D,D]")
     ptr = lambda t: None if t is None else t.data_ptr()
+    if isinstance(snapshots, tuple):
+        # the padded layout of a ragged chunk list (what the forward returned)
+        snaps, row_source, first = snapshots
+        Tp = row_source.numel() // B
+        _check(D == 64 and r.dtype == torch.bfloat16 and Tp * B == row_source.numel()
+               and Tp % 16 == 0 and tuple(snaps.shape) == (B, H, Tp // 16, D, D)
+               and first.numel() == B, "snapshots do not match the padded chunk layout")
+        if grad_output is None:
+            grad_output = torch.zeros_like(r)
+        lib = N.load()
+        nbytes = lib.fr2_wkv7_statetune_padded_workspace_bytes(B, Tp, H, 1)
+        _check(nbytes > 0, "statetune backward: unsupported shape")
+        ws = torch.empty(nbytes, device=r.device, dtype=torch.uint8)
+        with _on_device(final_state.device):
+            rc = lib.fr2_wkv7_statetune_padded_backward(
+                B, Tp, H, row_source.data_ptr(), first.data_ptr(), r.data_ptr(),
+                decay_logits.data_ptr(), k.data_ptr(), v.data_ptr(), a.data_ptr(), b.data_ptr(),
+                state_dot_a.data_ptr(), grad_output.data_ptr(), ptr(grad_final_state),
+                boundary.data_ptr(), snaps.data_ptr(), ws.data_ptr(),
+                *(g.data_ptr() for g, _ in grads), grad_initial_state.data_ptr(), float(scale),
+                _stream(final_state.device))
+        N.check(rc, "statetune_tmix_wkv7_recurrent_fp32io16_backward")
+        return
     if snapshots is not None and grad_output is not None:
         per_seq = T // B
         _check(T % B == 0 and C % B == 0 and T % C == 0,

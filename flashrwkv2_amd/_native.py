@@ -140,6 +140,16 @@ SIGNATURES: dict[str, tuple] = {
     "fr2_wkv7_statetune_uniform_backward_workspace_floats": (
         c_int64, [c_int32] * 3,
     ),
+    "fr2_wkv7_statetune_padded_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32]),
+    "fr2_wkv7_statetune_padded_forward": (
+        c_int32,
+        [c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p] + [c_void_p] * 12
+        + [c_float, c_void_p],
+    ),
+    "fr2_wkv7_statetune_padded_backward": (
+        c_int32,
+        [c_int32, c_int32, c_int32, c_void_p, c_void_p] + [c_void_p] * 19 + [c_float, c_void_p],
+    ),
     "fr2_wkv7_statetune_uniform_backward": (
         c_int32, [c_int32] * 4 + [c_void_p] * 19 + [c_float, c_void_p],
     ),

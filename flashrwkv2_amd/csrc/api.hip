@@ -819,6 +819,75 @@ extern "C" int fr2_wkv7_statetune_uniform_backward(
                                                 workspace, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int64_t fr2_wkv7_statetune_padded_workspace_bytes(int32_t batch,
+                                                             int32_t padded_tokens,
+                                                             int32_t num_heads,
+                                                             int32_t backward) {
+  if (batch <= 0 || batch > 65535 || padded_tokens <= 0 || padded_tokens % 16 != 0 ||
+      num_heads <= 0)
+    return -1;
+  return fr2::statetune_padded_workspace_bytes(batch, padded_tokens, num_heads, backward != 0);
+}
+
+extern "C" int fr2_wkv7_statetune_padded_forward(
+    int32_t batch, int32_t padded_tokens, int32_t num_heads, int32_t num_chunks,
+    const int32_t* row_source, const int32_t* chunk_seq, const int32_t* chunk_pstart,
+    float* state, const void* r, const void* decay_logits, const void* k, const void* v,
+    const void* a, const void* b, void* output, float* boundary, float* state_dot_a,
+    float* snapshots, void* workspace, float scale, void* stream) {
+  if (!state || !tokens_ok(r, decay_logits, k, v, a, b, output) || !boundary || !state_dot_a ||
+      !snapshots || !workspace || !row_source || !chunk_seq || !chunk_pstart ||
+      !aligned16(workspace))
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (batch <= 0 || batch > 65535 || padded_tokens <= 0 || padded_tokens % 16 != 0 ||
+      num_heads <= 0 || num_chunks <= 0)
+    return FR2_ERR_INVALID_ARGUMENT;
+  fr2::StateTuneArgs p;
+  p.heads = num_heads;
+  p.r = r; p.w = decay_logits; p.k = k; p.v = v; p.a = a; p.b = b;
+  p.scale = scale;
+  p.state = state;
+  p.y = output;
+  p.sa = state_dot_a;
+  p.boundary = boundary;
+  return fr2::launch_statetune_padded_forward(batch, padded_tokens, num_heads, num_chunks,
+                                              row_source, chunk_seq, chunk_pstart, p, snapshots,
+                                              workspace, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fr2_wkv7_statetune_padded_backward(
+    int32_t batch, int32_t padded_tokens, int32_t num_heads, const int32_t* row_source,
+    const int32_t* seq_first_chunk, const void* r, const void* decay_logits, const void* k,
+    const void* v, const void* a, const void* b, const float* state_dot_a,
+    const void* grad_output, const float* grad_final_state, const float* boundary,
+    const float* snapshots, void* workspace, void* grad_r, void* grad_decay_logits,
+    void* grad_k, void* grad_v, void* grad_a, void* grad_b, float* grad_initial_state,
+    float scale, void* stream) {
+  if (!tokens_ok(r, decay_logits, k, v, a, b, grad_output) || !state_dot_a || !boundary ||
+      !snapshots || !workspace || !aligned16(workspace) || !row_source || !seq_first_chunk ||
+      !grad_initial_state || !params_aligned({grad_r, grad_decay_logits, grad_k, grad_v, grad_a,
+                                              grad_b, state_dot_a}) ||
+      !grad_r || !grad_decay_logits || !grad_k || !grad_v || !grad_a || !grad_b)
+    return FR2_ERR_INVALID_ARGUMENT;
+  if (batch <= 0 || batch > 65535 || padded_tokens <= 0 || padded_tokens % 16 != 0 ||
+      num_heads <= 0)
+    return FR2_ERR_INVALID_ARGUMENT;
+  fr2::StateTuneArgs p;
+  p.heads = num_heads;
+  p.r = r; p.w = decay_logits; p.k = k; p.v = v; p.a = a; p.b = b;
+  p.scale = scale;
+  p.sa = const_cast<float*>(state_dot_a);
+  p.boundary = const_cast<float*>(boundary);
+  p.dy = grad_output;
+  p.dfinal = grad_final_state;
+  p.dr = grad_r; p.dw = grad_decay_logits; p.dk = grad_k; p.dv = grad_v;
+  p.da = grad_a; p.db = grad_b;
+  p.dstate0 = grad_initial_state;
+  return fr2::launch_statetune_padded_backward(batch, padded_tokens, num_heads, row_source,
+                                               seq_first_chunk, p, snapshots, workspace,
+                                               static_cast<hipStream_t>(stream));
+}
+
 // ---------------------------------------------------------------------------
 // producer / consumer stages of the layer (fp16)
 // ---------------------------------------------------------------------------

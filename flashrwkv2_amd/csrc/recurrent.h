@@ -250,6 +250,19 @@ int launch_statetune_uniform_forward(int B, int T, int H, int chunk_len, const S
                                      float* snap, hipStream_t s);
 int launch_statetune_uniform_backward(int B, int T, int H, int chunk_len, const StateTuneArgs& a,
                                       const float* snap, float* workspace, hipStream_t s);
+// Any chunk list at D = 64, bf16, on the chunked MFMA kernels: the chunks of
+// sequence b laid out from padded row b * Tp on, each starting on a 16-token
+// boundary, identity tokens in between (row_source [B*Tp]: packed row or -1;
+// chunk_seq / chunk_pstart [C]: each chunk's sequence and padded start).
+// snap [B,H,Tp/16,64,64]; ws of statetune_padded_workspace_bytes bytes.
+int64_t statetune_padded_workspace_bytes(int B, int Tp, int H, bool backward);
+int launch_statetune_padded_forward(int B, int Tp, int H, int C, const int32_t* row_source,
+                                    const int32_t* chunk_seq, const int32_t* chunk_pstart,
+                                    const StateTuneArgs& a, float* snap, void* ws, hipStream_t s);
+// seq_first_chunk [B]: the index of each sequence's first chunk, -1 if none
+int launch_statetune_padded_backward(int B, int Tp, int H, const int32_t* row_source,
+                                     const int32_t* seq_first_chunk, const StateTuneArgs& a,
+                                     const float* snap, void* ws, hipStream_t s);
 
 // Elementwise producer / consumer stages of the layer (fp16 I/O).
 int launch_kk_a_gate(int64_t tokens, int H, int D, const void* k, const void* k_k, const void* a0,

@@ -524,6 +524,107 @@ __global__ __launch_bounds__(256) void st_gather_kernel(int H, int nck, int chun
     reinterpret_cast<f4*>(dst)[x] = reinterpret_cast<const f4*>(src)[x];
 }
 
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// ---- ragged chunk lists on the chunked kernels (the padded layout) ----
+// Each sequence's chunks are laid out back to back in a [B, Tp] token grid,
+// every chunk starting on a 16-token boundary; the rows in between (and at
+// the end of a sequence) hold identity tokens (r = k = v = a = b = 0 and a
+// decay logit of -80, whose retention is exactly 1 in fp32), which leave the
+// state, and the backward's adjoint, exactly unchanged.  row_source[pr] is
+// the packed token row of padded row pr, or -1 for an identity row.
+
+// dst[n][pr] = src[n][row_source[pr]] (16-byte pieces of a row of row_bytes),
+// or the fill pattern for identity rows; n < ntens.
+struct PadRowsArgs {
+  const void* src[8];
+  void* dst[8];
+  uint32_t fill[8];   // 32-bit fill pattern of identity rows
+  int ntens = 0;
+};
+__global__ __launch_bounds__(256) void pad_rows_kernel(PadRowsArgs a, const int32_t* row_source,
+                                                       int64_t rows, int row_pieces) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= rows * row_pieces) return;
+  const int64_t pr = idx / row_pieces;
+  const int piece = static_cast<int>(idx - pr * row_pieces);
+  const int32_t srow = row_source[pr];
+  for (int n = 0; n < a.ntens; ++n) {
+    u4 val;
+    if (srow >= 0) {
+      val = reinterpret_cast<const u4*>(a.src[n])[static_cast<int64_t>(srow) * row_pieces + piece];
+    } else {
+      val = u4{a.fill[n], a.fill[n], a.fill[n], a.fill[n]};
+    }
+    reinterpret_cast<u4*>(a.dst[n])[pr * row_pieces + piece] = val;
+  }
+}
+// dst[n][row_source[pr]] = src[n][pr] for the rows that have a source
+__global__ __launch_bounds__(256) void unpad_rows_kernel(PadRowsArgs a, const int32_t* row_source,
+                                                         int64_t rows, int row_pieces) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= rows * row_pieces) return;
+  const int64_t pr = idx / row_pieces;
+  const int piece = static_cast<int>(idx - pr * row_pieces);
+  const int32_t srow = row_source[pr];
+  if (srow < 0) return;
+  for (int n = 0; n < a.ntens; ++n)
+    reinterpret_cast<u4*>(a.dst[n])[static_cast<int64_t>(srow) * row_pieces + piece] =
+        reinterpret_cast<const u4*>(a.src[n])[pr * row_pieces + piece];
+}
+
+// boundary[c] = the state at padded position chunk_pstart[c] of sequence
+// chunk_seq[c]: the initial state when that is 0 (first pass, before the
+// forward replaces it), else the post-16-token snapshot ending there
+__global__ __launch_bounds__(256) void st_gather_padded_kernel(
+    int H, const int32_t* chunk_seq, const int32_t* chunk_pstart, bool first, const float* state,
+    const float* snap, int snaps_per_seq, float* boundary) {
+  constexpr int DD = 64 * 64;
+  const int c = blockIdx.x / H, h = blockIdx.x % H;
+  const int b = chunk_seq[c], ps = chunk_pstart[c];
+  if ((ps == 0) != first) return;
+  const float* src =
+      ps == 0 ? state + (static_cast<int64_t>(b) * H + h) * DD
+              : snap + ((static_cast<int64_t>(b) * H + h) * snaps_per_seq + ps / 16 - 1) * DD;
+  float* dst = boundary + static_cast<int64_t>(blockIdx.x) * DD;
+  for (int x = threadIdx.x; x < DD / 4; x += 256)
+    reinterpret_cast<f4*>(dst)[x] = reinterpret_cast<const f4*>(src)[x];
+}
+
+// init[b] = boundary[seq_first_chunk[b]] (its initial state), or zeros for a
+// sequence without chunks (its rows are all identity tokens)
+__global__ __launch_bounds__(256) void st_initial_states_kernel(int H,
+                                                                const int32_t* seq_first_chunk,
+                                                                const float* boundary,
+                                                                float* init) {
+  constexpr int DD = 64 * 64;
+  const int b = blockIdx.x / H, h = blockIdx.x % H;
+  const int c = seq_first_chunk[b];
+  float* dst = init + static_cast<int64_t>(blockIdx.x) * DD;
+  for (int x = threadIdx.x; x < DD / 4; x += 256)
+    reinterpret_cast<f4*>(dst)[x] =
+        c >= 0 ? reinterpret_cast<const f4*>(boundary + (static_cast<int64_t>(c) * H + h) * DD)[x]
+               : f4{0.f, 0.f, 0.f, 0.f};
+}
+
+// bf16 fill patterns of the identity rows
+constexpr uint32_t kZeroPair = 0u;
+constexpr uint32_t kIdentityLogitPair = 0xC2A0C2A0u;   // bf16 -80.0 twice
+
+int pad_rows(const PadRowsArgs& a, const int32_t* row_source, int64_t rows, int row_pieces,
+             bool unpad, hipStream_t s) {
+  const int64_t n = rows * row_pieces;
+  const int64_t blocks = (n + 255) / 256;
+  if (blocks > 0x7fffffff) return FR2_ERR_INVALID_ARGUMENT;
+  if (unpad)
+    hipLaunchKernelGGL(unpad_rows_kernel, dim3(blocks), dim3(256), 0, s, a, row_source, rows,
+                       row_pieces);
+  else
+    hipLaunchKernelGGL(pad_rows_kernel, dim3(blocks), dim3(256), 0, s, a, row_source, rows,
+                       row_pieces);
+  return FR2_OK;
+}
+
 }  // namespace
 
 int launch_statetune_uniform_forward(int B, int T, int H, int chunk_len, const StateTuneArgs& a,
@@ -597,6 +698,131 @@ int launch_statetune_backward(int D, int dtype, StateTuneArgs p, float* workspac
     case 256: return bf ? backward_d<256, IoBF16>(p, s) : backward_d<256, IoF16>(p, s);
     default: return FR2_ERR_UNSUPPORTED;
   }
+}
+
+int64_t statetune_padded_workspace_bytes(int B, int Tp, int H, bool backward) {
+  const int64_t rows = static_cast<int64_t>(B) * Tp, row = static_cast<int64_t>(H) * 64;
+  if (!backward) return rows * row * (7 * 2 + 4);   // r w k v a b y (bf16), sa (fp32)
+  // r w k v a b dy and the six gradients (bf16), sa (fp32), the initial
+  // states, then the pretrain backward's own workspace
+  return rows * row * (13 * 2 + 4) + static_cast<int64_t>(B) * H * 64 * 64 * 4 +
+         (pretrain_backward_workspace_floats(B, Tp, H, 64) + static_cast<int64_t>(B) * H * 64 * 64) *
+             4;
+}
+
+int launch_statetune_padded_forward(int B, int Tp, int H, int C, const int32_t* row_source,
+                                    const int32_t* chunk_seq, const int32_t* chunk_pstart,
+                                    const StateTuneArgs& a, float* snap, void* ws,
+                                    hipStream_t s) {
+  const int64_t rows = static_cast<int64_t>(B) * Tp;
+  const int64_t row = static_cast<int64_t>(H) * 64;
+  const int pieces = static_cast<int>(row * 2 / 16);   // 16-byte pieces of a bf16 row
+  char* w = static_cast<char*>(ws);
+  void* pad[7];
+  for (int n = 0; n < 7; ++n) pad[n] = w + n * rows * row * 2;
+  float* sa_pad = reinterpret_cast<float*>(w + 7 * rows * row * 2);
+  PadRowsArgs g;
+  const void* src[6] = {a.r, a.w, a.k, a.v, a.a, a.b};
+  for (int n = 0; n < 6; ++n) {
+    g.src[n] = src[n];
+    g.dst[n] = pad[n];
+    g.fill[n] = n == 1 ? kIdentityLogitPair : kZeroPair;
+  }
+  g.ntens = 6;
+  int rc = pad_rows(g, row_source, rows, pieces, false, s);
+  if (rc != FR2_OK) return rc;
+  const int64_t cblocks = static_cast<int64_t>(C) * H;
+  if (cblocks > 0x7fffffff) return FR2_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(st_gather_padded_kernel, dim3(cblocks), dim3(256), 0, s, H, chunk_seq,
+                     chunk_pstart, true, a.state, snap, Tp / 16, a.boundary);
+  SegArgs v;
+  v.uniform_len = Tp;
+  v.num_heads = H;
+  v.out_elems = rows * row;
+  v.state_in = a.state;
+  v.state_out = a.state;
+  v.r = pad[0]; v.logits = pad[1]; v.k = pad[2]; v.v = pad[3]; v.a = pad[4]; v.b = pad[5];
+  v.y = pad[6];
+  v.sa_out = sa_pad;
+  v.boundary = snap;
+  v.boundary_len = 16;
+  v.boundary_per_seg = Tp / 16;
+  v.scale = a.scale;
+  rc = launch_chunked(FR2_DTYPE_BFLOAT16, v, B, Tp, s);
+  if (rc != FR2_OK) return rc;
+  hipLaunchKernelGGL(st_gather_padded_kernel, dim3(cblocks), dim3(256), 0, s, H, chunk_seq,
+                     chunk_pstart, false, a.state, snap, Tp / 16, a.boundary);
+  // y and sa back to the packed rows
+  PadRowsArgs u;
+  u.src[0] = pad[6];
+  u.dst[0] = a.y;
+  u.ntens = 1;
+  rc = pad_rows(u, row_source, rows, pieces, true, s);
+  if (rc != FR2_OK) return rc;
+  u.src[0] = sa_pad;
+  u.dst[0] = a.sa;
+  rc = pad_rows(u, row_source, rows, pieces * 2, true, s);
+  if (rc != FR2_OK) return rc;
+  return record_launch();
+}
+
+int launch_statetune_padded_backward(int B, int Tp, int H, const int32_t* row_source,
+                                     const int32_t* seq_first_chunk, const StateTuneArgs& a,
+                                     const float* snap, void* ws, hipStream_t s) {
+  const int64_t rows = static_cast<int64_t>(B) * Tp;
+  const int64_t row = static_cast<int64_t>(H) * 64;
+  const int pieces = static_cast<int>(row * 2 / 16);
+  char* w = static_cast<char*>(ws);
+  void* pad[13];   // r w k v a b dy, then dr dw dk dv da db
+  for (int n = 0; n < 13; ++n) pad[n] = w + n * rows * row * 2;
+  float* sa_pad = reinterpret_cast<float*>(w + 13 * rows * row * 2);
+  float* init = sa_pad + rows * row;
+  float* bws = init + static_cast<int64_t>(B) * H * 64 * 64;
+  PadRowsArgs g;
+  const void* src[7] = {a.r, a.w, a.k, a.v, a.a, a.b, a.dy};
+  for (int n = 0; n < 7; ++n) {
+    g.src[n] = src[n];
+    g.dst[n] = pad[n];
+    g.fill[n] = n == 1 ? kIdentityLogitPair : kZeroPair;
+  }
+  g.ntens = 7;
+  int rc = pad_rows(g, row_source, rows, pieces, false, s);
+  if (rc != FR2_OK) return rc;
+  PadRowsArgs gs;
+  gs.src[0] = a.sa;
+  gs.dst[0] = sa_pad;
+  gs.fill[0] = 0u;
+  gs.ntens = 1;
+  rc = pad_rows(gs, row_source, rows, pieces * 2, false, s);
+  if (rc != FR2_OK) return rc;
+  hipLaunchKernelGGL(st_initial_states_kernel, dim3(B * H), dim3(256), 0, s, H, seq_first_chunk,
+                     a.boundary, init);
+  PretrainBwdArgs p;
+  p.batch = B; p.tokens = Tp; p.heads = H;
+  p.r = pad[0]; p.w = pad[1]; p.k = pad[2]; p.v = pad[3]; p.a = pad[4]; p.b = pad[5];
+  p.dy = pad[6];
+  p.boundary = snap;
+  p.state_dot_a = sa_pad;
+  p.workspace = bws;
+  p.dr = pad[7]; p.dw = pad[8]; p.dk = pad[9]; p.dv = pad[10]; p.da = pad[11]; p.db = pad[12];
+  p.scale = a.scale;
+  p.state0 = init;
+  p.state0_stride = static_cast<int64_t>(H) * 64 * 64;
+  p.dfinal = a.dfinal;
+  p.dstate0 = a.dstate0;
+  p.pfirst = bws + pretrain_backward_workspace_floats(B, Tp, H, 64);
+  rc = launch_pretrain_backward(64, p, s);
+  if (rc != FR2_OK) return rc;
+  PadRowsArgs u;
+  void* dst[6] = {a.dr, a.dw, a.dk, a.dv, a.da, a.db};
+  for (int n = 0; n < 6; ++n) {
+    u.src[n] = pad[7 + n];
+    u.dst[n] = dst[n];
+  }
+  u.ntens = 6;
+  rc = pad_rows(u, row_source, rows, pieces, true, s);
+  if (rc != FR2_OK) return rc;
+  return record_launch();
 }
 
 }  // namespace fr2

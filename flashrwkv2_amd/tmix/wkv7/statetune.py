@@ -77,12 +77,14 @@ class _StateTuneWKV7(torch.autograd.Function):
         out = torch.empty_like(v)
         boundary = state.new_empty((starts.numel(),) + tuple(state.shape[1:]))
         sa = torch.empty_like(r, dtype=torch.float32)
-        # On the uniform layout (D = 64, bf16, equal sequences and chunks) the
-        # native forward runs the chunked MFMA kernels and also returns the
-        # post-16-token state snapshots its backward reads; otherwise None.
+        # At D = 64 in bf16 the native forward runs the chunked MFMA kernels
+        # and also returns what its backward reads: the post-16-token state
+        # snapshots (uniform layout) or those plus the padded grid's tables
+        # (other chunk lists); otherwise None.
         snapshots = _extension().statetune_tmix_wkv7_recurrent_fp32io16_forward(
             offsets, starts, ends, state, *tokens, out, boundary, sa, scale)
-        extra = () if snapshots is None else (snapshots,)
+        extra = () if snapshots is None else tuple(snapshots) if isinstance(snapshots, tuple) \
+            else (snapshots,)
         ctx.scale = scale
         ctx.save_for_backward(offsets, starts, ends, state, *tokens, sa, boundary, *extra)
         ctx.mark_non_differentiable(boundary, sa)
@@ -100,7 +102,8 @@ class _StateTuneWKV7(torch.autograd.Function):
         d_initial = torch.empty_like(final)
         _extension().statetune_tmix_wkv7_recurrent_fp32io16_backward(
             offsets, starts, ends, final, *tokens, sa, d_out, d_final, boundary, *d_tokens,
-            d_initial, ctx.scale, snapshots=extra[0] if extra else None)
+            d_initial, ctx.scale,
+            snapshots=None if not extra else extra[0] if len(extra) == 1 else tuple(extra))
         return (None, d_initial, None, None, None, *d_tokens)
 
 

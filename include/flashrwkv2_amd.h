@@ -572,6 +572,51 @@ int fr2_wkv7_statetune_uniform_backward(
     void* grad_decay_logits, void* grad_k, void* grad_v, void* grad_a, void* grad_b,
     float* grad_initial_state, float scale, void* stream);
 
+/*
+ * StateTune over any chunk list (ragged, empty or gapped chunks) at
+ * head_size 64 with bf16 tokens, on the chunked MFMA kernels: each
+ * sequence's chunks are laid out back to back in a [batch, padded_tokens]
+ * token grid (padded_tokens a multiple of 16), every chunk starting on a
+ * 16-token boundary, with identity tokens in between (zero r, k, v, a, b and
+ * a decay logit of -80, whose retention is 1 in fp32: the state and the
+ * adjoint pass them unchanged).  row_source [batch * padded_tokens] maps a
+ * grid row to its packed token row, or -1 for an identity row;
+ * chunk_seq / chunk_pstart [num_chunks] give each chunk's sequence and its
+ * start in the grid.  The caller (the host, from the chunk metadata) builds
+ * the three tables.  Outputs as fr2_wkv7_statetune_forward, plus snapshots
+ * [batch, H, padded_tokens/16, 64, 64] fp32 for the backward; workspace of
+ * fr2_wkv7_statetune_padded_workspace_bytes(..., 0) bytes (16-byte
+ * aligned).  Token rows that belong to no chunk are not written.
+ * Same reference interface as fr2_wkv7_statetune_forward
+ * (csrc/sm120/tmix/wkv7/statetune_recurrent_fp32io16_forward.cpp:26-56).
+ */
+int64_t fr2_wkv7_statetune_padded_workspace_bytes(int32_t batch, int32_t padded_tokens,
+                                                  int32_t num_heads, int32_t backward);
+int fr2_wkv7_statetune_padded_forward(
+    int32_t batch, int32_t padded_tokens, int32_t num_heads, int32_t num_chunks,
+    const int32_t* row_source, const int32_t* chunk_seq, const int32_t* chunk_pstart,
+    float* state, const void* r, const void* decay_logits, const void* k, const void* v,
+    const void* a, const void* b, void* output, float* boundary, float* state_dot_a,
+    float* snapshots, void* workspace, float scale, void* stream);
+
+/*
+ * Backward of fr2_wkv7_statetune_padded_forward on the same grid
+ * (seq_first_chunk [batch]: each sequence's first chunk, -1 if it has none);
+ * grad_output and every gradient are required; workspace of
+ * fr2_wkv7_statetune_padded_workspace_bytes(..., 1) bytes.  Gradient rows of
+ * tokens that belong to no chunk are not written.
+ * Same reference interface as fr2_wkv7_statetune_backward
+ * (csrc/sm120/tmix/wkv7/statetune_recurrent_fp32io16_backward.cpp:34-82).
+ */
+int fr2_wkv7_statetune_padded_backward(
+    int32_t batch, int32_t padded_tokens, int32_t num_heads, const int32_t* row_source,
+    const int32_t* seq_first_chunk, const void* r, const void* decay_logits, const void* k,
+    const void* v, const void* a, const void* b, const float* state_dot_a,
+    const void* grad_output, const float* grad_final_state, const float* boundary,
+    const float* snapshots, void* workspace, void* grad_r, void* grad_decay_logits,
+    void* grad_k, void* grad_v, void* grad_a, void* grad_b, float* grad_initial_state,
+    float scale, void* stream);
+
 /* ------------------------------------------------------------------------
  * Producer and consumer stages of the WKV7 path (fp16 tensors, fp32 math).
  * ---------------------------------------------------------------------- */

@@ -285,9 +285,9 @@ def test_statetune_uniform_layout_runs_chunked_kernels(B, per_seq, length, scale
 
 
 def test_statetune_uniform_autograd_and_fallbacks():
-    """The public function takes the chunked path on the uniform layout
-    (its results match the oracle); an fp16 or a ragged layout of the same
-    tokens falls back to the token-serial kernels with the same results."""
+    """The public function takes the chunked path on the uniform layout and
+    the padded chunked path on a ragged layout of the same tokens; both match
+    the oracle and each other."""
     require_gpu()
     g = torch.Generator().manual_seed(77)
     B, per_seq, length, H, D = 2, 96, 32, 2, 64
@@ -307,3 +307,72 @@ def test_statetune_uniform_autograd_and_fallbacks():
         _check_strong(runs[name], ref, ("y", "dstate0", *TOKEN_GRADS))
     for key in ("y", "state", "dstate0", *TOKEN_GRADS):
         assert relative_rmse(to_np(runs["uniform"][key]), to_np(runs["ragged"][key])) <= 1e-2, key
+
+
+def _ragged_meta(B, per_seq, rng, gap=0):
+    """B sequences of per_seq tokens packed back to back, each cut into
+    chunks of random lengths (some empty, some not a multiple of 16), with
+    `gap` tokens at the end of every sequence in no chunk."""
+    offsets, starts, ends = [0], [], []
+    for b in range(B):
+        t, end = b * per_seq, (b + 1) * per_seq - gap
+        while t < end:
+            n = min(int(rng.integers(0, 300)), end - t)
+            starts.append(t)
+            ends.append(t + n)
+            t += n
+        offsets.append(len(starts))
+    return _meta(offsets, starts, ends)
+
+
+@pytest.mark.parametrize("B,per_seq,H,gap", [(3, 700, 2, 0), (2, 1500, 3, 37)])
+def test_statetune_ragged_chunk_list_runs_the_padded_chunked_path(B, per_seq, H, gap):
+    """A ragged chunk list at D = 64 in bf16 runs on the chunked MFMA kernels
+    over the padded grid (the forward returns the grid's tables); forward,
+    final state, boundaries and every gradient match the fp64 oracle and the
+    token-serial kernels on the same inputs."""
+    C = require_gpu()
+    import flashrwkv2_amd._C as CC
+
+    rng = np.random.default_rng(B * per_seq + gap)
+    g = torch.Generator().manual_seed(B * per_seq + H)
+    D, T = 64, B * per_seq
+    vals = _structured(T, H, D, torch.bfloat16, g, logit_scale=1.5)
+    state0 = (torch.randn((B, H, D, D), generator=g) * 0.5).cuda()
+    meta = _ragged_meta(B, per_seq, rng, gap)
+    print(f"case statetune ragged B={B} T={per_seq} H={H} gap={gap} chunks={meta[1].numel()}",
+          flush=True)
+    dy = torch.randn((T, H, D), generator=g).to(torch.bfloat16).cuda()
+    dfin = torch.randn((B, H, D, D), generator=g).cuda()
+    # the forward takes the padded path (tables returned for the backward)
+    st = state0.clone()
+    probe = C.statetune_tmix_wkv7_recurrent_fp32io16_forward(
+        *meta, st, *vals, torch.empty_like(vals[3]),
+        torch.empty((meta[1].numel(), H, D, D), device="cuda"),
+        torch.empty((T, H, D), device="cuda"), 1.0)
+    assert isinstance(probe, tuple) and len(probe) == 3
+    runs = {}
+    for name, serial in (("padded", False), ("serial", True)):
+        CC._statetune_force_serial = serial
+        try:
+            state, leaves, (y, fin, bnd, sa) = _run(state0, meta, vals, 1.0)
+            torch.autograd.backward([y, fin], [dy, dfin])
+            torch.cuda.synchronize()
+        finally:
+            CC._statetune_force_serial = False
+        runs[name] = {"y": y, "sa": sa, "state": fin, "boundary": bnd, **_grads(state, leaves)}
+    ref = _oracle(state0, meta, vals, 1.0, dy=dy, dfinal=dfin)
+    starts, ends = meta[1].cpu().numpy(), meta[2].cpu().numpy()
+    used = np.concatenate([np.arange(s0, e0) for s0, e0 in zip(starts, ends)])
+    got = runs["padded"]
+    _check_strong({k: got[k][used] for k in ("y", "sa")}, {k: ref[k][used] for k in ("y", "sa")},
+                  ("y", "sa"), rel=5e-3)
+    for key in ("state", "boundary"):
+        assert relative_rmse(to_np(got[key]), ref[key]) <= 2e-3, key
+    _check_strong({k: got[k][used] for k in TOKEN_GRADS}, {k: ref[k][used] for k in TOKEN_GRADS},
+                  TOKEN_GRADS)
+    _check_strong(got, ref, ("dstate0",))
+    for key in ("y", "sa", *TOKEN_GRADS):
+        assert relative_rmse(to_np(got[key][used]), to_np(runs["serial"][key][used])) <= 1e-2, key
+    for key in ("state", "boundary", "dstate0"):
+        assert relative_rmse(to_np(got[key]), to_np(runs["serial"][key])) <= 1e-2, key
