@@ -36,10 +36,12 @@ HBM_PEAK_GBS = 8000.0
 BYTES_PER_TOKEN_HEAD = 896          # 6 bf16 inputs x 64 + bf16 output x 64
 STATE_BYTES = 64 * 64 * 4           # one fp32 64x64 state
 MFMA_PEAK_TFLOPS = 2500.0           # dense bf16
-# v_mfma_f32_16x16x32_bf16 instructions the chunked kernel issues per 16-token
-# chunk of one head: 24 token-token products + 16 for T on the key side, 4 x 30
-# on the state side (bf16 hi/lo split products)
-MFMA_PER_CHUNK = 160
+# v_mfma_f32_16x16x32_bf16 instructions the ring chunked kernel issues per
+# 16-token chunk of one head: 30 token-token products (5 products x 3 split
+# terms x 2 key halves) + 16 for T on the key side, 4 x 30 on the state side
+# (bf16 hi/lo split products); rocprofv3 SQ_INSTS_MFMA reads 166 x 65 536
+# chunks per config-1 dispatch
+MFMA_PER_CHUNK = 166
 MFMA_FLOPS = 16 * 16 * 32 * 2
 
 
@@ -510,7 +512,7 @@ def time_kk_fused(torch, flashrwkv2_amd, steps: int, serving: bool = False):
     else:
         w = workloads.config(1, "cuda", dtype=torch.float16)
         rec_kernel, kk_kernel, ro_kernel = (
-            "chunk64_kernel<IoF16,false>", "chunk64_kernel<IoF16,false,false,false,true>",
+            "chunk64r_kernel<IoF16>", "chunk64_kernel<IoF16,false,false,false,true>",
             "chunk64_kernel<IoF16,false,false,false,true,true>")
         name = "cfg1_prefill_B8_T4096_H32_fp16_kk_gate"
     T, H, D = w.total_tokens, w.num_heads, 64
@@ -631,14 +633,14 @@ def time_long_context(torch, flashrwkv2_amd, steps: int):
     out = {
         "workload": w.name, "ms_per_step": round(ms, 4),
         "tokens_per_s": round(w.total_tokens / (ms * 1e-3), 1),
-        "kernels": "chunk64_kernel piece 0 (second stream) concurrent with the summary pass, "
-                   "split_combine_kernel, chunk64_kernel pieces 1..P-1",
+        "kernels": "chunk64r_kernel piece 0 (second stream) concurrent with the summary pass "
+                   "(chunk64_kernel), split_combine_kernel, chunk64r_kernel pieces 1..P-1",
         "pieces": pieces, "piece_len": piece_len, "lead_len": lead_len, "workspace_bytes": ws,
         "roofline": roofline_obj(nbytes, ms, measured_traffic(
             "split:lead+summary+combine+pieces", w.name)),
         "unsplit": {"ms_per_step": round(unsplit_ms, 4),
                     "tokens_per_s": round(w.total_tokens / (unsplit_ms * 1e-3), 1),
-                    "kernel": "chunk64_kernel<IoBF16,false> (one block per head)",
+                    "kernel": "chunk64r_kernel<IoBF16> (one block per head)",
                     "roofline": roofline_obj(nbytes, unsplit_ms)},
         "algorithmic_bytes": nbytes,
     }
@@ -686,7 +688,7 @@ def time_mid_length(torch, flashrwkv2_amd, steps: int, n: int = 2048, length: in
     kms = run.time_kernel(steps)
     nbytes = algorithmic_bytes(w.total_tokens, w.num_heads, w.state_indices.numel())
     forced = {}
-    for kern, name in ((0, "serial64w_kernel<IoBF16,StF32>"), (2, "chunk64_kernel<IoBF16,false>"),
+    for kern, name in ((0, "serial64w_kernel<IoBF16,StF32>"), (2, "chunk64r_kernel<IoBF16>"),
                        (4, "chunk64w_kernel<IoBF16,false>")):
         f = lambda k=kern: run.C.tmix_wkv7_recurrent_fp32_kernel_forced(
             k, w.cu_seqlens, w.state_indices, run.state, *w.tokens, run.out, 1.0, None,
@@ -726,7 +728,7 @@ def time_short_batches(torch, flashrwkv2_amd, steps: int, heads: int = 32):
         forced = {}
         for kern, name in ((0, "serial64w_kernel<IoBF16,StF32>"),
                            (1, "decode64_kernel<IoBF16,StF32>"),
-                           (2, "chunk64_kernel<IoBF16,false>"),
+                           (2, "chunk64r_kernel<IoBF16>"),
                            (4, "chunk64w_kernel<IoBF16,false>")):
             f = lambda k=kern: run.C.tmix_wkv7_recurrent_fp32_kernel_forced(
                 k, w.cu_seqlens, w.state_indices, run.state, *w.tokens, run.out, 1.0, None,
@@ -1212,7 +1214,7 @@ def mfma_obj(w, kernel_ms: float):
     # (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs), the MfmaUtil metric)
     path = ROOT / "profiles" / "mfma_counters.json"
     if path.exists():
-        m = json.loads(path.read_text()).get("chunk64_kernel<IoBF16,false>")
+        m = json.loads(path.read_text()).get("chunk64r_kernel<IoBF16>")
         if m is not None and m.get("workload") == w.name:
             out["measured_util"] = m["mfma_util"]
             out["measured_sclk_mhz"] = m["effective_sclk_mhz"]

@@ -133,6 +133,14 @@ def _set_handoff_stall(on: bool) -> None:
     N.check(N.load().fr2_debug_set_handoff_stall(int(bool(on))), "fr2_debug_set_handoff_stall")
 
 
+def _set_chunk_ring(on: bool) -> None:
+    """Test hook: selects the workgroup chunked kernel's variant for later
+    fp32-state launches: True = one key wave per whole chunk over a ring of
+    four chunk operator blocks (the default), False = two key waves per chunk
+    with the token-token blocks summed through LDS."""
+    N.check(N.load().fr2_debug_set_chunk_ring(int(bool(on))), "fr2_debug_set_chunk_ring")
+
+
 # ---------------------------------------------------------------------------
 # Metadata tickets
 # ---------------------------------------------------------------------------
@@ -670,7 +678,7 @@ def _library_split_plan(num_sequences: int, num_heads: int, head_size: int,
 _FAMILY_KERNELS = {
     N.KERNEL_SERIAL: "serial64w_kernel<{io},StF32>",
     N.KERNEL_DECODE: "decode64_kernel<{io},StF32>",
-    N.KERNEL_CHUNKED: "chunk64_kernel<{io},false>",
+    N.KERNEL_CHUNKED: "chunk64r_kernel<{io}>",
     N.KERNEL_CHUNKED_WAVE: "chunk64w_kernel<{io},false>",
     5: "chunk64w_kernel<{io},true>",
 }

@@ -41,6 +41,7 @@ SIGNATURES: dict[str, tuple] = {
     "fr2_handoff_fault_count": (c_int32, [_i32p, c_int32, c_void_p]),
     "fr2_debug_set_handoff_spin_limit": (c_int32, [c_int32]),
     "fr2_debug_set_handoff_stall": (c_int32, [c_int32]),
+    "fr2_debug_set_chunk_ring": (c_int32, [c_int32]),
     "fr2_wkv7_prepare_metadata": (
         c_int32,
         [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p,

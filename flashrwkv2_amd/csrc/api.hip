@@ -1067,6 +1067,14 @@ extern "C" int fr2_debug_set_handoff_spin_limit(int32_t polls) {
   return FR2_OK;
 }
 
+// Variant switch of the workgroup-per-unit chunked kernel for the plain
+// contract (0: two key waves per chunk, 1: one key wave per chunk, a ring
+// of four chunks): for measuring the two against each other.
+extern "C" int fr2_debug_set_chunk_ring(int32_t on) {
+  fr2::set_chunk_ring(on);
+  return FR2_OK;
+}
+
 // Test hook: while on, the chunked kernel's key waves never publish their
 // operators to the state waves, so every block stalls at its first
 // operator wait and, after the spin limit, fails closed; every kernel still

@@ -1094,6 +1094,341 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
 
 }
 
+
+// ===========================================================================
+// Ring variant of the workgroup-per-unit kernel (plain inference contract).
+// Each key wave builds WHOLE chunks: key wave w (4..7) takes chunks
+// w - 4, w, w + 4, ... of the unit, both key halves one after the other,
+// accumulating the token-token blocks over all 64 keys in its own matrix
+// accumulators, then forms T and the masked blocks itself.  So no partial
+// blocks go through LDS and no key wave waits on a partner; operator blocks
+// are a ring of four chunks in LDS (chunk c in slot c % 4), and a key wave
+// may build chunk c as soon as the state waves have finished chunk c - 4,
+// three chunk periods ahead of its use.  The state waves run chunk after
+// chunk as in chunk64_kernel.
+// ===========================================================================
+template <bool kVExact>
+struct alignas(16) SmemR {
+  ChunkOps<kVExact> ops[4];           // ring by chunk index mod 4
+  uint16_t yb[4][L][YP];              // staged outputs by chunk index mod 4
+  // progress counters, each written by one wave only: chunks key wave w has
+  // built (its chunks are w, w + 4, ...), chunks state wave w has finished,
+  // chunks whose output rows state wave w has written back
+  int ready[4], consumed[4], drained[4];
+  int fault;
+};
+
+// Token-token products of the whole chunk, accumulated over both key halves:
+// ab = Mab in accumulator layout (item e: Mab[4q+e][i]); abt, ak, rb, rk in
+// A-operand layout (item e: X[i][4q+e]).
+struct KeyAccR {
+  f32x4 ab, abt, ak, rb, rk;
+};
+
+// One key half hh of chunk operators: as key_part1 (plain contract) plus the
+// operand-row stores of key_part2, with the token-token products accumulated.
+template <class Io, bool kVExact, bool kFull>
+__device__ __forceinline__ void key_half_ring(ChunkOps<kVExact>& op, const u32x4 (&raw)[6],
+                                              const float (&nbias8)[8], bool valid, int hh,
+                                              int i, int q, KeyAccR& acc) {
+  const int kbase = 32 * hh + 8 * q;
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
+  auto tok = [&](int j) { return (kFull || valid) ? raw[j] : zero4; };
+  float xr[8], xl[8], xk[8], xa[8], xb[8];
+  unpack8<Io>(tok(0), xr);
+  unpack8<Io>(raw[1], xl);
+  unpack8<Io>(tok(2), xk);
+  unpack8<Io>(tok(4), xa);
+  unpack8<Io>(tok(5), xb);
+  constexpr float kC = kNegExpHalf * kLog2e;
+  constexpr float kInvC = 1.0f / kC;
+  float g2[8], gm[8], gp[8], at[8], rt[8], bh[8], kh[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    g2[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(xl[e], -kLog2e, nbias8[e]));
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float lw2 = __builtin_amdgcn_rcpf(__builtin_fmaf(g2[e], kInvC, kInvC));
+    if constexpr (!kFull) lw2 = valid ? lw2 : 0.0f;
+    g2[e] = lw2;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) g2[e] += row_shr<1>(g2[e]);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) g2[e] += row_shr<2>(g2[e]);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) g2[e] += row_shr<4>(g2[e]);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) g2[e] += row_shr<8>(g2[e]);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) gm[e] = __builtin_amdgcn_exp2f(g2[e]);      // gamma_t
+#pragma unroll
+  for (int e = 0; e < 8; ++e) gp[e] = row_prev(gm[e], 1.0f);              // gamma_{t-1}
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float ig = __builtin_amdgcn_exp2f(-g2[e]);                     // 1 / gamma_t
+    at[e] = xa[e] * gp[e];
+    rt[e] = xr[e] * gm[e];
+    bh[e] = xb[e] * ig;
+    kh[e] = xk[e] * ig;
+  }
+  if (i == L - 1) {
+    *reinterpret_cast<f32x4*>(&op.gl[kbase]) = f32x4{gm[0], gm[1], gm[2], gm[3]};
+    *reinterpret_cast<f32x4*>(&op.gl[kbase + 4]) = f32x4{gm[4], gm[5], gm[6], gm[7]};
+  }
+  const Sp8 As = split8(at), Rs = split8(rt), Bs = split8(bh), Ks = split8(kh);
+  Sp8 Vs;
+  const u32x4 vraw = tok(3);
+  if constexpr (kVExact) {
+    Vs.hi = __builtin_bit_cast(bf16x8, vraw);
+  } else {
+    float xv[8];
+    unpack8<Io>(vraw, xv);
+    Vs = split8(xv);
+  }
+  // operand rows for the state waves (keys kbase..kbase+7 land in two 4-key
+  // runs of the permuted A~ / R~ rows)
+  const int p0 = key_pos(kbase), p1 = key_pos(kbase + 4);
+  *reinterpret_cast<bf16x4*>(&op.r_h[i][p0]) = Rs.hi.lo;
+  *reinterpret_cast<bf16x4*>(&op.r_h[i][p1]) = Rs.hi.hi;
+  *reinterpret_cast<bf16x4*>(&op.r_l[i][p0]) = Rs.lo.lo;
+  *reinterpret_cast<bf16x4*>(&op.r_l[i][p1]) = Rs.lo.hi;
+  *reinterpret_cast<bf16x4*>(&op.at_h[i][p0]) = As.hi.lo;
+  *reinterpret_cast<bf16x4*>(&op.at_h[i][p1]) = As.hi.hi;
+  *reinterpret_cast<bf16x4*>(&op.at_l[i][p0]) = As.lo.lo;
+  *reinterpret_cast<bf16x4*>(&op.at_l[i][p1]) = As.lo.hi;
+  *reinterpret_cast<bf16x8*>(&op.b_h[i][kbase]) = Bs.hi;
+  *reinterpret_cast<bf16x8*>(&op.b_l[i][kbase]) = Bs.lo;
+  *reinterpret_cast<bf16x8*>(&op.k_h[i][kbase]) = Ks.hi;
+  *reinterpret_cast<bf16x8*>(&op.k_l[i][kbase]) = Ks.lo;
+  *reinterpret_cast<bf16x8*>(&op.v_h[i][kbase]) = Vs.hi;
+  if constexpr (!kVExact) *reinterpret_cast<bf16x8*>(&op.v_l[i][kbase]) = Vs.lo;
+  // mma32x3(X, Y), X, Y in the load layout: item e = X_{4q+e} . Y_i over
+  // this lane's keys
+  acc.ab = mma32x3(As, Bs, acc.ab);
+  acc.abt = mma32x3(Bs, As, acc.abt);
+  acc.ak = mma32x3(Ks, As, acc.ak);
+  acc.rb = mma32x3(Bs, Rs, acc.rb);
+  acc.rk = mma32x3(Ks, Rs, acc.rk);
+}
+
+// T and the masked Mak, Mrb, Mrk of a chunk from its accumulated products
+__device__ __forceinline__ void key_blocks_ring(ChunkOps<true>* op_t, ChunkOps<false>* op_f,
+                                                const KeyAccR& acc, int i, int q) {
+  f32x4 M, Mt, mak, mrb, mrk;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int r = 4 * q + e;
+    M[e] = (r > i) ? acc.ab[e] : 0.f;
+    Mt[e] = (i > r) ? acc.abt[e] : 0.f;
+    mak[e] = (i > r) ? acc.ak[e] : 0.f;
+    mrb[e] = (i >= r) ? acc.rb[e] : 0.f;
+    mrk[e] = (i >= r) ? acc.rk[e] : 0.f;
+  }
+  const AOp t = t_inverse(M, Mt, i, q);
+  if (op_t != nullptr) {
+    store_aop(op_t->t, i, q, t);
+    store_aop(op_t->mak, i, q, as_a(split4(mak)));
+    store_aop(op_t->mrb, i, q, as_a(split4(mrb)));
+    store_aop(op_t->mrk, i, q, as_a(split4(mrk)));
+  } else {
+    store_aop(op_f->t, i, q, t);
+    store_aop(op_f->mak, i, q, as_a(split4(mak)));
+    store_aop(op_f->mrb, i, q, as_a(split4(mrb)));
+    store_aop(op_f->mrk, i, q, as_a(split4(mrk)));
+  }
+}
+
+template <class Io>
+__global__ __launch_bounds__(NT) void chunk64r_kernel(SegArgs p) {
+  using raw = typename Io::raw;
+  constexpr bool kVExact = !__is_same(Io, IoF16);
+  __shared__ SmemR<kVExact> sm;
+
+  const int h = blockIdx.x;
+  const int seg = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 15;
+  const int q = lane >> 4;
+  const int H = p.num_heads;
+
+  // sequence split (real pieces): which sequence and piece this block is
+  const int npc = p.split_pieces;
+  int seq = seg, piece = 0;
+  if (npc > 0) {
+    const int cnt = p.split_count > 0 ? p.split_count : npc;
+    seq = seg / cnt;
+    piece = p.split_first + seg % cnt;
+  }
+  if (p.status != nullptr) {
+    if (p.status[0] != 0) {
+      const int64_t blk = static_cast<int64_t>(seg) * gridDim.x + h;
+      const int64_t nblk = static_cast<int64_t>(gridDim.x) * gridDim.y;
+      fill_output_nan<Io>(static_cast<raw*>(p.y), p.out_elems, blk, nblk);
+      return;
+    }
+    if (seq >= p.status[2]) return;
+  }
+  int t0, t1;
+  bool last_piece = true;
+  if (npc > 0) {
+    const int q0 = p.bounds[seq], q1 = p.bounds[seq + 1];
+    int start, plen, last;
+    split_piece(p, q1 - q0, piece, start, plen, last);
+    if (piece > last) return;
+    last_piece = piece == last;
+    t0 = q0 + start;
+    t1 = min(t0 + plen, q1);
+  } else if (p.uniform_len > 0) {
+    t0 = seg * p.uniform_len;
+    t1 = t0 + p.uniform_len;
+  } else {
+    t0 = p.bounds[seg];
+    t1 = p.bounds[seg + 1];
+  }
+  const int slot = p.slots ? p.slots[seq] : seq;
+  const int64_t head_off = static_cast<int64_t>(h) * D;
+  const int64_t row_stride = static_cast<int64_t>(H) * D;
+  const int nchunks = (t1 - t0 + L - 1) / L;
+  raw* yout = static_cast<raw*>(p.y);
+
+  if (tid < 13) (&sm.ready[0])[tid] = 0;
+  __syncthreads();   // the only workgroup barrier before the end: counters are zero
+
+  const int vcol = 16 * (wv & 3) + i;
+  const int64_t sbase = (static_cast<int64_t>(slot) * H + h) * D * D;
+  const int64_t pbase = (static_cast<int64_t>(seq) * (npc > 0 ? npc : 1) + piece) * H + h;
+  if (wv < 4) {
+    // ---------------- state waves: columns [16wv, 16wv+16)
+    f32x4 S[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) S[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (npc > 0 && !(piece == 0 && p.split_lead_pass)) {
+      const float* sin = p.split_state + pbase * D * D;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[kb][e] = sin[(kb * 16 + 4 * q + e) * D + vcol];
+    } else if (p.state_in != nullptr) {
+      const float* sin = static_cast<const float*>(p.state_in) + sbase + vcol;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[kb][e] = sin[(kb * 16 + 4 * q + e) * D];
+    }
+    // output rows of a finished pair of chunks (2k, 2k+1), one pair late:
+    // row tid/8 of the pair, elements 8*(tid%8)..
+    const int o_tok = tid >> 3, o_c8 = tid & 7;
+    auto write_pair = [&](int k) {
+      if (k < 0) return;
+      wait_min_ge(sm.consumed, min(2 * k + 2, nchunks), p.spin_limit, &sm.fault);
+      const int c = 2 * k + (o_tok >> 4);
+      const int row = t0 + c * L + (o_tok & 15);
+      if (row < t1)
+        *reinterpret_cast<u32x4*>(yout + static_cast<int64_t>(row) * row_stride + head_off +
+                                  o_c8 * 8) =
+            *reinterpret_cast<const u32x4*>(&sm.yb[c & 3][o_tok & 15][o_c8 * 8]);
+      signal(&sm.drained[wv], k + 1);
+    };
+    for (int c = 0; c < nchunks; ++c) {
+      wait_ge(&sm.ready[c & 3], (c >> 2) + 1, p.spin_limit, &sm.fault);   // operators of c
+      // y slot of chunk c free: the pair of chunk c - 4 written back
+      if ((c & 1) == 0) wait_min_ge(sm.drained, (c >> 1) - 1, p.spin_limit, &sm.fault);
+      const StateOps<kVExact> o = state_load(sm.ops[c & 3], vcol, i, q);
+      state_compute<Io, kVExact>(o, S, &sm.yb[c & 3][0], vcol, i, q, p.scale);
+      signal(&sm.consumed[wv], c + 1);
+      if (c & 1) write_pair((c >> 1) - 1);
+    }
+    // the pairs not yet written: the last, and before it the one an odd
+    // final chunk left behind
+    if (nchunks & 1) write_pair(((nchunks - 1) >> 1) - 1);
+    write_pair((nchunks - 1) >> 1);
+    __syncthreads();
+    if (peek(&sm.fault) != 0) {
+      if (tid == 0 && p.handoff_fault != nullptr) atomicAdd(p.handoff_fault, 1);
+      const float qnan = quiet_nan();
+      const raw nanv = Io::from_f32(qnan);
+      if (yout != nullptr)
+        for (int64_t e = tid; e < static_cast<int64_t>(t1 - t0) * D; e += 256)
+          yout[(t0 + e / D) * row_stride + head_off + e % D] = nanv;
+      if (npc > 0 && p.split_lead_pass && piece == 0 && !last_piece) {
+        float* sout = p.split_state + (pbase + H) * D * D;
+        for (int e = tid; e < D * D; e += 256) sout[e] = qnan;
+      }
+      return;
+    }
+    if (!last_piece) {
+      if (p.split_lead_pass && piece == 0) {
+        float* sout = p.split_state + (pbase + H) * D * D;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
+      }
+    } else if (p.state_out != nullptr) {
+      float* sout = static_cast<float*>(p.state_out) + sbase + vcol;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D] = S[kb][e];
+    }
+  } else {
+    // ---------------- key waves: whole chunks kw, kw + 4, ...
+    const int kw = wv & 3;
+    float nbias[2][8];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        nbias[hh][e] = p.bias ? -kLog2e * Io::to_f32(static_cast<const raw*>(p.bias)[
+                                             head_off + 32 * hh + 8 * q + e])
+                              : 0.f;
+    const raw* src[6] = {
+        static_cast<const raw*>(p.r), static_cast<const raw*>(p.logits),
+        static_cast<const raw*>(p.k), static_cast<const raw*>(p.v),
+        static_cast<const raw*>(p.a), static_cast<const raw*>(p.b)};
+    u32x4 rawc[2][6];
+    // rows past the sequence end are loaded from its last row (in bounds);
+    // key_half_ring zeroes them
+    auto load_chunk = [&](int c) {
+      const int row = min(t0 + c * L + i, t1 - 1);
+      const int64_t off = static_cast<int64_t>(row) * row_stride + head_off + 8 * q;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int j = 0; j < 6; ++j)
+          rawc[hh][j] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4*>(src[j] + off + 32 * hh));
+    };
+    if (kw < nchunks) load_chunk(kw);
+    for (int c = kw; c < nchunks; c += 4) {
+      wait_min_ge(sm.consumed, c - 3, p.spin_limit, &sm.fault);   // chunk c - 4 no longer read
+      ChunkOps<kVExact>& op = sm.ops[c & 3];
+      const bool full = t0 + c * L + L <= t1;
+      const bool valid = t0 + c * L + i < t1;
+      KeyAccR acc;
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      acc.ab = z; acc.abt = z; acc.ak = z; acc.rb = z; acc.rk = z;
+      if (full) {
+        key_half_ring<Io, kVExact, true>(op, rawc[0], nbias[0], true, 0, i, q, acc);
+        key_half_ring<Io, kVExact, true>(op, rawc[1], nbias[1], true, 1, i, q, acc);
+      } else {
+        key_half_ring<Io, kVExact, false>(op, rawc[0], nbias[0], valid, 0, i, q, acc);
+        key_half_ring<Io, kVExact, false>(op, rawc[1], nbias[1], valid, 1, i, q, acc);
+      }
+      if (c + 4 < nchunks) load_chunk(c + 4);
+      if constexpr (kVExact)
+        key_blocks_ring(&op, nullptr, acc, i, q);
+      else
+        key_blocks_ring(nullptr, &op, acc, i, q);
+      if (!p.handoff_stall) signal(&sm.ready[kw], ((c - kw) >> 2) + 1);
+    }
+    __syncthreads();   // pairs with the state waves' final barrier
+  }
+}
+
 }  // namespace
 
 namespace {
@@ -1102,6 +1437,7 @@ namespace {
 __device__ int g_handoff_faults;
 std::atomic<int> g_spin_limit{1 << 20};
 std::atomic<bool> g_handoff_stall{false};
+std::atomic<int> g_chunk_ring{1};
 std::atomic<int*> g_fault_ptr[64];
 }  // namespace
 
@@ -1119,9 +1455,19 @@ int* handoff_fault_word() {
 }
 int handoff_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
 bool handoff_stall() { return g_handoff_stall.load(std::memory_order_relaxed); }
+bool chunk_ring_enabled() { return g_chunk_ring.load(std::memory_order_relaxed) != 0; }
+void set_chunk_ring(int on) { g_chunk_ring.store(on, std::memory_order_relaxed); }
 void set_handoff_stall(bool on) { g_handoff_stall.store(on, std::memory_order_relaxed); }
 void set_handoff_spin_limit(int polls) {
   g_spin_limit.store(polls < 0 ? (1 << 20) : polls, std::memory_order_relaxed);
+}
+
+// the ring variant covers the plain fp32-state contract only: no chunk
+// lists or segment ends, no boundary snapshots, no sa or read-out outputs
+bool ring_contract(const SegArgs& p) {
+  return chunk_ring_enabled() && !p.state_bf16 && p.chunk_offsets == nullptr &&
+         p.ends == nullptr && p.boundary == nullptr && p.sa_out == nullptr &&
+         p.ro_out == nullptr;
 }
 
 int launch_chunked(int dtype, const SegArgs& args, int nseg, int max_seqlen, hipStream_t s) {
@@ -1143,10 +1489,17 @@ int launch_chunked(int dtype, const SegArgs& args, int nseg, int max_seqlen, hip
       hipLaunchKernelGGL((chunk64_kernel<IoBF16, true, true>), grid, dim3(NT), 0, s, p);
     else
       hipLaunchKernelGGL((chunk64_kernel<IoBF16, true>), grid, dim3(NT), 0, s, p);
+  } else if (!ring_contract(p)) {
+    if (dtype == FR2_DTYPE_BFLOAT16)
+      hipLaunchKernelGGL((chunk64_kernel<IoBF16, false>), grid, dim3(NT), 0, s, p);
+    else if (dtype == FR2_DTYPE_FLOAT16)
+      hipLaunchKernelGGL((chunk64_kernel<IoF16, false>), grid, dim3(NT), 0, s, p);
+    else
+      return FR2_ERR_UNSUPPORTED;
   } else if (dtype == FR2_DTYPE_BFLOAT16) {
-    hipLaunchKernelGGL((chunk64_kernel<IoBF16, false>), grid, dim3(NT), 0, s, p);
+    hipLaunchKernelGGL((chunk64r_kernel<IoBF16>), grid, dim3(NT), 0, s, p);
   } else if (dtype == FR2_DTYPE_FLOAT16) {
-    hipLaunchKernelGGL((chunk64_kernel<IoF16, false>), grid, dim3(NT), 0, s, p);
+    hipLaunchKernelGGL((chunk64r_kernel<IoF16>), grid, dim3(NT), 0, s, p);
   } else {
     return FR2_ERR_UNSUPPORTED;
   }
@@ -1286,6 +1639,16 @@ bool split_events(SplitEvents*& ev) {
   return true;
 }
 
+// a real (non-summary) pass of the plain contract: the ring variant when it
+// is selected and the state is fp32
+template <class Io>
+void launch_real_pass(dim3 grid, hipStream_t s, const SegArgs& p) {
+  if (ring_contract(p))
+    hipLaunchKernelGGL((chunk64r_kernel<Io>), grid, dim3(NT), 0, s, p);
+  else
+    hipLaunchKernelGGL((chunk64_kernel<Io, false>), grid, dim3(NT), 0, s, p);
+}
+
 template <class Io>
 int launch_split_kernels(const SegArgs& p, int nseg, int pieces, hipStream_t s,
                          hipStream_t aux) {
@@ -1295,7 +1658,7 @@ int launch_split_kernels(const SegArgs& p, int nseg, int pieces, hipStream_t s,
     const dim3 gsum(H, nseg * (pieces - 1)), gcomb(H, nseg), greal(H, nseg * pieces);
     hipLaunchKernelGGL((chunk64_kernel<Io, false, false, true>), gsum, dim3(NT_SUM), 0, s, p);
     hipLaunchKernelGGL(split_combine_kernel, gcomb, dim3(256), 0, s, p);
-    hipLaunchKernelGGL((chunk64_kernel<Io, false>), greal, dim3(NT), 0, s, p);
+    launch_real_pass<Io>(greal, s, p);
     return FR2_OK;
   }
   // lead: piece 0 (from the slot) on the aux stream, concurrently with the
@@ -1315,7 +1678,7 @@ int launch_split_kernels(const SegArgs& p, int nseg, int pieces, hipStream_t s,
   pl.split_first = 0;
   pl.split_count = 1;
   pl.split_lead_pass = true;
-  hipLaunchKernelGGL((chunk64_kernel<Io, false>), dim3(H, nseg), dim3(NT), 0, s_lead, pl);
+  launch_real_pass<Io>(dim3(H, nseg), s_lead, pl);
   SegArgs ps = p;
   ps.split_first = 1;
   ps.split_count = pieces - 2;
@@ -1333,8 +1696,7 @@ int launch_split_kernels(const SegArgs& p, int nseg, int pieces, hipStream_t s,
   SegArgs pr = p;
   pr.split_first = 1;
   pr.split_count = pieces - 1;
-  hipLaunchKernelGGL((chunk64_kernel<Io, false>), dim3(H, nseg * (pieces - 1)), dim3(NT), 0, s,
-                     pr);
+  launch_real_pass<Io>(dim3(H, nseg * (pieces - 1)), s, pr);
   return FR2_OK;
 }
 

@@ -177,6 +177,8 @@ int handoff_spin_limit();
 void set_handoff_spin_limit(int polls);   // negative: the default
 bool handoff_stall();
 void set_handoff_stall(bool on);
+bool chunk_ring_enabled();
+void set_chunk_ring(int on);
 int launch_chunked_split(int dtype, SegArgs p, int nseg, int pieces, int piece_len,
                          int lead_len, float* workspace, hipStream_t s, hipStream_t aux);
 

@@ -95,6 +95,19 @@ int fr2_debug_set_handoff_spin_limit(int32_t polls);
 int fr2_debug_set_handoff_stall(int32_t on);
 
 /*
+ * Test hook: selects the variant of the workgroup-per-unit chunked kernel
+ * that the plain fp32-state contract runs, for later launches in the
+ * process: 0 = two key waves per chunk (each a key half, partial token-token
+ * blocks summed through LDS), 1 = one key wave per whole chunk over a ring
+ * of four chunk operator blocks (the default).  The ring variant serves the
+ * plain fp32-state contract and the sequence split's real passes; chunk
+ * lists, segment ends, boundary snapshots, sa / read-out outputs and the
+ * bf16-state entry always run the key-half variant.  No counterpart in the
+ * reference.
+ */
+int fr2_debug_set_chunk_ring(int32_t on);
+
+/*
  * Device-side validation of packed metadata, one 256-thread workgroup.
  * Writes status[3]; copies query_start_loc/state_indices into the snapshot
  * buffers when they are non-null (static tickets) and validates the copies.

@@ -27,6 +27,15 @@ from wkv7_testlib import (
 
 pytestmark = pytest.mark.gpu
 
+
+@pytest.fixture(autouse=True)
+def _default_chunk_variant():
+    """Tests that select the workgroup chunked kernel's variant leave the
+    default (the ring variant) behind, pass or fail."""
+    yield
+    if torch.cuda.is_available():
+        require_gpu()._set_chunk_ring(True)
+
 CHUNKED = 2
 
 
@@ -44,9 +53,11 @@ def _forced_chunked(C, case, pool):
     return out
 
 
-def test_handoff_give_up_fails_closed_and_is_counted():
+@pytest.mark.parametrize("ring", [True, False])
+def test_handoff_give_up_fails_closed_and_is_counted(ring):
     C = require_gpu()
-    print("case handoff spin limit 0, lengths (200, 300), H=2", flush=True)
+    print(f"case handoff spin limit 0, lengths (200, 300), H=2, ring={ring}", flush=True)
+    C._set_chunk_ring(ring)
     case = make_case(lengths=(200, 300), num_heads=2, seed=71)
     C.handoff_fault_count(reset=True)
     pool = case["state_pool"].clone()
@@ -69,9 +80,11 @@ def test_handoff_give_up_fails_closed_and_is_counted():
     y_ref, pool_ref = oracle_expect(case)
     assert_output_close(to_np(out), y_ref)
     assert_state_close(to_np(pool), pool_ref)
+    C._set_chunk_ring(True)
 
 
-def test_real_stall_fails_closed_after_one_wait():
+@pytest.mark.parametrize("ring", [True, False])
+def test_real_stall_fails_closed_after_one_wait(ring):
     """A producer that never publishes (forced from the host: the key waves
     skip their operator signal) makes the first operator wait give up; every
     later wait of that block must then return at once instead of polling to
@@ -79,7 +92,8 @@ def test_real_stall_fails_closed_after_one_wait():
     import time
 
     C = require_gpu()
-    print("case handoff stall, spin limit 20000, length 16384, H=1", flush=True)
+    print(f"case handoff stall, spin limit 20000, length 16384, H=1, ring={ring}", flush=True)
+    C._set_chunk_ring(ring)
     case = make_case(lengths=(16384,), num_heads=1, seed=72)
     C.handoff_fault_count(reset=True)
     pool = case["state_pool"].clone()
@@ -95,6 +109,7 @@ def test_real_stall_fails_closed_after_one_wait():
     finally:
         C._set_handoff_stall(False)
         C._set_handoff_spin_limit(-1)
+        C._set_chunk_ring(True)
     print(f"stalled call took {dt * 1e3:.1f} ms", flush=True)
     assert C.handoff_fault_count(reset=True) == 1
     assert torch.isnan(out.float()).all()

@@ -26,6 +26,15 @@ from wkv7_testlib import (
 
 pytestmark = pytest.mark.gpu
 
+
+@pytest.fixture(autouse=True)
+def _default_chunk_variant():
+    """Tests that select the workgroup chunked kernel's variant leave the
+    default (the ring variant) behind, pass or fail."""
+    yield
+    if torch.cuda.is_available():
+        require_gpu()._set_chunk_ring(True)
+
 from flashrwkv2_amd.tmix.wkv7 import (  # noqa: E402
     infer_tmix_wkv7_recurrent_fp32io16_forward_varlen as wkv7,
     prepare_tmix_wkv7_recurrent_metadata,
@@ -93,6 +102,37 @@ def test_each_kernel_family_matches_oracle(kernel, lengths, dtype):
     active = case["state_indices"].long()
     assert_output_close(out, y_ref)
     assert_state_close(pool[active], pool_ref[active.cpu().numpy()])
+
+
+@pytest.mark.parametrize("ring", [False, True])
+@pytest.mark.parametrize("kw", [
+    dict(lengths=(1, 15, 16, 17, 65), num_heads=2),
+    dict(lengths=(40, 1, 63, 130, 17), num_heads=3, with_decay_bias=True),
+    dict(lengths=(5,), num_heads=1),
+    dict(lengths=(300, 64, 96, 41), num_heads=4, with_decay_bias=True),
+    dict(lengths=(1000, 777), num_heads=2, dtype=torch.float16),
+    dict(lengths=(2048,), num_heads=2, scales=(0.5, 2.0, 0.5, 0.5, 0.2, 0.2)),
+])
+def test_both_workgroup_chunk_variants_match_oracle(ring, kw):
+    """The workgroup chunked kernel has two key-side organisations (a ring of
+    whole chunks per key wave, the default; key halves per wave pair): each
+    matches the oracle over partial chunks, ragged batches, a decay bias,
+    fp16 tokens and large-magnitude inputs, and leaves unused slots alone."""
+    C = require_gpu()
+    print(f"case ring={ring} {kw}", flush=True)
+    case = make_case(seed=11, **kw)
+    y_ref, pool_ref = oracle_expect(case, scale=0.8)
+    pool = case["state_pool"].clone()
+    C._set_chunk_ring(ring)
+    try:
+        out = _run_kernel(C, CHUNKED, case, pool, scale=0.8)
+    finally:
+        C._set_chunk_ring(True)
+    active = case["state_indices"].long()
+    assert_output_close(out, y_ref)
+    assert_state_close(pool[active], pool_ref[active.cpu().numpy()])
+    untouched = np.setdiff1d(np.arange(pool.shape[0]), active.cpu().numpy())
+    assert torch.equal(pool[untouched], case["state_pool"][untouched])
 
 
 def test_serial_and_decode_agree_closely():
