@@ -1101,20 +1101,28 @@ __global__ __launch_bounds__(kSum ? NT_SUM : NT) void chunk64_kernel(SegArgs p) 
 // w - 4, w, w + 4, ... of the unit, both key halves one after the other,
 // accumulating the token-token blocks over all 64 keys in its own matrix
 // accumulators, then forms T and the masked blocks itself.  So no partial
-// blocks go through LDS and no key wave waits on a partner; operator blocks
-// are a ring of four chunks in LDS (chunk c in slot c % 4), and a key wave
-// may build chunk c as soon as the state waves have finished chunk c - 4,
-// three chunk periods ahead of its use.  The state waves run chunk after
-// chunk as in chunk64_kernel.
+// blocks go through LDS and no key wave waits on a partner.  Operator blocks
+// are a ring of R chunks in LDS (chunk c in slot c % R; R = 6 for bf16
+// tokens, 5 for fp16), and a key wave may build chunk c as soon as the state
+// waves have finished chunk c - R.  A key wave takes about three chunk
+// periods to build a chunk, so with R = 4 the state waves waited on the
+// ring; with R = 6 the four key waves' throughput sets the period.  The
+// state waves run chunk after chunk as in chunk64_kernel and each writes its
+// own 16 output columns, so they never wait on one another.
 // ===========================================================================
+// operator slots of the ring kernel (fp16 tokens carry V's lo part and
+// fit one slot fewer in the 160 KB of LDS)
+template <bool kVExact> constexpr int kRingOf = kVExact ? 6 : 5;
+constexpr int kKeyW = 4;   // key waves of the ring kernel
+constexpr int NTR = 64 * (4 + kKeyW);
 template <bool kVExact>
 struct alignas(16) SmemR {
-  ChunkOps<kVExact> ops[4];           // ring by chunk index mod 4
-  uint16_t yb[4][L][YP];              // staged outputs by chunk index mod 4
+  ChunkOps<kVExact> ops[kRingOf<kVExact>];   // ring by chunk index mod kRing
+  uint16_t yb[L][YP];                 // staged output rows of the current chunk
   // progress counters, each written by one wave only: chunks key wave w has
-  // built (its chunks are w, w + 4, ...), chunks state wave w has finished,
-  // chunks whose output rows state wave w has written back
-  int ready[4], consumed[4], drained[4];
+  // built (its chunks are w, w + kKeyW, ...) and chunks state wave w has
+  // finished
+  int ready[kKeyW], consumed[4];
   int fault;
 };
 
@@ -1240,10 +1248,11 @@ __device__ __forceinline__ void key_blocks_ring(ChunkOps<true>* op_t, ChunkOps<f
 }
 
 template <class Io>
-__global__ __launch_bounds__(NT) void chunk64r_kernel(SegArgs p) {
+__global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
   using raw = typename Io::raw;
   constexpr bool kVExact = !__is_same(Io, IoF16);
   __shared__ SmemR<kVExact> sm;
+  constexpr int kRing = kRingOf<kVExact>;
 
   const int h = blockIdx.x;
   const int seg = blockIdx.y;
@@ -1294,7 +1303,7 @@ __global__ __launch_bounds__(NT) void chunk64r_kernel(SegArgs p) {
   const int nchunks = (t1 - t0 + L - 1) / L;
   raw* yout = static_cast<raw*>(p.y);
 
-  if (tid < 13) (&sm.ready[0])[tid] = 0;
+  if (tid < kKeyW + 5) (&sm.ready[0])[tid] = 0;
   __syncthreads();   // the only workgroup barrier before the end: counters are zero
 
   const int vcol = 16 * (wv & 3) + i;
@@ -1318,33 +1327,25 @@ __global__ __launch_bounds__(NT) void chunk64r_kernel(SegArgs p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) S[kb][e] = sin[(kb * 16 + 4 * q + e) * D];
     }
-    // output rows of a finished pair of chunks (2k, 2k+1), one pair late:
-    // row tid/8 of the pair, elements 8*(tid%8)..
-    const int o_tok = tid >> 3, o_c8 = tid & 7;
-    auto write_pair = [&](int k) {
-      if (k < 0) return;
-      wait_min_ge(sm.consumed, min(2 * k + 2, nchunks), p.spin_limit, &sm.fault);
-      const int c = 2 * k + (o_tok >> 4);
-      const int row = t0 + c * L + (o_tok & 15);
-      if (row < t1)
-        *reinterpret_cast<u32x4*>(yout + static_cast<int64_t>(row) * row_stride + head_off +
-                                  o_c8 * 8) =
-            *reinterpret_cast<const u32x4*>(&sm.yb[c & 3][o_tok & 15][o_c8 * 8]);
-      signal(&sm.drained[wv], k + 1);
-    };
+    // Each state wave writes its own 16 output columns: the chunk's rows are
+    // staged in the wave's column band of yb (2-byte stores from the
+    // accumulators) and read back as 16-byte pieces, lane l < 32 taking
+    // row l / 2, columns 16 (wv % 4) + 8 (l % 2) .. + 7.  The band belongs
+    // to this wave alone and its LDS accesses complete in order, so no wave
+    // waits for another over the output.
+    const int y_row = lane >> 1, y_c0 = 16 * (wv & 3) + 8 * (lane & 1);
     for (int c = 0; c < nchunks; ++c) {
-      wait_ge(&sm.ready[c & 3], (c >> 2) + 1, p.spin_limit, &sm.fault);   // operators of c
-      // y slot of chunk c free: the pair of chunk c - 4 written back
-      if ((c & 1) == 0) wait_min_ge(sm.drained, (c >> 1) - 1, p.spin_limit, &sm.fault);
-      const StateOps<kVExact> o = state_load(sm.ops[c & 3], vcol, i, q);
-      state_compute<Io, kVExact>(o, S, &sm.yb[c & 3][0], vcol, i, q, p.scale);
+      wait_ge(&sm.ready[c % kKeyW], c / kKeyW + 1, p.spin_limit, &sm.fault);   // operators of c
+      const StateOps<kVExact> o = state_load(sm.ops[c % kRing], vcol, i, q);
+      state_compute<Io, kVExact>(o, S, &sm.yb[0], vcol, i, q, p.scale);
+      const int row = t0 + c * L + y_row;
+      if (lane < 32 && row < t1) {
+        const u32x4 piece = *reinterpret_cast<const u32x4*>(&sm.yb[y_row][y_c0]);
+        *reinterpret_cast<u32x4*>(yout + static_cast<int64_t>(row) * row_stride + head_off +
+                                  y_c0) = piece;
+      }
       signal(&sm.consumed[wv], c + 1);
-      if (c & 1) write_pair((c >> 1) - 1);
     }
-    // the pairs not yet written: the last, and before it the one an odd
-    // final chunk left behind
-    if (nchunks & 1) write_pair(((nchunks - 1) >> 1) - 1);
-    write_pair((nchunks - 1) >> 1);
     __syncthreads();
     if (peek(&sm.fault) != 0) {
       if (tid == 0 && p.handoff_fault != nullptr) atomicAdd(p.handoff_fault, 1);
@@ -1376,7 +1377,7 @@ __global__ __launch_bounds__(NT) void chunk64r_kernel(SegArgs p) {
     }
   } else {
     // ---------------- key waves: whole chunks kw, kw + 4, ...
-    const int kw = wv & 3;
+    const int kw = wv - 4;
     float nbias[2][8];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
@@ -1403,9 +1404,10 @@ __global__ __launch_bounds__(NT) void chunk64r_kernel(SegArgs p) {
               reinterpret_cast<const u32x4*>(src[j] + off + 32 * hh));
     };
     if (kw < nchunks) load_chunk(kw);
-    for (int c = kw; c < nchunks; c += 4) {
-      wait_min_ge(sm.consumed, c - 3, p.spin_limit, &sm.fault);   // chunk c - 4 no longer read
-      ChunkOps<kVExact>& op = sm.ops[c & 3];
+    for (int c = kw; c < nchunks; c += kKeyW) {
+      // chunk c - kRing no longer read
+      wait_min_ge(sm.consumed, c - kRing + 1, p.spin_limit, &sm.fault);
+      ChunkOps<kVExact>& op = sm.ops[c % kRing];
       const bool full = t0 + c * L + L <= t1;
       const bool valid = t0 + c * L + i < t1;
       KeyAccR acc;
@@ -1418,12 +1420,12 @@ __global__ __launch_bounds__(NT) void chunk64r_kernel(SegArgs p) {
         key_half_ring<Io, kVExact, false>(op, rawc[0], nbias[0], valid, 0, i, q, acc);
         key_half_ring<Io, kVExact, false>(op, rawc[1], nbias[1], valid, 1, i, q, acc);
       }
-      if (c + 4 < nchunks) load_chunk(c + 4);
+      if (c + kKeyW < nchunks) load_chunk(c + kKeyW);
       if constexpr (kVExact)
         key_blocks_ring(&op, nullptr, acc, i, q);
       else
         key_blocks_ring(nullptr, &op, acc, i, q);
-      if (!p.handoff_stall) signal(&sm.ready[kw], ((c - kw) >> 2) + 1);
+      if (!p.handoff_stall) signal(&sm.ready[kw], (c - kw) / kKeyW + 1);
     }
     __syncthreads();   // pairs with the state waves' final barrier
   }
@@ -1497,9 +1499,9 @@ int launch_chunked(int dtype, const SegArgs& args, int nseg, int max_seqlen, hip
     else
       return FR2_ERR_UNSUPPORTED;
   } else if (dtype == FR2_DTYPE_BFLOAT16) {
-    hipLaunchKernelGGL((chunk64r_kernel<IoBF16>), grid, dim3(NT), 0, s, p);
+    hipLaunchKernelGGL((chunk64r_kernel<IoBF16>), grid, dim3(NTR), 0, s, p);
   } else if (dtype == FR2_DTYPE_FLOAT16) {
-    hipLaunchKernelGGL((chunk64r_kernel<IoF16>), grid, dim3(NT), 0, s, p);
+    hipLaunchKernelGGL((chunk64r_kernel<IoF16>), grid, dim3(NTR), 0, s, p);
   } else {
     return FR2_ERR_UNSUPPORTED;
   }
@@ -1644,7 +1646,7 @@ bool split_events(SplitEvents*& ev) {
 template <class Io>
 void launch_real_pass(dim3 grid, hipStream_t s, const SegArgs& p) {
   if (ring_contract(p))
-    hipLaunchKernelGGL((chunk64r_kernel<Io>), grid, dim3(NT), 0, s, p);
+    hipLaunchKernelGGL((chunk64r_kernel<Io>), grid, dim3(NTR), 0, s, p);
   else
     hipLaunchKernelGGL((chunk64_kernel<Io, false>), grid, dim3(NT), 0, s, p);
 }
