@@ -1135,7 +1135,8 @@ struct KeyAccR {
 
 // One key half hh of chunk operators: as key_part1 (plain contract) plus the
 // operand-row stores of key_part2, with the token-token products accumulated.
-template <class Io, bool kVExact, bool kFull>
+// kSum (summary pass): no R~ operand, no R-side products.
+template <class Io, bool kVExact, bool kFull, bool kSum = false>
 __device__ __forceinline__ void key_half_ring(ChunkOps<kVExact>& op, const u32x4 (&raw)[6],
                                               const float (&nbias8)[8], bool valid, int hh,
                                               int i, int q, KeyAccR& acc) {
@@ -1143,7 +1144,7 @@ __device__ __forceinline__ void key_half_ring(ChunkOps<kVExact>& op, const u32x4
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
   auto tok = [&](int j) { return (kFull || valid) ? raw[j] : zero4; };
   float xr[8], xl[8], xk[8], xa[8], xb[8];
-  unpack8<Io>(tok(0), xr);
+  if constexpr (!kSum) unpack8<Io>(tok(0), xr);
   unpack8<Io>(raw[1], xl);
   unpack8<Io>(tok(2), xk);
   unpack8<Io>(tok(4), xa);
@@ -1176,7 +1177,7 @@ __device__ __forceinline__ void key_half_ring(ChunkOps<kVExact>& op, const u32x4
   for (int e = 0; e < 8; ++e) {
     const float ig = __builtin_amdgcn_exp2f(-g2[e]);                     // 1 / gamma_t
     at[e] = xa[e] * gp[e];
-    rt[e] = xr[e] * gm[e];
+    if constexpr (!kSum) rt[e] = xr[e] * gm[e];
     bh[e] = xb[e] * ig;
     kh[e] = xk[e] * ig;
   }
@@ -1184,7 +1185,9 @@ __device__ __forceinline__ void key_half_ring(ChunkOps<kVExact>& op, const u32x4
     *reinterpret_cast<f32x4*>(&op.gl[kbase]) = f32x4{gm[0], gm[1], gm[2], gm[3]};
     *reinterpret_cast<f32x4*>(&op.gl[kbase + 4]) = f32x4{gm[4], gm[5], gm[6], gm[7]};
   }
-  const Sp8 As = split8(at), Rs = split8(rt), Bs = split8(bh), Ks = split8(kh);
+  Sp8 Rs;
+  if constexpr (!kSum) Rs = split8(rt);
+  const Sp8 As = split8(at), Bs = split8(bh), Ks = split8(kh);
   Sp8 Vs;
   const u32x4 vraw = tok(3);
   if constexpr (kVExact) {
@@ -1197,10 +1200,12 @@ __device__ __forceinline__ void key_half_ring(ChunkOps<kVExact>& op, const u32x4
   // operand rows for the state waves (keys kbase..kbase+7 land in two 4-key
   // runs of the permuted A~ / R~ rows)
   const int p0 = key_pos(kbase), p1 = key_pos(kbase + 4);
-  *reinterpret_cast<bf16x4*>(&op.r_h[i][p0]) = Rs.hi.lo;
-  *reinterpret_cast<bf16x4*>(&op.r_h[i][p1]) = Rs.hi.hi;
-  *reinterpret_cast<bf16x4*>(&op.r_l[i][p0]) = Rs.lo.lo;
-  *reinterpret_cast<bf16x4*>(&op.r_l[i][p1]) = Rs.lo.hi;
+  if constexpr (!kSum) {
+    *reinterpret_cast<bf16x4*>(&op.r_h[i][p0]) = Rs.hi.lo;
+    *reinterpret_cast<bf16x4*>(&op.r_h[i][p1]) = Rs.hi.hi;
+    *reinterpret_cast<bf16x4*>(&op.r_l[i][p0]) = Rs.lo.lo;
+    *reinterpret_cast<bf16x4*>(&op.r_l[i][p1]) = Rs.lo.hi;
+  }
   *reinterpret_cast<bf16x4*>(&op.at_h[i][p0]) = As.hi.lo;
   *reinterpret_cast<bf16x4*>(&op.at_h[i][p1]) = As.hi.hi;
   *reinterpret_cast<bf16x4*>(&op.at_l[i][p0]) = As.lo.lo;
@@ -1216,8 +1221,10 @@ __device__ __forceinline__ void key_half_ring(ChunkOps<kVExact>& op, const u32x4
   acc.ab = mma32x3(As, Bs, acc.ab);
   acc.abt = mma32x3(Bs, As, acc.abt);
   acc.ak = mma32x3(Ks, As, acc.ak);
-  acc.rb = mma32x3(Bs, Rs, acc.rb);
-  acc.rk = mma32x3(Ks, Rs, acc.rk);
+  if constexpr (!kSum) {
+    acc.rb = mma32x3(Bs, Rs, acc.rb);
+    acc.rk = mma32x3(Ks, Rs, acc.rk);
+  }
 }
 
 // T and the masked Mak, Mrb, Mrk of a chunk from its accumulated products
@@ -1245,6 +1252,22 @@ __device__ __forceinline__ void key_blocks_ring(ChunkOps<true>* op_t, ChunkOps<f
     store_aop(op_f->mrb, i, q, as_a(split4(mrb)));
     store_aop(op_f->mrk, i, q, as_a(split4(mrk)));
   }
+}
+
+// T and the masked Mak of a summary chunk (no R-side blocks)
+template <bool kVExact>
+__device__ __forceinline__ void key_blocks_ring_sum(ChunkOps<kVExact>& op, const KeyAccR& acc,
+                                                    int i, int q) {
+  f32x4 M, Mt, mak;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int r = 4 * q + e;
+    M[e] = (r > i) ? acc.ab[e] : 0.f;
+    Mt[e] = (i > r) ? acc.abt[e] : 0.f;
+    mak[e] = (i > r) ? acc.ak[e] : 0.f;
+  }
+  store_aop(op.t, i, q, t_inverse(M, Mt, i, q));
+  store_aop(op.mak, i, q, as_a(split4(mak)));
 }
 
 template <class Io>
@@ -1425,6 +1448,138 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
         key_blocks_ring(&op, nullptr, acc, i, q);
       else
         key_blocks_ring(nullptr, &op, acc, i, q);
+      if (!p.handoff_stall) signal(&sm.ready[kw], (c - kw) / kKeyW + 1);
+    }
+    __syncthreads();   // pairs with the state waves' final barrier
+  }
+}
+
+// Summary pass of a sequence split on the ring layout: block y = n * count +
+// j summarises piece split_first + j of sequence n (only pieces before the
+// sequence's last).  Four key waves build whole chunks into the operator
+// ring as in chunk64r_kernel, without R~ and the R-side blocks.  Each of the
+// four state waves carries, for its 16 columns, both the piece's zero-start
+// final state F and its transition Phi (identity start, V = 0): two
+// independent chains over the same operands, read from LDS once.  Writes
+// split_summary[(y * 2 + {0: F, 1: Phi}) * H + h]; nothing else.
+template <class Io>
+__global__ __launch_bounds__(NTR) void chunk64rs_kernel(SegArgs p) {
+  using raw = typename Io::raw;
+  constexpr bool kVExact = !__is_same(Io, IoF16);
+  __shared__ SmemR<kVExact> sm;
+  constexpr int kRing = kRingOf<kVExact>;
+
+  const int h = blockIdx.x;
+  const int seg = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 15;
+  const int q = lane >> 4;
+  const int H = p.num_heads;
+  const int cnt = p.split_count > 0 ? p.split_count : p.split_pieces - 1;
+  const int seq = seg / cnt, piece = p.split_first + seg % cnt;
+  if (p.status != nullptr && (p.status[0] != 0 || seq >= p.status[2])) return;
+  const int q0 = p.bounds[seq], q1 = p.bounds[seq + 1];
+  int start, plen, last;
+  split_piece(p, q1 - q0, piece, start, plen, last);
+  if (piece >= last) return;
+  const int t0 = q0 + start;
+  const int t1 = min(t0 + plen, q1);
+  const int64_t head_off = static_cast<int64_t>(h) * D;
+  const int64_t row_stride = static_cast<int64_t>(H) * D;
+  const int nchunks = (t1 - t0 + L - 1) / L;
+
+  if (tid < kKeyW + 5) (&sm.ready[0])[tid] = 0;
+  __syncthreads();   // the only workgroup barrier before the end: counters are zero
+
+  const int vcol = 16 * (wv & 3) + i;
+  if (wv < 4) {
+    f32x4 F[4], Phi[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        F[kb][e] = 0.0f;
+        Phi[kb][e] = (kb * 16 + 4 * q + e == vcol) ? 1.0f : 0.0f;
+      }
+    for (int c = 0; c < nchunks; ++c) {
+      wait_ge(&sm.ready[c % kKeyW], c / kKeyW + 1, p.spin_limit, &sm.fault);   // operators of c
+      // every operand is in registers before the slot is released
+      const StateOps<kVExact> o = state_load<kVExact, true>(sm.ops[c % kRing], vcol, i, q);
+      signal(&sm.consumed[wv], c + 1);
+      state_compute<Io, kVExact, false, true>(o, F, nullptr, vcol, i, q, 1.0f, SaRows{},
+                                              nullptr, false);
+      state_compute<Io, kVExact, false, true>(o, Phi, nullptr, vcol, i, q, 1.0f, SaRows{},
+                                              nullptr, true);
+    }
+    __syncthreads();
+    float* sout = p.split_summary + (static_cast<int64_t>(seg) * 2 * H + h) * D * D;
+    float* pout = sout + static_cast<int64_t>(H) * D * D;
+    if (peek(&sm.fault) != 0) {
+      // the pieces that start from this summary come out NaN as well
+      if (tid == 0 && p.handoff_fault != nullptr) atomicAdd(p.handoff_fault, 1);
+      const float qnan = quiet_nan();
+      for (int e = tid; e < D * D; e += 256) {
+        sout[e] = qnan;
+        pout[e] = qnan;
+      }
+      return;
+    }
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sout[(kb * 16 + 4 * q + e) * D + vcol] = F[kb][e];
+        pout[(kb * 16 + 4 * q + e) * D + vcol] = Phi[kb][e];
+      }
+  } else {
+    // ---------------- key waves: whole chunks kw, kw + 4, ...
+    const int kw = wv - 4;
+    float nbias[2][8];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        nbias[hh][e] = p.bias ? -kLog2e * Io::to_f32(static_cast<const raw*>(p.bias)[
+                                             head_off + 32 * hh + 8 * q + e])
+                              : 0.f;
+    const raw* src[6] = {
+        nullptr, static_cast<const raw*>(p.logits),
+        static_cast<const raw*>(p.k), static_cast<const raw*>(p.v),
+        static_cast<const raw*>(p.a), static_cast<const raw*>(p.b)};
+    u32x4 rawc[2][6];
+    auto load_chunk = [&](int c) {
+      const int row = min(t0 + c * L + i, t1 - 1);
+      const int64_t off = static_cast<int64_t>(row) * row_stride + head_off + 8 * q;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        rawc[hh][0] = u32x4{0u, 0u, 0u, 0u};   // r: not read by the summary
+#pragma unroll
+        for (int j = 1; j < 6; ++j)
+          rawc[hh][j] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4*>(src[j] + off + 32 * hh));
+      }
+    };
+    if (kw < nchunks) load_chunk(kw);
+    for (int c = kw; c < nchunks; c += kKeyW) {
+      // chunk c - kRing no longer read
+      wait_min_ge(sm.consumed, c - kRing + 1, p.spin_limit, &sm.fault);
+      ChunkOps<kVExact>& op = sm.ops[c % kRing];
+      const bool full = t0 + c * L + L <= t1;
+      const bool valid = t0 + c * L + i < t1;
+      KeyAccR acc;
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      acc.ab = z; acc.abt = z; acc.ak = z; acc.rb = z; acc.rk = z;
+      if (full) {
+        key_half_ring<Io, kVExact, true, true>(op, rawc[0], nbias[0], true, 0, i, q, acc);
+        key_half_ring<Io, kVExact, true, true>(op, rawc[1], nbias[1], true, 1, i, q, acc);
+      } else {
+        key_half_ring<Io, kVExact, false, true>(op, rawc[0], nbias[0], valid, 0, i, q, acc);
+        key_half_ring<Io, kVExact, false, true>(op, rawc[1], nbias[1], valid, 1, i, q, acc);
+      }
+      if (c + kKeyW < nchunks) load_chunk(c + kKeyW);
+      key_blocks_ring_sum(op, acc, i, q);
       if (!p.handoff_stall) signal(&sm.ready[kw], (c - kw) / kKeyW + 1);
     }
     __syncthreads();   // pairs with the state waves' final barrier
@@ -1651,6 +1806,15 @@ void launch_real_pass(dim3 grid, hipStream_t s, const SegArgs& p) {
     hipLaunchKernelGGL((chunk64_kernel<Io, false>), grid, dim3(NT), 0, s, p);
 }
 
+// the summary pass: the ring variant when it is selected
+template <class Io>
+void launch_summary_pass(dim3 grid, hipStream_t s, const SegArgs& p) {
+  if (chunk_ring_enabled())
+    hipLaunchKernelGGL((chunk64rs_kernel<Io>), grid, dim3(NTR), 0, s, p);
+  else
+    hipLaunchKernelGGL((chunk64_kernel<Io, false, false, true>), grid, dim3(NT_SUM), 0, s, p);
+}
+
 template <class Io>
 int launch_split_kernels(const SegArgs& p, int nseg, int pieces, hipStream_t s,
                          hipStream_t aux) {
@@ -1658,7 +1822,7 @@ int launch_split_kernels(const SegArgs& p, int nseg, int pieces, hipStream_t s,
   if (p.split_lead <= 0) {
     // classic: summaries of pieces 0..P-2, combine from the slot, every piece
     const dim3 gsum(H, nseg * (pieces - 1)), gcomb(H, nseg), greal(H, nseg * pieces);
-    hipLaunchKernelGGL((chunk64_kernel<Io, false, false, true>), gsum, dim3(NT_SUM), 0, s, p);
+    launch_summary_pass<Io>(gsum, s, p);
     hipLaunchKernelGGL(split_combine_kernel, gcomb, dim3(256), 0, s, p);
     launch_real_pass<Io>(greal, s, p);
     return FR2_OK;
@@ -1685,8 +1849,7 @@ int launch_split_kernels(const SegArgs& p, int nseg, int pieces, hipStream_t s,
   ps.split_first = 1;
   ps.split_count = pieces - 2;
   if (pieces > 2)
-    hipLaunchKernelGGL((chunk64_kernel<Io, false, false, true>), dim3(H, nseg * (pieces - 2)),
-                       dim3(NT_SUM), 0, s, ps);
+    launch_summary_pass<Io>(dim3(H, nseg * (pieces - 2)), s, ps);
   if (aux != nullptr) {
     // the join cannot be replaced by a host wait: that is illegal while the
     // streams are being captured into a graph
