@@ -1316,6 +1316,13 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
   } else if (p.uniform_len > 0) {
     t0 = seg * p.uniform_len;
     t1 = t0 + p.uniform_len;
+  } else if (p.chunk_offsets != nullptr) {
+    // a sequence's list of contiguous chunks (the rl_infctx forward)
+    t0 = p.bounds[p.chunk_offsets[seg]];
+    t1 = p.ends[p.chunk_offsets[seg + 1] - 1];
+  } else if (p.ends != nullptr) {
+    t0 = p.bounds[seg];
+    t1 = p.ends[seg];
   } else {
     t0 = p.bounds[seg];
     t1 = p.bounds[seg + 1];
@@ -1343,6 +1350,14 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) S[kb][e] = sin[(kb * 16 + 4 * q + e) * D + vcol];
+    } else if (p.state_in != nullptr && p.state_bf16) {
+      // (bf16-state contract) widened once; the state stays fp32 for the
+      // whole call and is rounded back once at the end
+      const uint16_t* sinb = static_cast<const uint16_t*>(p.state_in) + sbase + vcol;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[kb][e] = IoBF16::to_f32(sinb[(kb * 16 + 4 * q + e) * D]);
     } else if (p.state_in != nullptr) {
       const float* sin = static_cast<const float*>(p.state_in) + sbase + vcol;
 #pragma unroll
@@ -1391,6 +1406,13 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) sout[(kb * 16 + 4 * q + e) * D + vcol] = S[kb][e];
       }
+    } else if (p.state_out != nullptr && p.state_bf16) {
+      uint16_t* soutb = static_cast<uint16_t*>(p.state_out) + sbase + vcol;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          soutb[(kb * 16 + 4 * q + e) * D] = IoBF16::from_f32(S[kb][e]);
     } else if (p.state_out != nullptr) {
       float* sout = static_cast<float*>(p.state_out) + sbase + vcol;
 #pragma unroll
@@ -1619,11 +1641,11 @@ void set_handoff_spin_limit(int polls) {
   g_spin_limit.store(polls < 0 ? (1 << 20) : polls, std::memory_order_relaxed);
 }
 
-// the ring variant covers the plain fp32-state contract only: no chunk
-// lists or segment ends, no boundary snapshots, no sa or read-out outputs
+// the ring variant covers the inference contracts (fp32 or bf16 state,
+// packed, uniform or chunk-list segments); the training outputs (boundary
+// snapshots, sa) and the fused read-out stay on chunk64_kernel
 bool ring_contract(const SegArgs& p) {
-  return chunk_ring_enabled() && !p.state_bf16 && p.chunk_offsets == nullptr &&
-         p.ends == nullptr && p.boundary == nullptr && p.sa_out == nullptr &&
+  return chunk_ring_enabled() && p.boundary == nullptr && p.sa_out == nullptr &&
          p.ro_out == nullptr;
 }
 
@@ -1796,8 +1818,7 @@ bool split_events(SplitEvents*& ev) {
   return true;
 }
 
-// a real (non-summary) pass of the plain contract: the ring variant when it
-// is selected and the state is fp32
+// a real (non-summary) pass: the ring variant when it is selected
 template <class Io>
 void launch_real_pass(dim3 grid, hipStream_t s, const SegArgs& p) {
   if (ring_contract(p))
