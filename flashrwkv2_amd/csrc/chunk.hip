@@ -1136,10 +1136,23 @@ struct KeyAccR {
 // One key half hh of chunk operators: as key_part1 (plain contract) plus the
 // operand-row stores of key_part2, with the token-token products accumulated.
 // kSum (summary pass): no R~ operand, no R-side products.
-template <class Io, bool kVExact, bool kFull, bool kSum = false>
+// Per-lane channel parameters of the fused kk / a-gate stage for the lane's
+// eight keys of one key half: the kk scale, the a-gate bias a0 and k_a.
+struct KkHalf {
+  float kks[8], a0[8], ka[8];
+};
+
+// kKK (fused kk / a-gate stage): slot 4 of raw holds the a-gate logits a12,
+// slot 5 is unused; kinv = 1 / max(|k k_k|, 1e-12) over the token's 64 keys;
+// the gated key k' is stored to nk_row (when the token is in the segment):
+//   kk = k k_k kinv, g = sigmoid(a0 + a12), k' = k (1 + (g - 1) k_a),
+//   a = -kk, b = kk g.
+template <class Io, bool kVExact, bool kFull, bool kSum = false, bool kKK = false>
 __device__ __forceinline__ void key_half_ring(ChunkOps<kVExact>& op, const u32x4 (&raw)[6],
                                               const float (&nbias8)[8], bool valid, int hh,
-                                              int i, int q, KeyAccR& acc) {
+                                              int i, int q, KeyAccR& acc,
+                                              const KkHalf* kp = nullptr, float kinv = 0.0f,
+                                              typename Io::raw* nk_row = nullptr) {
   const int kbase = 32 * hh + 8 * q;
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
   auto tok = [&](int j) { return (kFull || valid) ? raw[j] : zero4; };
@@ -1147,8 +1160,35 @@ __device__ __forceinline__ void key_half_ring(ChunkOps<kVExact>& op, const u32x4
   if constexpr (!kSum) unpack8<Io>(tok(0), xr);
   unpack8<Io>(raw[1], xl);
   unpack8<Io>(tok(2), xk);
-  unpack8<Io>(tok(4), xa);
-  unpack8<Io>(tok(5), xb);
+  if constexpr (kKK) {
+    float x12[8], nk[8];
+    unpack8<Io>(tok(4), x12);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float kk = xk[e] * kp->kks[e] * kinv;
+      const float g = __builtin_amdgcn_rcpf(
+          1.0f + __builtin_amdgcn_exp2f(-kLog2e * (kp->a0[e] + x12[e])));
+      nk[e] = xk[e] * __builtin_fmaf(g - 1.0f, kp->ka[e], 1.0f);
+      xa[e] = -kk;
+      xb[e] = kk * g;
+    }
+    if (nk_row != nullptr && (kFull || valid)) {
+      u32x4 packed;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = __builtin_bit_cast(uint16_t, Io::from_f32(nk[2 * j]));
+        const uint32_t hi = __builtin_bit_cast(uint16_t, Io::from_f32(nk[2 * j + 1]));
+        packed[j] = lo | (hi << 16);
+      }
+      *reinterpret_cast<u32x4*>(nk_row + kbase) = packed;
+    }
+    // the recurrence uses the gated key (masked rows stay zero)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xk[e] = (kFull || valid) ? nk[e] : 0.0f;
+  } else {
+    unpack8<Io>(tok(4), xa);
+    unpack8<Io>(tok(5), xb);
+  }
   constexpr float kC = kNegExpHalf * kLog2e;
   constexpr float kInvC = 1.0f / kC;
   float g2[8], gm[8], gp[8], at[8], rt[8], bh[8], kh[8];
@@ -1270,7 +1310,10 @@ __device__ __forceinline__ void key_blocks_ring_sum(ChunkOps<kVExact>& op, const
   store_aop(op.mak, i, q, as_a(split4(mak)));
 }
 
-template <class Io>
+// kKK: wkv_prepare's kk / a-gate stage fused into the key waves' load stage
+// (p.k is the projected key, p.a the a-gate logits a12; the gated key goes
+// to p.new_k), as in chunk64_kernel.
+template <class Io, bool kKK = false>
 __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
   using raw = typename Io::raw;
   constexpr bool kVExact = !__is_same(Io, IoF16);
@@ -1434,8 +1477,20 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
     const raw* src[6] = {
         static_cast<const raw*>(p.r), static_cast<const raw*>(p.logits),
         static_cast<const raw*>(p.k), static_cast<const raw*>(p.v),
-        static_cast<const raw*>(p.a), static_cast<const raw*>(p.b)};
+        static_cast<const raw*>(p.a), kKK ? nullptr : static_cast<const raw*>(p.b)};
     u32x4 rawc[2][6];
+    KkHalf kph[2];
+    if constexpr (kKK) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int64_t ch = head_off + 32 * hh + 8 * q + e;
+          kph[hh].kks[e] = Io::to_f32(static_cast<const raw*>(p.kk_scale)[ch]);
+          kph[hh].a0[e] = Io::to_f32(static_cast<const raw*>(p.a_bias)[ch]);
+          kph[hh].ka[e] = Io::to_f32(static_cast<const raw*>(p.k_a)[ch]);
+        }
+    }
     // rows past the sequence end are loaded from its last row (in bounds);
     // key_half_ring zeroes them
     auto load_chunk = [&](int c) {
@@ -1445,8 +1500,10 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
         for (int j = 0; j < 6; ++j)
-          rawc[hh][j] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x4*>(src[j] + off + 32 * hh));
+          rawc[hh][j] = (kKK && j == 5)   // b is formed from the key
+                            ? u32x4{0u, 0u, 0u, 0u}
+                            : __builtin_nontemporal_load(
+                                  reinterpret_cast<const u32x4*>(src[j] + off + 32 * hh));
     };
     if (kw < nchunks) load_chunk(kw);
     for (int c = kw; c < nchunks; c += kKeyW) {
@@ -1458,12 +1515,38 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
       KeyAccR acc;
       const f32x4 z = {0.f, 0.f, 0.f, 0.f};
       acc.ab = z; acc.abt = z; acc.ak = z; acc.rb = z; acc.rk = z;
+      float kinv = 0.0f;
+      raw* nk_row = nullptr;
+      if constexpr (kKK) {
+        // 1 / |k k_k| over the token's 64 keys (the four lanes of token i
+        // hold 16 each)
+        float ss = 0.0f;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          float xk[8];
+          unpack8<Io>(rawc[hh][2], xk);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float u = xk[e] * kph[hh].kks[e];
+            ss = __builtin_fmaf(u, u, ss);
+          }
+        }
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        kinv = __builtin_amdgcn_rcpf(fmaxf(__builtin_sqrtf(ss), 1.0e-12f));
+        nk_row = static_cast<raw*>(p.new_k) +
+                 static_cast<int64_t>(t0 + c * L + i) * row_stride + head_off;
+      }
       if (full) {
-        key_half_ring<Io, kVExact, true>(op, rawc[0], nbias[0], true, 0, i, q, acc);
-        key_half_ring<Io, kVExact, true>(op, rawc[1], nbias[1], true, 1, i, q, acc);
+        key_half_ring<Io, kVExact, true, false, kKK>(op, rawc[0], nbias[0], true, 0, i, q, acc,
+                                                     &kph[0], kinv, nk_row);
+        key_half_ring<Io, kVExact, true, false, kKK>(op, rawc[1], nbias[1], true, 1, i, q, acc,
+                                                     &kph[1], kinv, nk_row);
       } else {
-        key_half_ring<Io, kVExact, false>(op, rawc[0], nbias[0], valid, 0, i, q, acc);
-        key_half_ring<Io, kVExact, false>(op, rawc[1], nbias[1], valid, 1, i, q, acc);
+        key_half_ring<Io, kVExact, false, false, kKK>(op, rawc[0], nbias[0], valid, 0, i, q,
+                                                      acc, &kph[0], kinv, nk_row);
+        key_half_ring<Io, kVExact, false, false, kKK>(op, rawc[1], nbias[1], valid, 1, i, q,
+                                                      acc, &kph[1], kinv, nk_row);
       }
       if (c + kKeyW < nchunks) load_chunk(c + kKeyW);
       if constexpr (kVExact)
@@ -1699,10 +1782,15 @@ int launch_chunked_kk(int dtype, const SegArgs& args, int nseg, hipStream_t s) {
   if (ro && (p.ro_g == nullptr || p.ro_rk == nullptr || p.ro_lnw == nullptr ||
              p.ro_lnb == nullptr))
     return FR2_ERR_INVALID_ARGUMENT;
+  // the fused read-out needs a token's whole output row at the write-back:
+  // chunk64_kernel; the kk / a-gate stage alone runs on the ring variant
+  const bool ring = !ro && ring_contract(p);
   if (dtype == FR2_DTYPE_BFLOAT16) {
     if (ro)
       hipLaunchKernelGGL((chunk64_kernel<IoBF16, false, false, false, true, true>), grid,
                          dim3(NT), 0, s, p);
+    else if (ring)
+      hipLaunchKernelGGL((chunk64r_kernel<IoBF16, true>), grid, dim3(NTR), 0, s, p);
     else
       hipLaunchKernelGGL((chunk64_kernel<IoBF16, false, false, false, true>), grid, dim3(NT), 0,
                          s, p);
@@ -1710,6 +1798,8 @@ int launch_chunked_kk(int dtype, const SegArgs& args, int nseg, hipStream_t s) {
     if (ro)
       hipLaunchKernelGGL((chunk64_kernel<IoF16, false, false, false, true, true>), grid, dim3(NT),
                          0, s, p);
+    else if (ring)
+      hipLaunchKernelGGL((chunk64r_kernel<IoF16, true>), grid, dim3(NTR), 0, s, p);
     else
       hipLaunchKernelGGL((chunk64_kernel<IoF16, false, false, false, true>), grid, dim3(NT), 0,
                          s, p);
