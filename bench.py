@@ -524,7 +524,7 @@ def time_kk_fused(torch, flashrwkv2_amd, steps: int, serving: bool = False):
     else:
         w = workloads.config(1, "cuda", dtype=torch.float16)
         rec_kernel, kk_kernel, ro_kernel = (
-            "chunk64r_kernel<IoF16>", "chunk64_kernel<IoF16,false,false,false,true>",
+            "chunk64r_kernel<IoF16>", "chunk64r_kernel<IoF16,kk>",
             "chunk64_kernel<IoF16,false,false,false,true,true>")
         name = "cfg1_prefill_B8_T4096_H32_fp16_kk_gate"
     T, H, D = w.total_tokens, w.num_heads, 64
