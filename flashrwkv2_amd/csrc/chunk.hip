@@ -57,14 +57,15 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegExpHalf = -0.6065306597126334f;   // -exp(-1/2)
 
 // Operators of one chunk consumed by the state path.  For bf16 tokens V is
-// exact in bf16 (no lo part); fp16 tokens need V's lo part, and their token
-// rows take a smaller pad so that the key rows keep theirs within the LDS
-// budget (unpadded 128-byte key rows put the eight lanes of each 16-byte
-// read on the same banks: 0.438 vs 0.344 ms on config 1 in fp16).
+// exact in bf16 (no lo part); fp16 tokens need V's lo part.
+//
+// Every row array is addressed through the piece swizzles a_col, b_col and
+// aop_piece (unswizzled, the same accesses cost ~430 bank-conflict cycles
+// per chunk).
 template <bool kVExact>
 struct alignas(16) ChunkOps {
-  static constexpr int RP = D + 8;                  // key row length
-  static constexpr int TP = kVExact ? D + 16 : D + 8;   // token row of B^, K^, V
+  static constexpr int RP = D;                      // key row length
+  static constexpr int TP = D + 16;                 // token row of B^, K^, V
   float gl[D];                        // gamma_L (read as 16-byte vectors)
   __bf16 at_h[L][RP], at_l[L][RP];    // A~ rows, keys at key_pos()
   __bf16 r_h[L][RP], r_l[L][RP];      // R~ rows, keys at key_pos()
@@ -120,16 +121,16 @@ template <int RP>
 __device__ __forceinline__ Sp8 rows_vs_state(const __bf16 (*xh)[RP], const __bf16 (*xl)[RP],
                                              int m, int i, int q) {
   Sp8 s;
-  s.hi = *reinterpret_cast<const bf16x8*>(&xh[i][32 * m + 8 * q]);
-  s.lo = *reinterpret_cast<const bf16x8*>(&xl[i][32 * m + 8 * q]);
+  s.hi = *reinterpret_cast<const bf16x8*>(&xh[i][a_col(i, 32 * m + 8 * q)]);
+  s.lo = *reinterpret_cast<const bf16x8*>(&xl[i][a_col(i, 32 * m + 8 * q)]);
   return s;
 }
 
 __device__ __forceinline__ AOp load_aop(const __bf16 (*x)[2 * L], int i, int q) {
-  return *reinterpret_cast<const AOp*>(&x[i][8 * q]);
+  return *reinterpret_cast<const AOp*>(&x[i][8 * aop_piece(i, q)]);
 }
 __device__ __forceinline__ void store_aop(__bf16 (*x)[2 * L], int i, int q, const AOp& v) {
-  *reinterpret_cast<AOp*>(&x[i][8 * q]) = v;
+  *reinterpret_cast<AOp*>(&x[i][8 * aop_piece(i, q)]) = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -332,22 +333,22 @@ __device__ __forceinline__ void key_part2(Smem<kVExact>& sm, ChunkOps<kVExact>& 
     // keys kbase..kbase+7 land in two 4-key runs of the permuted rows
     const int p0 = key_pos(kbase), p1 = key_pos(kbase + 4);
     if constexpr (!kSum) {
-      *reinterpret_cast<bf16x4*>(&op.r_h[i][p0]) = kr.Rs.hi.lo;
-      *reinterpret_cast<bf16x4*>(&op.r_h[i][p1]) = kr.Rs.hi.hi;
-      *reinterpret_cast<bf16x4*>(&op.r_l[i][p0]) = kr.Rs.lo.lo;
-      *reinterpret_cast<bf16x4*>(&op.r_l[i][p1]) = kr.Rs.lo.hi;
+      *reinterpret_cast<bf16x4*>(&op.r_h[i][a_col(i, p0)]) = kr.Rs.hi.lo;
+      *reinterpret_cast<bf16x4*>(&op.r_h[i][a_col(i, p1)]) = kr.Rs.hi.hi;
+      *reinterpret_cast<bf16x4*>(&op.r_l[i][a_col(i, p0)]) = kr.Rs.lo.lo;
+      *reinterpret_cast<bf16x4*>(&op.r_l[i][a_col(i, p1)]) = kr.Rs.lo.hi;
     }
-    *reinterpret_cast<bf16x4*>(&op.at_h[i][p0]) = kr.As.hi.lo;
-    *reinterpret_cast<bf16x4*>(&op.at_h[i][p1]) = kr.As.hi.hi;
-    *reinterpret_cast<bf16x4*>(&op.at_l[i][p0]) = kr.As.lo.lo;
-    *reinterpret_cast<bf16x4*>(&op.at_l[i][p1]) = kr.As.lo.hi;
+    *reinterpret_cast<bf16x4*>(&op.at_h[i][a_col(i, p0)]) = kr.As.hi.lo;
+    *reinterpret_cast<bf16x4*>(&op.at_h[i][a_col(i, p1)]) = kr.As.hi.hi;
+    *reinterpret_cast<bf16x4*>(&op.at_l[i][a_col(i, p0)]) = kr.As.lo.lo;
+    *reinterpret_cast<bf16x4*>(&op.at_l[i][a_col(i, p1)]) = kr.As.lo.hi;
   }
-  *reinterpret_cast<bf16x8*>(&op.b_h[i][kbase]) = kr.Bs.hi;
-  *reinterpret_cast<bf16x8*>(&op.b_l[i][kbase]) = kr.Bs.lo;
-  *reinterpret_cast<bf16x8*>(&op.k_h[i][kbase]) = kr.Ks.hi;
-  *reinterpret_cast<bf16x8*>(&op.k_l[i][kbase]) = kr.Ks.lo;
-  *reinterpret_cast<bf16x8*>(&op.v_h[i][kbase]) = kr.Vs.hi;
-  if constexpr (!kVExact) *reinterpret_cast<bf16x8*>(&op.v_l[i][kbase]) = kr.Vs.lo;
+  *reinterpret_cast<bf16x8*>(&op.b_h[i][b_col(i, kbase)]) = kr.Bs.hi;
+  *reinterpret_cast<bf16x8*>(&op.b_l[i][b_col(i, kbase)]) = kr.Bs.lo;
+  *reinterpret_cast<bf16x8*>(&op.k_h[i][b_col(i, kbase)]) = kr.Ks.hi;
+  *reinterpret_cast<bf16x8*>(&op.k_l[i][b_col(i, kbase)]) = kr.Ks.lo;
+  *reinterpret_cast<bf16x8*>(&op.v_h[i][b_col(i, kbase)]) = kr.Vs.hi;
+  if constexpr (!kVExact) *reinterpret_cast<bf16x8*>(&op.v_l[i][b_col(i, kbase)]) = kr.Vs.lo;
   // P[t][s] of block b, summed over the two key halves, is
   // mp0[0][b][s][t] + mp0[1][b][s][t]
   const float (*mp0)[4][L][MPP] = sm.mpart[mp][cc];
@@ -409,8 +410,8 @@ __device__ __forceinline__ void state_load_early(StateOps<kVExact>& o, const Chu
   // transposed operands straight from the token rows (see tr_rows)
   const int trow = 4 * q + (i >> 2), tcol = 4 * (i & 3);
   const int vc0 = 16 * (vcol >> 4) + tcol;
-  o.vh = tr_rows(&op.v_h[trow][vc0]);                                   // V[4q+e][vcol]
-  if constexpr (!kVExact) o.vl = tr_rows(&op.v_l[trow][vc0]);
+  o.vh = tr_rows(&op.v_h[trow][b_col(trow, vc0)]);                                   // V[4q+e][vcol]
+  if constexpr (!kVExact) o.vl = tr_rows(&op.v_l[trow][b_col(trow, vc0)]);
   o.Aa0 = rows_vs_state(op.at_h, op.at_l, 0, i, q);
   o.Aa1 = rows_vs_state(op.at_h, op.at_l, 1, i, q);
   if constexpr (!kSum) {
@@ -429,11 +430,11 @@ __device__ __forceinline__ void state_load_late(StateOps<kVExact>& o, const Chun
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
     // B^^T, K^^T as A operands: row 16kb+i, K = token
-    o.Bt[kb] = __builtin_shufflevector(tr_rows(&op.b_h[trow][kb * 16 + tcol]),
-                                       tr_rows(&op.b_l[trow][kb * 16 + tcol]), 0, 1, 2, 3, 4,
+    o.Bt[kb] = __builtin_shufflevector(tr_rows(&op.b_h[trow][b_col(trow, kb * 16 + tcol)]),
+                                       tr_rows(&op.b_l[trow][b_col(trow, kb * 16 + tcol)]), 0, 1, 2, 3, 4,
                                        5, 6, 7);
-    o.Kt[kb] = __builtin_shufflevector(tr_rows(&op.k_h[trow][kb * 16 + tcol]),
-                                       tr_rows(&op.k_l[trow][kb * 16 + tcol]), 0, 1, 2, 3, 4,
+    o.Kt[kb] = __builtin_shufflevector(tr_rows(&op.k_h[trow][b_col(trow, kb * 16 + tcol)]),
+                                       tr_rows(&op.k_l[trow][b_col(trow, kb * 16 + tcol)]), 0, 1, 2, 3, 4,
                                        5, 6, 7);
     o.gl[kb] = *reinterpret_cast<const f32x4*>(&op.gl[kb * 16 + 4 * q]);
   }
@@ -1241,21 +1242,21 @@ __device__ __forceinline__ void key_half_ring(ChunkOps<kVExact>& op, const u32x4
   // runs of the permuted A~ / R~ rows)
   const int p0 = key_pos(kbase), p1 = key_pos(kbase + 4);
   if constexpr (!kSum) {
-    *reinterpret_cast<bf16x4*>(&op.r_h[i][p0]) = Rs.hi.lo;
-    *reinterpret_cast<bf16x4*>(&op.r_h[i][p1]) = Rs.hi.hi;
-    *reinterpret_cast<bf16x4*>(&op.r_l[i][p0]) = Rs.lo.lo;
-    *reinterpret_cast<bf16x4*>(&op.r_l[i][p1]) = Rs.lo.hi;
+    *reinterpret_cast<bf16x4*>(&op.r_h[i][a_col(i, p0)]) = Rs.hi.lo;
+    *reinterpret_cast<bf16x4*>(&op.r_h[i][a_col(i, p1)]) = Rs.hi.hi;
+    *reinterpret_cast<bf16x4*>(&op.r_l[i][a_col(i, p0)]) = Rs.lo.lo;
+    *reinterpret_cast<bf16x4*>(&op.r_l[i][a_col(i, p1)]) = Rs.lo.hi;
   }
-  *reinterpret_cast<bf16x4*>(&op.at_h[i][p0]) = As.hi.lo;
-  *reinterpret_cast<bf16x4*>(&op.at_h[i][p1]) = As.hi.hi;
-  *reinterpret_cast<bf16x4*>(&op.at_l[i][p0]) = As.lo.lo;
-  *reinterpret_cast<bf16x4*>(&op.at_l[i][p1]) = As.lo.hi;
-  *reinterpret_cast<bf16x8*>(&op.b_h[i][kbase]) = Bs.hi;
-  *reinterpret_cast<bf16x8*>(&op.b_l[i][kbase]) = Bs.lo;
-  *reinterpret_cast<bf16x8*>(&op.k_h[i][kbase]) = Ks.hi;
-  *reinterpret_cast<bf16x8*>(&op.k_l[i][kbase]) = Ks.lo;
-  *reinterpret_cast<bf16x8*>(&op.v_h[i][kbase]) = Vs.hi;
-  if constexpr (!kVExact) *reinterpret_cast<bf16x8*>(&op.v_l[i][kbase]) = Vs.lo;
+  *reinterpret_cast<bf16x4*>(&op.at_h[i][a_col(i, p0)]) = As.hi.lo;
+  *reinterpret_cast<bf16x4*>(&op.at_h[i][a_col(i, p1)]) = As.hi.hi;
+  *reinterpret_cast<bf16x4*>(&op.at_l[i][a_col(i, p0)]) = As.lo.lo;
+  *reinterpret_cast<bf16x4*>(&op.at_l[i][a_col(i, p1)]) = As.lo.hi;
+  *reinterpret_cast<bf16x8*>(&op.b_h[i][b_col(i, kbase)]) = Bs.hi;
+  *reinterpret_cast<bf16x8*>(&op.b_l[i][b_col(i, kbase)]) = Bs.lo;
+  *reinterpret_cast<bf16x8*>(&op.k_h[i][b_col(i, kbase)]) = Ks.hi;
+  *reinterpret_cast<bf16x8*>(&op.k_l[i][b_col(i, kbase)]) = Ks.lo;
+  *reinterpret_cast<bf16x8*>(&op.v_h[i][b_col(i, kbase)]) = Vs.hi;
+  if constexpr (!kVExact) *reinterpret_cast<bf16x8*>(&op.v_l[i][b_col(i, kbase)]) = Vs.lo;
   // mma32x3(X, Y), X, Y in the load layout: item e = X_{4q+e} . Y_i over
   // this lane's keys
   acc.ab = mma32x3(As, Bs, acc.ab);

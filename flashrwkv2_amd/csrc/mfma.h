@@ -160,6 +160,26 @@ __device__ __forceinline__ AOp t_inverse(f32x4 M, f32x4 Mt, int i, int q) {
   return as_a(split4(Tt));                                              // = A operand of T
 }
 
+// LDS row swizzles of the chunk operators: the 16-byte pieces of a row are
+// permuted by an XOR with bits of the row index, so that the lanes of one
+// LDS access spread over the banks.  Each was chosen from bank-conflict
+// counter readings (SQ_LDS_BANK_CONFLICT) of its array's access patterns on
+// gfx950.  Columns are in bf16 units; an access never crosses a piece.
+//   a_col: the A~ / R~ rows (128 bytes), piece XOR row & 7: the 16-byte
+//     reads against the state conflict-free, the 8-byte operand stores at
+//     half the unswizzled excess;
+//   b_col: the B^ / K^ / V token rows (160 bytes), piece XOR (row >> 2) & 3:
+//     the 16-byte row stores and the transposed 8-byte reads conflict-free;
+//   aop_piece: the 16 x 16 token-token blocks (64-byte rows), piece XOR
+//     (row >> 1) & 3: their 16-byte stores and reads conflict-free.
+__device__ __forceinline__ int a_col(int row, int col) {
+  return (((col >> 3) ^ (row & 7)) << 3) | (col & 7);
+}
+__device__ __forceinline__ int b_col(int row, int col) {
+  return (((col >> 3) ^ ((row >> 2) & 3)) << 3) | (col & 7);
+}
+__device__ __forceinline__ int aop_piece(int i, int q) { return q ^ ((i >> 1) & 3); }
+
 // Inclusive prefix sum over the 16 lanes of a DPP row (the token axis).
 template <int N>
 __device__ __forceinline__ float row_shr(float x) {
