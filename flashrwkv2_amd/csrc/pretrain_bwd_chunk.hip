@@ -105,6 +105,10 @@ __device__ __forceinline__ float row_allsum(float x) {
   x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x121, 0xf, 0xf, false));
   return x;
 }
+// lane 15 of the lane's DPP row, in every lane of the row (row_newbcast)
+__device__ __forceinline__ float row_last(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x15f, 0xf, 0xf, false));
+}
 // inclusive suffix sum over the 16 lanes of a DPP row (row_shl: lane l
 // reads lane l+N, zero past the row end)
 __device__ __forceinline__ float row_suffix(float x) {
@@ -241,7 +245,7 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
         const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLg2e * x));
         const float lw2 = kCl * sg;
         const float G = row_scan(lw2);
-        const float G15 = __shfl(G, (lane & 48) + 15);
+        const float G15 = row_last(G);
         const float Gp = G - lw2;
         const float ig = __builtin_amdgcn_exp2f(-G);
         sm.gm[key][tp] = __builtin_amdgcn_exp2f(G);
@@ -354,13 +358,18 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
     float dr[4], da[4], dk[4], db[4], dw[4];
     {
       const int t = n;
-#pragma unroll
       // raw per-(row, token) values are rebuilt from the stored scaled ones:
       // b = B^ gamma, k = K^ gamma, r = R^ gamma_15 / gamma, a = A^ gamma_15 / gamma_{t-1}
+      // (branch-free: token 0's terms are masked arithmetically, so that the
+      // four rows' LDS reads and scans form one block the scheduler can
+      // interleave, instead of a divergent branch per row)
+      const float tpos = t > 0 ? 1.0f : 0.0f;
+#pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int rk = 16 * wv + 4 * q + e;
         const float g = sm.gm[rk][t], g15 = sm.gm[rk][15];
-        const float gp = t > 0 ? sm.gm[rk][max(t - 1, 0)] : 1.0f;
+        const float gm1 = sm.gm[rk][max(t - 1, 0)];
+        const float gp = t > 0 ? gm1 : 1.0f;   // gamma_{t-1} (1 at t = 0)
         const float rho = g15 * __builtin_amdgcn_rcpf(g);   // gamma_15 / gamma_t
         dr[e] = p.scale * g * DR[e];
         da[e] = gp * DA[e];
@@ -370,14 +379,15 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
         const float bhv = sm.bh[rk][t], khv = sm.kh[rk][t];
         const float part = row_allsum(bhv * DB0[e] + khv * DK0[e]);
         const float rs0 = __shfl(pcs0, 4 * q + e);   // lanes 4q+e hold row 16wv+4q+e
-        const float dr15 = __shfl(dr[e], (lane & 48) + 15);
+        const float dr15 = row_last(dr[e]);
         const float z15 = sm.rh[rk][15] * dr15 + g15 * (rs0 + part);
         const float bd = bhv * g * db[e] + khv * g * dk[e];
         // inc_t = -b_t db_t - k_t dk_t + a_t da_t + r_{t-1} dr_{t-1}   (t >= 1)
         const float drp = row_prev(dr[e], 0.0f);
-        const float rp = t > 0 ? sm.rh[rk][max(t - 1, 0)] * g15 * __builtin_amdgcn_rcpf(gp) : 0.0f;
-        const float av = sm.ah[rk][t] * g15 * __builtin_amdgcn_rcpf(gp);
-        const float inc = t > 0 ? -bd + av * da[e] + rp * drp : 0.0f;
+        const float igp = __builtin_amdgcn_rcpf(gp);
+        const float rp = sm.rh[rk][max(t - 1, 0)] * g15 * igp;
+        const float av = sm.ah[rk][t] * g15 * igp;
+        const float inc = tpos * (-bd + av * da[e] + rp * drp);
         const float z = z15 + row_suffix(inc) - inc;   // Z_t
         dw[e] = (z - bd) * sm.wsf[rk][t];
       }
