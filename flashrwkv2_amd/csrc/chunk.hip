@@ -1148,12 +1148,17 @@ struct KkHalf {
 // the gated key k' is stored to nk_row (when the token is in the segment):
 //   kk = k k_k kinv, g = sigmoid(a0 + a12), k' = k (1 + (g - 1) k_a),
 //   a = -kk, b = kk g.
-template <class Io, bool kVExact, bool kFull, bool kSum = false, bool kKK = false>
+// kRev (the training backward's value pass): unit_w marks a lane whose
+// shifted retention row lies past the segment (unit retention), and K^ is
+// scaled by kscale (k is r_t there, times the output scale).
+template <class Io, bool kVExact, bool kFull, bool kSum = false, bool kKK = false,
+          bool kRev = false>
 __device__ __forceinline__ void key_half_ring(ChunkOps<kVExact>& op, const u32x4 (&raw)[6],
                                               const float (&nbias8)[8], bool valid, int hh,
                                               int i, int q, KeyAccR& acc,
                                               const KkHalf* kp = nullptr, float kinv = 0.0f,
-                                              typename Io::raw* nk_row = nullptr) {
+                                              typename Io::raw* nk_row = nullptr,
+                                              bool unit_w = false, float kscale = 1.0f) {
   const int kbase = 32 * hh + 8 * q;
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
   auto tok = [&](int j) { return (kFull || valid) ? raw[j] : zero4; };
@@ -1200,6 +1205,7 @@ __device__ __forceinline__ void key_half_ring(ChunkOps<kVExact>& op, const u32x4
   for (int e = 0; e < 8; ++e) {
     float lw2 = __builtin_amdgcn_rcpf(__builtin_fmaf(g2[e], kInvC, kInvC));
     if constexpr (!kFull) lw2 = valid ? lw2 : 0.0f;
+    if constexpr (kRev) lw2 = unit_w ? 0.0f : lw2;
     g2[e] = lw2;
   }
 #pragma unroll
@@ -1221,6 +1227,7 @@ __device__ __forceinline__ void key_half_ring(ChunkOps<kVExact>& op, const u32x4
     if constexpr (!kSum) rt[e] = xr[e] * gm[e];
     bh[e] = xb[e] * ig;
     kh[e] = xk[e] * ig;
+    if constexpr (kRev) kh[e] *= kscale;
   }
   if (i == L - 1) {
     *reinterpret_cast<f32x4*>(&op.gl[kbase]) = f32x4{gm[0], gm[1], gm[2], gm[3]};
@@ -1314,7 +1321,14 @@ __device__ __forceinline__ void key_blocks_ring_sum(ChunkOps<kVExact>& op, const
 // kKK: wkv_prepare's kk / a-gate stage fused into the key waves' load stage
 // (p.k is the projected key, p.a the a-gate logits a12; the gated key goes
 // to p.new_k), as in chunk64_kernel.
-template <class Io, bool kKK = false>
+// kRev: the training backward's value pass (uniform segments, a multiple of
+// 16 tokens): the recurrence runs from the segment's last token to its
+// first, tensor j read one row later when bit j of p.shift_mask is set (a
+// shifted row past the end reads as zero, with unit retention); y, the
+// per-token sa (p.sa_out, fp32) and the state snapshots (p.boundary, at
+// index boundary_per_seg - 1 - c for every boundary_every-th chunk) are
+// written at the mirrored positions, as chunk64_kernel's reverse mode does.
+template <class Io, bool kKK = false, bool kRev = false>
 __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
   using raw = typename Io::raw;
   constexpr bool kVExact = !__is_same(Io, IoF16);
@@ -1416,12 +1430,37 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
     // to this wave alone and its LDS accesses complete in order, so no wave
     // waits for another over the output.
     const int y_row = lane >> 1, y_c0 = 16 * (wv & 3) + 8 * (lane & 1);
+    // value pass: sa column of this lane and its snapshot column
+    float* const sa_base = kRev ? p.sa_out + head_off + vcol : nullptr;
+    const int nsnap = kRev ? (p.boundary_per_seg + p.boundary_every - 1) / p.boundary_every : 0;
+    float* const bnd_base =
+        (kRev && p.boundary != nullptr)
+            ? p.boundary + (static_cast<int64_t>(seg) * H + h) * nsnap * D * D + vcol
+            : nullptr;
     for (int c = 0; c < nchunks; ++c) {
       wait_ge(&sm.ready[c % kKeyW], c / kKeyW + 1, p.spin_limit, &sm.fault);   // operators of c
       const StateOps<kVExact> o = state_load(sm.ops[c % kRing], vcol, i, q);
-      state_compute<Io, kVExact>(o, S, &sm.yb[0], vcol, i, q, p.scale);
-      const int row = t0 + c * L + y_row;
-      if (lane < 32 && row < t1) {
+      if constexpr (kRev) {
+        // rows t0 + (n - pos) mod n of the segment, which is t1 - pos except
+        // at pos = 0
+        const int pos0 = c * L + 4 * q;
+        SaRows sa_rows;
+        sa_rows.col = sa_base;
+        sa_rows.row_stride = row_stride;
+        sa_rows.row0 = t1 - pos0;
+        sa_rows.dir = -1;
+        sa_rows.wrap = pos0 == 0 ? t0 : -1;
+        const int bi = p.boundary_per_seg - 1 - c;
+        const bool keep = bnd_base != nullptr && bi % p.boundary_every == 0;
+        state_compute<Io, kVExact, true>(
+            o, S, &sm.yb[0], vcol, i, q, p.scale, sa_rows,
+            keep ? bnd_base + static_cast<int64_t>(bi / p.boundary_every) * D * D : nullptr);
+      } else {
+        state_compute<Io, kVExact>(o, S, &sm.yb[0], vcol, i, q, p.scale);
+      }
+      const int pos = c * L + y_row;   // position in processing order
+      const int row = kRev ? t1 - 1 - pos : t0 + pos;
+      if (lane < 32 && pos < t1 - t0) {
         const u32x4 piece = *reinterpret_cast<const u32x4*>(&sm.yb[y_row][y_c0]);
         *reinterpret_cast<u32x4*>(yout + static_cast<int64_t>(row) * row_stride + head_off +
                                   y_c0) = piece;
@@ -1436,6 +1475,10 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
       if (yout != nullptr)
         for (int64_t e = tid; e < static_cast<int64_t>(t1 - t0) * D; e += 256)
           yout[(t0 + e / D) * row_stride + head_off + e % D] = nanv;
+      if constexpr (kRev) {
+        for (int64_t e = tid; e < static_cast<int64_t>(t1 - t0) * D; e += 256)
+          p.sa_out[(t0 + e / D) * row_stride + head_off + e % D] = qnan;
+      }
       if (npc > 0 && p.split_lead_pass && piece == 0 && !last_piece) {
         float* sout = p.split_state + (pbase + H) * D * D;
         for (int e = tid; e < D * D; e += 256) sout[e] = qnan;
@@ -1495,16 +1538,22 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
     // rows past the sequence end are loaded from its last row (in bounds);
     // key_half_ring zeroes them
     auto load_chunk = [&](int c) {
-      const int row = min(t0 + c * L + i, t1 - 1);
+      // reverse: position c L + i reads row t1 - 1 - pos, one row later for
+      // the shifted tensors (clamped into the segment; the row past its end
+      // is zeroed where it is consumed)
+      const int row = kRev ? t1 - 1 - (c * L + i) : min(t0 + c * L + i, t1 - 1);
       const int64_t off = static_cast<int64_t>(row) * row_stride + head_off + 8 * q;
+      const int64_t off_sh = static_cast<int64_t>(min(row + 1, t1 - 1)) * row_stride + head_off + 8 * q;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-        for (int j = 0; j < 6; ++j)
+        for (int j = 0; j < 6; ++j) {
+          const int64_t o = (kRev && ((p.shift_mask >> j) & 1)) ? off_sh : off;
           rawc[hh][j] = (kKK && j == 5)   // b is formed from the key
                             ? u32x4{0u, 0u, 0u, 0u}
                             : __builtin_nontemporal_load(
-                                  reinterpret_cast<const u32x4*>(src[j] + off + 32 * hh));
+                                  reinterpret_cast<const u32x4*>(src[j] + o + 32 * hh));
+        }
     };
     if (kw < nchunks) load_chunk(kw);
     for (int c = kw; c < nchunks; c += kKeyW) {
@@ -1538,7 +1587,22 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
         nk_row = static_cast<raw*>(p.new_k) +
                  static_cast<int64_t>(t0 + c * L + i) * row_stride + head_off;
       }
-      if (full) {
+      if constexpr (kRev) {
+        // position 0 of the segment: its shifted rows lie past the end
+        const bool void_row = c == 0 && i == 0;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int j = 0; j < 6; ++j)
+            if (j != 1 && void_row && ((p.shift_mask >> j) & 1)) rawc[hh][j] = u32x4{0u, 0u, 0u, 0u};
+        const bool unit_w = void_row && ((p.shift_mask >> 1) & 1);
+        key_half_ring<Io, kVExact, true, false, false, true>(op, rawc[0], nbias[0], true, 0, i, q,
+                                                            acc, nullptr, 0.0f, nullptr, unit_w,
+                                                            p.kv_scale);
+        key_half_ring<Io, kVExact, true, false, false, true>(op, rawc[1], nbias[1], true, 1, i, q,
+                                                            acc, nullptr, 0.0f, nullptr, unit_w,
+                                                            p.kv_scale);
+      } else if (full) {
         key_half_ring<Io, kVExact, true, false, kKK>(op, rawc[0], nbias[0], true, 0, i, q, acc,
                                                      &kph[0], kinv, nk_row);
         key_half_ring<Io, kVExact, true, false, kKK>(op, rawc[1], nbias[1], true, 1, i, q, acc,
@@ -1748,7 +1812,9 @@ int launch_chunked(int dtype, const SegArgs& args, int nseg, int max_seqlen, hip
     if (p.sa_out == nullptr || (p.boundary == nullptr && !p.reverse) || p.boundary_len != L ||
         p.uniform_len <= 0 || p.uniform_len % L != 0 || dtype != FR2_DTYPE_BFLOAT16)
       return FR2_ERR_UNSUPPORTED;
-    if (p.reverse)
+    if (p.reverse && chunk_ring_enabled())
+      hipLaunchKernelGGL((chunk64r_kernel<IoBF16, false, true>), grid, dim3(NTR), 0, s, p);
+    else if (p.reverse)
       hipLaunchKernelGGL((chunk64_kernel<IoBF16, true, true>), grid, dim3(NT), 0, s, p);
     else
       hipLaunchKernelGGL((chunk64_kernel<IoBF16, true>), grid, dim3(NT), 0, s, p);

@@ -4,7 +4,8 @@ kk / a-gate stage, the real and summary passes of the sequence split).  With
 the ring switched off (`_C._set_chunk_ring(False)`) the same entries run on
 the key-half kernel instead; these cases re-run representative parity tests
 of each entry in that configuration, so both kernels stay checked against
-the fp64 oracle."""
+the fp64 oracle.  The training backward's value pass (the reverse mode) is
+on the ring as well, and is re-run here on the key-half kernel too."""
 
 from __future__ import annotations
 
@@ -13,7 +14,9 @@ import torch
 
 import test_gpu_kk_fused as kk_tests
 import test_gpu_other_entries as entry_tests
+import test_gpu_pretrain_backward as bwd_tests
 import test_gpu_split as split_tests
+import test_gpu_statetune as st_tests
 from wkv7_testlib import require_gpu
 
 pytestmark = pytest.mark.gpu
@@ -48,3 +51,13 @@ def test_fused_kk_gate_on_the_key_half_kernel(ring_off, dtype):
                                             ((700, 64, 1, 129, 1024), (4, 320))])
 def test_split_summary_on_the_key_half_kernel(ring_off, lengths, pieces):
     split_tests.test_split_matches_oracle_and_unsplit(lengths, pieces, torch.bfloat16)
+
+
+def test_pretrain_backward_value_pass_on_the_key_half_kernel(ring_off):
+    bwd_tests.test_backward_multi_chunk_strong_inputs(1, 256, 2, 64)
+    bwd_tests.test_backward_long_sequence()
+    bwd_tests.test_backward_extreme_decay(-6.0)
+
+
+def test_statetune_value_pass_on_the_key_half_kernel(ring_off):
+    st_tests.test_statetune_uniform_layout_runs_chunked_kernels(2, 256, 16, 0.75)
