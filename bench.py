@@ -901,7 +901,7 @@ def _bwd_traffic(B, T, H):
     """Measured HBM bytes of the two backward kernels (PMC, committed), when
     the workload is the measured one."""
     wl = f"cfg1_shape_training_B{B}_T{T}_H{H}"
-    parts = [measured_traffic(k, wl) for k in ("chunk64_kernel<IoBF16,true,true>", "key_chunk_kernel")]
+    parts = [measured_traffic(k, wl) for k in ("chunk64r_kernel<IoBF16,false,true>", "key_chunk_kernel")]
     return None if any(x is None for x in parts) else sum(parts)
 
 
@@ -964,7 +964,7 @@ def time_pretrain_training(torch, w, steps: int):
         "backward_roofline": roofline_obj(bwd_bytes, bwd_ms, _bwd_traffic(B, T, H)),
         "gradients_finite": ok,
         "kernels": ["chunk64_kernel<IoBF16,true> (forward: y, sa, boundary)",
-                    "chunk64_kernel<IoBF16,true,true> (value pass: dv, dsa, P snapshots)",
+                    "chunk64r_kernel<IoBF16,false,true> (value pass: dv, dsa, P snapshots)",
                     "key_chunk_kernel (key pass: dr, dw, dk, db, da)"],
     }
 
@@ -1160,7 +1160,7 @@ def time_statetune_training(torch, w, steps: int, chunk_len: int = 1024):
                          "backward_roofline": roofline_obj(bwd_bytes, sb)},
         "gradients_finite": ok,
         "kernels": ["chunk64_kernel<IoBF16,true> (forward) + st_gather_kernel (boundaries)",
-                    "chunk64_kernel<IoBF16,true,true> + first_token_kernel + key_chunk_kernel "
+                    "chunk64r_kernel<IoBF16,false,true> + first_token_kernel + key_chunk_kernel "
                     "(backward)",
                     "token-serial: st_forward_kernel, st_value_kernel, st_key_kernel"],
     }
