@@ -74,8 +74,10 @@ struct alignas(32) KSmem {
   // masked token-token blocks in B-operand form, one per lane: the [lo | hi]
   // half of the BOp (its upper half is zero)
   bf16x8 gram[8][64];
-  // DY and DSA (hi, lo) of the chunk, [token][value], for transposed reads
-  __bf16 dyh[kL][kTP], dsh[kL][kTP], dsl[kL][kTP];
+  // the chunk's DY and V, and SA and DSA as bf16 (hi, lo) splits,
+  // [token][value]: staged once per workgroup, read by every wave as matrix
+  // operands and (DY, DSA) transposed by the carry
+  __bf16 dyh[kL][kTP], vh[kL][kTP], sah[kL][kTP], sal[kL][kTP], dsh[kL][kTP], dsl[kL][kTP];
   float dsa0[kD];   // dsa of the chunk's first token (fp32)
 };
 
@@ -119,9 +121,17 @@ __device__ __forceinline__ float row_suffix(float x) {
   return x;
 }
 
-__device__ __forceinline__ bf16x4 ld_bf4(const uint16_t* p) {
-  return __builtin_bit_cast(bf16x4, *reinterpret_cast<const u32x2*>(p));
+// Workgroup barrier over LDS only: the waves exchange data through LDS
+// alone, so the barrier waits for the wave's own LDS operations (lgkmcnt)
+// and not for its outstanding global loads, which __syncthreads' release
+// fence would wait for (the next chunk's requests stay in flight).
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
+
 __device__ __forceinline__ f32x4 ld_f4(const float* p) {
   return *reinterpret_cast<const f32x4*>(p);
 }
@@ -172,29 +182,33 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
     for (int vb = 0; vb < 4; ++vb) PcT[vb] = ld_f4(Pf + 16 * vb + 4 * q);
   }
 
-  // global inputs of one chunk
-  struct In {
-    bf16x4 DYb[4], Vb[4];
-    f32x4 SA4[4], DS4[4];
+  // Global inputs of one chunk, requested a chunk ahead.  The inputs every
+  // wave needs (dy, v, sa, dsa of the chunk's 16 tokens) are read once per
+  // workgroup: thread (token tid / 16, values 4 (tid % 16)..+3) holds its
+  // piece until the chunk starts and then stages it in LDS; the prep role's
+  // rows (w, r, k, a, b of token tid % 16, keys 4 (tid / 16)..+3) are its
+  // own.  About 22 registers stay live across a chunk, where the inputs
+  // themselves (48 per lane for each wave's full copy) could not.
+  struct Pf {
+    u32x2 dy, v;
+    f32x4 sa, ds;
     u32x2 rw, rr, rk, ra, rb;
   };
   const int tp = tid & 15, kg = tid >> 4;   // prep role: token tp, keys 4kg..4kg+3
-  auto load = [&](In& in, int m) {
+  const int st_tok = tid >> 4, st_v = 4 * (tid & 15);   // staging role
+  auto load = [&](Pf& f, int m) {
     const int t0 = kL * m;
-#pragma unroll
-    for (int vb = 0; vb < 4; ++vb) {
-      const int j0 = 16 * vb + 4 * q;
-      in.DYb[vb] = ld_bf4(p.dy + tok(t0 + n) + j0);
-      in.Vb[vb] = ld_bf4(p.v + tok(t0 + n) + j0);
-      in.SA4[vb] = ld_f4(p.sa + tok(t0 + n) + j0);
-      in.DS4[vb] = ld_f4(p.dsa + tok(t0 + n) + j0);
-    }
+    const int64_t sbase = tok(t0 + st_tok) + st_v;
+    f.dy = *reinterpret_cast<const u32x2*>(p.dy + sbase);
+    f.v = *reinterpret_cast<const u32x2*>(p.v + sbase);
+    f.sa = ld_f4(p.sa + sbase);
+    f.ds = ld_f4(p.dsa + sbase);
     const int64_t pbase = tok(t0 + tp) + 4 * kg;
-    in.rw = *reinterpret_cast<const u32x2*>(p.w + pbase);
-    in.rr = *reinterpret_cast<const u32x2*>(p.r + pbase);
-    in.rk = *reinterpret_cast<const u32x2*>(p.k + pbase);
-    in.ra = *reinterpret_cast<const u32x2*>(p.a + pbase);
-    in.rb = *reinterpret_cast<const u32x2*>(p.b + pbase);
+    f.rw = *reinterpret_cast<const u32x2*>(p.w + pbase);
+    f.rr = *reinterpret_cast<const u32x2*>(p.r + pbase);
+    f.rk = *reinterpret_cast<const u32x2*>(p.k + pbase);
+    f.ra = *reinterpret_cast<const u32x2*>(p.a + pbase);
+    f.rb = *reinterpret_cast<const u32x2*>(p.b + pbase);
   };
   auto load_s0 = [&](f32x4 (&S04)[4], int m) {
     // chunk 0 starts from state0, or from the zero state (then row 0 of
@@ -210,27 +224,30 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
   };
   f32x4 S04[4];
   load_s0(S04, m_hi);
+  Pf pf;
+  load(pf, m_hi);
   auto body = [&](int m) {
     const int t0 = kL * m;
-    In in;
-    load(in, m);
-    bf16x4 DYb[4], Vb[4];
-    float SAf[16], DSf[16], S0f[16];
-#pragma unroll
-    for (int vb = 0; vb < 4; ++vb) {
-      DYb[vb] = in.DYb[vb];
-      Vb[vb] = in.Vb[vb];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        SAf[4 * vb + e] = in.SA4[vb][e];
-        DSf[4 * vb + e] = in.DS4[vb][e];
-        S0f[4 * vb + e] = (m > 0 || p.state0 != nullptr) ? S04[vb][e] : 0.0f;
-      }
+    // the previous chunk's readers are done with the shared tiles (the
+    // barriers order LDS only: the requests for the next chunk stay in
+    // flight across them)
+    lds_barrier();
+    // ---------------- stage the chunk's shared inputs
+    {
+      *reinterpret_cast<u32x2*>(&sm.dyh[st_tok][st_v]) = pf.dy;
+      *reinterpret_cast<u32x2*>(&sm.vh[st_tok][st_v]) = pf.v;
+      uint32_t h0, l0, h1, l1;
+      split2(pf.sa[0], pf.sa[1], h0, l0);
+      split2(pf.sa[2], pf.sa[3], h1, l1);
+      *reinterpret_cast<u32x2*>(&sm.sah[st_tok][st_v]) = u32x2{h0, h1};
+      *reinterpret_cast<u32x2*>(&sm.sal[st_tok][st_v]) = u32x2{l0, l1};
+      split2(pf.ds[0], pf.ds[1], h0, l0);
+      split2(pf.ds[2], pf.ds[3], h1, l1);
+      *reinterpret_cast<u32x2*>(&sm.dsh[st_tok][st_v]) = u32x2{h0, h1};
+      *reinterpret_cast<u32x2*>(&sm.dsl[st_tok][st_v]) = u32x2{l0, l1};
+      if (st_tok == 0) *reinterpret_cast<f32x4*>(&sm.dsa0[st_v]) = pf.ds;
     }
-    const u32x2 rw = in.rw, rr = in.rr, rk = in.rk, ra = in.ra, rb = in.rb;
-
-    // the previous chunk's readers are done with the shared tiles
-    __syncthreads();
+    const u32x2 rw = pf.rw, rr = pf.rr, rk = pf.rk, ra = pf.ra, rb = pf.rb;
 
     // ---------------- prep: decays and scaled per-(key, token) factors
     {
@@ -257,29 +274,33 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
         sm.ah[key][tp] = xa * __builtin_amdgcn_exp2f(Gp - G15);
       }
     }
-    // ---------------- value-side tiles for the transposed carry product
-    {
-      Sp8 ds0 = split8(&DSf[0]), ds1 = split8(&DSf[8]);
-      const u32x4 h0 = __builtin_bit_cast(u32x4, ds0.hi), l0 = __builtin_bit_cast(u32x4, ds0.lo);
-      const u32x4 h1 = __builtin_bit_cast(u32x4, ds1.hi), l1 = __builtin_bit_cast(u32x4, ds1.lo);
+    lds_barrier();   // the staged inputs and the factors are in place
+
+    // ---------------- operand blocks (K = 32: value blocks {2mb, 2mb+1}),
+    // lane (n, q): token n, values 16vb + 4q..+3 of the staged rows
+    bf16x4 DYb[4], Vb[4], SAh[4], SAl[4], DSh[4], DSl[4];
 #pragma unroll
-      for (int vb = 0; vb < 4; ++vb) {
-        const int j0 = 16 * vb + 4 * q;
-        *reinterpret_cast<bf16x4*>(&sm.dyh[n][j0]) = DYb[vb];
-        const u32x4& hh = vb < 2 ? h0 : h1;
-        const u32x4& ll = vb < 2 ? l0 : l1;
-        const int o = (vb & 1) * 2;
-        *reinterpret_cast<u32x2*>(&sm.dsh[n][j0]) = u32x2{hh[o], hh[o + 1]};
-        *reinterpret_cast<u32x2*>(&sm.dsl[n][j0]) = u32x2{ll[o], ll[o + 1]};
-        if (n == 0) *reinterpret_cast<f32x4*>(&sm.dsa0[j0]) =
-            f32x4{DSf[4 * vb], DSf[4 * vb + 1], DSf[4 * vb + 2], DSf[4 * vb + 3]};
-      }
+    for (int vb = 0; vb < 4; ++vb) {
+      const int j0 = 16 * vb + 4 * q;
+      DYb[vb] = *reinterpret_cast<const bf16x4*>(&sm.dyh[n][j0]);
+      Vb[vb] = *reinterpret_cast<const bf16x4*>(&sm.vh[n][j0]);
+      SAh[vb] = *reinterpret_cast<const bf16x4*>(&sm.sah[n][j0]);
+      SAl[vb] = *reinterpret_cast<const bf16x4*>(&sm.sal[n][j0]);
+      DSh[vb] = *reinterpret_cast<const bf16x4*>(&sm.dsh[n][j0]);
+      DSl[vb] = *reinterpret_cast<const bf16x4*>(&sm.dsl[n][j0]);
     }
-    // ---------------- operand blocks (K = 32: value blocks {2mb, 2mb+1})
     const bf16x8 DY0 = cat8(DYb[0], DYb[1]), DY1 = cat8(DYb[2], DYb[3]);
     const bf16x8 V0 = cat8(Vb[0], Vb[1]), V1 = cat8(Vb[2], Vb[3]);
-    const Sp8 SA0 = split8(&SAf[0]), SA1 = split8(&SAf[8]);
-    const Sp8 DS0 = split8(&DSf[0]), DS1 = split8(&DSf[8]);
+    const Sp8 SA0{cat8(SAh[0], SAh[1]), cat8(SAl[0], SAl[1])};
+    const Sp8 SA1{cat8(SAh[2], SAh[3]), cat8(SAl[2], SAl[3])};
+    const Sp8 DS0{cat8(DSh[0], DSh[1]), cat8(DSl[0], DSl[1])};
+    const Sp8 DS1{cat8(DSh[2], DSh[3]), cat8(DSl[2], DSl[3])};
+    float S0f[16];
+#pragma unroll
+    for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        S0f[4 * vb + e] = (m > 0 || p.state0 != nullptr) ? S04[vb][e] : 0.0f;
     // ---------------- token-token blocks, two per wave
     {
       const f32x4 z = {0.f, 0.f, 0.f, 0.f};
@@ -336,10 +357,15 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
       for (int e = 0; e < 4; ++e) pcs0 = fmaf(PcT[vb][e], S0f[4 * vb + e], pcs0);
     pcs0 += __shfl_xor(pcs0, 16);
     pcs0 += __shfl_xor(pcs0, 32);
-    // the next (earlier) chunk's start state is requested here, a chunk ahead
-    if (m > m_lo) load_s0(S04, m - 1);
+    // the next (earlier) chunk's start state and inputs are requested here,
+    // a chunk ahead (after the products, whose operands would otherwise
+    // share the registers with them)
+    if (m > m_lo) {
+      load_s0(S04, m - 1);
+      load(pf, m - 1);
+    }
 
-    __syncthreads();
+    lds_barrier();
 
     // ---------------- token-side products
     const f32x4 bh4 = ld_f4_lds(&sm.bh[row][4 * q]), kh4 = ld_f4_lds(&sm.kh[row][4 * q]);
