@@ -196,19 +196,31 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
   };
   const int tp = tid & 15, kg = tid >> 4;   // prep role: token tp, keys 4kg..4kg+3
   const int st_tok = tid >> 4, st_v = 4 * (tid & 15);   // staging role
+  // Addresses: a block-uniform 64-bit chunk base plus a 32-bit lane offset
+  // formed at each request (opaque to loop-invariant hoisting), so that no
+  // per-lane 64-bit address stays live across the loop: such values
+  // spilled, and each reload waited for every request in flight (the
+  // vector-memory counter is in order).
+  const int ih = static_cast<int>(stride);
+  // the lane index rebuilt from the lane mask (no live input register)
+  auto lane_now = [] {
+    int l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    asm volatile("" : "+v"(l));
+    return l;
+  };
   auto load = [&](Pf& f, int m) {
-    const int t0 = kL * m;
-    const int64_t sbase = tok(t0 + st_tok) + st_v;
-    f.dy = *reinterpret_cast<const u32x2*>(p.dy + sbase);
-    f.v = *reinterpret_cast<const u32x2*>(p.v + sbase);
-    f.sa = ld_f4(p.sa + sbase);
-    f.ds = ld_f4(p.dsa + sbase);
-    const int64_t pbase = tok(t0 + tp) + 4 * kg;
-    f.rw = *reinterpret_cast<const u32x2*>(p.w + pbase);
-    f.rr = *reinterpret_cast<const u32x2*>(p.r + pbase);
-    f.rk = *reinterpret_cast<const u32x2*>(p.k + pbase);
-    f.ra = *reinterpret_cast<const u32x2*>(p.a + pbase);
-    f.rb = *reinterpret_cast<const u32x2*>(p.b + pbase);
+    const int64_t cb = tok(kL * m);
+    const int t = 64 * wv + lane_now();   // the thread index
+    const int so = (t >> 4) * ih + 4 * (t & 15), po = (t & 15) * ih + 4 * (t >> 4);
+    f.dy = *reinterpret_cast<const u32x2*>(p.dy + cb + static_cast<uint32_t>(so));
+    f.v = *reinterpret_cast<const u32x2*>(p.v + cb + static_cast<uint32_t>(so));
+    f.sa = ld_f4(p.sa + cb + static_cast<uint32_t>(so));
+    f.ds = ld_f4(p.dsa + cb + static_cast<uint32_t>(so));
+    f.rw = *reinterpret_cast<const u32x2*>(p.w + cb + static_cast<uint32_t>(po));
+    f.rr = *reinterpret_cast<const u32x2*>(p.r + cb + static_cast<uint32_t>(po));
+    f.rk = *reinterpret_cast<const u32x2*>(p.k + cb + static_cast<uint32_t>(po));
+    f.ra = *reinterpret_cast<const u32x2*>(p.a + cb + static_cast<uint32_t>(po));
+    f.rb = *reinterpret_cast<const u32x2*>(p.b + cb + static_cast<uint32_t>(po));
   };
   auto load_s0 = [&](f32x4 (&S04)[4], int m) {
     // chunk 0 starts from state0, or from the zero state (then row 0 of
@@ -218,9 +230,10 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
             ? p.state0 + static_cast<int64_t>(bidx) * p.state0_stride +
                   static_cast<int64_t>(h) * kD * kD
             : p.bnd + (static_cast<int64_t>(bh) * nchunk + max(m - 1, 0)) * kD * kD;
+    const int l = lane_now();
+    const int ro = (16 * wv + (l & 15)) * kD + 4 * (l >> 4);
 #pragma unroll
-    for (int vb = 0; vb < 4; ++vb)
-      S04[vb] = ld_f4(s0 + static_cast<int64_t>(row) * kD + 16 * vb + 4 * q);
+    for (int vb = 0; vb < 4; ++vb) S04[vb] = ld_f4(s0 + static_cast<uint32_t>(ro + 16 * vb));
   };
   f32x4 S04[4];
   load_s0(S04, m_hi);
