@@ -464,15 +464,18 @@ struct SaRows {
 };
 
 // With kTrain the chunk also writes its per-token sa rows (U, fp32) of tokens
-// 4q..4q+3 to sa_rows.at(0..3) and, when bnd_col is set, its post-chunk state
-// column to bnd_col[key * D].
+// 4q..4q+3 to sa_rows.at(0..3) — or, with sa_lds set, stages them in that
+// [token][column] LDS tile for the caller to write back — and, when bnd_col
+// is set, its post-chunk state column to bnd_col[key * D].
 // kSum (summary pass): the state update only, no outputs; with no_v the
 // value rows count as zero (the transition of the chunk).
+constexpr int UP = D + 4;   // padded row of a staged sa tile (fp32)
 template <class Io, bool kVExact, bool kTrain = false, bool kSum = false>
 __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 (&S)[4],
                                               uint16_t (*yrows)[YP], int vcol, int i, int q,
                                               float scale, const SaRows& sa_rows = SaRows{},
-                                              float* bnd_col = nullptr, bool no_v = false) {
+                                              float* bnd_col = nullptr, bool no_v = false,
+                                              float (*sa_lds)[UP] = nullptr) {
   using raw = typename Io::raw;
   // S split as B operand against the permuted A~ / R~ rows: K positions
   // 8q..8q+7 = rows 32m + 4q + (0..3) then 32m + 16 + 4q + (0..3)
@@ -518,7 +521,12 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
     Y = mm_ab(o.Mrb, Us, Y);
     if constexpr (kTrain) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) *sa_rows.at(e) = Uf[e];
+      for (int e = 0; e < 4; ++e) {
+        if (sa_lds != nullptr)
+          sa_lds[4 * q + e][vcol] = Uf[e];
+        else
+          *sa_rows.at(e) = Uf[e];
+      }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -550,7 +558,12 @@ __device__ __forceinline__ void state_compute(const StateOps<kVExact>& o, f32x4 
     Y = mm_ab(o.Mrb, Us, Y);
     if constexpr (kTrain) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) *sa_rows.at(e) = Uf[e];
+      for (int e = 0; e < 4; ++e) {
+        if (sa_lds != nullptr)
+          sa_lds[4 * q + e][vcol] = Uf[e];
+        else
+          *sa_rows.at(e) = Uf[e];
+      }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -1120,6 +1133,7 @@ template <bool kVExact>
 struct alignas(16) SmemR {
   ChunkOps<kVExact> ops[kRingOf<kVExact>];   // ring by chunk index mod kRing
   uint16_t yb[L][YP];                 // staged output rows of the current chunk
+  float ub[L][UP];                    // staged sa rows (the value pass)
   // progress counters, each written by one wave only: chunks key wave w has
   // built (its chunks are w, w + kKeyW, ...) and chunks state wave w has
   // finished
@@ -1454,7 +1468,16 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
         const bool keep = bnd_base != nullptr && bi % p.boundary_every == 0;
         state_compute<Io, kVExact, true>(
             o, S, &sm.yb[0], vcol, i, q, p.scale, sa_rows,
-            keep ? bnd_base + static_cast<int64_t>(bi / p.boundary_every) * D * D : nullptr);
+            keep ? bnd_base + static_cast<int64_t>(bi / p.boundary_every) * D * D : nullptr,
+            false, &sm.ub[0]);
+        // the staged sa rows of this wave's 16 columns as 16-byte pieces:
+        // lane l takes token l / 4, columns 16 (wv % 4) + 4 (l % 4)..+3 (the
+        // band is this wave's alone and its LDS accesses complete in order)
+        const int u_tok = lane >> 2, u_c = 16 * (wv & 3) + 4 * (lane & 3);
+        const int upos = c * L + u_tok;
+        const int urow = upos == 0 ? t0 : t1 - upos;
+        *reinterpret_cast<f32x4*>(sa_base - vcol + static_cast<int64_t>(urow) * row_stride + u_c) =
+            *reinterpret_cast<const f32x4*>(&sm.ub[u_tok][u_c]);
       } else {
         state_compute<Io, kVExact>(o, S, &sm.yb[0], vcol, i, q, p.scale);
       }
