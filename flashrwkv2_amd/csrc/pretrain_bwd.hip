@@ -531,7 +531,7 @@ int launch_d(const PretrainBwdArgs& p, hipStream_t s) {
     // dsa.  At D = 64 it runs on the chunked MFMA kernel's reverse mode and
     // keeps P at the start of every span of chunks for the chunk-form key
     // pass (csrc/pretrain_bwd_chunk.hip).
-    const int cps = key_chunk_span(p.tokens);
+    const int cps = key_chunk_span(p.batch, p.tokens, p.heads);
     const int nchunk = p.tokens / kChunk;
     const int nspan = (nchunk + cps - 1) / cps;
     float* pbnd = p.workspace + static_cast<int64_t>(p.batch) * p.tokens * p.heads * D;
@@ -579,7 +579,7 @@ int launch_d(const PretrainBwdArgs& p, hipStream_t s) {
 int64_t pretrain_backward_workspace_floats(int B, int T, int H, int D) {
   int64_t n = static_cast<int64_t>(B) * T * H * D;
   if (D == 64) {
-    const int cps = key_chunk_span(T);
+    const int cps = key_chunk_span(B, T, H);
     const int nspan = (T / kChunk + cps - 1) / cps;
     n += static_cast<int64_t>(B) * H * nspan * D * D;
   }

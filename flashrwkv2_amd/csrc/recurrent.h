@@ -210,7 +210,9 @@ int launch_pretrain_backward(int D, const PretrainBwdArgs& p, hipStream_t s);
 // fp32 elements of the backward's workspace: dsa [B,T,H,D], and at D = 64
 // the value pass's P snapshots [B,H,spans,D,D] (one per span of chunks)
 int64_t pretrain_backward_workspace_floats(int B, int T, int H, int D);
-int key_chunk_span(int tokens);
+// chunks per workgroup span of the key pass (and per P snapshot of the
+// value pass) for a [B, T, H] backward
+int key_chunk_span(int batch, int tokens, int heads);
 int launch_key_chunk(const PretrainBwdArgs& a, const float* pbnd, int nspan, int cps,
                      hipStream_t s);
 
