@@ -116,3 +116,33 @@ def test_real_stall_fails_closed_after_one_wait(ring):
     assert torch.equal(pool, before)
     # 512 groups; polling every hand-off to the limit takes seconds
     assert dt < 0.5, dt
+
+
+@pytest.mark.parametrize("ring", [True, False])
+def test_value_pass_give_up_fails_closed(ring):
+    """The training backward's value pass (the chunked kernel's reverse mode)
+    under a spin limit of zero: every block gives up at its first wait,
+    counts itself and writes NaN for dv (and for the dsa the key pass reads),
+    so no finite gradient of v comes out of a failed hand-off."""
+    C = require_gpu()
+    from flashrwkv2_amd.tmix.wkv7 import pretrain_tmix_wkv7_recurrent_bf16
+
+    print(f"case value pass spin limit 0, B=2 T=64 H=2, ring={ring}", flush=True)
+    C._set_chunk_ring(ring)
+    g = torch.Generator().manual_seed(74)
+    shape = (2, 64, 2 * 64)
+    vals = [(torch.randn(shape, generator=g) * 0.1).to(torch.bfloat16).cuda().requires_grad_()
+            for _ in range(6)]
+    dy = torch.randn(shape, generator=g).to(torch.bfloat16).cuda()
+    y = pretrain_tmix_wkv7_recurrent_bf16(*vals, head_size=64)   # forward at the normal limit
+    torch.cuda.synchronize()
+    C.handoff_fault_count(reset=True)
+    C._set_handoff_spin_limit(0)
+    try:
+        y.backward(dy)
+        torch.cuda.synchronize()
+    finally:
+        C._set_handoff_spin_limit(-1)
+        C._set_chunk_ring(True)
+    assert C.handoff_fault_count(reset=True) == 4   # one per (batch, head) block
+    assert torch.isnan(vals[3].grad.float()).all()
