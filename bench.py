@@ -1043,7 +1043,9 @@ def time_statetune_ragged(torch, w, steps: int):
         finally:
             CC._statetune_force_serial = False
         out[name] = {"forward_ms": round(f_ms, 4), "backward_ms": round(b_ms, 4),
-                     "path": type(res["snap"]).__name__}
+                     # the chunked forward returns its padded-grid plan for the
+                     # backward; the token-serial one returns nothing
+                     "path": "padded_chunked" if res["snap"] is not None else "token_serial"}
     out["gradients_finite"] = all(bool(torch.isfinite(t).all()) for t in (*grads, g0))
     del state, dy, y, boundary, sa, grads, res
     torch.cuda.empty_cache()
