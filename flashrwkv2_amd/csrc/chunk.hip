@@ -1493,13 +1493,11 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
       wait_ge(&sm.ready[c % kKeyW], c / kKeyW + 1, p.spin_limit, &sm.fault);   // operators of c
       const StateOps<kVExact> o = state_load(sm.ops[c % kRing], vcol, i, q);
       if constexpr (kRev) {
-        // sa rows t0 + (n - pos) mod n of the segment, which is t1 - pos
-        // except at pos = 0 (written from the staged tile below; sa_rows is
-        // not used)
-        SaRows sa_rows;
-        const int bi = kRev ? p.boundary_per_seg - 1 - c : c;
+        // sa goes to the staged tile (written back below), the snapshot is
+        // stored here: state_compute gets neither row pointers nor a column
+        const int bi = p.boundary_per_seg - 1 - c;
         const bool keep = bnd_base != nullptr && bi % p.boundary_every == 0;
-        state_compute<Io, kVExact, true>(o, S, &sm.yb[0], vcol, i, q, p.scale, sa_rows, nullptr,
+        state_compute<Io, kVExact, true>(o, S, &sm.yb[0], vcol, i, q, p.scale, SaRows{}, nullptr,
                                          false, &sm.ub[0]);
         if (keep) {
           // the post-chunk state as 16-byte row pieces (store_state_tile)
@@ -1509,7 +1507,9 @@ __global__ __launch_bounds__(NTR) void chunk64r_kernel(SegArgs p) {
         }
         // the staged sa rows of this wave's 16 columns as 16-byte pieces:
         // lane l takes token l / 4, columns 16 (wv % 4) + 4 (l % 4)..+3 (the
-        // band is this wave's alone and its LDS accesses complete in order)
+        // band is this wave's alone and its LDS accesses complete in order),
+        // to row t0 + (n - pos) mod n of the segment, which is t1 - pos
+        // except at pos = 0
         const int u_tok = lane >> 2, u_c = 16 * (wv & 3) + 4 * (lane & 3);
         const int upos = c * L + u_tok;
         const int urow = upos == 0 ? t0 : t1 - upos;
