@@ -122,6 +122,10 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
   using raw = typename Io::raw;
   constexpr bool kVExact = !__is_same(Io, IoF16);
   __shared__ WaveLds<kVExact, kRO> lds[WPB];
+  // per-channel parameters of each wave's head, staged once: -log2(e) times
+  // the decay bias, and (fused stages) k_k, the a-gate bias a0, k_a, r_k
+  // (kept apart from the wave blocks, whose layout they would shift)
+  __shared__ __attribute__((aligned(16))) float chp_all[WPB][(kKK || kRO) ? 5 : 1][D];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -225,10 +229,27 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
   // they would otherwise hold 16-64 registers across the whole loop)
   // (called with the chunk's opaque lane index, so that the per-lane
   // addresses are formed per chunk instead of being hoisted and spilled)
-  auto channel8 = [&](const void* base, int m, float* out, int lq) {
-    const char* hb = static_cast<const char*>(base) + head_off * static_cast<int64_t>(sizeof(raw));
-    unpack8<Io>(*reinterpret_cast<const u32x4*>(hb + static_cast<uint32_t>(16 * lq + 64 * m)), out);
+  // They come from the wave's LDS copy (staged below): a global load here
+  // would be issued after the next chunk's row requests, and the vector-
+  // memory counter is in order, so waiting for it waited for those rows.
+  auto channel8 = [&](int which, int m, float* out, int lq) {
+    const float* a = &chp_all[wv][which][32 * m + 8 * lq];
+    *reinterpret_cast<f32x4*>(out) = *reinterpret_cast<const f32x4*>(a);
+    *reinterpret_cast<f32x4*>(out + 4) = *reinterpret_cast<const f32x4*>(a + 4);
   };
+  {
+    auto stage = [&](int which, const void* base, float scale) {
+      chp_all[wv][which][lane] =
+          base != nullptr ? scale * Io::to_f32(static_cast<const raw*>(base)[head_off + lane]) : 0.0f;
+    };
+    if (bias != nullptr) stage(0, bias, -kLog2e);
+    if constexpr (kKK) {
+      stage(1, p.kk_scale, 1.0f);
+      stage(2, p.a_bias, 1.0f);
+      stage(3, p.k_a, 1.0f);
+    }
+    if constexpr (kRO) stage(4, p.ro_rk, 1.0f);
+  }
 
   constexpr float kC = kNegExpHalf * kLog2e;
   constexpr float kInvC = 1.0f / kC;
@@ -259,7 +280,7 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
       for (int m = 0; m < 2; ++m) {
         float xk[8], kks[8];
         unpack8<Io>(rows[2][m], xk);
-        channel8(p.kk_scale, m, kks, lq);
+        channel8(1, m, kks, lq);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float u = xk[e] * kks[e];
@@ -283,9 +304,9 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
         float kks[8], a0[8], ka[8], x12[8];
         unpack8<Io>(rows[2][m], xk);
         unpack8<Io>(rows[4][m], x12);
-        channel8(p.kk_scale, m, kks, lq);
-        channel8(p.a_bias, m, a0, lq);
-        channel8(p.k_a, m, ka, lq);
+        channel8(1, m, kks, lq);
+        channel8(2, m, a0, lq);
+        channel8(3, m, ka, lq);
         u32x4 packed;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -308,7 +329,7 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
           // the readout's residual weight uses the key as stored
           float kq[8], rk[8];
           unpack8<Io>(packed, kq);
-          channel8(p.ro_rk, m, rk, lq);
+          channel8(4, m, rk, lq);
 #pragma unroll
           for (int e = 0; e < 8; ++e) rkv_part = __builtin_fmaf(xr[e] * kq[e], rk[e], rkv_part);
         }
@@ -317,11 +338,9 @@ __global__ __launch_bounds__(64 * WPB, 2) void chunk64w_kernel(SegArgs p, int nu
         unpack8<Io>(valid ? rows[4][m] : zero4, xa);
         unpack8<Io>(valid ? rows[5][m] : zero4, xb);
       }
-      float nb[8];
+      float nb[8];   // -log2(e) decay_bias
       if (bias != nullptr) {
-        channel8(bias, m, nb, lq);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) nb[e] *= -kLog2e;
+        channel8(0, m, nb, lq);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) nb[e] = 0.f;
