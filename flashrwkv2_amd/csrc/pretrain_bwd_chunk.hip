@@ -147,8 +147,14 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
   __shared__ KSmem sm;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int n = lane & 15, q = lane >> 4;
-  const int span = blockIdx.x % p.nspan;
-  const int bh = blockIdx.x / p.nspan;
+  // Workgroup order: every (batch, head)'s spans but its last first, then
+  // the last spans (shorter when the span length does not divide the chunk
+  // count), which fill the final round of workgroups.
+  const int nfull = p.nspan - 1;
+  const int nlead = static_cast<int>(gridDim.x / p.nspan) * nfull;
+  const int gid = static_cast<int>(blockIdx.x);
+  const int span = gid < nlead ? gid % nfull : nfull;
+  const int bh = gid < nlead ? gid / nfull : gid - nlead;
   const int bidx = bh / p.H, h = bh % p.H;
   const int nchunk = p.T / kL;
   const int64_t stride = static_cast<int64_t>(p.H) * kD;
@@ -469,15 +475,74 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
 
 }  // namespace
 
-// Spans of 16 chunks halve the P snapshots (their writes in the value pass
-// and reads here) and the per-span start-up, and measured 1.4 % faster at
-// the config-1 shape (1.157 vs 1.173 ms; 4 chunks: 1.187 ms).  They are
-// used when the pass still has at least 2 048 workgroups (about 2.7 waves
-// of three per CU on 256 CUs); shorter problems keep spans of 8 chunks for
-// the parallelism.
+// Span length.  Short problems (fewer than 2 048 workgroups at 16-chunk
+// spans, about 2.7 per slot of the 768 below) keep 8-chunk spans for the
+// parallelism.  Larger ones take the length from 8 to 17 chunks that gives
+// the shortest modelled makespan: the workgroups run three per CU on
+// MI355X's 256 CUs (768 slots), each costing its chunks plus one chunk of
+// span start-up, dispatched in the kernel's order (full spans first, each
+// (batch, head)'s shorter last span after them) onto the least loaded slot.
+// A length that leaves the last round mostly empty loses up to a round: at
+// the config-1 shape (256 (batch, head) units of 256 chunks) 16-chunk spans
+// are 4 096 workgroups = 5.3 rounds, and 17-chunk spans (15 full + one of a
+// single chunk) run the whole backward 1.141 -> 1.086 ms (11: 1.081,
+// 15: 1.086, 18: 1.092).  The choice depends on the shape alone, so the
+// workspace query and the launch agree.
+namespace {
+
+// makespan of n_full jobs of length d then n_short of length e (e <= d),
+// each on the least loaded of `slots` equal slots
+double greedy_makespan(int64_t n_full, double d, int64_t n_short, double e, int64_t slots) {
+  struct Level { double load; int64_t count; };
+  Level g[3] = {{static_cast<double>(n_full / slots) * d, slots - n_full % slots},
+                {static_cast<double>(n_full / slots + 1) * d, n_full % slots},
+                {0.0, 0}};
+  int ng = g[1].count > 0 ? 2 : 1;
+  int64_t left = n_short;
+  while (left > 0) {
+    int lo = 0;
+    for (int j = 1; j < ng; ++j)
+      if (g[j].load < g[lo].load) lo = j;
+    if (left < g[lo].count) {          // some slots of the level take one more
+      g[ng++] = {g[lo].load + e, left};
+      g[lo].count -= left;
+      left = 0;
+    } else {                           // the whole level takes one more
+      left -= g[lo].count;
+      g[lo].load += e;
+    }
+    // merge equal levels (the short jobs catch up with the long ones)
+    if (ng == 2 && g[0].load == g[1].load) {
+      g[0].count += g[1].count;
+      ng = 1;
+    }
+  }
+  double m = 0.0;
+  for (int j = 0; j < ng; ++j)
+    if (g[j].count > 0) m = fmax(m, g[j].load);
+  return m;
+}
+
+}  // namespace
+
 int key_chunk_span(int batch, int tokens, int heads) {
-  const int64_t spans16 = static_cast<int64_t>(batch) * heads * ((tokens / kL + 15) / 16);
-  return spans16 >= 2048 ? 16 : 8;
+  const int64_t units = static_cast<int64_t>(batch) * heads;
+  const int nchunk = tokens / kL;
+  if (units * ((nchunk + 15) / 16) < 2048) return 8;
+  constexpr int64_t kSlots = 3 * 256;
+  constexpr double kStart = 1.0;   // span start-up, in chunks
+  int best = 16;
+  double best_t = 0.0;
+  for (int cps = 17; cps >= 8; --cps) {   // ties keep the longer span
+    const int nspan = (nchunk + cps - 1) / cps;
+    const int last = nchunk - (nspan - 1) * cps;
+    const double t = greedy_makespan(units * (nspan - 1), cps + kStart, units, last + kStart, kSlots);
+    if (cps == 17 || t < best_t) {
+      best = cps;
+      best_t = t;
+    }
+  }
+  return best;
 }
 
 int launch_key_chunk(const PretrainBwdArgs& a, const float* pbnd, int nspan, int cps,

@@ -207,3 +207,37 @@ def test_dispatch_query_rejects_bad_arguments(lib):
         N.FR2_ERR_INVALID_ARGUMENT
     assert lib.fr2_wkv7_recurrent_fp32_dispatch(4, 4, 96, 10, 10, ctypes.byref(fam)) == \
         N.FR2_ERR_UNSUPPORTED
+
+
+def _brute_span(batch, tokens, heads):
+    """The key pass's span length by brute force: every candidate's
+    workgroups (each (batch, head)'s full spans first, then its last span)
+    placed one by one on the least loaded of 768 slots, each costing its
+    chunks plus one; the shortest makespan wins, ties to the longer span."""
+    import heapq
+
+    units, nchunk = batch * heads, tokens // 16
+    if units * ((nchunk + 15) // 16) < 2048:
+        return 8
+    best = None
+    for cps in range(17, 7, -1):
+        nspan = -(-nchunk // cps)
+        last = nchunk - (nspan - 1) * cps
+        slots = [0.0] * 768
+        for d in [cps + 1.0] * (units * (nspan - 1)) + [last + 1.0] * units:
+            heapq.heappush(slots, heapq.heappop(slots) + d)
+        t = max(slots)
+        if best is None or t < best[1]:
+            best = (cps, t)
+    return best[0]
+
+
+@pytest.mark.parametrize("batch,tokens,heads", [
+    (8, 4096, 32), (1, 4096, 128), (4, 8192, 64), (8, 2048, 32), (64, 1024, 64),
+    (2, 4096, 32), (3, 6144, 48), (16, 4096, 40),
+])
+def test_key_pass_span_matches_a_brute_force_schedule(lib, batch, tokens, heads):
+    ws = lib.fr2_wkv7_pretrain_backward_workspace_floats(batch, tokens, heads, 64)
+    nspan = (ws - batch * tokens * heads * 64) // (batch * heads * 64 * 64)
+    cps = _brute_span(batch, tokens, heads)
+    assert nspan == -(-(tokens // 16) // cps)
