@@ -267,6 +267,11 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
       if (st_tok == 0) *reinterpret_cast<f32x4*>(&sm.dsa0[st_v]) = pf.ds;
     }
     const u32x2 rw = pf.rw, rr = pf.rr, rk = pf.rk, ra = pf.ra, rb = pf.rb;
+    // the next (earlier) chunk's shared inputs are requested as soon as this
+    // chunk's are staged: issued here rather than after the state products
+    // they measured 2.3 % faster over the whole backward (1.088 -> 1.062 ms
+    // at the config-1 shape), bit-identical
+    if (m > m_lo) load(pf, m - 1);
 
     // ---------------- prep: decays and scaled per-(key, token) factors
     {
@@ -376,13 +381,10 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
       for (int e = 0; e < 4; ++e) pcs0 = fmaf(PcT[vb][e], S0f[4 * vb + e], pcs0);
     pcs0 += __shfl_xor(pcs0, 16);
     pcs0 += __shfl_xor(pcs0, 32);
-    // the next (earlier) chunk's start state and inputs are requested here,
-    // a chunk ahead (after the products, whose operands would otherwise
-    // share the registers with them)
-    if (m > m_lo) {
-      load_s0(S04, m - 1);
-      load(pf, m - 1);
-    }
+    // the next (earlier) chunk's start state is requested here, a chunk
+    // ahead (after the products, whose operands would otherwise share the
+    // registers with it)
+    if (m > m_lo) load_s0(S04, m - 1);
 
     lds_barrier();
 
