@@ -905,6 +905,30 @@ def _bwd_traffic(B, T, H):
     return None if any(x is None for x in parts) else sum(parts)
 
 
+def _launch_ms(torch, stream, call, name, steps, warmup=5, passes=3):
+    """Per-launch time (ms) of a C-ABI call returning a status: `warmup`
+    untimed launches, then `passes` passes of `steps` launches, each between
+    HIP events on the launch stream; the median pass."""
+    from flashrwkv2_amd import _native as N
+
+    for _ in range(warmup):
+        N.check(call(), name)
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(passes):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            rc = call()
+            if rc:
+                N.check(rc, name)
+        end.record(stream)
+        torch.cuda.synchronize()
+        per.append(start.elapsed_time(end) / steps)
+    return sorted(per)[len(per) // 2]
+
+
 def lib_ws(B, T, H, D):
     from flashrwkv2_amd import _native as N
 
@@ -914,8 +938,9 @@ def lib_ws(B, T, H, D):
 def time_pretrain_training(torch, w, steps: int):
     """The [B,T,H,D] training path on a config-1-shaped batch: per-launch
     times (ms) of the forward (y, state_dot_a, boundary) and of the backward
-    (two kernels), each launched `steps` times through the C ABI between HIP
-    events on the launch stream."""
+    (two kernels) through the C ABI: the median of three passes of `steps`
+    launches between HIP events on the launch stream, after five warm-up
+    launches (`_launch_ms`)."""
     from flashrwkv2_amd import _native as N
 
     B, T, H = w.info["B"], w.info["T"], w.info["H"]
@@ -938,18 +963,7 @@ def time_pretrain_training(torch, w, steps: int):
                 work.data_ptr(), *(t.data_ptr() for t in grads), stream.cuda_stream)
 
     def timed(fn, args, name):
-        N.check(fn(*args), name)  # warm-up
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(steps):
-            rc = fn(*args)
-            if rc:
-                N.check(rc, name)
-        end.record(stream)
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / steps
+        return _launch_ms(torch, stream, lambda: fn(*args), name, steps)
 
     fwd_ms = timed(lib.fr2_wkv7_pretrain_forward, fwd_args, "fr2_wkv7_pretrain_forward")
     bwd_ms = timed(lib.fr2_wkv7_pretrain_backward, bwd_args, "fr2_wkv7_pretrain_backward")
@@ -1120,18 +1134,7 @@ def time_statetune_training(torch, w, steps: int, chunk_len: int = 1024):
             work_s.data_ptr(), *gptrs, g0.data_ptr(), 1.0, hs)
 
     def timed(fn, name):
-        N.check(fn(), name)
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(steps):
-            rc = fn()
-            if rc:
-                N.check(rc, name)
-        end.record(stream)
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / steps
+        return _launch_ms(torch, stream, fn, name, steps)
 
     sf = timed(fwd_serial, "fr2_wkv7_statetune_forward")
     sb = timed(bwd_serial, "fr2_wkv7_statetune_backward")
