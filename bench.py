@@ -211,7 +211,7 @@ def cpu_info() -> dict:
 
 
 def cpu_baseline_plan(threads: int, repeats: int = 20) -> dict:
-    """The CPU baseline BASELINE.md plans: the pure-torch per-token fp32 loop
+    """The planned pure-torch CPU baseline: the per-token fp32 loop
     (the form of the reference's test oracle, vectorised over heads) on config
     0 and on one config-2 decode step, median of `repeats` timed runs after a
     warm-up, with torch limited to `threads` threads."""

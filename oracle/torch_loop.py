@@ -3,8 +3,8 @@
 The form of the reference's own test oracle (tests/tmix/wkv7/test.py:66-83:
 one Python iteration per token, the state as a [H, D, D] tensor, the decay
 from the logits by csrc/sm120/tmix/wkv7/recurrent_decay.cuh:10-22), here
-vectorised over heads.  ``bench.py`` times it on the host as the CPU baseline
-BASELINE.md's plan names (config 0 and one config-2 decode step); it is
+vectorised over heads.  ``bench.py`` times it on the host as the planned
+pure-torch CPU baseline (config 0 and one config-2 decode step); it is
 checked against the fp64 C oracle in tests/test_oracle.py.
 """
 
