@@ -493,36 +493,36 @@ __global__ __launch_bounds__(kKNT, 3) void key_chunk_kernel(KPassArgs p) {
 namespace {
 
 // makespan of n_full jobs of length d then n_short of length e (e <= d),
-// each on the least loaded of `slots` equal slots
+// each on the least loaded of `slots` equal slots, in closed form: the full
+// jobs leave two levels d apart; the short ones fill the lower level up to
+// the upper one, then go round all slots, the lower of the two levels first
 double greedy_makespan(int64_t n_full, double d, int64_t n_short, double e, int64_t slots) {
-  struct Level { double load; int64_t count; };
-  Level g[3] = {{static_cast<double>(n_full / slots) * d, slots - n_full % slots},
-                {static_cast<double>(n_full / slots + 1) * d, n_full % slots},
-                {0.0, 0}};
-  int ng = g[1].count > 0 ? 2 : 1;
+  const int64_t k = n_full / slots, r = n_full % slots;
+  double lo = static_cast<double>(k) * d, hi = lo + d;
+  int64_t clo = slots - r;
+  const int64_t chi = r;
   int64_t left = n_short;
-  while (left > 0) {
-    int lo = 0;
-    for (int j = 1; j < ng; ++j)
-      if (g[j].load < g[lo].load) lo = j;
-    if (left < g[lo].count) {          // some slots of the level take one more
-      g[ng++] = {g[lo].load + e, left};
-      g[lo].count -= left;
-      left = 0;
-    } else {                           // the whole level takes one more
-      left -= g[lo].count;
-      g[lo].load += e;
-    }
-    // merge equal levels (the short jobs catch up with the long ones)
-    if (ng == 2 && g[0].load == g[1].load) {
-      g[0].count += g[1].count;
-      ng = 1;
-    }
+  if (left == 0) return chi > 0 ? hi : lo;
+  if (chi == 0) return lo + static_cast<double>(left / slots) * e + (left % slots ? e : 0.0);
+  const int64_t rounds = static_cast<int64_t>(ceil((hi - lo) / e));
+  if (left <= rounds * clo)
+    return fmax(hi, lo + static_cast<double>(left / clo) * e + (left % clo ? e : 0.0));
+  left -= rounds * clo;
+  lo += static_cast<double>(rounds) * e;   // now within e above hi
+  double a = hi, b = lo;
+  int64_t ca = chi;
+  if (b < a) {
+    const double t = a;
+    a = b;
+    b = t;
+    ca = clo;
   }
-  double m = 0.0;
-  for (int j = 0; j < ng; ++j)
-    if (g[j].count > 0) m = fmax(m, g[j].load);
-  return m;
+  const double full = static_cast<double>(left / slots) * e;
+  const int64_t rem = left % slots;
+  a += full;
+  b += full;
+  if (rem == 0) return fmax(a, b);
+  return rem <= ca ? fmax(b, a + e) : b + e;
 }
 
 }  // namespace

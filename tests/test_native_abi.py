@@ -234,7 +234,8 @@ def _brute_span(batch, tokens, heads):
 
 @pytest.mark.parametrize("batch,tokens,heads", [
     (8, 4096, 32), (1, 4096, 128), (4, 8192, 64), (8, 2048, 32), (64, 1024, 64),
-    (2, 4096, 32), (3, 6144, 48), (16, 4096, 40),
+    (2, 4096, 32), (3, 6144, 48), (16, 4096, 40), (64, 4096, 64), (5, 3072, 24),
+    (1, 16384, 40), (7, 4000, 33),
 ])
 def test_key_pass_span_matches_a_brute_force_schedule(lib, batch, tokens, heads):
     ws = lib.fr2_wkv7_pretrain_backward_workspace_floats(batch, tokens, heads, 64)
